@@ -1,0 +1,471 @@
+// api.hip — the extern "C" entry points of include/ditch_hip.h.
+//
+// Every function catches everything (nothing unwinds across the boundary),
+// returns a status code and leaves a message in ditch_hip_last_error; a NULL
+// context fails cleanly (src/metal/shim.h:6-7 conventions).
+#include <string.h>
+
+#include <memory>
+
+#include "internal.h"
+#include "model.h"
+
+namespace ditch {
+void dequant_to_host(ditch_hip *h, void *out, const ditch_weight *w, uint64_t row0, uint64_t nrows);
+ditch_hip_model *model_create(ditch_hip *h, const ditch_model_config *cfg);
+void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_weight *w);
+void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64_t rank, const float *a,
+                     const float *b);
+void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight);
+void model_reset_deltas(ditch_hip_model *m);
+uint64_t model_bytes(const ditch_hip_model *m);
+void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vector<ditch_row> &rows,
+                   const ditch_row *d_rows, int64_t n, const uint64_t *d_capture, int64_t n_capture, float *d_res,
+                   const uint64_t *d_logit_rows, int64_t n_logit, float *d_logits);
+
+// Device buffer owned for the duration of one call.
+struct Tmp {
+    void *p = nullptr;
+    explicit Tmp(size_t bytes) { p = dev_alloc(bytes); }
+    ~Tmp() { dev_free(p); }
+    template <typename T>
+    T *as() { return (T *)p; }
+};
+
+static void h2d(void *d, const void *hsrc, size_t bytes, hipStream_t s) {
+    if (bytes) DITCH_TRY_HIP(hipMemcpyAsync(d, hsrc, bytes, hipMemcpyHostToDevice, s));
+}
+static void d2h(void *hdst, const void *d, size_t bytes, hipStream_t s) {
+    if (bytes) DITCH_TRY_HIP(hipMemcpyAsync(hdst, d, bytes, hipMemcpyDeviceToHost, s));
+}
+
+template <typename F>
+static int32_t guarded(ditch_hip *h, F &&f) {
+    if (!h) return DITCH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(h->mu);
+    try {
+        f();
+        h->last_error.clear();
+        return DITCH_OK;
+    } catch (const Error &e) {
+        h->last_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        h->last_error = "host out of memory";
+        return DITCH_OUT_OF_MEMORY;
+    } catch (...) {
+        h->last_error = "unexpected failure";
+        return DITCH_DEVICE_FAILED;
+    }
+}
+
+}  // namespace ditch
+
+using namespace ditch;
+
+extern "C" {
+
+ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
+    auto fail = [&](const std::string &m) -> ditch_hip * {
+        if (err && err_len) {
+            strncpy(err, m.c_str(), err_len - 1);
+            err[err_len - 1] = 0;
+        }
+        return nullptr;
+    };
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return fail("no HIP device");
+    if (device < 0 || device >= count) return fail("device index out of range");
+    if (hipSetDevice(device) != hipSuccess) return fail("hipSetDevice failed");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return fail("hipGetDeviceProperties failed");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(std::string("this library is built for gfx950, the device is ") + prop.gcnArchName);
+    auto *h = new (std::nothrow) ditch_hip();
+    if (!h) return fail("host out of memory");
+    h->device = device;
+    h->cu_count = prop.multiProcessorCount;
+    h->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete h;
+        return fail("hipStreamCreate failed");
+    }
+    return h;
+}
+
+void ditch_hip_close(ditch_hip *h) {
+    if (!h) return;
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+const char *ditch_hip_name(ditch_hip *h) { return h ? h->name.c_str() : ""; }
+const char *ditch_hip_last_error(ditch_hip *h) { return h ? h->last_error.c_str() : "null context"; }
+void ditch_hip_forget_weights(ditch_hip *h) { (void)h; }
+void *ditch_hip_stream(ditch_hip *h) { return h ? (void *)h->stream : nullptr; }
+int32_t ditch_hip_sync(ditch_hip *h) {
+    return guarded(h, [&] { DITCH_TRY_HIP(hipStreamSynchronize(h->stream)); });
+}
+
+// ---------------------------------------------------------------------------
+// VTable operations, host memory
+
+int32_t ditch_hip_matmulT(ditch_hip *h, float *out, const float *x, uint64_t n, const ditch_weight *w) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && out && x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0 || w->rows == 0) return;
+        hipStream_t s = h->stream;
+        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        Tmp dx(n * w->cols * 4), dout(n * w->rows * 4);
+        h2d(dx.p, x, n * w->cols * 4, s);
+        launch_matmul(t->v, dout.as<float>(), dx.as<float>(), (int64_t)n, MatmulEpilogue{}, s);
+        d2h(out, dout.p, n * w->rows * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_matvecTMulti(ditch_hip *h, float *out, const ditch_weight *w, const float *y, uint64_t q) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && out && y, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (q == 0) return;
+        hipStream_t s = h->stream;
+        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        Tmp dy(q * w->rows * 4), dout(q * w->cols * 4), part(matvecT_partials_floats(t->v, q) * 4);
+        h2d(dy.p, y, q * w->rows * 4, s);
+        launch_matvecT(dout.as<float>(), t->v, dy.as<float>(), (int64_t)q, s, part.as<float>());
+        d2h(out, dout.p, q * w->cols * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_rowNorms(ditch_hip *h, float *out, const ditch_weight *w) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && out, DITCH_INVALID_ARGUMENT, "NULL argument");
+        hipStream_t s = h->stream;
+        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        Tmp dout(w->rows * 4);
+        launch_row_norms(dout.as<float>(), t->v, s);
+        d2h(out, dout.p, w->rows * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_attentionScores(ditch_hip *h, float *scores, uint64_t n_keys, const float *q, uint64_t hd,
+                                  const float *k, uint64_t stride, float scale) {
+    return guarded(h, [&] {
+        DITCH_CHECK(scores && q && k && stride >= hd, DITCH_INVALID_ARGUMENT, "attentionScores arguments");
+        if (n_keys == 0) return;
+        hipStream_t s = h->stream;
+        size_t kb = ((n_keys - 1) * stride + hd) * 4;
+        Tmp dq(hd * 4), dk(kb), ds(n_keys * 4);
+        h2d(dq.p, q, hd * 4, s);
+        h2d(dk.p, k, kb, s);
+        launch_attention_scores(ds.as<float>(), n_keys, dq.as<float>(), hd, dk.as<float>(), stride, scale, s);
+        d2h(scores, ds.p, n_keys * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_attentionValues(ditch_hip *h, float *out, uint64_t vd, const float *scores, uint64_t n_keys,
+                                  const float *v, uint64_t stride) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out && scores && v && stride >= vd, DITCH_INVALID_ARGUMENT, "attentionValues arguments");
+        hipStream_t s = h->stream;
+        if (vd == 0) return;
+        size_t vb = n_keys ? ((n_keys - 1) * stride + vd) * 4 : 4;
+        Tmp dsc(n_keys * 4 + 4), dv(vb), dout(vd * 4);
+        h2d(dsc.p, scores, n_keys * 4, s);
+        if (n_keys) h2d(dv.p, v, vb, s);
+        launch_attention_values(dout.as<float>(), vd, dsc.as<float>(), n_keys, dv.as<float>(), stride, s);
+        d2h(out, dout.p, vd * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_gatedActivation(ditch_hip *h, uint32_t act, float *out, const float *gate, const float *up,
+                                  uint64_t n, uint64_t len, uint64_t in_stride, uint64_t out_stride) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out && gate && act <= 5 && in_stride >= len && out_stride >= len, DITCH_INVALID_ARGUMENT,
+                    "gatedActivation arguments");
+        if (n == 0 || len == 0) return;
+        hipStream_t s = h->stream;
+        size_t ib = ((n - 1) * in_stride + len) * 4, ob = ((n - 1) * out_stride + len) * 4;
+        Tmp dg(ib), du(up ? ib : 4), dout(ob);
+        h2d(dg.p, gate, ib, s);
+        if (up) h2d(du.p, up, ib, s);
+        // rows of `out` between the written spans keep their contents
+        h2d(dout.p, out, ob, s);
+        launch_gated_act(act, dout.as<float>(), dg.as<float>(), up ? du.as<float>() : nullptr, n, len, in_stride,
+                         out_stride, s);
+        d2h(out, dout.p, ob, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_rmsnormRows(ditch_hip *h, float *out, const float *x, const float *weight, uint64_t weight_len,
+                              uint64_t n, uint64_t len, float eps, int32_t gemma_style) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out && x && (weight_len == 0 || (weight && weight_len >= len)), DITCH_INVALID_ARGUMENT,
+                    "rmsnormRows arguments");
+        if (n == 0 || len == 0) return;
+        hipStream_t s = h->stream;
+        Tmp dx(n * len * 4), dw(weight_len * 4 + 4), dout(n * len * 4);
+        h2d(dx.p, x, n * len * 4, s);
+        if (weight_len) h2d(dw.p, weight, len * 4, s);
+        launch_rmsnorm(dout.as<float>(), dx.as<float>(), dw.as<float>(), weight_len ? (int64_t)len : 0, n, len, eps,
+                       gemma_style, s);
+        d2h(out, dout.p, n * len * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_layernormRows(ditch_hip *h, float *out, const float *x, const float *weight, uint64_t weight_len,
+                                const float *bias, uint64_t n, uint64_t len, float eps, int32_t one_plus) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out && x && (weight_len == 0 || (weight && weight_len >= len)), DITCH_INVALID_ARGUMENT,
+                    "layernormRows arguments");
+        if (n == 0 || len == 0) return;
+        hipStream_t s = h->stream;
+        Tmp dx(n * len * 4), dw(len * 4), db(len * 4), dout(n * len * 4);
+        h2d(dx.p, x, n * len * 4, s);
+        if (weight_len) h2d(dw.p, weight, len * 4, s);
+        if (bias) h2d(db.p, bias, len * 4, s);
+        launch_layernorm(dout.as<float>(), dx.as<float>(), dw.as<float>(), weight_len ? (int64_t)len : 0,
+                         bias ? db.as<float>() : nullptr, n, len, eps, one_plus, s);
+        d2h(out, dout.p, n * len * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_softmaxRows(ditch_hip *h, float *x, uint64_t n, uint64_t len) {
+    return guarded(h, [&] {
+        DITCH_CHECK(x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0 || len == 0) return;
+        hipStream_t s = h->stream;
+        Tmp dx(n * len * 4);
+        h2d(dx.p, x, n * len * 4, s);
+        launch_softmax_rows(dx.as<float>(), n, len, s);
+        d2h(x, dx.p, n * len * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_ropeRows(ditch_hip *h, float *x, uint64_t n, uint64_t dim, const float *cos_table,
+                           const float *sin_table, uint64_t table_len, uint64_t half, const uint32_t *pos,
+                           uint32_t style) {
+    return guarded(h, [&] {
+        DITCH_CHECK(x && cos_table && sin_table && pos && style <= 1 && 2 * half >= dim, DITCH_INVALID_ARGUMENT,
+                    "ropeRows arguments");
+        for (uint64_t i = 0; i < n; i++) DITCH_CHECK(pos[i] < table_len, DITCH_INVALID_ARGUMENT, "position beyond the table");
+        if (n == 0 || dim == 0) return;
+        hipStream_t s = h->stream;
+        Tmp dx(n * dim * 4), dc(table_len * half * 4), dsn(table_len * half * 4), dp(n * 4);
+        h2d(dx.p, x, n * dim * 4, s);
+        h2d(dc.p, cos_table, table_len * half * 4, s);
+        h2d(dsn.p, sin_table, table_len * half * 4, s);
+        h2d(dp.p, pos, n * 4, s);
+        launch_rope_rows(dx.as<float>(), n, dim, dc.as<float>(), dsn.as<float>(), half, dp.as<uint32_t>(), style, s);
+        d2h(x, dx.p, n * dim * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Decode
+
+int32_t ditch_hip_dequant(ditch_hip *h, void *out, const ditch_weight *w, uint64_t row0, uint64_t nrows) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && out, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (nrows == 0) return;
+        dequant_to_host(h, out, w, row0, nrows);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Resident tensors
+
+ditch_hip_tensor *ditch_hip_upload(ditch_hip *h, const ditch_weight *w) {
+    ditch_hip_tensor *t = nullptr;
+    int32_t rc = guarded(h, [&] {
+        DITCH_CHECK(w, DITCH_INVALID_ARGUMENT, "NULL weight");
+        t = upload_weight(h, w, h->stream);
+    });
+    return rc == DITCH_OK ? t : nullptr;
+}
+
+void ditch_hip_tensor_free(ditch_hip *h, ditch_hip_tensor *t) {
+    if (h) (void)hipStreamSynchronize(h->stream);
+    free_tensor(t);
+}
+
+uint64_t ditch_hip_tensor_bytes(const ditch_hip_tensor *t) { return t ? t->bytes : 0; }
+
+int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, const ditch_hip_tensor *t, uint64_t row0,
+                                 uint64_t nrows) {
+    return guarded(h, [&] {
+        DITCH_CHECK(t && d_out && row0 + nrows <= (uint64_t)t->v.rows, DITCH_INVALID_ARGUMENT, "tensor_dequant range");
+        launch_dequant(t->v, d_out, (int64_t)row0, (int64_t)nrows, h->stream);
+    });
+}
+
+int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x, uint64_t n, const ditch_hip_tensor *w,
+                                 const float *d_bias, int32_t accumulate, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && d_out && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        MatmulEpilogue ep;
+        ep.bias = d_bias;
+        ep.accumulate = accumulate;
+        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Model
+
+ditch_hip_model *ditch_hip_model_create(ditch_hip *h, const ditch_model_config *cfg) {
+    ditch_hip_model *m = nullptr;
+    int32_t rc = guarded(h, [&] {
+        DITCH_CHECK(cfg, DITCH_INVALID_ARGUMENT, "NULL config");
+        m = model_create(h, cfg);
+    });
+    return rc == DITCH_OK ? m : nullptr;
+}
+
+void ditch_hip_model_free(ditch_hip_model *m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->h->stream);
+    delete m;
+}
+
+int32_t ditch_hip_model_set(ditch_hip_model *m, int32_t layer, int32_t slot, int32_t expert, const ditch_weight *w) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(w, DITCH_INVALID_ARGUMENT, "NULL weight");
+        model_set(m, layer, slot, expert, w);
+    });
+}
+
+int32_t ditch_hip_model_set_delta(ditch_hip_model *m, int32_t layer, int32_t slot, int32_t expert, uint64_t rank,
+                                  const float *a, const float *b) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(rank == 0 || (a && b), DITCH_INVALID_ARGUMENT, "NULL delta");
+        model_set_delta(m, layer, slot, expert, rank, a, b);
+    });
+}
+
+int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] { model_reset_deltas(m); });
+}
+
+uint64_t ditch_hip_model_bytes(const ditch_hip_model *m) { return m ? model_bytes(m) : 0; }
+
+int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens, const ditch_row *rows, uint64_t n,
+                          const uint64_t *capture_rows, uint64_t n_capture, float *residuals,
+                          const uint64_t *logit_rows, uint64_t n_logit, float *logits) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(tokens && rows, DITCH_INVALID_ARGUMENT, "NULL tokens/rows");
+        DITCH_CHECK(n_capture == 0 || (capture_rows && residuals), DITCH_INVALID_ARGUMENT, "capture buffers");
+        DITCH_CHECK(n_logit == 0 || (logit_rows && logits), DITCH_INVALID_ARGUMENT, "logit buffers");
+        if (n == 0) return;
+        const ditch_model_config &c = m->c;
+        for (uint64_t i = 0; i < n; i++)
+            DITCH_CHECK(tokens[i] < (m->embed.t ? (uint64_t)m->embed.t->v.rows : 0), DITCH_INVALID_ARGUMENT,
+                        "token id outside the embedding table");
+        for (uint64_t i = 0; i < n_capture; i++) DITCH_CHECK(capture_rows[i] < n, DITCH_INVALID_ARGUMENT, "capture row");
+        for (uint64_t i = 0; i < n_logit; i++) DITCH_CHECK(logit_rows[i] < n, DITCH_INVALID_ARGUMENT, "logit row");
+        hipStream_t s = m->h->stream;
+        std::vector<ditch_row> hrows(rows, rows + n);
+        size_t res_bytes = (c.layers + 1) * n_capture * c.hidden * 4, log_bytes = n_logit * c.vocab * 4;
+        Tmp dt(n * 4), dr(n * sizeof(ditch_row)), dc(n_capture * 8 + 8), dl(n_logit * 8 + 8), dres(res_bytes + 4),
+            dlog(log_bytes + 4);
+        h2d(dt.p, tokens, n * 4, s);
+        h2d(dr.p, rows, n * sizeof(ditch_row), s);
+        h2d(dc.p, capture_rows, n_capture * 8, s);
+        h2d(dl.p, logit_rows, n_logit * 8, s);
+        model_forward(m, dt.as<uint32_t>(), hrows, dr.as<ditch_row>(), (int64_t)n, dc.as<uint64_t>(),
+                      (int64_t)n_capture, n_capture ? dres.as<float>() : nullptr, dl.as<uint64_t>(), (int64_t)n_logit,
+                      n_logit ? dlog.as<float>() : nullptr);
+        d2h(residuals, dres.p, n_capture ? res_bytes : 0, s);
+        d2h(logits, dlog.p, n_logit ? log_bytes : 0, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_forward_device(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, uint64_t n,
+                                 const uint64_t *d_capture_rows, uint64_t n_capture, float *d_residuals,
+                                 const uint64_t *d_logit_rows, uint64_t n_logit, float *d_logits) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(d_tokens && d_rows, DITCH_INVALID_ARGUMENT, "NULL tokens/rows");
+        if (n == 0) return;
+        hipStream_t s = m->h->stream;
+        // the row descriptors size the KV cache: read them back once
+        std::vector<ditch_row> hrows(n);
+        d2h(hrows.data(), d_rows, n * sizeof(ditch_row), s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+        model_forward(m, d_tokens, hrows, d_rows, (int64_t)n, d_capture_rows, (int64_t)n_capture, d_residuals,
+                      d_logit_rows, (int64_t)n_logit, d_logits);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Edit, log-softmax, KL
+
+int32_t ditch_hip_edit_delta(ditch_hip *h, float *a, float *b, const ditch_weight *w, const float *v, uint64_t k,
+                             float weight) {
+    return guarded(h, [&] {
+        DITCH_CHECK(a && b && w && v && k > 0, DITCH_INVALID_ARGUMENT, "edit_delta arguments");
+        hipStream_t s = h->stream;
+        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        Tmp dv(k * w->rows * 4), da(k * w->cols * 4), part(matvecT_partials_floats(t->v, k) * 4);
+        h2d(dv.p, v, k * w->rows * 4, s);
+        launch_matvecT(da.as<float>(), t->v, dv.as<float>(), (int64_t)k, s, part.as<float>());
+        d2h(a, da.p, k * w->cols * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+        for (uint64_t i = 0; i < w->rows; i++)
+            for (uint64_t j = 0; j < k; j++) b[i * k + j] = -weight * v[j * w->rows + i];
+    });
+}
+
+int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot, int32_t expert, const float *v,
+                             uint64_t k, float weight) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(v && k > 0, DITCH_INVALID_ARGUMENT, "edit arguments");
+        model_edit(m, layer, slot, expert, v, k, weight);
+    });
+}
+
+int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x, uint64_t n, uint64_t len) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out && x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0 || len == 0) return;
+        hipStream_t s = h->stream;
+        Tmp dx(n * len * 4), dout(n * len * 4);
+        h2d(dx.p, x, n * len * 4, s);
+        launch_log_softmax_rows(dout.as<float>(), dx.as<float>(), n, len, s);
+        d2h(out, dout.p, n * len * 4, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_klRows(ditch_hip *h, double *kl, const float *base_logprobs, const float *trial_logits, uint64_t n,
+                         uint64_t vocab) {
+    return guarded(h, [&] {
+        DITCH_CHECK(kl && base_logprobs && trial_logits, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0) return;
+        hipStream_t s = h->stream;
+        Tmp db(n * vocab * 4), dt(n * vocab * 4), dk(n * 8);
+        h2d(db.p, base_logprobs, n * vocab * 4, s);
+        h2d(dt.p, trial_logits, n * vocab * 4, s);
+        launch_kl_rows(dk.as<double>(), db.as<float>(), dt.as<float>(), n, vocab, s);
+        d2h(kl, dk.p, n * 8, s);
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,165 @@
+// internal.h — shared declarations of libditch_hip (not part of the ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/ditch_hip.h"
+
+namespace ditch {
+
+// ---------------------------------------------------------------------------
+// Errors: every entry point returns a status and records a message.
+
+struct Error {
+    int32_t code;
+    std::string msg;
+};
+
+#define DITCH_TRY_HIP(expr)                                                          \
+    do {                                                                             \
+        hipError_t e_ = (expr);                                                      \
+        if (e_ != hipSuccess)                                                        \
+            throw ::ditch::Error{e_ == hipErrorOutOfMemory ? DITCH_OUT_OF_MEMORY     \
+                                                           : DITCH_DEVICE_FAILED,    \
+                                 std::string(#expr) + ": " + hipGetErrorString(e_)}; \
+    } while (0)
+
+#define DITCH_CHECK(cond, code, msg)                                  \
+    do {                                                              \
+        if (!(cond)) throw ::ditch::Error{(code), std::string(msg)}; \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Weight tiles in HBM.
+//
+// Codes are re-tiled at upload so that one 16-byte load per lane yields the
+// lane's B operand of v_mfma_f32_16x16x32_bf16 (weight row n = lane % 16,
+// k = 8 * (lane / 16) .. +8 within a 32-wide k tile). A "unit" is 16 weight
+// rows by unit_k columns, 64 lanes x 16 bytes (32 for f32):
+//   TF_BF16, TF_F16 : unit_k 32,  one k tile per 16 B
+//   TF_F32          : unit_k 32,  32 B per lane (two 16 B halves)
+//   TF_Q8, TF_FP8   : unit_k 64,  8 codes for each of 2 k tiles
+//   TF_MX4, TF_INT4 : unit_k 128, 8 nibbles for each of 4 k tiles
+// Units are stored [n / 16][k / unit_k] (k fastest). Rows pad to 16 and
+// columns to unit_k with zero codes. Scales stay in plain row-major arrays.
+enum TileFormat : int32_t {
+    TF_BF16 = 0,
+    TF_F16 = 1,
+    TF_F32 = 2,
+    TF_Q8 = 3,    // GGUF Q8_0: int8 codes, f16 scale per (row, 32 columns)
+    TF_FP8 = 4,   // E4M3/E5M2 codes, scale grid
+    TF_MX4 = 5,   // E2M1 codes, E8M0 scale per (row, 32 columns)
+    TF_INT4 = 6,  // 4-bit pack-quantized: (q - zp) * scale per group
+};
+
+__host__ __device__ inline int unit_k_of(int tf) {
+    return (tf == TF_Q8 || tf == TF_FP8) ? 64 : (tf == TF_MX4 || tf == TF_INT4) ? 128 : 32;
+}
+__host__ __device__ inline int unit_bytes_of(int tf) { return tf == TF_F32 ? 2048 : 1024; }
+
+// Kernel-side view of a resident weight (passed by value).
+struct TileView {
+    const uint8_t *codes;
+    const void *scale;      // Q8: f16 [rows][kt]; MX4: u8 [rows][kt]; FP8: grid; INT4: [rows][groups]
+    const uint8_t *zero;    // INT4: zero point (field value) [rows][groups], or null
+    int32_t tf;
+    int32_t scale_type;     // decode.h ScaleType
+    int64_t rows, cols;     // logical
+    int64_t units_k;        // units per 16-row group
+    int64_t scale_cols;     // row stride of the scale array (FP8: grid cols)
+    int64_t block_rows, block_cols, row_shard;  // FP8 grid
+    int64_t group;          // INT4 group size
+    int32_t e5m2;
+    int32_t orig_dtype;     // ditch_weight dtype the tensor came from
+};
+
+}  // namespace ditch
+
+struct ditch_hip_tensor {
+    ditch::TileView v;
+    void *codes = nullptr;
+    void *scale = nullptr;
+    void *zero = nullptr;
+    uint64_t bytes = 0;
+};
+
+struct ditch_hip {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    std::string last_error;
+    std::mutex mu;
+    // scratch buffers reused by the host-memory entry points
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    int cu_count = 0;
+};
+
+namespace ditch {
+
+// Device memory helpers (all on the context stream).
+void *dev_alloc(size_t bytes);
+void dev_free(void *p);
+void *ctx_scratch(ditch_hip *h, size_t bytes);
+
+// tiles.hip
+ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s);
+void free_tensor(ditch_hip_tensor *t);
+void launch_dequant(const TileView &v, void *out, int64_t row0, int64_t nrows, hipStream_t s);
+bool is_bf16_virtual(int32_t dtype);
+
+// gemm.hip
+struct MatmulEpilogue {
+    const float *bias = nullptr;  // [rows]
+    int accumulate = 0;           // out += result
+    // low-rank delta: out[i][r] += sum_j b[r][j] * xa[i][j]
+    const float *delta_b = nullptr;  // [rows][rank]
+    const float *delta_xa = nullptr; // [n][rank]
+    int delta_rank = 0;
+};
+void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
+                   hipStream_t s, const int32_t *row_index = nullptr);
+// One product per segment (routed experts): segment z multiplies rows
+// [off, off + cnt) of x (through row_index when given) by its own weight
+// into rows [off, off + cnt) of out. Every segment has rows x cols weights
+// of tile format tf.
+struct GroupSeg {
+    TileView w;
+    int64_t off, cnt;
+    const float *delta_b;
+    int delta_rank;
+};
+void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols,
+                           int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
+                           const float *delta_xa, hipStream_t s);
+
+// ops.hip
+void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
+                    float eps, int gemma, hipStream_t s, const int64_t *row_index = nullptr);
+void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
+                            int64_t in_stride, int64_t out_stride, float eps, hipStream_t s);
+void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
+                      int64_t len, float eps, int one_plus, hipStream_t s);
+void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
+void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s);
+void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s);
+void launch_gated_act(uint32_t act, float *out, const float *gate, const float *up, int64_t n, int64_t len,
+                      int64_t in_stride, int64_t out_stride, hipStream_t s);
+void launch_rope_rows(float *x, int64_t n, int64_t dim, const float *cos_t, const float *sin_t, int64_t half,
+                      const uint32_t *pos, uint32_t style, hipStream_t s);
+void launch_attention_scores(float *scores, int64_t n_keys, const float *q, int64_t hd, const float *k,
+                             int64_t stride, float scale, hipStream_t s);
+void launch_attention_values(float *out, int64_t vd, const float *scores, int64_t n_keys, const float *v,
+                             int64_t stride, hipStream_t s);
+void launch_row_norms(float *out, const TileView &w, hipStream_t s);
+void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials);
+size_t matvecT_partials_floats(const TileView &w, int64_t q);
+void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank,
+                     hipStream_t s);
+
+}  // namespace ditch

@@ -1,0 +1,886 @@
+// model.hip — the resident forward pass (model.zig:4619-4959), routed MoE
+// (moe.zig:998-1228) and DeepSeek MLA (model.zig:3292-3342) over weights
+// registered in HBM. Activations stay on the device for the whole call.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+
+#include "decode.h"
+#include "internal.h"
+#include "tiled.h"
+#include "model.h"
+
+namespace ditch {
+
+
+static int grid_for(int64_t total, int block = 256) {
+    int64_t g = (total + block - 1) / block;
+    if (g > 65536) g = 65536;
+    return g < 1 ? 1 : (int)g;
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+
+// x[i] = embedding row tokens[i] widened to f32 (model.zig:4673-4675).
+__global__ void embed_kernel(float *x, TileView w, const uint32_t *tokens, int64_t n) {
+    int64_t total = n * w.cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = i / w.cols, c = i % w.cols;
+        uint16_t b;
+        x[i] = tiled_element_f32(w, (int64_t)tokens[r], c, &b);
+    }
+}
+
+// residuals[entry][ci] = x[capture_rows[ci]] (model.zig:4856-4862)
+__global__ void capture_kernel(float *res, const float *x, const uint64_t *rows, int64_t n_capture, int64_t hidden) {
+    int64_t total = n_capture * hidden;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t ci = i / hidden, c = i % hidden;
+        res[i] = x[(int64_t)rows[ci] * hidden + c];
+    }
+}
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Per row: q/k head RMSNorm (qwen3 "head"), RoPE of [off, off + rot) of every
+// head, and the k/v rows written into the cache slot (b, pos)
+// (model.zig:4253-4295). One block per row, one wave per head.
+struct RopeArgs {
+    float *q, *k;
+    const float *v;
+    float *kc, *vc;
+    const ditch_row *rows;
+    const float *cos_t, *sin_t;
+    const float *q_norm, *k_norm;
+    int64_t n, heads, kv_heads, hd, rope_off, rot, half, rope_len, T, kvd;
+    float eps;
+    int style;
+};
+
+// One head vector: optional RMSNorm (x * inv * w, tensor.zig:1167-1179), then
+// RoPE of [rope_off, rope_off + rot) on the normalised values. Every element
+// is read and then written by exactly one lane, after the wave has reduced
+// the sum of squares, so the update is in place without a hazard. `dst2`
+// (the cache slot of a key head) receives the same values.
+__device__ void head_norm_rope(float *x, float *dst2, const float *nw, const RopeArgs &a, int64_t pos) {
+    int lane = threadIdx.x & 63;
+    float inv = 1.0f;
+    if (nw) {
+        float ss = 0.f;
+        for (int64_t d = lane; d < a.hd; d += 64) ss = __builtin_fmaf(x[d], x[d], ss);
+        ss = wave_sum64(ss);
+        inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)a.hd), a.eps)));
+    }
+    auto val = [&](int64_t d) { return nw ? __fmul_rn(__fmul_rn(x[d], inv), nw[d]) : x[d]; };
+    int64_t r0 = a.rot > 0 ? a.rope_off : a.hd, r1 = a.rot > 0 ? a.rope_off + 2 * a.half : a.hd;
+    // coordinates outside the rotated range
+    for (int64_t d = lane; d < a.hd; d += 64) {
+        if (d >= r0 && d < r1) continue;
+        float v = val(d);
+        x[d] = v;
+        if (dst2) dst2[d] = v;
+    }
+    if (a.rot > 0) {
+        int64_t p = pos < a.rope_len - 1 ? pos : a.rope_len - 1;
+        const float *cr = a.cos_t + p * a.half, *sr = a.sin_t + p * a.half;
+        for (int64_t i = lane; i < a.half; i += 64) {
+            int64_t ia = a.rope_off + (a.style == DITCH_ROPE_GPTJ ? 2 * i : i);
+            int64_t ib = a.rope_off + (a.style == DITCH_ROPE_GPTJ ? 2 * i + 1 : i + a.half);
+            float x1 = val(ia), x2 = val(ib), c = cr[i], s = sr[i];
+            float ya = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+            float yb = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+            x[ia] = ya;
+            x[ib] = yb;
+            if (dst2) {
+                dst2[ia] = ya;
+                dst2[ib] = yb;
+            }
+        }
+    }
+}
+
+__global__ void qk_rope_cache_kernel(RopeArgs a) {
+    int64_t i = blockIdx.x;
+    int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int64_t pos = a.rows[i].pos, b = a.rows[i].b;
+    float *kd = a.kc + (b * a.T + pos) * a.kvd, *vd = a.vc + (b * a.T + pos) * a.kvd;
+    for (int64_t h = wave; h < a.heads + a.kv_heads; h += nw) {
+        if (h < a.heads) {
+            head_norm_rope(a.q + (i * a.heads + h) * a.hd, nullptr, a.q_norm, a, pos);
+        } else {
+            int64_t kh = h - a.heads;
+            head_norm_rope(a.k + (i * a.kv_heads + kh) * a.hd, kd + kh * a.hd, a.k_norm, a, pos);
+        }
+    }
+    for (int64_t d = threadIdx.x; d < a.kvd; d += blockDim.x) vd[d] = a.v[i * a.kvd + d];
+}
+
+// Causal attention of one (row, head) per wave (model.zig:2935-2986): scores
+// for keys 0..pos of the row's prompt, softmax (Cephes exp, tensor.zig:
+// 1181-1200), then the weighted sum of values. Output compacted to
+// [n][heads][vd] (model.zig:4338-4345).
+struct AttnArgs {
+    const float *q, *kc, *vc;
+    float *out;
+    const ditch_row *rows;
+    int64_t n, heads, groups, hd, vd, T, kvd;
+    float scale;
+};
+
+constexpr int ATT_MAXK = 1024;  // keys per row held in LDS
+
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+    __shared__ float sc[4][ATT_MAXK];
+    __shared__ float qs[4][512];
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int64_t task = (int64_t)blockIdx.x * 4 + wave;
+    if (task >= a.n * a.heads) return;
+    int64_t r = task / a.heads, h = task % a.heads;
+    int64_t pos = a.rows[r].pos, b = a.rows[r].b;
+    int64_t kvh = h / a.groups;
+    const float *q = a.q + (r * a.heads + h) * a.hd;
+    for (int64_t d = lane; d < a.hd; d += 64) qs[wave][d] = q[d];
+    __builtin_amdgcn_wave_barrier();
+    int64_t n_keys = pos + 1;
+    const float *kb = a.kc + (b * a.T) * a.kvd + kvh * a.hd;
+    const float *vb = a.vc + (b * a.T) * a.kvd + kvh * a.hd;
+    float m = -INFINITY;
+    for (int64_t p = lane; p < n_keys; p += 64) {
+        const float *kr = kb + p * a.kvd;
+        float s = 0.f;
+        for (int64_t d = 0; d < a.hd; d++) s = __builtin_fmaf(kr[d], qs[wave][d], s);
+        s = __fmul_rn(s, a.scale);
+        sc[wave][p] = s;
+        m = fmaxf(m, s);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float sum = 0.f;
+    for (int64_t p = lane; p < n_keys; p += 64) {
+        float e = exp_cephes(__fsub_rn(sc[wave][p], m));
+        sc[wave][p] = e;
+        sum += e;
+    }
+    sum = wave_sum64(sum);
+    float inv = __fdiv_rn(1.0f, sum);
+    __builtin_amdgcn_wave_barrier();
+    float *o = a.out + (r * a.heads + h) * a.vd;
+    for (int64_t d = lane; d < a.vd; d += 64) {
+        float acc = 0.f;
+        for (int64_t p = 0; p < n_keys; p++) acc = __builtin_fmaf(vb[p * a.kvd + d], __fmul_rn(sc[wave][p], inv), acc);
+        o[d] = acc;
+    }
+}
+
+// MLA: k = [kv_b nope | k_pe], v = [kv_b v | 0] per head (model.zig:3330-3341)
+__global__ void mla_assemble_kernel(float *k, float *v, const float *kvb, const float *kva, int64_t n, int64_t heads,
+                                    int64_t hd, int64_t nope, int64_t rd, int64_t vd, int64_t kv_lora) {
+    int64_t total = n * heads * hd;
+    int64_t kvr = kv_lora + rd, kvb_rows = heads * (nope + vd);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t t = i / (heads * hd), h = (i / hd) % heads, d = i % hd;
+        const float *src = kvb + t * kvb_rows + h * (nope + vd);
+        k[i] = d < nope ? src[d] : kva[t * kvr + kv_lora + (d - nope)];
+        v[i] = d < vd ? src[nope + d] : 0.f;
+    }
+}
+
+// Router (moe.zig:1011-1101) for one token per thread: softmax or sigmoid
+// scores, correction bias, group-limited masking, top-k with strict '>',
+// renormalisation and scaling.
+struct RouteArgs {
+    float *logits;          // [n][E], scores in place
+    const float *corr;      // [E] or null
+    int32_t *sel;           // [n][k]
+    float *selw;            // [n][k]
+    int64_t n, E, k, n_group, topk_group;
+    int scoring, group_limited, norm_topk;
+    float scaling;
+};
+
+constexpr int ROUTE_MAXE = 512;
+constexpr int ROUTE_MAXG = 64;
+
+__global__ void route_kernel(RouteArgs a) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= a.n) return;
+    float *row = a.logits + t * a.E;
+    if (a.scoring == DITCH_SCORING_SOFTMAX) {
+        float m = -INFINITY;
+        for (int64_t e = 0; e < a.E; e++) m = fmaxf(m, row[e]);
+        float s = 0.f;
+        for (int64_t e = 0; e < a.E; e++) {
+            float v = exp_cephes(__fsub_rn(row[e], m));
+            row[e] = v;
+            s = __fadd_rn(s, v);
+        }
+        float inv = __fdiv_rn(1.0f, s);
+        for (int64_t e = 0; e < a.E; e++) row[e] = __fmul_rn(row[e], inv);
+    } else {
+        for (int64_t e = 0; e < a.E; e++) row[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-row[e])));
+    }
+    float choice[ROUTE_MAXE];
+    for (int64_t e = 0; e < a.E; e++) choice[e] = __fadd_rn(row[e], a.corr ? a.corr[e] : 0.0f);
+    if (a.group_limited && a.n_group > 1) {
+        int64_t per = a.E / a.n_group;
+        float gs[ROUTE_MAXG];
+        bool kept[ROUTE_MAXG];
+        for (int64_t g = 0; g < a.n_group; g++) {
+            kept[g] = false;
+            const float *s = choice + g * per;
+            if (a.corr) {
+                float b1 = -INFINITY, b2 = -INFINITY;
+                for (int64_t i = 0; i < per; i++) {
+                    if (s[i] > b1) { b2 = b1; b1 = s[i]; }
+                    else if (s[i] > b2) b2 = s[i];
+                }
+                gs[g] = __fadd_rn(b1, per > 1 ? b2 : 0.0f);
+            } else {
+                float best = -INFINITY;
+                for (int64_t i = 0; i < per; i++) best = fmaxf(best, s[i]);
+                gs[g] = best;
+            }
+        }
+        int64_t keep = a.topk_group < a.n_group ? a.topk_group : a.n_group;
+        for (int64_t kk = 0; kk < keep; kk++) {
+            int64_t best = 0;
+            float bv = -INFINITY;
+            for (int64_t g = 0; g < a.n_group; g++)
+                if (!kept[g] && gs[g] > bv) { bv = gs[g]; best = g; }
+            // a group already kept scores NaN in the reference and never wins again
+            kept[best] = true;
+            gs[best] = __uint_as_float(0x7fc00000u);
+        }
+        for (int64_t g = 0; g < a.n_group; g++)
+            if (!kept[g])
+                for (int64_t i = 0; i < per; i++) choice[g * per + i] = -INFINITY;
+    }
+    float sum = 0.f;
+    for (int64_t j = 0; j < a.k; j++) {
+        int64_t best = 0;
+        float bv = -INFINITY;
+        for (int64_t e = 0; e < a.E; e++)
+            if (choice[e] > bv) { bv = choice[e]; best = e; }
+        a.sel[t * a.k + j] = (int32_t)best;
+        a.selw[t * a.k + j] = row[best];
+        choice[best] = -INFINITY;
+        sum = __fadd_rn(sum, row[best]);
+    }
+    if (a.norm_topk && sum > 0)
+        for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fdiv_rn(a.selw[t * a.k + j], sum);
+    if (a.scaling != 1.0f)
+        for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fmul_rn(a.selw[t * a.k + j], a.scaling);
+}
+
+// Per-expert token counts.
+__global__ void expert_count_kernel(const int32_t *sel, int64_t nk, int32_t *counts) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nk; i += (int64_t)gridDim.x * blockDim.x)
+        atomicAdd(&counts[sel[i]], 1);
+}
+
+// Expert e's pair list in (token, slot) order (moe.zig:1174-1188): one block
+// per expert walks the selections in order and compacts its matches.
+__global__ void expert_list_kernel(const int32_t *sel, int64_t n, int64_t k, const int32_t *offsets, int32_t *pair_token,
+                                   int32_t *pair_of) {
+    __shared__ int32_t base;
+    int e = blockIdx.x;
+    if (threadIdx.x == 0) base = offsets[e];
+    __syncthreads();
+    int64_t nk = n * k;
+    for (int64_t c0 = 0; c0 < nk; c0 += blockDim.x) {
+        int64_t i = c0 + threadIdx.x;
+        bool hit = i < nk && sel[i] == e;
+        // block-wide exclusive scan of hits
+        __shared__ int32_t wave_cnt[4];
+        unsigned long long ballot = __ballot(hit);
+        int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        int before = __popcll(ballot & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_cnt[wave] = __popcll(ballot);
+        __syncthreads();
+        int prefix = 0;
+        for (int w = 0; w < wave; w++) prefix += wave_cnt[w];
+        int total = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+        if (hit) {
+            int p = base + prefix + before;
+            pair_token[p] = (int32_t)(i / k);
+            pair_of[i] = p;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) base += total;
+        __syncthreads();
+    }
+}
+
+// out[t] = x[t] + (sum over the token's experts in ascending index of
+// w * eo + shared) (moe.zig:1197-1227 then the residual add).
+__global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared, const int32_t *sel,
+                                   const float *selw, const int32_t *pair_of, int64_t n, int64_t k, int64_t hidden) {
+    int64_t total = n * hidden;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t t = i / hidden, c = i % hidden;
+        // experts of this token in ascending index order (k is small)
+        int32_t order[16];
+        for (int64_t j = 0; j < k; j++) order[j] = (int32_t)j;
+        for (int64_t a1 = 1; a1 < k; a1++)
+            for (int64_t b1 = a1; b1 > 0 && sel[t * k + order[b1]] < sel[t * k + order[b1 - 1]]; b1--) {
+                int32_t tmp = order[b1];
+                order[b1] = order[b1 - 1];
+                order[b1 - 1] = tmp;
+            }
+        float m = 0.f;
+        for (int64_t j = 0; j < k; j++) {
+            int64_t s = t * k + order[j];
+            m = __fadd_rn(m, __fmul_rn(selw[s], eo[(int64_t)pair_of[s] * hidden + c]));
+        }
+        if (eo_shared) m = __fadd_rn(m, eo_shared[i]);
+        x[i] = __fadd_rn(x[i], m);
+    }
+}
+
+__global__ void add_rows_kernel(float *x, const float *y, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = __fadd_rn(x[i], y[i]);
+}
+
+// xa[p][j] = dot(a_e_j, x_row(p)) for the pairs of every expert segment
+struct SegDelta {
+    const float *a;  // [rank][cols] or null
+    int64_t off, cnt;
+    int rank;
+};
+__global__ void grouped_delta_xa_kernel(float *xa, const float *x, const int32_t *row_index, const SegDelta *segs,
+                                        int64_t cols, int max_rank) {
+    int lane = threadIdx.x & 63;
+    const SegDelta &s = segs[blockIdx.y];
+    int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (s.rank == 0 || t >= s.cnt * s.rank) return;
+    int64_t pl = t / s.rank, j = t % s.rank;
+    int64_t p = s.off + pl;
+    int64_t src = row_index ? row_index[p] : p;
+    float acc = 0.f;
+    for (int64_t c = lane; c < cols; c += 64) acc = __builtin_fmaf(s.a[j * cols + c], x[src * cols + c], acc);
+    acc = wave_sum64(acc);
+    if (lane == 0) xa[p * s.rank + j] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+}  // namespace ditch
+
+namespace ditch {
+
+static void host_fill_rope(const ditch_model_config &c, std::vector<float> &cos_t, std::vector<float> &sin_t);
+
+static Vec upload_vec(const ditch_weight *w, hipStream_t s) {
+    // norms / biases: widen to f32 on the host side of the upload
+    int64_t len = (int64_t)(w->rows * w->cols);
+    std::vector<float> host(len);
+    for (int64_t i = 0; i < len; i++) {
+        switch (w->dtype) {
+        case DITCH_F32: host[i] = ((const float *)w->data)[i]; break;
+        case DITCH_BF16: {
+            uint32_t b = (uint32_t)((const uint16_t *)w->data)[i] << 16;
+            memcpy(&host[i], &b, 4);
+            break;
+        }
+        case DITCH_F16: {
+            uint16_t hb = ((const uint16_t *)w->data)[i];
+            uint32_t sign = (uint32_t)(hb & 0x8000u) << 16, e = (hb >> 10) & 0x1fu, m = hb & 0x3ffu, bits;
+            if (e == 0) {
+                float f = (float)m * 5.9604644775390625e-08f;
+                host[i] = sign ? -f : f;
+                continue;
+            }
+            bits = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+            memcpy(&host[i], &bits, 4);
+            break;
+        }
+        default: throw Error{DITCH_UNSUPPORTED, "norm/bias vectors must be f32, f16 or bf16"};
+        }
+    }
+    Vec v;
+    v.len = len;
+    v.p = (float *)dev_alloc(len * 4);
+    DITCH_TRY_HIP(hipMemcpyAsync(v.p, host.data(), len * 4, hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipStreamSynchronize(s));
+    return v;
+}
+
+static bool vector_slot(int slot) {
+    switch (slot) {
+    case DITCH_SLOT_FINAL_NORM: case DITCH_SLOT_ATTN_NORM: case DITCH_SLOT_Q_BIAS: case DITCH_SLOT_K_BIAS:
+    case DITCH_SLOT_V_BIAS: case DITCH_SLOT_Q_NORM: case DITCH_SLOT_K_NORM: case DITCH_SLOT_FFN_NORM:
+    case DITCH_SLOT_ROUTER_CORRECTION: case DITCH_SLOT_MLA_Q_A_NORM: case DITCH_SLOT_MLA_KV_A_NORM: return true;
+    default: return false;
+    }
+}
+
+static Vec *vec_slot(ditch_hip_model *m, int layer, int slot) {
+    if (slot == DITCH_SLOT_FINAL_NORM) return &m->final_norm;
+    DITCH_CHECK(layer >= 0 && (uint64_t)layer < m->c.layers, DITCH_INVALID_ARGUMENT, "layer index");
+    Layer &L = m->layers[layer];
+    switch (slot) {
+    case DITCH_SLOT_ATTN_NORM: return &L.attn_norm;
+    case DITCH_SLOT_Q_BIAS: return &L.q_bias;
+    case DITCH_SLOT_K_BIAS: return &L.k_bias;
+    case DITCH_SLOT_V_BIAS: return &L.v_bias;
+    case DITCH_SLOT_Q_NORM: return &L.q_norm;
+    case DITCH_SLOT_K_NORM: return &L.k_norm;
+    case DITCH_SLOT_FFN_NORM: return &L.ffn_norm;
+    case DITCH_SLOT_ROUTER_CORRECTION: return &L.corr;
+    case DITCH_SLOT_MLA_Q_A_NORM: return &L.q_a_norm;
+    case DITCH_SLOT_MLA_KV_A_NORM: return &L.kv_a_norm;
+    default: throw Error{DITCH_INVALID_ARGUMENT, "not a vector slot"};
+    }
+}
+
+static Mat *mat_slot(ditch_hip_model *m, int layer, int slot, int expert) {
+    if (slot == DITCH_SLOT_EMBED) return &m->embed;
+    if (slot == DITCH_SLOT_LM_HEAD) return &m->lm_head;
+    DITCH_CHECK(layer >= 0 && (uint64_t)layer < m->c.layers, DITCH_INVALID_ARGUMENT, "layer index");
+    Layer &L = m->layers[layer];
+    switch (slot) {
+    case DITCH_SLOT_Q: return &L.q;
+    case DITCH_SLOT_K: return &L.k;
+    case DITCH_SLOT_V: return &L.v;
+    case DITCH_SLOT_O: return &L.o;
+    case DITCH_SLOT_GATE: return &L.gate;
+    case DITCH_SLOT_UP: return &L.up;
+    case DITCH_SLOT_DOWN: return &L.down;
+    case DITCH_SLOT_ROUTER: return &L.router;
+    case DITCH_SLOT_SHARED_GATE: return &L.sh_gate;
+    case DITCH_SLOT_SHARED_UP: return &L.sh_up;
+    case DITCH_SLOT_SHARED_DOWN: return &L.sh_down;
+    case DITCH_SLOT_MLA_Q_A: return &L.q_a;
+    case DITCH_SLOT_MLA_Q_B: return &L.q_b;
+    case DITCH_SLOT_MLA_KV_A: return &L.kv_a;
+    case DITCH_SLOT_MLA_KV_B: return &L.kv_b;
+    case DITCH_SLOT_EXPERT_GATE: case DITCH_SLOT_EXPERT_UP: case DITCH_SLOT_EXPERT_DOWN: {
+        DITCH_CHECK(expert >= 0 && (uint64_t)expert < m->c.n_experts && !L.eg.empty(), DITCH_INVALID_ARGUMENT,
+                    "expert index (or the layer is not a routed MoE layer)");
+        return slot == DITCH_SLOT_EXPERT_GATE ? &L.eg[expert] : slot == DITCH_SLOT_EXPERT_UP ? &L.eu[expert] : &L.ed[expert];
+    }
+    default: throw Error{DITCH_INVALID_ARGUMENT, "unknown slot " + std::to_string(slot)};
+    }
+}
+
+ditch_hip_model *model_create(ditch_hip *h, const ditch_model_config *cfg) {
+    DITCH_CHECK(cfg->hidden > 0 && cfg->layers > 0 && cfg->heads > 0 && cfg->head_dim > 0, DITCH_INVALID_ARGUMENT,
+                "model config");
+    DITCH_CHECK(cfg->n_experts <= (uint64_t)ROUTE_MAXE && cfg->n_group <= (uint64_t)ROUTE_MAXG && cfg->top_k <= 16,
+                DITCH_UNSUPPORTED, "router limits: <= 512 experts, <= 64 groups, top_k <= 16");
+    auto *m = new ditch_hip_model();
+    m->h = h;
+    m->c = *cfg;
+    m->moe_layers.assign(cfg->layers, 0);
+    if (cfg->moe_layers) memcpy(m->moe_layers.data(), cfg->moe_layers, cfg->layers);
+    m->c.moe_layers = m->moe_layers.data();
+    m->layers.resize(cfg->layers);
+    for (uint64_t l = 0; l < cfg->layers; l++)
+        if (cfg->n_experts && m->moe_layers[l]) {
+            m->layers[l].eg.resize(cfg->n_experts);
+            m->layers[l].eu.resize(cfg->n_experts);
+            m->layers[l].ed.resize(cfg->n_experts);
+        }
+    std::vector<float> cs, sn;
+    host_fill_rope(m->c, cs, sn);
+    m->c.rope_factors = nullptr;  // not kept past creation
+    size_t bytes = (cs.size() + 1) * 4;
+    try {
+        m->rope_cos = (float *)dev_alloc(bytes);
+        m->rope_sin = (float *)dev_alloc(bytes);
+        if (!cs.empty()) {
+            DITCH_TRY_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, h->stream));
+            DITCH_TRY_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, h->stream));
+        }
+        DITCH_TRY_HIP(hipStreamSynchronize(h->stream));
+    } catch (...) {
+        delete m;
+        throw;
+    }
+    return m;
+}
+
+void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_weight *w) {
+    hipStream_t s = m->h->stream;
+    if (vector_slot(slot)) {
+        Vec *v = vec_slot(m, layer, slot);
+        Vec nv = upload_vec(w, s);
+        v->release();
+        *v = nv;
+        return;
+    }
+    Mat *mt = mat_slot(m, layer, slot, expert);
+    ditch_hip_tensor *t = upload_weight(m->h, w, s);
+    mt->release();
+    mt->t = t;
+}
+
+void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64_t rank, const float *a,
+                     const float *b) {
+    Mat *mt = mat_slot(m, layer, slot, expert);
+    DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "delta on an empty slot");
+    DITCH_CHECK(rank <= 64, DITCH_UNSUPPORTED, "delta rank above 64");
+    mt->clear_delta();
+    if (rank == 0) return;
+    hipStream_t s = m->h->stream;
+    size_t ab = rank * mt->t->v.cols * 4, bb = mt->t->v.rows * rank * 4;
+    mt->da = (float *)dev_alloc(ab);
+    mt->db = (float *)dev_alloc(bb);
+    DITCH_TRY_HIP(hipMemcpyAsync(mt->da, a, ab, hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipMemcpyAsync(mt->db, b, bb, hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipStreamSynchronize(s));
+    mt->rank = (int)rank;
+}
+
+// The same edit as abliterate.computeOutputDelta (none mode): a = V^T W on
+// the device over the resident codes, b = -weight V.
+void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight) {
+    Mat *mt = mat_slot(m, layer, slot, expert);
+    DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "edit of an empty slot");
+    hipStream_t s = m->h->stream;
+    const TileView &w = mt->t->v;
+    DevBuf dv, part;
+    float *d_v = dv.get<float>(k * w.rows + k * w.cols);
+    float *d_a = d_v + k * w.rows;
+    DITCH_TRY_HIP(hipMemcpyAsync(d_v, v, k * w.rows * 4, hipMemcpyHostToDevice, s));
+    launch_matvecT(d_a, w, d_v, (int64_t)k, s, part.get<float>(matvecT_partials_floats(w, k)));
+    std::vector<float> b(w.rows * k);
+    for (int64_t i = 0; i < w.rows; i++)
+        for (uint64_t j = 0; j < k; j++) b[i * k + j] = -weight * v[j * w.rows + i];
+    mt->clear_delta();
+    mt->da = (float *)dev_alloc(k * w.cols * 4);
+    mt->db = (float *)dev_alloc(w.rows * k * 4);
+    DITCH_TRY_HIP(hipMemcpyAsync(mt->da, d_a, k * w.cols * 4, hipMemcpyDeviceToDevice, s));
+    DITCH_TRY_HIP(hipMemcpyAsync(mt->db, b.data(), w.rows * k * 4, hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipStreamSynchronize(s));
+    mt->rank = (int)k;
+}
+
+void model_reset_deltas(ditch_hip_model *m) {
+    for (auto &L : m->layers) {
+        for (Mat *mt : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.router, &L.sh_gate, &L.sh_up, &L.sh_down,
+                        &L.q_a, &L.q_b, &L.kv_a, &L.kv_b})
+            mt->clear_delta();
+        for (auto *vec : {&L.eg, &L.eu, &L.ed})
+            for (auto &mt : *vec) mt.clear_delta();
+    }
+    m->embed.clear_delta();
+    m->lm_head.clear_delta();
+}
+
+uint64_t model_bytes(const ditch_hip_model *m) {
+    uint64_t b = 0;
+    auto add = [&](const Mat &mt) {
+        if (mt.t) b += mt.t->bytes;
+    };
+    add(m->embed);
+    add(m->lm_head);
+    for (auto &L : m->layers) {
+        for (const Mat *mt : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.router, &L.sh_gate, &L.sh_up,
+                              &L.sh_down, &L.q_a, &L.q_b, &L.kv_a, &L.kv_b})
+            add(*mt);
+        for (auto *vec : {&L.eg, &L.eu, &L.ed})
+            for (auto &mt : *vec) add(mt);
+    }
+    return b;
+}
+
+// matmul with the slot's delta (tensor.zig:1036-1042) and an epilogue.
+static void mm(ditch_hip_model *m, const Mat &mt, float *out, const float *x, int64_t n, const float *bias,
+               int accumulate, hipStream_t s) {
+    DITCH_CHECK(mt.ok(), DITCH_INVALID_ARGUMENT, "forward: a weight slot is empty");
+    MatmulEpilogue ep;
+    ep.bias = bias;
+    ep.accumulate = accumulate;
+    if (mt.rank > 0) {
+        float *xa = m->xa.get<float>((size_t)n * mt.rank);
+        launch_delta_xa(xa, x, mt.da, n, mt.t->v.cols, mt.rank, s);
+        ep.delta_b = mt.db;
+        ep.delta_xa = xa;
+        ep.delta_rank = mt.rank;
+    }
+    launch_matmul(mt.t->v, out, x, n, ep, s);
+}
+
+// Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).
+static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, int64_t n, hipStream_t s) {
+    const ditch_model_config &c = m->c;
+    int64_t E = (int64_t)c.n_experts, k = (int64_t)c.top_k, hidden = (int64_t)c.hidden, inter = (int64_t)c.moe_inter;
+    float *logits = m->r_logits.get<float>(n * E);
+    mm(m, L.router, logits, h, n, nullptr, 0, s);
+    int32_t *sel = m->r_sel.get<int32_t>(n * k);
+    float *selw = m->r_selw.get<float>(n * k);
+    RouteArgs ra{logits, L.corr.p, sel, selw, n, E, k, (int64_t)c.n_group, (int64_t)c.topk_group, c.scoring,
+                 c.group_limited, c.norm_topk_prob, c.routed_scaling};
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, ra);
+    DITCH_TRY_HIP(hipGetLastError());
+    int32_t *counts = m->r_counts.get<int32_t>(E);
+    DITCH_TRY_HIP(hipMemsetAsync(counts, 0, E * 4, s));
+    hipLaunchKernelGGL(expert_count_kernel, dim3(grid_for(n * k)), dim3(256), 0, s, sel, n * k, counts);
+    DITCH_TRY_HIP(hipGetLastError());
+    std::vector<int32_t> hc(E), ho(E);
+    DITCH_TRY_HIP(hipMemcpyAsync(hc.data(), counts, E * 4, hipMemcpyDeviceToHost, s));
+    DITCH_TRY_HIP(hipStreamSynchronize(s));
+    int32_t acc = 0, max_cnt = 0;
+    for (int64_t e = 0; e < E; e++) {
+        ho[e] = acc;
+        acc += hc[e];
+        max_cnt = std::max(max_cnt, hc[e]);
+    }
+    int64_t P = acc;  // == n * k
+    int32_t *offsets = m->r_offsets.get<int32_t>(E);
+    DITCH_TRY_HIP(hipMemcpyAsync(offsets, ho.data(), E * 4, hipMemcpyHostToDevice, s));
+    int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
+    int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
+    hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(256), 0, s, sel, n, k, offsets, pair_token, pair_of);
+    DITCH_TRY_HIP(hipGetLastError());
+    // segments (experts with tokens), in index order
+    std::vector<GroupSeg> sg, su, sd;
+    std::vector<SegDelta> dd;
+    int max_rank = 0;
+    for (int64_t e = 0; e < E; e++) {
+        if (hc[e] == 0) continue;
+        DITCH_CHECK(L.eg[e].ok() && L.eu[e].ok() && L.ed[e].ok(), DITCH_INVALID_ARGUMENT, "forward: expert weights missing");
+        GroupSeg g{L.eg[e].t->v, ho[e], hc[e], nullptr, 0};
+        GroupSeg u{L.eu[e].t->v, ho[e], hc[e], nullptr, 0};
+        GroupSeg d{L.ed[e].t->v, ho[e], hc[e], L.ed[e].db, L.ed[e].rank};
+        sg.push_back(g);
+        su.push_back(u);
+        sd.push_back(d);
+        dd.push_back(SegDelta{L.ed[e].da, ho[e], hc[e], L.ed[e].rank});
+        max_rank = std::max(max_rank, L.ed[e].rank);
+    }
+    unsigned nseg = (unsigned)sg.size();
+    GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * nseg);
+    DITCH_TRY_HIP(hipMemcpyAsync(dsegs, sg.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+    DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+    const TileView &vg = L.eg[0].t->v, &vd = L.ed[0].t->v;
+    float *gate = m->e_gate.get<float>(P * inter), *up = m->e_up.get<float>(P * inter);
+    float *eo = m->e_out.get<float>(P * hidden);
+    launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, s);
+    launch_matmul_grouped(dsegs + nseg, nseg, L.eu[0].t->v.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, s);
+    launch_gated_act(0, gate, gate, up, P, inter, inter, inter, s);
+    float *dxa = nullptr;
+    if (max_rank > 0) {
+        SegDelta *dsd = m->segd.get<SegDelta>(nseg);
+        DITCH_TRY_HIP(hipMemcpyAsync(dsd, dd.data(), nseg * sizeof(SegDelta), hipMemcpyHostToDevice, s));
+        dxa = m->e_xa.get<float>(P * max_rank);
+        dim3 grid((unsigned)((max_cnt * max_rank + 3) / 4), nseg);
+        hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
+    launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, s);
+    float *esh = nullptr;
+    if (L.sh_gate.ok()) {
+        int64_t si = L.sh_gate.t->v.rows;
+        float *sgb = m->g.get<float>(n * si), *sub = m->u.get<float>(n * si);
+        mm(m, L.sh_gate, sgb, h, n, nullptr, 0, s);
+        mm(m, L.sh_up, sub, h, n, nullptr, 0, s);
+        launch_gated_act(0, sgb, sgb, sub, n, si, si, si, s);
+        esh = m->e_shared.get<float>(n * hidden);
+        mm(m, L.sh_down, esh, sgb, n, nullptr, 0, s);
+    }
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(grid_for(n * hidden)), dim3(256), 0, s, x, eo, esh, sel, selw, pair_of,
+                       n, k, hidden);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vector<ditch_row> &rows,
+                   const ditch_row *d_rows, int64_t n, const uint64_t *d_capture, int64_t n_capture, float *d_res,
+                   const uint64_t *d_logit_rows, int64_t n_logit, float *d_logits) {
+    const ditch_model_config &c = m->c;
+    hipStream_t s = m->h->stream;
+    if (n <= 0) return;
+    DITCH_CHECK(m->embed.ok(), DITCH_INVALID_ARGUMENT, "forward: no embedding");
+    int64_t hidden = (int64_t)c.hidden;
+    int64_t B = 0, T = 0;
+    for (auto &r : rows) {
+        B = std::max<int64_t>(B, (int64_t)r.b + 1);
+        T = std::max<int64_t>(T, (int64_t)r.pos + 1);
+    }
+    DITCH_CHECK(T <= ATT_MAXK, DITCH_UNSUPPORTED, "forward: positions beyond 1024 per prompt");
+    int64_t nh = (int64_t)c.heads, nkv = c.mla ? nh : (int64_t)c.kv_heads, hd = (int64_t)c.head_dim;
+    int64_t vd = c.mla ? (int64_t)c.v_head_dim : hd;
+    DITCH_CHECK(hd <= 512, DITCH_UNSUPPORTED, "forward: head_dim above 512");
+    int64_t qd = nh * hd, kvd = nkv * hd;
+    float *x = m->x.get<float>(n * hidden);
+    float *h = m->hbuf.get<float>(n * hidden);
+    float *q = m->q.get<float>(n * qd), *kk = m->k.get<float>(n * kvd), *vv = m->v.get<float>(n * kvd);
+    float *att = m->att.get<float>(n * nh * vd);
+    float *kc = m->kc.get<float>(B * T * kvd), *vc = m->vc.get<float>(B * T * kvd);
+
+    hipLaunchKernelGGL(embed_kernel, dim3(grid_for(n * hidden)), dim3(256), 0, s, x, m->embed.t->v, d_tokens, n);
+    DITCH_TRY_HIP(hipGetLastError());
+    auto capture = [&](int64_t entry) {
+        if (!d_res || n_capture == 0) return;
+        hipLaunchKernelGGL(capture_kernel, dim3(grid_for(n_capture * hidden)), dim3(256), 0, s,
+                           d_res + entry * n_capture * hidden, x, d_capture, n_capture, hidden);
+        DITCH_TRY_HIP(hipGetLastError());
+    };
+    capture(0);
+    for (int64_t li = 0; li < (int64_t)c.layers; li++) {
+        Layer &L = m->layers[li];
+        launch_rmsnorm(h, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
+        if (c.mla) {
+            int64_t nope = (int64_t)c.qk_nope_dim, rd = (int64_t)c.qk_rope_dim, kvl = (int64_t)c.kv_lora_rank;
+            if (L.q_a.ok()) {
+                int64_t qlr = (int64_t)c.q_lora_rank;
+                float *qa = m->mla_a.get<float>(n * qlr);
+                mm(m, L.q_a, qa, h, n, nullptr, 0, s);
+                launch_rmsnorm(qa, qa, L.q_a_norm.p, L.q_a_norm.len, n, qlr, c.mla_norm_eps, 0, s);
+                mm(m, L.q_b, q, qa, n, nullptr, 0, s);
+            } else {
+                mm(m, L.q_b, q, h, n, nullptr, 0, s);
+            }
+            float *kva = m->mla_b.get<float>(n * (kvl + rd));
+            mm(m, L.kv_a, kva, h, n, nullptr, 0, s);
+            float *ckv = m->mla_c.get<float>(n * kvl);
+            launch_rmsnorm_strided(ckv, kva, L.kv_a_norm.p, L.kv_a_norm.len, n, kvl, kvl + rd, kvl, c.mla_norm_eps, s);
+            float *kvb = m->o.get<float>(n * nh * (nope + vd));
+            mm(m, L.kv_b, kvb, ckv, n, nullptr, 0, s);
+            hipLaunchKernelGGL(mla_assemble_kernel, dim3(grid_for(n * nh * hd)), dim3(256), 0, s, kk, vv, kvb, kva, n,
+                               nh, hd, nope, rd, vd, kvl);
+            DITCH_TRY_HIP(hipGetLastError());
+        } else {
+            mm(m, L.q, q, h, n, L.q_bias.p, 0, s);
+            mm(m, L.k, kk, h, n, L.k_bias.p, 0, s);
+            mm(m, L.v, vv, h, n, L.v_bias.p, 0, s);
+        }
+        RopeArgs ra{};
+        ra.q = q;
+        ra.k = kk;
+        ra.v = vv;
+        ra.kc = kc;
+        ra.vc = vc;
+        ra.rows = d_rows;
+        ra.cos_t = m->rope_cos;
+        ra.sin_t = m->rope_sin;
+        ra.q_norm = c.qk_norm ? L.q_norm.p : nullptr;
+        ra.k_norm = c.qk_norm ? L.k_norm.p : nullptr;
+        ra.n = n;
+        ra.heads = nh;
+        ra.kv_heads = nkv;
+        ra.hd = hd;
+        ra.rope_off = c.mla ? (int64_t)c.qk_nope_dim : 0;
+        ra.rot = (int64_t)(c.rotary_dim / 2 * 2);
+        ra.half = (int64_t)(c.rotary_dim / 2);
+        ra.rope_len = (int64_t)c.rope_len;
+        ra.T = T;
+        ra.kvd = kvd;
+        ra.eps = c.rms_eps;
+        ra.style = c.rope_style;
+        hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
+        DITCH_TRY_HIP(hipGetLastError());
+        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale};
+        hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);
+        DITCH_TRY_HIP(hipGetLastError());
+        mm(m, L.o, x, att, n, nullptr, 1, s);  // x += o(att)
+        launch_rmsnorm(h, x, L.ffn_norm.p, L.ffn_norm.len, n, hidden, c.rms_eps, 0, s);
+        if (c.n_experts && m->moe_layers[li]) {
+            moe_forward(m, L, x, h, n, s);
+        } else {
+            int64_t inter = L.gate.t ? L.gate.t->v.rows : 0;
+            float *g = m->g.get<float>(n * inter), *u = m->u.get<float>(n * inter);
+            mm(m, L.gate, g, h, n, nullptr, 0, s);
+            mm(m, L.up, u, h, n, nullptr, 0, s);
+            launch_gated_act(0, g, g, u, n, inter, inter, inter, s);
+            mm(m, L.down, x, g, n, nullptr, 1, s);  // x += down(act)
+        }
+        capture(li + 1);
+    }
+    if (n_logit > 0 && d_logits) {
+        float *hl = m->logit_h.get<float>(n_logit * hidden);
+        launch_rmsnorm(hl, x, m->final_norm.p, m->final_norm.len, n_logit, hidden, c.rms_eps, 0, s,
+                       (const int64_t *)d_logit_rows);
+        const Mat &lm = m->lm_head.ok() ? m->lm_head : m->embed;
+        mm(m, lm, d_logits, hl, n_logit, nullptr, 0, s);
+    }
+}
+
+// RoPE tables (model.zig:2200-2282), computed in f64 on the host as the
+// reference does.
+static void host_fill_rope(const ditch_model_config &c, std::vector<float> &cos_t, std::vector<float> &sin_t) {
+    size_t len = c.rope_len, dim = c.rotary_dim, half = dim / 2;
+    cos_t.assign(len * half, 0.f);
+    sin_t.assign(len * half, 0.f);
+    if (half == 0) return;
+    std::vector<double> inv(half);
+    double theta = (double)c.rope_theta;
+    for (size_t i = 0; i < half; i++) inv[i] = 1.0 / pow(theta, (double)(2 * i) / (double)dim);
+    double attention_factor = 1.0;
+    const double pi = 3.14159265358979323846;
+    if (c.rope_scaling == DITCH_ROPE_SCALING_LINEAR) {
+        for (auto &f : inv) f /= (double)c.rope_factor;
+    } else if (c.rope_scaling == DITCH_ROPE_SCALING_LLAMA3) {
+        double low_wavelen = (double)(c.rope_original_max_position / c.rope_low_freq_factor);
+        double high_wavelen = (double)(c.rope_original_max_position / c.rope_high_freq_factor);
+        double band = (double)(c.rope_high_freq_factor - c.rope_low_freq_factor);
+        for (auto &f : inv) {
+            double wavelen = 2.0 * pi / f;
+            if (wavelen < high_wavelen) {
+            } else if (wavelen > low_wavelen) {
+                f /= (double)c.rope_factor;
+            } else {
+                double smooth = ((double)c.rope_original_max_position / wavelen - (double)c.rope_low_freq_factor) / band;
+                f = (1.0 - smooth) * f / (double)c.rope_factor + smooth * f;
+            }
+        }
+    } else if (c.rope_scaling == DITCH_ROPE_SCALING_YARN) {
+        double dimf = (double)dim, maxp = (double)c.rope_original_max_position;
+        double low = (dimf * log(maxp / ((double)c.yarn_beta_fast * 2.0 * pi))) / (2.0 * log(theta));
+        double high = (dimf * log(maxp / ((double)c.yarn_beta_slow * 2.0 * pi))) / (2.0 * log(theta));
+        if (c.yarn_truncate) {
+            low = floor(low);
+            high = ceil(high);
+        }
+        if (low < 0) low = 0;
+        if (high > dimf - 1) high = dimf - 1;
+        if (low == high) high += 0.001;
+        for (size_t i = 0; i < half; i++) {
+            double ramp = ((double)i - low) / (high - low);
+            ramp = ramp < 0 ? 0 : ramp > 1 ? 1 : ramp;
+            double extrapolation = 1.0 - ramp;
+            double interp = inv[i] / (double)c.rope_factor;
+            inv[i] = interp * (1.0 - extrapolation) + inv[i] * extrapolation;
+        }
+        attention_factor = (double)c.yarn_attention_factor;
+    } else if (c.rope_scaling == DITCH_ROPE_SCALING_FACTORS && c.rope_factors) {
+        for (size_t i = 0; i < half; i++) inv[i] /= (double)c.rope_factors[i];
+    }
+    for (size_t pos = 0; pos < len; pos++)
+        for (size_t i = 0; i < half; i++) {
+            double angle = (double)pos * inv[i];
+            cos_t[pos * half + i] = (float)(cos(angle) * attention_factor);
+            sin_t[pos * half + i] = (float)(sin(angle) * attention_factor);
+        }
+}
+
+}  // namespace ditch
+
+ditch_hip_model::~ditch_hip_model() {
+    for (auto &L : layers) {
+        for (ditch::Vec *v : {&L.attn_norm, &L.q_bias, &L.k_bias, &L.v_bias, &L.q_norm, &L.k_norm, &L.ffn_norm,
+                              &L.corr, &L.q_a_norm, &L.kv_a_norm})
+            v->release();
+        for (ditch::Mat *mt : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.router, &L.sh_gate, &L.sh_up,
+                               &L.sh_down, &L.q_a, &L.q_b, &L.kv_a, &L.kv_b})
+            mt->release();
+        for (auto *vec : {&L.eg, &L.eu, &L.ed})
+            for (auto &mt : *vec) mt.release();
+    }
+    embed.release();
+    lm_head.release();
+    final_norm.release();
+    ditch::dev_free(rope_cos);
+    ditch::dev_free(rope_sin);
+}

@@ -1,0 +1,389 @@
+// ops.hip — element-wise and reduction kernels of the forward pass and of
+// the VTable's per-row operations (compute.zig:107-119), plus row norms and
+// W^T y over resident weights (tensor.zig:1056-1122).
+#include "decode.h"
+#include "internal.h"
+#include "tiled.h"
+
+namespace ditch {
+
+static int grid_1d(int64_t total, int block = 256) {
+    int64_t g = (total + block - 1) / block;
+    if (g > 65536) g = 65536;
+    return g < 1 ? 1 : (int)g;
+}
+
+// ---------------------------------------------------------------------------
+// Reductions inside one 256-thread block.
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T *sh) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    T r = sh[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = op(r, sh[w]);
+    return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *sh) {
+    v = wave_sum(v);
+    return block_reduce(v, [](float a, float b) { return a + b; }, sh);
+}
+__device__ __forceinline__ double block_sum_d(double v, double *sh) {
+    v = wave_sum_d(v);
+    return block_reduce(v, [](double a, double b) { return a + b; }, sh);
+}
+__device__ __forceinline__ float block_max(float v, float *sh) {
+    v = wave_max(v);
+    return block_reduce(v, [](float a, float b) { return fmaxf(a, b); }, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Activation.applyVec (tensor.zig:1257-1274); gelu (2) has no vector form
+// and uses Abramowitz-Stegun erf (tensor.zig:1220-1225).
+__device__ float act_apply(uint32_t act, float x) {
+    switch (act) {
+    case 0: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(-x)));
+    case 1: {
+        float u = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
+        float t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(exp_cephes(__fadd_rn(u, u)), 1.0f)));
+        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, t));
+    }
+    case 2: {
+        float z = __fdiv_rn(x, 1.41421356237309504880f);
+        float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, fabsf(z))));
+        float p = __fsub_rn(__fmul_rn(1.061405429f, t), 1.453152027f);
+        p = __fadd_rn(__fmul_rn(p, t), 1.421413741f);
+        p = __fsub_rn(__fmul_rn(p, t), 0.284496736f);
+        p = __fadd_rn(__fmul_rn(p, t), 0.254829592f);
+        float y = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(p, t), expf(-__fmul_rn(z, z))));
+        float erf_v = z >= 0 ? y : -y;
+        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erf_v));
+    }
+    case 3: return fmaxf(x, 0.0f);
+    case 4: { float r = fmaxf(x, 0.0f); return __fmul_rn(r, r); }
+    case 5: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(__fmul_rn(-1.702f, x))));
+    default: return x;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm / LayerNorm rows (tensor.zig:1167-1179, 1343-1358): one block per
+// row. `row_index` gathers input rows (the logit rows of model.zig:4798-4852).
+
+__global__ void rmsnorm_kernel(float *out, const float *x, const float *w, int64_t wlen, int64_t len, float eps,
+                               int gemma, const int64_t *row_index, int64_t in_stride, int64_t out_stride) {
+    __shared__ float sh[8];
+    int64_t r = blockIdx.x;
+    int64_t src = row_index ? row_index[r] : r;
+    const float *xr = x + src * in_stride;
+    float ss = 0.f;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, sh);
+    float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps)));
+    float *o = out + r * out_stride;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) {
+        float v = __fmul_rn(xr[i], inv);
+        if (wlen > 0) v = __fmul_rn(v, gemma ? __fadd_rn(1.0f, w[i]) : w[i]);
+        o[i] = v;
+    }
+}
+
+__global__ void layernorm_kernel(float *out, const float *x, const float *w, int64_t wlen, const float *bias,
+                                 int64_t len, float eps, int one_plus) {
+    __shared__ float sh[8];
+    int64_t r = blockIdx.x;
+    const float *xr = x + r * len;
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) s += xr[i];
+    float mean = __fdiv_rn(block_sum(s, sh), (float)len);
+    float v2 = 0.f;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) {
+        float d = __fsub_rn(xr[i], mean);
+        v2 = __builtin_fmaf(d, d, v2);
+    }
+    float var = __fdiv_rn(block_sum(v2, sh), (float)len);
+    float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+    float *o = out + r * len;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) {
+        float y = __fmul_rn(__fsub_rn(xr[i], mean), inv);
+        if (wlen > 0) y = __fmul_rn(y, one_plus ? __fadd_rn(1.0f, w[i]) : w[i]);
+        if (bias) y = __fadd_rn(y, bias[i]);
+        o[i] = y;
+    }
+}
+
+// In-place softmax (tensor.zig:1181-1200).
+__global__ void softmax_kernel(float *x, int64_t len) {
+    __shared__ float sh[8];
+    float *xr = x + (int64_t)blockIdx.x * len;
+    float m = -INFINITY;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) m = fmaxf(m, xr[i]);
+    m = block_max(m, sh);
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) {
+        float e = exp_cephes(__fsub_rn(xr[i], m));
+        xr[i] = e;
+        s += e;
+    }
+    s = block_sum(s, sh);
+    float inv = __fdiv_rn(1.0f, s);
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) xr[i] = __fmul_rn(xr[i], inv);
+}
+
+// log-softmax (tensor.zig:1203-1210): f32 max, f64 sum of exp, f32 x - lse.
+__global__ void log_softmax_kernel(float *out, const float *x, int64_t len) {
+    __shared__ float shf[8];
+    __shared__ double shd[8];
+    const float *xr = x + (int64_t)blockIdx.x * len;
+    float m = -INFINITY;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) m = fmaxf(m, xr[i]);
+    m = block_max(m, shf);
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) s += exp((double)__fsub_rn(xr[i], m));
+    s = block_sum_d(s, shd);
+    float lse = __fadd_rn(m, (float)log(s));
+    float *o = out + (int64_t)blockIdx.x * len;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) o[i] = __fsub_rn(xr[i], lse);
+}
+
+// KL(base || trial) per row (scorers.zig:387-394): the trial row's
+// log-softmax, then sum exp(lb) (lb - lt) in f64.
+__global__ void kl_kernel(double *kl, const float *base, const float *trial, int64_t vocab) {
+    __shared__ float shf[8];
+    __shared__ double shd[8];
+    const float *tr = trial + (int64_t)blockIdx.x * vocab;
+    const float *br = base + (int64_t)blockIdx.x * vocab;
+    float m = -INFINITY;
+    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) m = fmaxf(m, tr[i]);
+    m = block_max(m, shf);
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) s += exp((double)__fsub_rn(tr[i], m));
+    s = block_sum_d(s, shd);
+    float lse = __fadd_rn(m, (float)log(s));
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) {
+        double lb = (double)br[i];
+        double lt = (double)__fsub_rn(tr[i], lse);
+        acc += exp(lb) * (lb - lt);
+    }
+    acc = block_sum_d(acc, shd);
+    if (threadIdx.x == 0) kl[blockIdx.x] = acc;
+}
+
+// out[i][j] = act(gate[i][j]) * up[i][j] (tensor.zig:1296-1337)
+__global__ void gated_act_kernel(uint32_t act, float *out, const float *gate, const float *up, int64_t n, int64_t len,
+                                 int64_t in_stride, int64_t out_stride) {
+    int64_t total = n * len;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = i / len, j = i % len;
+        float v = act_apply(act, gate[r * in_stride + j]);
+        if (up) v = __fmul_rn(v, up[r * in_stride + j]);
+        out[r * out_stride + j] = v;
+    }
+}
+
+// RoPE (tensor.zig:1360-1381) of n head vectors at pos[i].
+__global__ void rope_kernel(float *x, int64_t n, int64_t dim, const float *cos_t, const float *sin_t, int64_t half,
+                            const uint32_t *pos, uint32_t style) {
+    int64_t hd = dim / 2;
+    int64_t total = n * hd;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = t / hd, i = t % hd;
+        float c = cos_t[(int64_t)pos[r] * half + i], s = sin_t[(int64_t)pos[r] * half + i];
+        float *row = x + r * dim;
+        int64_t a = style == DITCH_ROPE_GPTJ ? 2 * i : i, b = style == DITCH_ROPE_GPTJ ? 2 * i + 1 : i + hd;
+        float x1 = row[a], x2 = row[b];
+        row[a] = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+        row[b] = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+    }
+}
+
+// scores[p] = scale * dot(q, k[p]) (tensor.zig:1126-1144): one wave per key.
+__global__ void attn_scores_kernel(float *scores, int64_t n_keys, const float *q, int64_t hd, const float *k,
+                                   int64_t stride, float scale) {
+    int lane = threadIdx.x & 63;
+    int64_t p = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (p >= n_keys) return;
+    float a = 0.f;
+    for (int64_t d = lane; d < hd; d += 64) a = __builtin_fmaf(k[p * stride + d], q[d], a);
+    a = wave_sum(a);
+    if (lane == 0) scores[p] = __fmul_rn(a, scale);
+}
+
+// out[j] = sum_p scores[p] v[p][j] (tensor.zig:1148-1160)
+__global__ void attn_values_kernel(float *out, int64_t vd, const float *scores, int64_t n_keys, const float *v,
+                                   int64_t stride) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= vd) return;
+    float a = 0.f;
+    for (int64_t p = 0; p < n_keys; p++) a = __builtin_fmaf(v[p * stride + j], scores[p], a);
+    out[j] = a;
+}
+
+// Row norms of a resident weight: one block per row.
+__global__ void row_norms_kernel(float *out, TileView w) {
+    __shared__ float sh[8];
+    int64_t r = blockIdx.x;
+    float s = 0.f;
+    for (int64_t c = threadIdx.x; c < w.cols; c += blockDim.x) {
+        uint16_t b;
+        float v = tiled_element_f32(w, r, c, &b);
+        s = __builtin_fmaf(v, v, s);
+    }
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) out[r] = __fsqrt_rn(s);
+}
+
+// W^T y, first pass: block (column chunk, row chunk) -> partial sums
+// [row_chunk][q][cols]; the second pass adds the chunks in order.
+constexpr int MVT_ROWS = 256;
+constexpr int MVT_MAXQ = 8;
+
+__global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q) {
+    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t rc = blockIdx.y;
+    int64_t r0 = rc * MVT_ROWS, r1 = r0 + MVT_ROWS < w.rows ? r0 + MVT_ROWS : w.rows;
+    if (c >= w.cols) return;
+    float acc[MVT_MAXQ];
+#pragma unroll
+    for (int j = 0; j < MVT_MAXQ; j++) acc[j] = 0.f;
+    for (int64_t r = r0; r < r1; r++) {
+        uint16_t b;
+        float v = tiled_element_f32(w, r, c, &b);
+#pragma unroll
+        for (int j = 0; j < MVT_MAXQ; j++)
+            if (j < q) acc[j] = __builtin_fmaf(y[j * w.rows + r], v, acc[j]);
+    }
+    for (int j = 0; j < q; j++) partials[(rc * q + j) * w.cols + c] = acc[j];
+}
+
+__global__ void matvecT_reduce_kernel(float *out, const float *partials, int64_t chunks, int64_t qc) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= qc) return;
+    float s = 0.f;
+    for (int64_t k = 0; k < chunks; k++) s += partials[k * qc + i];
+    out[i] = s;
+}
+
+// xa[i][j] = dot(a_j, x_i) for the low-rank delta (tensor.zig:1036-1042)
+__global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank) {
+    int lane = threadIdx.x & 63;
+    int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= n * rank) return;
+    int64_t i = t / rank, j = t % rank;
+    float s = 0.f;
+    for (int64_t c = lane; c < cols; c += 64) s = __builtin_fmaf(a[j * cols + c], x[i * cols + c], s);
+    s = wave_sum(s);
+    if (lane == 0) xa[t] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+
+void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len, float eps,
+                    int gemma, hipStream_t s, const int64_t *row_index) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, gemma, row_index,
+                       len, len);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
+                            int64_t in_stride, int64_t out_stride, float eps, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, 0, nullptr,
+                       in_stride, out_stride);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
+                      int64_t len, float eps, int one_plus, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, bias, len, eps, one_plus);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)n), dim3(256), 0, s, x, len);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(log_softmax_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, len);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(kl_kernel, dim3((unsigned)n), dim3(256), 0, s, kl, base, trial, vocab);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_gated_act(uint32_t act, float *out, const float *gate, const float *up, int64_t n, int64_t len,
+                      int64_t in_stride, int64_t out_stride, hipStream_t s) {
+    if (n * len <= 0) return;
+    hipLaunchKernelGGL(gated_act_kernel, dim3(grid_1d(n * len)), dim3(256), 0, s, act, out, gate, up, n, len,
+                       in_stride, out_stride);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_rope_rows(float *x, int64_t n, int64_t dim, const float *cos_t, const float *sin_t, int64_t half,
+                      const uint32_t *pos, uint32_t style, hipStream_t s) {
+    if (n * dim <= 0) return;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_1d(n * dim / 2)), dim3(256), 0, s, x, n, dim, cos_t, sin_t, half, pos,
+                       style);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_attention_scores(float *scores, int64_t n_keys, const float *q, int64_t hd, const float *k,
+                             int64_t stride, float scale, hipStream_t s) {
+    if (n_keys <= 0) return;
+    hipLaunchKernelGGL(attn_scores_kernel, dim3((unsigned)((n_keys + 3) / 4)), dim3(256), 0, s, scores, n_keys, q, hd,
+                       k, stride, scale);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_attention_values(float *out, int64_t vd, const float *scores, int64_t n_keys, const float *v,
+                             int64_t stride, hipStream_t s) {
+    if (vd <= 0) return;
+    hipLaunchKernelGGL(attn_values_kernel, dim3(grid_1d(vd)), dim3(256), 0, s, out, vd, scores, n_keys, v, stride);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_row_norms(float *out, const TileView &w, hipStream_t s) {
+    if (w.rows <= 0) return;
+    hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)w.rows), dim3(256), 0, s, out, w);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+size_t matvecT_partials_floats(const TileView &w, int64_t q) {
+    int64_t chunks = (w.rows + MVT_ROWS - 1) / MVT_ROWS;
+    return (size_t)chunks * q * w.cols;
+}
+void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials) {
+    DITCH_CHECK(q >= 1 && q <= MVT_MAXQ, DITCH_UNSUPPORTED, "matvecTMulti: q must be 1..8");
+    int64_t chunks = (w.rows + MVT_ROWS - 1) / MVT_ROWS;
+    dim3 grid((unsigned)((w.cols + 255) / 256), (unsigned)chunks);
+    hipLaunchKernelGGL(matvecT_partial_kernel, grid, dim3(256), 0, s, partials, w, y, q);
+    DITCH_TRY_HIP(hipGetLastError());
+    hipLaunchKernelGGL(matvecT_reduce_kernel, dim3(grid_1d(q * w.cols)), dim3(256), 0, s, out, partials, chunks,
+                       q * w.cols);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank, hipStream_t s) {
+    if (n * rank <= 0) return;
+    hipLaunchKernelGGL(delta_xa_kernel, dim3((unsigned)((n * rank + 3) / 4)), dim3(256), 0, s, xa, x, a, n, cols, rank);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+}  // namespace ditch

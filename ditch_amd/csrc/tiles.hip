@@ -1,0 +1,660 @@
+// tiles.hip — weight upload: raw checkpoint layouts -> HBM tiles, and the
+// element decoders over both layouts.
+//
+// Raw layouts are the ones the reference reads (tensor.Weight rows, GGUF
+// blocks quant.zig:27-42, the quantised-safetensors groups of dequant.zig:
+// 477-673). Fused formats (TF_Q8/FP8/MX4/INT4/BF16/F16/F32) keep their codes
+// and are re-tiled for the matmul kernels; the others are decoded once at
+// upload to the reference's virtual dtype (bf16, or f32 for GGUF blocks).
+#include "decode.h"
+#include "internal.h"
+#include "tiled.h"
+
+namespace ditch {
+
+bool is_bf16_virtual(int32_t dt) {
+    return dt == DITCH_FP8 || dt == DITCH_MXFP4 || dt == DITCH_MXFP4_T || dt == DITCH_INT_PACKED;
+}
+
+__host__ __device__ static int gguf_block_size(int dt) {
+    switch (dt) {
+    case DITCH_Q8_0: case DITCH_Q4_0: case DITCH_Q4_1: case DITCH_Q5_0: case DITCH_Q5_1: return 32;
+    case DITCH_Q4_K: case DITCH_Q6_K: case DITCH_Q8_K: return 256;
+    default: return 0;
+    }
+}
+__host__ __device__ static int gguf_block_bytes(int dt) {
+    switch (dt) {
+    case DITCH_Q8_0: return 34;
+    case DITCH_Q4_0: return 18;
+    case DITCH_Q4_1: return 20;
+    case DITCH_Q5_0: return 22;
+    case DITCH_Q5_1: return 24;
+    case DITCH_Q4_K: return 144;
+    case DITCH_Q6_K: return 210;
+    case DITCH_Q8_K: return 292;
+    default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Raw-layout element decode. One thread per output element.
+
+struct RawView {
+    const uint8_t *data;
+    const uint8_t *scale;
+    const uint8_t *zero;
+    const int32_t *g_idx;
+    int32_t dtype, scale_type;
+    int64_t rows, cols;
+    int64_t scale_cols, block_rows, block_cols, row_shard;
+    int32_t e5m2, bits;
+    int64_t group, groups;
+};
+
+__device__ __forceinline__ float rd_f16(const uint8_t *b) { return f16_to_f32((uint16_t)(b[0] | (b[1] << 8))); }
+__device__ __forceinline__ uint32_t rd_u32(const uint8_t *b) {
+    return (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
+}
+
+// Element e of a GGUF block `b` (quant.zig:81-199), as f32.
+__device__ float gguf_element(int dt, const uint8_t *b, int e) {
+    switch (dt) {
+    case DITCH_Q8_0: return __fmul_rn((float)(int8_t)b[2 + e], rd_f16(b));
+    case DITCH_Q4_0: {
+        int j = e & 15;
+        int x = (e < 16 ? (b[2 + j] & 0x0f) : (b[2 + j] >> 4)) - 8;
+        return __fmul_rn((float)x, rd_f16(b));
+    }
+    case DITCH_Q4_1: {
+        int j = e & 15;
+        int x = e < 16 ? (b[4 + j] & 0x0f) : (b[4 + j] >> 4);
+        return __fadd_rn(__fmul_rn((float)x, rd_f16(b)), rd_f16(b + 2));
+    }
+    case DITCH_Q5_0: {
+        uint32_t qh = rd_u32(b + 2);
+        int j = e & 15;
+        int x;
+        if (e < 16) x = (int)((b[6 + j] & 0x0f) | (((qh >> j) << 4) & 0x10u)) - 16;
+        else x = (int)((b[6 + j] >> 4) | ((qh >> (j + 12)) & 0x10u)) - 16;
+        return __fmul_rn((float)x, rd_f16(b));
+    }
+    case DITCH_Q5_1: {
+        uint32_t qh = rd_u32(b + 4);
+        int j = e & 15;
+        uint32_t x;
+        if (e < 16) x = (b[8 + j] & 0x0f) | (((qh >> j) << 4) & 0x10u);
+        else x = (b[8 + j] >> 4) | ((qh >> (j + 12)) & 0x10u);
+        return __fadd_rn(__fmul_rn((float)x, rd_f16(b)), rd_f16(b + 2));
+    }
+    case DITCH_Q4_K: {
+        float d = rd_f16(b), mn = rd_f16(b + 2);
+        const uint8_t *sc = b + 4;
+        int chunk = e / 64, within = e % 64;
+        int is = 2 * chunk + (within >= 32 ? 1 : 0);
+        uint32_t s, m;
+        if (is < 4) { s = sc[is] & 63; m = sc[is + 4] & 63; }
+        else { s = (sc[is + 4] & 0xf) | ((sc[is - 4] >> 6) << 4); m = (sc[is + 4] >> 4) | ((sc[is] >> 6) << 4); }
+        uint8_t qb = b[16 + 32 * chunk + (within & 31)];
+        uint32_t q = within < 32 ? (qb & 0xf) : (qb >> 4);
+        float dd = __fmul_rn(d, (float)s), mm = __fmul_rn(mn, (float)m);
+        return __fsub_rn(__fmul_rn(dd, (float)q), mm);
+    }
+    case DITCH_Q6_K: {
+        int n128 = e / 128, rem = e % 128, l = rem % 32, quarter = rem / 32;
+        const uint8_t *ql = b + 64 * n128, *qh = b + 128 + 32 * n128, *sc = b + 192 + 8 * n128;
+        float d = rd_f16(b + 208);
+        uint8_t lb = ql[l + 32 * (quarter & 1)];
+        uint32_t nib = quarter >= 2 ? (lb >> 4) : (lb & 0xf);
+        int q = (int)(nib | (((qh[l] >> (2 * quarter)) & 3u) << 4)) - 32;
+        float s = (float)(int8_t)sc[l / 16 + 2 * quarter];
+        return __fmul_rn(__fmul_rn(d, s), (float)q);
+    }
+    case DITCH_Q8_K: return __fmul_rn(u2f(rd_u32(b)), (float)(int8_t)b[4 + e]);
+    default: return 0.0f;
+    }
+}
+
+__device__ __forceinline__ uint32_t field_mask(int bits) { return bits >= 32 ? 0xffffffffu : ((1u << bits) - 1u); }
+
+__device__ __forceinline__ uint32_t unpack_field(const uint32_t *words, int64_t i, int bits) {
+    int64_t start = i * bits;
+    int64_t w = start / 32;
+    int off = (int)(start % 32);
+    int lo = (32 - off) < bits ? (32 - off) : bits;
+    uint32_t v = (words[w] >> off) & field_mask(lo);
+    if (lo < bits) v |= (words[w + 1] & field_mask(bits - lo)) << lo;
+    return v;
+}
+
+
+// Raw element (r, c): bf16 bits for the virtual-bf16 formats, f32 otherwise.
+__device__ float raw_element_f32(const RawView &v, int64_t r, int64_t c) {
+    switch (v.dtype) {
+    case DITCH_F32: return ((const float *)v.data)[r * v.cols + c];
+    case DITCH_F16: return f16_to_f32(((const uint16_t *)v.data)[r * v.cols + c]);
+    case DITCH_BF16: return bf16_to_f32(((const uint16_t *)v.data)[r * v.cols + c]);
+    default: {
+        int bs = gguf_block_size(v.dtype), bb = gguf_block_bytes(v.dtype);
+        const uint8_t *row = v.data + r * (v.cols / bs) * bb;
+        return gguf_element(v.dtype, row + (c / bs) * bb, (int)(c % bs));
+    }
+    }
+}
+
+__device__ uint16_t raw_element_bf16(const RawView &v, int64_t r, int64_t c) {
+    switch (v.dtype) {
+    case DITCH_FP8: {
+        uint32_t code = v.data[r * v.cols + c];
+        int64_t sr = fp8_scale_row(r, v.block_rows, v.row_shard);
+        float s = load_scale(v.scale, sr * v.scale_cols + c / v.block_cols, v.scale_type);
+        return f32_to_bf16(mul_x86(fp8_value(code, v.e5m2), s));
+    }
+    case DITCH_MXFP4: {
+        uint8_t byte = v.data[r * (v.cols / 2) + c / 2];
+        uint32_t nib = (c & 1) ? (byte >> 4) : (byte & 0x0f);
+        float sc = e8m0_scale(v.scale[r * (v.cols / 32) + c / 32]);
+        return f32_to_bf16(mul_x86(e2m1_value(nib), sc));
+    }
+    case DITCH_MXFP4_T: {
+        // view (h = r, j = c) is source row j, element h (dequant.zig:603-637)
+        int64_t nblk = v.rows / 32;
+        int64_t h = r, j = c;
+        uint8_t byte = v.data[(j * nblk + h / 32) * 16 + (h % 32) / 2];
+        uint32_t nib = (h & 1) ? (byte >> 4) : (byte & 0x0f);
+        float sc = e8m0_scale(v.scale[j * nblk + h / 32]);
+        return f32_to_bf16(mul_x86(e2m1_value(nib), sc));
+    }
+    case DITCH_INT_PACKED: {
+        int bits = v.bits;
+        int64_t wpr = (v.cols * bits + 31) / 32;
+        int offset = 1 << (bits - 1);
+        int64_t g = v.g_idx ? (int64_t)v.g_idx[c] : c / v.group;
+        int zp = 0;
+        if (v.zero) {
+            const uint32_t *zw = (const uint32_t *)v.zero;
+            int64_t start = r * bits;
+            int64_t wi = start / 32;
+            int off = (int)(start % 32);
+            int lo = (32 - off) < bits ? (32 - off) : bits;
+            uint32_t z = (zw[wi * v.groups + g] >> off) & field_mask(lo);
+            if (lo < bits) z |= (zw[(wi + 1) * v.groups + g] & field_mask(bits - lo)) << lo;
+            zp = (int)z - offset;
+        }
+        int q = (int)unpack_field((const uint32_t *)v.data + r * wpr, c, bits) - offset;
+        float s = load_scale(v.scale, r * v.groups + g, v.scale_type);
+        return f32_to_bf16(mul_x86((float)(q - zp), s));
+    }
+    default: return f32_to_bf16(raw_element_f32(v, r, c));
+    }
+}
+
+__global__ void raw_dequant_kernel(RawView v, void *out, int64_t row0, int64_t nrows, int bf16_out) {
+    int64_t total = nrows * v.cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = row0 + i / v.cols, c = i % v.cols;
+        if (bf16_out) ((uint16_t *)out)[i] = raw_element_bf16(v, r, c);
+        else ((float *)out)[i] = raw_element_f32(v, r, c);
+    }
+}
+
+__global__ void tiled_dequant_kernel(TileView v, void *out, int64_t row0, int64_t nrows, int bf16_out) {
+    int64_t total = nrows * v.cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = row0 + i / v.cols, c = i % v.cols;
+        uint16_t b = 0;
+        float f = tiled_element_f32(v, r, c, &b);
+        if (bf16_out) ((uint16_t *)out)[i] = b;
+        else ((float *)out)[i] = f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Re-tiling kernels: one thread per (unit, lane) writes the lane's word(s).
+
+struct RetileArgs {
+    RawView src;        // raw codes on device
+    uint8_t *codes;     // tiled output
+    int32_t tf;
+    int64_t rows, cols, units_k, groups_n;
+    // decoded source (bf16 or f32 row-major) for TF_BF16/TF_F32 built by decode
+    const void *dense;
+    int32_t dense_f32;
+};
+
+__device__ __forceinline__ uint32_t src_code(const RetileArgs &a, int64_t n, int64_t k) {
+    // raw code of element (n, k) for the fused formats; 0 outside the matrix
+    if (n >= a.rows || k >= a.cols) return 0u;
+    const RawView &s = a.src;
+    switch (a.tf) {
+    case TF_Q8: {
+        const uint8_t *row = s.data + n * (s.cols / 32) * 34;
+        return row[(k / 32) * 34 + 2 + (k % 32)];
+    }
+    case TF_FP8: return s.data[n * s.cols + k];
+    case TF_MX4: {
+        uint8_t byte = s.data[n * (s.cols / 2) + k / 2];
+        return (k & 1) ? (byte >> 4) : (byte & 0x0f);
+    }
+    case TF_INT4: {
+        int64_t wpr = (s.cols * 4 + 31) / 32;
+        return unpack_field((const uint32_t *)s.data + n * wpr, k, 4);
+    }
+    case TF_BF16: case TF_F16: return ((const uint16_t *)(a.dense ? a.dense : s.data))[n * a.cols + k];
+    case TF_F32: return ((const uint32_t *)(a.dense ? a.dense : s.data))[n * a.cols + k];
+    default: return 0u;
+    }
+}
+
+__global__ void retile_kernel(RetileArgs a) {
+    int64_t total = a.groups_n * a.units_k * 64;
+    int uk = unit_k_of(a.tf);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int lane = (int)(i % 64);
+        int64_t unit = i / 64;
+        int64_t g = unit / a.units_k, u = unit % a.units_k;
+        int64_t n = g * 16 + lane % 16;
+        int kq = lane / 16;
+        uint8_t *base = a.codes + unit * unit_bytes_of(a.tf);
+        switch (a.tf) {
+        case TF_BF16: case TF_F16: {
+            uint16_t w[8];
+            for (int j = 0; j < 8; j++) w[j] = (uint16_t)src_code(a, n, u * uk + 8 * kq + j);
+            uint4 o;
+            o.x = w[0] | ((uint32_t)w[1] << 16); o.y = w[2] | ((uint32_t)w[3] << 16);
+            o.z = w[4] | ((uint32_t)w[5] << 16); o.w = w[6] | ((uint32_t)w[7] << 16);
+            *(uint4 *)(base + lane * 16) = o;
+            break;
+        }
+        case TF_F32: {
+            uint32_t w[8];
+            for (int j = 0; j < 8; j++) w[j] = src_code(a, n, u * uk + 8 * kq + j);
+            *(uint4 *)(base + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+            *(uint4 *)(base + 1024 + lane * 16) = make_uint4(w[4], w[5], w[6], w[7]);
+            break;
+        }
+        case TF_Q8: case TF_FP8: {
+            uint32_t w[4] = {0, 0, 0, 0};
+            for (int t = 0; t < 2; t++)
+                for (int j = 0; j < 8; j++) {
+                    uint32_t c = src_code(a, n, u * uk + 32 * t + 8 * kq + j) & 0xffu;
+                    int s = t * 8 + j;
+                    w[s / 4] |= c << (8 * (s % 4));
+                }
+            *(uint4 *)(base + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+            break;
+        }
+        case TF_MX4: case TF_INT4: {
+            uint32_t w[4] = {0, 0, 0, 0};
+            for (int t = 0; t < 4; t++)
+                for (int j = 0; j < 8; j++) {
+                    uint32_t c = src_code(a, n, u * uk + 32 * t + 8 * kq + j) & 0xfu;
+                    int s = t * 8 + j;  // nibble index in the 16 B word
+                    w[s / 8] |= c << (4 * (s % 8));
+                }
+            *(uint4 *)(base + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+            break;
+        }
+        }
+    }
+}
+
+// Q8_0 scales: f16 of block (n, kt) -> [rows_pad][kt_pad]
+__global__ void q8_scales_kernel(RawView s, uint16_t *out, int64_t rows, int64_t kt_src, int64_t kt_pad, int64_t rows_pad) {
+    int64_t total = rows_pad * kt_pad;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n = i / kt_pad, kt = i % kt_pad;
+        uint16_t v = 0;
+        if (n < rows && kt < kt_src) {
+            const uint8_t *b = s.data + (n * kt_src + kt) * 34;
+            v = (uint16_t)(b[0] | (b[1] << 8));
+        }
+        out[i] = v;
+    }
+}
+
+// Copy of a [rows][cols] byte matrix into a zero-padded [rows_pad][cols_pad] one.
+__global__ void pad_copy_kernel(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols_bytes, int64_t rows_pad,
+                                int64_t cols_pad_bytes) {
+    int64_t total = rows_pad * cols_pad_bytes;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = i / cols_pad_bytes, c = i % cols_pad_bytes;
+        dst[i] = (r < rows && c < cols_bytes) ? src[r * cols_bytes + c] : 0;
+    }
+}
+
+// INT4 zero points: packed along rows (dequant.zig:548-561) -> field value [rows_pad][groups_pad]
+__global__ void int_zero_kernel(const uint32_t *zw, uint8_t *out, int64_t rows, int64_t groups, int64_t rows_pad,
+                                int64_t groups_pad) {
+    int64_t total = rows_pad * groups_pad;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n = i / groups_pad, g = i % groups_pad;
+        uint8_t v = 8;  // field 8 = zero point 0
+        if (n < rows && g < groups) {
+            int64_t start = n * 4;
+            v = (uint8_t)((zw[(start / 32) * groups + g] >> (start % 32)) & 0xfu);
+        }
+        out[i] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+static int grid_for(int64_t total) {
+    int64_t g = (total + 255) / 256;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+void *dev_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (bytes == 0) bytes = 16;
+    DITCH_TRY_HIP(hipMalloc(&p, bytes));
+    return p;
+}
+void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+static size_t scale_elem_bytes(int32_t st) {
+    switch (st) {
+    case DITCH_F32: return 4;
+    case DITCH_F16: case DITCH_BF16: return 2;
+    case DITCH_E8M0: return 1;
+    default: return 0;
+    }
+}
+static int32_t scale_type_code(int32_t st) {
+    switch (st) {
+    case DITCH_F16: return SC_F16;
+    case DITCH_BF16: return SC_BF16;
+    case DITCH_E8M0: return SC_E8M0;
+    default: return SC_F32;
+    }
+}
+
+// Validates `w` and fills the raw view plus the byte sizes of its pieces.
+struct RawSizes {
+    size_t data, scale, zero, gidx;
+};
+
+static RawSizes raw_sizes(const ditch_weight *w) {
+    RawSizes z{0, 0, 0, 0};
+    int64_t rows = (int64_t)w->rows, cols = (int64_t)w->cols;
+    DITCH_CHECK(w->data != nullptr, DITCH_INVALID_ARGUMENT, "weight data is NULL");
+    switch (w->dtype) {
+    case DITCH_F32: z.data = rows * cols * 4; break;
+    case DITCH_F16: case DITCH_BF16: z.data = rows * cols * 2; break;
+    case DITCH_Q8_0: case DITCH_Q4_0: case DITCH_Q4_1: case DITCH_Q5_0: case DITCH_Q5_1:
+    case DITCH_Q4_K: case DITCH_Q6_K: case DITCH_Q8_K: {
+        int bs = gguf_block_size(w->dtype);
+        DITCH_CHECK(cols % bs == 0, DITCH_INVALID_ARGUMENT, "GGUF row length is not a whole number of blocks");
+        z.data = rows * (cols / bs) * gguf_block_bytes(w->dtype);
+        break;
+    }
+    case DITCH_FP8:
+        DITCH_CHECK(w->scale && w->block_rows > 0 && w->block_cols > 0 && w->scale_cols > 0 && w->scale_rows > 0,
+                    DITCH_INVALID_ARGUMENT, "FP8 weight needs a scale grid and block sizes");
+        DITCH_CHECK(scale_elem_bytes(w->scale_dtype) > 0, DITCH_INVALID_ARGUMENT, "FP8 scale dtype");
+        z.data = rows * cols;
+        z.scale = w->scale_rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
+        break;
+    case DITCH_MXFP4:
+        DITCH_CHECK(cols % 32 == 0 && w->scale, DITCH_INVALID_ARGUMENT, "MXFP4 needs cols % 32 == 0 and scales");
+        z.data = rows * cols / 2;
+        z.scale = rows * cols / 32;
+        break;
+    case DITCH_MXFP4_T:
+        DITCH_CHECK(rows % 32 == 0 && w->scale, DITCH_INVALID_ARGUMENT, "transposed MXFP4 needs rows % 32 == 0 and scales");
+        z.data = cols * rows / 2;
+        z.scale = cols * rows / 32;
+        break;
+    case DITCH_INT_PACKED: {
+        DITCH_CHECK(w->bits >= 1 && w->bits <= 8 && w->scale && w->scale_cols > 0, DITCH_INVALID_ARGUMENT,
+                    "pack-quantized weight needs 1..8 bits and scales");
+        DITCH_CHECK(w->g_idx || w->group > 0, DITCH_INVALID_ARGUMENT, "pack-quantized weight needs a group size");
+        DITCH_CHECK(scale_elem_bytes(w->scale_dtype) > 1, DITCH_INVALID_ARGUMENT, "pack-quantized scale dtype");
+        int64_t wpr = (cols * w->bits + 31) / 32;
+        z.data = rows * wpr * 4;
+        z.scale = rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
+        if (w->zero) z.zero = ((rows * w->bits + 31) / 32) * w->scale_cols * 4;
+        if (w->g_idx) z.gidx = cols * 4;
+        break;
+    }
+    default: throw Error{DITCH_UNSUPPORTED, "unsupported weight dtype " + std::to_string(w->dtype)};
+    }
+    return z;
+}
+
+// Copies the raw pieces of `w` to one device staging buffer.
+struct Staged {
+    void *buf = nullptr;
+    RawView v{};
+    ~Staged() { dev_free(buf); }
+};
+
+static void stage_raw(const ditch_weight *w, hipStream_t s, Staged &st) {
+    RawSizes z = raw_sizes(w);
+    auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+    size_t total = al(z.data) + al(z.scale) + al(z.zero) + al(z.gidx);
+    st.buf = dev_alloc(total);
+    uint8_t *p = (uint8_t *)st.buf;
+    RawView &v = st.v;
+    v = RawView{};
+    v.dtype = w->dtype;
+    v.rows = (int64_t)w->rows;
+    v.cols = (int64_t)w->cols;
+    v.data = p;
+    DITCH_TRY_HIP(hipMemcpyAsync(p, w->data, z.data, hipMemcpyHostToDevice, s));
+    p += al(z.data);
+    if (z.scale) {
+        v.scale = p;
+        DITCH_TRY_HIP(hipMemcpyAsync(p, w->scale, z.scale, hipMemcpyHostToDevice, s));
+        p += al(z.scale);
+    }
+    if (z.zero) {
+        v.zero = p;
+        DITCH_TRY_HIP(hipMemcpyAsync(p, w->zero, z.zero, hipMemcpyHostToDevice, s));
+        p += al(z.zero);
+    }
+    if (z.gidx) {
+        v.g_idx = (const int32_t *)p;
+        DITCH_TRY_HIP(hipMemcpyAsync(p, w->g_idx, z.gidx, hipMemcpyHostToDevice, s));
+        p += al(z.gidx);
+    }
+    v.scale_type = scale_type_code(w->scale_dtype);
+    v.scale_cols = (int64_t)w->scale_cols;
+    v.block_rows = (int64_t)w->block_rows;
+    v.block_cols = (int64_t)w->block_cols;
+    v.row_shard = (int64_t)w->row_shard;
+    v.e5m2 = w->fp8_e5m2;
+    v.bits = w->bits;
+    v.group = (int64_t)w->group;
+    v.groups = (int64_t)w->scale_cols;
+}
+
+void launch_raw_dequant(const RawView &v, void *out, int64_t row0, int64_t nrows, int bf16_out, hipStream_t s) {
+    int64_t total = nrows * v.cols;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(raw_dequant_kernel, dim3(grid_for(total)), dim3(256), 0, s, v, out, row0, nrows, bf16_out);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+void launch_dequant(const TileView &v, void *out, int64_t row0, int64_t nrows, hipStream_t s) {
+    int64_t total = nrows * v.cols;
+    if (total <= 0) return;
+    int bf16_out = is_bf16_virtual(v.orig_dtype) ? 1 : 0;
+    hipLaunchKernelGGL(tiled_dequant_kernel, dim3(grid_for(total)), dim3(256), 0, s, v, out, row0, nrows, bf16_out);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+// Host-memory decode of rows (ditch_hip_dequant): raw-layout path.
+void dequant_to_host(ditch_hip *h, void *out, const ditch_weight *w, uint64_t row0, uint64_t nrows) {
+    hipStream_t s = h->stream;
+    DITCH_CHECK(row0 + nrows <= w->rows, DITCH_INVALID_ARGUMENT, "row range outside the weight");
+    Staged st;
+    stage_raw(w, s, st);
+    int bf16_out = is_bf16_virtual(w->dtype) ? 1 : 0;
+    size_t bytes = nrows * w->cols * (bf16_out ? 2 : 4);
+    void *d_out = dev_alloc(bytes);
+    try {
+        launch_raw_dequant(st.v, d_out, (int64_t)row0, (int64_t)nrows, bf16_out, s);
+        DITCH_TRY_HIP(hipMemcpyAsync(out, d_out, bytes, hipMemcpyDeviceToHost, s));
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        dev_free(d_out);
+        throw;
+    }
+    dev_free(d_out);
+}
+
+void free_tensor(ditch_hip_tensor *t) {
+    if (!t) return;
+    dev_free(t->codes);
+    dev_free(t->scale);
+    dev_free(t->zero);
+    delete t;
+}
+
+ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s) {
+    (void)h;
+    DITCH_CHECK(w && w->rows > 0 && w->cols > 0, DITCH_INVALID_ARGUMENT, "empty weight");
+    Staged st;
+    stage_raw(w, s, st);
+    auto *t = new ditch_hip_tensor();
+    try {
+        TileView &v = t->v;
+        v = TileView{};
+        v.rows = (int64_t)w->rows;
+        v.cols = (int64_t)w->cols;
+        v.orig_dtype = w->dtype;
+        // choose the tile format
+        int tf;
+        void *dense = nullptr;
+        int dense_f32 = 0;
+        switch (w->dtype) {
+        case DITCH_F32: tf = TF_F32; break;
+        case DITCH_F16: tf = TF_F16; break;
+        case DITCH_BF16: tf = TF_BF16; break;
+        case DITCH_Q8_0: tf = TF_Q8; break;
+        case DITCH_FP8:
+            tf = (w->block_cols % 8 == 0) ? TF_FP8 : TF_BF16;
+            break;
+        case DITCH_MXFP4: tf = TF_MX4; break;
+        case DITCH_INT_PACKED: tf = (w->bits == 4 && !w->g_idx) ? TF_INT4 : TF_BF16; break;
+        case DITCH_MXFP4_T: tf = TF_BF16; break;
+        default: tf = TF_F32; break;  // other GGUF blocks: decoded to f32 once
+        }
+        bool decode_first = (tf == TF_BF16 && w->dtype != DITCH_BF16) || (tf == TF_F32 && w->dtype != DITCH_F32);
+        if (decode_first) {
+            dense_f32 = (tf == TF_F32) ? 1 : 0;
+            size_t bytes = (size_t)v.rows * v.cols * (dense_f32 ? 4 : 2);
+            dense = dev_alloc(bytes);
+            launch_raw_dequant(st.v, dense, 0, v.rows, dense_f32 ? 0 : 1, s);
+        }
+        v.tf = tf;
+        int uk = unit_k_of(tf);
+        int64_t rows_pad = pad_to(v.rows, 16), cols_pad = pad_to(v.cols, uk);
+        v.units_k = cols_pad / uk;
+        size_t code_bytes = (size_t)(rows_pad / 16) * v.units_k * unit_bytes_of(tf);
+        t->codes = dev_alloc(code_bytes);
+        t->bytes = code_bytes;
+        RetileArgs a{};
+        a.src = st.v;
+        a.codes = (uint8_t *)t->codes;
+        a.tf = tf;
+        a.rows = v.rows;
+        a.cols = v.cols;
+        a.units_k = v.units_k;
+        a.groups_n = rows_pad / 16;
+        a.dense = dense;
+        a.dense_f32 = dense_f32;
+        int64_t total = a.groups_n * a.units_k * 64;
+        hipLaunchKernelGGL(retile_kernel, dim3(grid_for(total)), dim3(256), 0, s, a);
+        DITCH_TRY_HIP(hipGetLastError());
+        // scales
+        switch (tf) {
+        case TF_Q8: {
+            int64_t kt_src = v.cols / 32, kt_pad = cols_pad / 32;
+            size_t b = rows_pad * kt_pad * 2;
+            t->scale = dev_alloc(b);
+            t->bytes += b;
+            hipLaunchKernelGGL(q8_scales_kernel, dim3(grid_for(rows_pad * kt_pad)), dim3(256), 0, s, st.v,
+                               (uint16_t *)t->scale, v.rows, kt_src, kt_pad, rows_pad);
+            v.scale_cols = kt_pad;
+            v.scale_type = SC_F16;
+            break;
+        }
+        case TF_MX4: {
+            int64_t kt_src = v.cols / 32, kt_pad = cols_pad / 32;
+            size_t b = rows_pad * kt_pad;
+            t->scale = dev_alloc(b);
+            t->bytes += b;
+            hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(rows_pad * kt_pad)), dim3(256), 0, s, st.v.scale,
+                               (uint8_t *)t->scale, v.rows, kt_src, rows_pad, kt_pad);
+            v.scale_cols = kt_pad;
+            v.scale_type = SC_E8M0;
+            break;
+        }
+        case TF_FP8: {
+            // the grid as given; rows beyond the matrix clamp to the last grid row in the kernels
+            size_t eb = scale_elem_bytes(w->scale_dtype);
+            int64_t sr_pad = (int64_t)w->scale_rows + 1, sc_pad = pad_to(cols_pad, w->block_cols) / w->block_cols;
+            if (sc_pad < (int64_t)w->scale_cols) sc_pad = (int64_t)w->scale_cols;
+            size_t b = sr_pad * sc_pad * eb;
+            t->scale = dev_alloc(b);
+            t->bytes += b;
+            DITCH_TRY_HIP(hipMemsetAsync(t->scale, 0, b, s));
+            hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(sr_pad * sc_pad * eb)), dim3(256), 0, s, st.v.scale,
+                               (uint8_t *)t->scale, (int64_t)w->scale_rows, (int64_t)(w->scale_cols * eb), sr_pad,
+                               (int64_t)(sc_pad * eb));
+            v.scale_cols = sc_pad;
+            v.scale_type = scale_type_code(w->scale_dtype);
+            v.block_rows = (int64_t)w->block_rows;
+            v.block_cols = (int64_t)w->block_cols;
+            v.row_shard = (int64_t)w->row_shard;
+            v.e5m2 = w->fp8_e5m2;
+            break;
+        }
+        case TF_INT4: {
+            size_t eb = scale_elem_bytes(w->scale_dtype);
+            int64_t groups = (int64_t)w->scale_cols;
+            int64_t groups_pad = (cols_pad + (int64_t)w->group - 1) / (int64_t)w->group;
+            if (groups_pad < groups) groups_pad = groups;
+            size_t b = rows_pad * groups_pad * eb;
+            t->scale = dev_alloc(b);
+            t->bytes += b;
+            hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(rows_pad * groups_pad * eb)), dim3(256), 0, s,
+                               st.v.scale, (uint8_t *)t->scale, v.rows, (int64_t)(groups * eb), rows_pad,
+                               (int64_t)(groups_pad * eb));
+            if (w->zero) {
+                size_t zb = rows_pad * groups_pad;
+                t->zero = dev_alloc(zb);
+                t->bytes += zb;
+                hipLaunchKernelGGL(int_zero_kernel, dim3(grid_for(rows_pad * groups_pad)), dim3(256), 0, s,
+                                   (const uint32_t *)st.v.zero, (uint8_t *)t->zero, v.rows, groups, rows_pad,
+                                   groups_pad);
+            }
+            v.scale_cols = groups_pad;
+            v.scale_type = scale_type_code(w->scale_dtype);
+            v.group = (int64_t)w->group;
+            break;
+        }
+        default: break;
+        }
+        DITCH_TRY_HIP(hipGetLastError());
+        v.codes = (const uint8_t *)t->codes;
+        v.scale = t->scale;
+        v.zero = (const uint8_t *)t->zero;
+        DITCH_TRY_HIP(hipStreamSynchronize(s));
+        dev_free(dense);
+    } catch (...) {
+        free_tensor(t);
+        throw;
+    }
+    return t;
+}
+
+}  // namespace ditch

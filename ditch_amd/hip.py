@@ -1,0 +1,251 @@
+"""ctypes binding of libditch_hip.so for Python callers.
+
+`Device` mirrors the operations of compute.zig's VTable (compute.zig:90-117)
+with numpy arrays; `Model` wraps the resident forward. Every call goes to the
+HIP library; a failing status raises `DeviceError` (there is no CPU path
+here, the reference's own tensor.zig is the CPU path of a Zig caller).
+"""
+import ctypes
+
+import numpy as np
+
+from . import abi, load_library
+from .weights import HostWeight
+
+
+class DeviceError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{abi.STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Device:
+    def __init__(self, index=0):
+        self.lib = load_library()
+        err = ctypes.create_string_buffer(512)
+        self.h = self.lib.ditch_hip_open(index, err, 512)
+        if not self.h:
+            raise DeviceError(abi.DEVICE_FAILED, err.value.decode())
+
+    def close(self):
+        if self.h:
+            self.lib.ditch_hip_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def name(self):
+        return self.lib.ditch_hip_name(self.h).decode()
+
+    @property
+    def stream(self):
+        return self.lib.ditch_hip_stream(self.h)
+
+    def check(self, rc):
+        if rc != abi.OK:
+            raise DeviceError(rc, self.lib.ditch_hip_last_error(self.h).decode())
+
+    def sync(self):
+        self.check(self.lib.ditch_hip_sync(self.h))
+
+    # VTable -----------------------------------------------------------------
+
+    def matmulT(self, x, w: HostWeight):
+        x = _f32(x)
+        n = x.shape[0]
+        out = np.empty((n, w.rows), dtype=np.float32)
+        self.check(self.lib.ditch_hip_matmulT(self.h, _p(out), _p(x), n, w.ref()))
+        return out
+
+    def matvecTMulti(self, w: HostWeight, y):
+        y = _f32(y)
+        q = y.shape[0]
+        out = np.empty((q, w.cols), dtype=np.float32)
+        self.check(self.lib.ditch_hip_matvecTMulti(self.h, _p(out), w.ref(), _p(y), q))
+        return out
+
+    def rowNorms(self, w: HostWeight):
+        out = np.empty(w.rows, dtype=np.float32)
+        self.check(self.lib.ditch_hip_rowNorms(self.h, _p(out), w.ref()))
+        return out
+
+    def attentionScores(self, q, k, n_keys, stride, scale):
+        q, k = _f32(q), _f32(k)
+        out = np.empty(n_keys, dtype=np.float32)
+        self.check(self.lib.ditch_hip_attentionScores(self.h, _p(out), n_keys, _p(q), q.size, _p(k), stride, scale))
+        return out
+
+    def attentionValues(self, scores, v, vd, stride):
+        scores, v = _f32(scores), _f32(v)
+        out = np.empty(vd, dtype=np.float32)
+        self.check(self.lib.ditch_hip_attentionValues(self.h, _p(out), vd, _p(scores), scores.size, _p(v), stride))
+        return out
+
+    def gatedActivation(self, act, gate, up, n, length, in_stride, out_stride, out=None):
+        gate = _f32(gate)
+        up = None if up is None else _f32(up)
+        if out is None:
+            out = np.zeros(((n - 1) * out_stride + length,), dtype=np.float32)
+        self.check(self.lib.ditch_hip_gatedActivation(self.h, act, _p(out), _p(gate), _p(up), n, length,
+                                                      in_stride, out_stride))
+        return out
+
+    def rmsnormRows(self, x, weight, eps, gemma_style=False):
+        x = _f32(x)
+        n, length = x.shape
+        w = None if weight is None else _f32(weight)
+        out = np.empty_like(x)
+        self.check(self.lib.ditch_hip_rmsnormRows(self.h, _p(out), _p(x), _p(w), 0 if w is None else w.size, n,
+                                                  length, eps, int(gemma_style)))
+        return out
+
+    def layernormRows(self, x, weight, bias, eps, one_plus=False):
+        x = _f32(x)
+        n, length = x.shape
+        w = None if weight is None else _f32(weight)
+        b = None if bias is None else _f32(bias)
+        out = np.empty_like(x)
+        self.check(self.lib.ditch_hip_layernormRows(self.h, _p(out), _p(x), _p(w), 0 if w is None else w.size,
+                                                    _p(b), n, length, eps, int(one_plus)))
+        return out
+
+    def softmaxRows(self, x):
+        x = _f32(x).copy()
+        n, length = x.shape
+        self.check(self.lib.ditch_hip_softmaxRows(self.h, _p(x), n, length))
+        return x
+
+    def ropeRows(self, x, cos_t, sin_t, pos, style):
+        x = _f32(x).copy()
+        n, dim = x.shape
+        cos_t, sin_t = _f32(cos_t), _f32(sin_t)
+        pos = np.ascontiguousarray(pos, dtype=np.uint32)
+        self.check(self.lib.ditch_hip_ropeRows(self.h, _p(x), n, dim, _p(cos_t), _p(sin_t), cos_t.shape[0],
+                                               cos_t.shape[1], _p(pos), style))
+        return x
+
+    # extensions ---------------------------------------------------------------
+
+    def dequant(self, w: HostWeight, row0=0, nrows=None):
+        nrows = w.rows - row0 if nrows is None else nrows
+        bf16 = w.dtype in (abi.FP8, abi.MXFP4, abi.MXFP4_T, abi.INT_PACKED)
+        out = np.empty((nrows, w.cols), dtype=np.uint16 if bf16 else np.float32)
+        self.check(self.lib.ditch_hip_dequant(self.h, _p(out), w.ref(), row0, nrows))
+        return out
+
+    def upload(self, w: HostWeight):
+        t = self.lib.ditch_hip_upload(self.h, w.ref())
+        if not t:
+            raise DeviceError(abi.DEVICE_FAILED, self.lib.ditch_hip_last_error(self.h).decode())
+        return Tensor(self, t, w)
+
+    def edit_delta(self, w: HostWeight, v, weight):
+        v = _f32(v)
+        k = v.shape[0]
+        a = np.empty((k, w.cols), dtype=np.float32)
+        b = np.empty((w.rows, k), dtype=np.float32)
+        self.check(self.lib.ditch_hip_edit_delta(self.h, _p(a), _p(b), w.ref(), _p(v), k, weight))
+        return a, b
+
+    def logSoftmaxRows(self, x):
+        x = _f32(x)
+        out = np.empty_like(x)
+        self.check(self.lib.ditch_hip_logSoftmaxRows(self.h, _p(out), _p(x), x.shape[0], x.shape[1]))
+        return out
+
+    def klRows(self, base_logprobs, trial_logits):
+        b, t = _f32(base_logprobs), _f32(trial_logits)
+        out = np.empty(b.shape[0], dtype=np.float64)
+        self.check(self.lib.ditch_hip_klRows(self.h, _p(out), _p(b), _p(t), b.shape[0], b.shape[1]))
+        return out
+
+
+class Tensor:
+    """A weight resident in HBM (ditch_hip_upload)."""
+
+    def __init__(self, dev, handle, host):
+        self.dev, self.handle, self.rows, self.cols = dev, handle, host.rows, host.cols
+        self.dtype = host.dtype
+
+    @property
+    def nbytes(self):
+        return self.dev.lib.ditch_hip_tensor_bytes(self.handle)
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.ditch_hip_tensor_free(self.dev.h, self.handle)
+            self.handle = None
+
+    def matmul_device(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None):
+        self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, d_x, n, self.handle, d_bias,
+                                                             int(accumulate), stream))
+
+    def dequant_device(self, d_out, row0, nrows):
+        self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, self.handle, row0, nrows))
+
+
+class Model:
+    """A resident model (ditch_hip_model) built from a ModelSpec."""
+
+    def __init__(self, dev: Device, spec):
+        self.dev = dev
+        self.spec = spec
+        self.cfg = spec.config_struct()
+        self.h = dev.lib.ditch_hip_model_create(dev.h, ctypes.byref(self.cfg))
+        if not self.h:
+            raise DeviceError(abi.DEVICE_FAILED, dev.lib.ditch_hip_last_error(dev.h).decode())
+        for (layer, slot, expert), w in spec.tensors.items():
+            dev.check(dev.lib.ditch_hip_model_set(self.h, layer, slot, expert, w.ref()))
+
+    def free(self):
+        if self.h:
+            self.dev.lib.ditch_hip_model_free(self.h)
+            self.h = None
+
+    @property
+    def nbytes(self):
+        return self.dev.lib.ditch_hip_model_bytes(self.h)
+
+    def set_delta(self, layer, slot, expert, a, b):
+        a, b = _f32(a), _f32(b)
+        rank = a.shape[0]
+        self.dev.check(self.dev.lib.ditch_hip_model_set_delta(self.h, layer, slot, expert, rank, _p(a), _p(b)))
+
+    def edit(self, layer, slot, expert, v, weight):
+        v = _f32(v)
+        self.dev.check(self.dev.lib.ditch_hip_model_edit(self.h, layer, slot, expert, _p(v), v.shape[0], weight))
+
+    def reset_deltas(self):
+        self.dev.check(self.dev.lib.ditch_hip_model_reset_deltas(self.h))
+
+    def forward(self, tokens, rows, capture_rows=(), logit_rows=()):
+        """tokens u32[n]; rows [(b, pos)]; returns (residuals [(L+1)][nc][hidden], logits [nl][vocab])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        rows_a = np.ascontiguousarray(rows, dtype=np.uint32).reshape(-1, 2)
+        cap = np.ascontiguousarray(capture_rows, dtype=np.uint64)
+        lr = np.ascontiguousarray(logit_rows, dtype=np.uint64)
+        c = self.spec.config
+        res = np.empty((c["layers"] + 1, cap.size, c["hidden"]), dtype=np.float32)
+        logits = np.empty((lr.size, c["vocab"]), dtype=np.float32)
+        self.dev.check(self.dev.lib.ditch_hip_forward(
+            self.h, _p(tokens), _p(rows_a), tokens.size, _p(cap) if cap.size else None, cap.size,
+            _p(res) if cap.size else None, _p(lr) if lr.size else None, lr.size,
+            _p(logits) if lr.size else None))
+        return res, logits
+
+    def forward_device(self, d_tokens, d_rows, n, d_capture, n_capture, d_res, d_logit_rows, n_logit, d_logits):
+        self.dev.check(self.dev.lib.ditch_hip_forward_device(self.h, d_tokens, d_rows, n, d_capture, n_capture,
+                                                             d_res, d_logit_rows, n_logit, d_logits))

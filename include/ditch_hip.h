@@ -1,0 +1,376 @@
+/*
+ * ditch_hip.h — C ABI of the MI355X (gfx950) device backend for ditch's
+ * operator seam.
+ *
+ * The reference routes every matrix product of its forward pass through
+ * `compute.zig` (compute.zig:90-117, `VTable`): a backend fills function
+ * pointers that take host slices, compute synchronously and return
+ * `error{Unsupported, DeviceFailed, OutOfMemory}` (compute.zig:54-60).
+ * The entry points below are exactly those operations as `extern "C"`
+ * functions (host pointers + sizes), plus the extensions the north star asks
+ * for: packed quantised weights handed to the device as-is (the `Dequant`
+ * descriptor of dequant.zig:346-375 folded into `ditch_weight`), weights
+ * registered once in HBM, the resident forward (model.zig:4619
+ * `forward(..., ForwardOptions)`), routed MoE (moe.zig:998), the rank-k edit
+ * (abliterate.zig:264-280) and the KL scorer's log-softmax/KL
+ * (tensor.zig:1203-1210, scorers.zig:378-402).
+ *
+ * Conventions follow the Metal shim (src/metal/shim.h:6-7): every function is
+ * safe to call with a NULL context (it then fails cleanly), nothing throws
+ * across the boundary, and the caller owns every buffer it passes. Calls on
+ * one context are serialised by a mutex inside the library (the Vulkan
+ * backend's one lock, vulkan/backend.zig:146-148, 229-230).
+ */
+#ifndef DITCH_HIP_H
+#define DITCH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status codes. 0..3 map one to one onto compute.zig:54-60
+ * (ok, error.Unsupported, error.DeviceFailed, error.OutOfMemory). A Zig
+ * caller maps DITCH_INVALID_ARGUMENT to error.DeviceFailed.                 */
+enum {
+    DITCH_OK = 0,
+    DITCH_UNSUPPORTED = 1,
+    DITCH_DEVICE_FAILED = 2,
+    DITCH_OUT_OF_MEMORY = 3,
+    DITCH_INVALID_ARGUMENT = 4
+};
+
+/* ------------------------------------------------------------------------ */
+/* Storage formats. 0..12 keep the numbering of tensor.zig:11-33 (`DType`:
+ * f32, f16, bf16, i64, i32, q8_0, q4_0, q4_1, q5_0, q5_1, q4_k, q6_k, q8_k);
+ * the quantised-safetensors formats of dequant.zig:70 (`Method`) follow.    */
+enum {
+    DITCH_F32 = 0,
+    DITCH_F16 = 1,
+    DITCH_BF16 = 2,
+    DITCH_I64 = 3,
+    DITCH_I32 = 4,
+    DITCH_Q8_0 = 5,
+    DITCH_Q4_0 = 6,
+    DITCH_Q4_1 = 7,
+    DITCH_Q5_0 = 8,
+    DITCH_Q5_1 = 9,
+    DITCH_Q4_K = 10,
+    DITCH_Q6_K = 11,
+    DITCH_Q8_K = 12,
+    /* FP8 (dequant.zig:477-514): `data` = E4M3 (or E5M2) codes [rows][cols],
+     * `scale` = grid [scale_rows][scale_cols] of f32/bf16/f16 or E8M0 bytes,
+     * one value per block_rows x block_cols elements. Value = bf16_rne(code * s). */
+    DITCH_FP8 = 32,
+    /* MXFP4 natural layout (mxfp4-pack-quantized / store_dtype,
+     * dequant.zig:643-673): `data` = [rows][cols/2] nibble pairs, low nibble
+     * first; `scale` = E8M0 [rows][cols/32]. Value = bf16_rne(e2m1 * 2^(s-127)). */
+    DITCH_MXFP4 = 33,
+    /* MXFP4 gpt-oss layout (dequant.zig:603-637): `data` = [cols][rows/32][16]
+     * blocks of the transpose, `scale` = E8M0 [cols][rows/32].               */
+    DITCH_MXFP4_T = 34,
+    /* compressed-tensors pack-quantized (dequant.zig:518-597): `data` = I32
+     * words [rows][ceil(cols*bits/32)], `scale` [rows][groups] (f16/bf16/f32),
+     * `zero` packed along rows [ceil(rows*bits/32)][groups] I32 or NULL,
+     * `g_idx` I32 [cols] or NULL. Value = bf16_rne((q - zp) * scale).       */
+    DITCH_INT_PACKED = 35,
+    /* Scale dtype only: E8M0 exponent bytes (2^(b-127), dequant.zig:446). */
+    DITCH_E8M0 = 40
+};
+
+/* A weight matrix as the kernels see it: `tensor.Weight{data, dtype, rows,
+ * cols}` (tensor.zig:517-521) widened with the pieces of a quantised group
+ * (dequant.zig:346-375). `rows` x `cols` is the logical matrix (the virtual
+ * bf16 tensor for FP8/MXFP4/INT, the f32 view for float and GGUF types).
+ * Unused fields are zero / NULL.                                           */
+typedef struct ditch_weight {
+    const void *data;
+    int32_t dtype;
+    int32_t scale_dtype;
+    uint64_t rows;
+    uint64_t cols;
+    const void *scale;
+    uint64_t scale_rows;   /* FP8 grid rows; INT: rows                      */
+    uint64_t scale_cols;   /* FP8 grid cols; INT: groups per row            */
+    uint64_t block_rows;   /* FP8 weight_block_size[0]                      */
+    uint64_t block_cols;   /* FP8 weight_block_size[1]                      */
+    uint64_t row_shard;    /* FP8 attn_row_shards (dequant.zig:471-475), 0 = none */
+    int32_t fp8_e5m2;      /* FP8: codes are E5M2 instead of E4M3           */
+    int32_t bits;          /* INT: field width (1..8)                       */
+    uint64_t group;        /* INT: columns per scale group                  */
+    const void *zero;      /* INT: packed zero points, NULL = symmetric     */
+    const int32_t *g_idx;  /* INT: actorder group per column, NULL = none   */
+} ditch_weight;
+
+/* ------------------------------------------------------------------------ */
+/* Context (one GPU).                                                        */
+typedef struct ditch_hip ditch_hip;
+
+/* Opens HIP device `device`. NULL on failure, with a message in `err`.     */
+ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len);
+void ditch_hip_close(ditch_hip *h);
+/* Device name, e.g. "AMD Instinct MI355X (gfx950)". Owned by the context. */
+const char *ditch_hip_name(ditch_hip *h);
+/* Message of the last failed call on this context ("" if none).           */
+const char *ditch_hip_last_error(ditch_hip *h);
+/* VTable.forgetWeights (compute.zig:96-97, 325-327): drops every weight the
+ * per-call entry points keep resident. Registered tensors are unaffected. */
+void ditch_hip_forget_weights(ditch_hip *h);
+/* The HIP stream every call of this context runs on (hipStream_t).         */
+void *ditch_hip_stream(ditch_hip *h);
+/* Waits for the context's stream.                                          */
+int32_t ditch_hip_sync(ditch_hip *h);
+
+/* ------------------------------------------------------------------------ */
+/* VTable operations (compute.zig:98-116). Host memory in and out; each call
+ * uploads, computes and copies back before it returns
+ * (vulkan/backend.zig:21-23). Replaces the bodies of `matmulTOn`,
+ * `matvecTMultiOn`, `rowNormsOn`, `attentionScoresOn`, ... (compute.zig:343-
+ * 560) when a Zig backend fills `VTable` with these.                       */
+
+/* out[n][w.rows] = x[n][w.cols] @ W^T          (compute.zig:100, tensor.zig:1023) */
+int32_t ditch_hip_matmulT(ditch_hip *h, float *out, const float *x, uint64_t n,
+                          const ditch_weight *w);
+/* out[q][w.cols] = y[q][w.rows] @ W            (compute.zig:102, tensor.zig:1079) */
+int32_t ditch_hip_matvecTMulti(ditch_hip *h, float *out, const ditch_weight *w,
+                               const float *y, uint64_t q);
+/* out[w.rows] = ||W_i||_2                      (compute.zig:104, tensor.zig:1114) */
+int32_t ditch_hip_rowNorms(ditch_hip *h, float *out, const ditch_weight *w);
+/* scores[p] = scale * dot(q[0..hd], k[p*stride ..])   (compute.zig:107, tensor.zig:1126) */
+int32_t ditch_hip_attentionScores(ditch_hip *h, float *scores, uint64_t n_keys,
+                                  const float *q, uint64_t hd, const float *k,
+                                  uint64_t stride, float scale);
+/* out[j] = sum_p scores[p] * v[p*stride + j], j < vd (compute.zig:109, tensor.zig:1148) */
+int32_t ditch_hip_attentionValues(ditch_hip *h, float *out, uint64_t vd,
+                                  const float *scores, uint64_t n_keys,
+                                  const float *v, uint64_t stride);
+/* out[i][j] = act(gate[i][j]) * up[i][j] (up may be NULL); `act` follows
+ * tensor.Activation order: silu, gelu_tanh, gelu, relu, relu2, quick_gelu
+ * (compute.zig:81-83, 111; tensor.zig:1227-1334)                           */
+int32_t ditch_hip_gatedActivation(ditch_hip *h, uint32_t act, float *out,
+                                  const float *gate, const float *up, uint64_t n,
+                                  uint64_t len, uint64_t in_stride,
+                                  uint64_t out_stride);
+/* RMS norm of n rows of len (weight_len 0 = weightless)  (compute.zig:113, tensor.zig:1167) */
+int32_t ditch_hip_rmsnormRows(ditch_hip *h, float *out, const float *x,
+                              const float *weight, uint64_t weight_len,
+                              uint64_t n, uint64_t len, float eps,
+                              int32_t gemma_style);
+/* LayerNorm of n rows (bias may be NULL)       (compute.zig:115, tensor.zig:1343) */
+int32_t ditch_hip_layernormRows(ditch_hip *h, float *out, const float *x,
+                                const float *weight, uint64_t weight_len,
+                                const float *bias, uint64_t n, uint64_t len,
+                                float eps, int32_t one_plus);
+/* In-place softmax of n rows of len             (compute.zig:117, tensor.zig:1181) */
+int32_t ditch_hip_softmaxRows(ditch_hip *h, float *x, uint64_t n, uint64_t len);
+/* RoPE of n head vectors of dim at pos[i] against [table_len][half] tables;
+ * style 0 = neox (rotate half), 1 = gptj (pairs)  (compute.zig:85, 119)     */
+int32_t ditch_hip_ropeRows(ditch_hip *h, float *x, uint64_t n, uint64_t dim,
+                           const float *cos_table, const float *sin_table,
+                           uint64_t table_len, uint64_t half, const uint32_t *pos,
+                           uint32_t style);
+
+/* ------------------------------------------------------------------------ */
+/* Decode (bit-exact with the CPU decoders). Rows [row0, row0+nrows) of `w`
+ * into host `out`: bf16 for DITCH_FP8/MXFP4/MXFP4_T/INT_PACKED (the virtual
+ * tensor of dequant.zig), f32 for float and GGUF types (tensor.Weight.row,
+ * tensor.zig:523-526 -> quant.zig:57-79).                                   */
+int32_t ditch_hip_dequant(ditch_hip *h, void *out, const ditch_weight *w,
+                          uint64_t row0, uint64_t nrows);
+
+/* ------------------------------------------------------------------------ */
+/* Weights resident in HBM. `ditch_hip_upload` copies a weight from host
+ * memory once and re-tiles it for the kernels (same bytes, no loss): the
+ * explicit-registration form of compute.zig's `Residency` (compute.zig:580-
+ * 693), for weights the caller keeps stable.                               */
+typedef struct ditch_hip_tensor ditch_hip_tensor;
+ditch_hip_tensor *ditch_hip_upload(ditch_hip *h, const ditch_weight *w);
+void ditch_hip_tensor_free(ditch_hip *h, ditch_hip_tensor *t);
+/* HBM bytes the tensor occupies (codes + scales).                          */
+uint64_t ditch_hip_tensor_bytes(const ditch_hip_tensor *t);
+/* Decode of a resident tensor into device memory (`d_out`), same output
+ * types as ditch_hip_dequant. Runs on the context stream.                   */
+int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out,
+                                 const ditch_hip_tensor *t, uint64_t row0,
+                                 uint64_t nrows);
+/* d_out[n][rows] (=|+=) d_x[n][cols] @ W^T (+ d_bias[rows]) on device
+ * memory, enqueued on `stream` (NULL = the context stream), not waited for.
+ * `accumulate` != 0 adds into d_out (the residual add of model.zig:4944).  */
+int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x,
+                                 uint64_t n, const ditch_hip_tensor *w,
+                                 const float *d_bias, int32_t accumulate,
+                                 void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Resident forward pass (model.zig:4619-4853 with ForwardOptions,
+ * model.zig:3136-3144), for the families of the benchmark configurations:
+ * dense GQA decoders (llama, qwen2 with q/k/v bias, qwen3 q/k head norm),
+ * routed MoE (qwen3_moe softmax top-k; deepseek_v3 sigmoid, correction bias,
+ * group-limited top-k, routed scaling, shared experts) and DeepSeek MLA.   */
+
+enum { DITCH_ROPE_NEOX = 0, DITCH_ROPE_GPTJ = 1 };
+enum {
+    DITCH_ROPE_SCALING_NONE = 0,
+    DITCH_ROPE_SCALING_LINEAR = 1,
+    DITCH_ROPE_SCALING_LLAMA3 = 2,
+    DITCH_ROPE_SCALING_YARN = 3,
+    /* per-frequency divisors (GGUF rope_freqs.weight, gguf_model.zig:171-180) */
+    DITCH_ROPE_SCALING_FACTORS = 4
+};
+enum { DITCH_SCORING_SOFTMAX = 0, DITCH_SCORING_SIGMOID = 1 };
+
+typedef struct ditch_model_config {
+    uint64_t hidden;        /* hidden_size                                  */
+    uint64_t inter;         /* intermediate_size (dense MLP)                */
+    uint64_t layers;        /* num_hidden_layers                            */
+    uint64_t heads;         /* num_attention_heads                          */
+    uint64_t kv_heads;      /* num_key_value_heads                          */
+    uint64_t head_dim;      /* q/k head dim (MLA: nope + rope)              */
+    uint64_t v_head_dim;    /* value head dim (== head_dim unless MLA)      */
+    uint64_t vocab;         /* vocab_size                                   */
+    float rms_eps;          /* rms_norm_eps                                 */
+    float attn_scale;       /* layer_attn_scale (arch.zig:1539, 1584-1591)  */
+    int32_t qkv_bias;       /* q/k/v biases present (qwen2)                 */
+    int32_t qk_norm;        /* per-head q/k RMSNorm before RoPE (qwen3 "head") */
+    int32_t tie_embeddings; /* lm_head = embedding                          */
+    /* RoPE (model.zig:2176-2282)                                           */
+    int32_t rope_style;     /* DITCH_ROPE_*                                 */
+    uint64_t rotary_dim;    /* rotated coordinates per head (MLA: rope dim) */
+    uint64_t rope_len;      /* table rows: clamp(max_position, 512, 8192)   */
+    float rope_theta;
+    int32_t rope_scaling;   /* DITCH_ROPE_SCALING_*                         */
+    float rope_factor;
+    float rope_low_freq_factor;
+    float rope_high_freq_factor;
+    float rope_original_max_position;
+    float yarn_beta_fast;
+    float yarn_beta_slow;
+    float yarn_attention_factor;
+    int32_t yarn_truncate;
+    const float *rope_factors; /* [rotary_dim / 2] for DITCH_ROPE_SCALING_FACTORS */
+    /* MoE (moe.zig:177-389, 998-1228)                                      */
+    uint64_t n_experts;     /* routed experts (0 = dense model)             */
+    uint64_t top_k;
+    uint64_t moe_inter;     /* expert FFN width                             */
+    uint64_t shared_inter;  /* shared-expert FFN width (0 = none)           */
+    int32_t scoring;        /* DITCH_SCORING_*                              */
+    int32_t norm_topk_prob;
+    int32_t group_limited;  /* topk_method group_limited (noaux_tc)         */
+    uint64_t n_group;
+    uint64_t topk_group;
+    float routed_scaling;
+    const uint8_t *moe_layers; /* [layers]: 1 = routed MoE MLP              */
+    /* MLA (model.zig:3292-3342); q_lora_rank 0 = q_b reads h directly       */
+    int32_t mla;
+    uint64_t q_lora_rank;
+    uint64_t kv_lora_rank;
+    uint64_t qk_nope_dim;
+    uint64_t qk_rope_dim;
+    float mla_norm_eps;     /* latent_norm_eps                              */
+} ditch_model_config;
+
+/* Tensor slots of ditch_hip_model_set. Per layer unless marked global.    */
+enum {
+    DITCH_SLOT_EMBED = 0,        /* global [vocab][hidden]                  */
+    DITCH_SLOT_FINAL_NORM = 1,   /* global [hidden]                         */
+    DITCH_SLOT_LM_HEAD = 2,      /* global [vocab][hidden] (absent if tied) */
+    DITCH_SLOT_ATTN_NORM = 10,
+    DITCH_SLOT_Q = 11,
+    DITCH_SLOT_K = 12,
+    DITCH_SLOT_V = 13,
+    DITCH_SLOT_O = 14,
+    DITCH_SLOT_Q_BIAS = 15,
+    DITCH_SLOT_K_BIAS = 16,
+    DITCH_SLOT_V_BIAS = 17,
+    DITCH_SLOT_Q_NORM = 18,
+    DITCH_SLOT_K_NORM = 19,
+    DITCH_SLOT_FFN_NORM = 20,
+    DITCH_SLOT_GATE = 21,
+    DITCH_SLOT_UP = 22,
+    DITCH_SLOT_DOWN = 23,
+    DITCH_SLOT_ROUTER = 30,
+    DITCH_SLOT_ROUTER_CORRECTION = 31, /* e_score_correction_bias [n_experts] */
+    DITCH_SLOT_EXPERT_GATE = 32,       /* `expert` selects the expert       */
+    DITCH_SLOT_EXPERT_UP = 33,
+    DITCH_SLOT_EXPERT_DOWN = 34,
+    DITCH_SLOT_SHARED_GATE = 35,
+    DITCH_SLOT_SHARED_UP = 36,
+    DITCH_SLOT_SHARED_DOWN = 37,
+    DITCH_SLOT_MLA_Q_A = 40,
+    DITCH_SLOT_MLA_Q_A_NORM = 41,
+    DITCH_SLOT_MLA_Q_B = 42,
+    DITCH_SLOT_MLA_KV_A = 43,
+    DITCH_SLOT_MLA_KV_A_NORM = 44,
+    DITCH_SLOT_MLA_KV_B = 45
+};
+
+/* model.Row (model.zig): prompt slot `b` and position `pos` of a token.   */
+typedef struct ditch_row {
+    uint32_t b;
+    uint32_t pos;
+} ditch_row;
+
+typedef struct ditch_hip_model ditch_hip_model;
+ditch_hip_model *ditch_hip_model_create(ditch_hip *h, const ditch_model_config *cfg);
+void ditch_hip_model_free(ditch_hip_model *m);
+/* Registers (uploads) one tensor. Norm/bias slots take DITCH_F32/BF16/F16
+ * vectors (rows = 1). `expert` is ignored except for expert slots.        */
+int32_t ditch_hip_model_set(ditch_hip_model *m, int32_t layer, int32_t slot,
+                            int32_t expert, const ditch_weight *w);
+/* Low-rank delta W' = W + B A on a matrix slot (tensor.zig:588-592; applied
+ * as the matmul epilogue of tensor.zig:871-880): a [rank][cols], b [rows][rank]. */
+int32_t ditch_hip_model_set_delta(ditch_hip_model *m, int32_t layer,
+                                  int32_t slot, int32_t expert, uint64_t rank,
+                                  const float *a, const float *b);
+/* model.resetDeltas (model.zig:2348).                                      */
+int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m);
+/* HBM bytes held by the model's weights.                                   */
+uint64_t ditch_hip_model_bytes(const ditch_hip_model *m);
+
+/* model.forward with ForwardOptions{capture_rows, residuals, logit_rows}:
+ * host buffers. residuals: [(layers+1)][n_capture][hidden] (entry 0 = the
+ * embedding, entry l+1 = after layer l, model.zig:4856-4862); logits:
+ * [n_logit][vocab]. Either output may be NULL when its count is 0.        */
+int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens,
+                          const ditch_row *rows, uint64_t n,
+                          const uint64_t *capture_rows, uint64_t n_capture,
+                          float *residuals, const uint64_t *logit_rows,
+                          uint64_t n_logit, float *logits);
+/* The same with every buffer in device memory, enqueued on the context
+ * stream and not waited for (for callers that keep activations resident). */
+int32_t ditch_hip_forward_device(ditch_hip_model *m, const uint32_t *d_tokens,
+                                 const ditch_row *d_rows, uint64_t n,
+                                 const uint64_t *d_capture_rows,
+                                 uint64_t n_capture, float *d_residuals,
+                                 const uint64_t *d_logit_rows, uint64_t n_logit,
+                                 float *d_logits);
+
+/* ------------------------------------------------------------------------ */
+/* Rank-k edit, `none` mode (abliterate.zig:264-280): a = V^T W ([k][cols]),
+ * b = -weight * V ([rows][k]) for directions v [k][rows]. Host buffers.    */
+int32_t ditch_hip_edit_delta(ditch_hip *h, float *a, float *b,
+                             const ditch_weight *w, const float *v, uint64_t k,
+                             float weight);
+/* The same on a registered model matrix, installing the delta in place of
+ * model.setDelta (abliterate.zig:193-197).                                 */
+int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot,
+                             int32_t expert, const float *v, uint64_t k,
+                             float weight);
+
+/* ------------------------------------------------------------------------ */
+/* log-softmax of n rows (tensor.zig:1203-1210: f32 max, f64 sum, f32 x-lse). */
+int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x,
+                                 uint64_t n, uint64_t len);
+/* Per-row KL(base || trial) in f64 (scorers.zig:387-394): base_logprobs are
+ * the baseline log-softmax rows, trial_logits raw logits.                 */
+int32_t ditch_hip_klRows(ditch_hip *h, double *kl, const float *base_logprobs,
+                         const float *trial_logits, uint64_t n, uint64_t vocab);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DITCH_HIP_H */

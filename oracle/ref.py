@@ -1,0 +1,256 @@
+"""ctypes binding of oracle/libcpu_ref.so (the C restatement in cpu_ref.c).
+
+TEST INFRASTRUCTURE ONLY: see oracle/__init__.py.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from ditch_amd import abi
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libcpu_ref.so")
+
+P, U64, I32, U32, FLT = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
+SZ = ctypes.c_size_t
+PROTOS = {
+    "ref_f32_to_bf16": (ctypes.c_uint16, [FLT]),
+    "ref_f16_to_f32": (FLT, [ctypes.c_uint16]),
+    "ref_f32_to_f16": (ctypes.c_uint16, [FLT]),
+    "ref_fp8_value": (FLT, [ctypes.c_uint8, ctypes.c_int]),
+    "ref_e8m0_scale": (FLT, [ctypes.c_uint8]),
+    "ref_f32_to_bf16_array": (None, [P, P, SZ]),
+    "ref_gguf_dequant": (ctypes.c_int, [ctypes.c_int, P, P, SZ]),
+    "ref_quantize_q8_0": (None, [P, SZ, P]),
+    "ref_dequant_rows": (ctypes.c_int, [P, SZ, SZ, P]),
+    "ref_dot": (FLT, [P, P, SZ]),
+    "ref_matmulT": (ctypes.c_int, [P, P, SZ, P, SZ, P, P, ctypes.c_int]),
+    "ref_matvecTMulti": (ctypes.c_int, [P, P, P, SZ, ctypes.c_int]),
+    "ref_rowNorms": (ctypes.c_int, [P, P, ctypes.c_int]),
+    "ref_attention_scores": (None, [P, SZ, P, SZ, P, SZ, FLT]),
+    "ref_attention_values": (None, [P, SZ, P, SZ, P, SZ]),
+    "ref_rmsnorm": (None, [P, P, P, SZ, SZ, FLT, ctypes.c_int]),
+    "ref_layernorm": (None, [P, P, P, SZ, P, SZ, FLT, ctypes.c_int]),
+    "ref_softmax_inplace": (None, [P, SZ]),
+    "ref_log_softmax": (None, [P, P, SZ]),
+    "ref_exp_cephes": (FLT, [FLT]),
+    "ref_gated_activation": (None, [U32, P, P, P, SZ, SZ, SZ, SZ]),
+    "ref_rope_rows": (None, [P, SZ, SZ, P, P, SZ, P, U32]),
+    "ref_fill_rope": (ctypes.c_int, [P, P, P]),
+    "ref_kl_row": (ctypes.c_double, [P, P, SZ]),
+    "ref_edit_delta": (ctypes.c_int, [P, P, P, P, SZ, FLT, ctypes.c_int]),
+    "ref_model_create": (P, [P]),
+    "ref_model_free": (None, [P]),
+    "ref_model_set": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]),
+    "ref_model_set_delta": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, SZ, P, P]),
+    "ref_model_edit": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, SZ, FLT]),
+    "ref_forward": (ctypes.c_int, [P, P, P, SZ, P, SZ, P, P, SZ, P]),
+    "ref_model_limit_layers": (None, [P, SZ, SZ]),
+    "ref_set_threads": (None, [P, ctypes.c_int]),
+    "ref_last_error": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+def build(path=LIB, arch=None):
+    """Compiles the oracle with its Makefile (gcc)."""
+    cmd = ["make", "-s", "-C", HERE, f"OUT={path}"]
+    if arch:
+        cmd.append(f"ARCH={arch}")
+    subprocess.run(cmd, check=True)
+    return path
+
+
+def load(path=LIB):
+    global _lib
+    if _lib is not None and path == LIB:
+        return _lib
+    if not os.path.exists(path):
+        build(path)
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in PROTOS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    if path == LIB:
+        _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+class Ref:
+    """The oracle's functions over numpy arrays."""
+
+    def __init__(self, path=LIB, threads=8):
+        self.lib = load(path)
+        self.threads = threads
+
+    def _check(self, rc):
+        if rc != 0:
+            raise OracleError(self.lib.ref_last_error().decode())
+
+    def f32_to_bf16(self, a):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        out = np.empty(a.shape, dtype=np.uint16)
+        self.lib.ref_f32_to_bf16_array(_p(a), _p(out), a.size)
+        return out
+
+    def dequant(self, w, row0=0, nrows=None):
+        nrows = w.rows - row0 if nrows is None else nrows
+        bf16 = w.dtype in (abi.FP8, abi.MXFP4, abi.MXFP4_T, abi.INT_PACKED)
+        out = np.empty((nrows, w.cols), dtype=np.uint16 if bf16 else np.float32)
+        self._check(self.lib.ref_dequant_rows(w.ref(), row0, nrows, _p(out)))
+        return out
+
+    def gguf_dequant(self, dtype, raw, n):
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        out = np.empty(n, dtype=np.float32)
+        self._check(self.lib.ref_gguf_dequant(dtype, _p(raw), _p(out), n))
+        return out
+
+    def quantize_q8_0(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+        self.lib.ref_quantize_q8_0(_p(x), x.size, _p(out))
+        return out
+
+    def matmulT(self, x, w, delta=None):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[0]
+        out = np.empty((n, w.rows), dtype=np.float32)
+        a = b = None
+        rank = 0
+        if delta is not None:
+            a, b = (np.ascontiguousarray(t, dtype=np.float32) for t in delta)
+            rank = a.shape[0]
+        self._check(self.lib.ref_matmulT(_p(out), _p(x), n, w.ref(), rank, _p(a), _p(b), self.threads))
+        return out
+
+    def matvecTMulti(self, w, y):
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        out = np.empty((y.shape[0], w.cols), dtype=np.float32)
+        self._check(self.lib.ref_matvecTMulti(_p(out), w.ref(), _p(y), y.shape[0], self.threads))
+        return out
+
+    def rowNorms(self, w):
+        out = np.empty(w.rows, dtype=np.float32)
+        self._check(self.lib.ref_rowNorms(_p(out), w.ref(), self.threads))
+        return out
+
+    def rmsnorm_rows(self, x, w, eps, gemma=False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        for i in range(x.shape[0]):
+            self.lib.ref_rmsnorm(_p(out[i]), _p(x[i]), _p(w), 0 if w is None else w.size, x.shape[1], eps, int(gemma))
+        return out
+
+    def softmax_rows(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        for i in range(x.shape[0]):
+            self.lib.ref_softmax_inplace(_p(x[i]), x.shape[1])
+        return x
+
+    def log_softmax_rows(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty_like(x)
+        for i in range(x.shape[0]):
+            self.lib.ref_log_softmax(_p(out[i]), _p(x[i]), x.shape[1])
+        return out
+
+    def gated(self, act, gate, up, n, length, in_stride, out_stride):
+        gate = np.ascontiguousarray(gate, dtype=np.float32)
+        up = None if up is None else np.ascontiguousarray(up, dtype=np.float32)
+        out = np.zeros(((n - 1) * out_stride + length,), dtype=np.float32)
+        self.lib.ref_gated_activation(act, _p(out), _p(gate), _p(up), n, length, in_stride, out_stride)
+        return out
+
+    def rope_rows(self, x, cos_t, sin_t, pos, style):
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        cos_t = np.ascontiguousarray(cos_t, dtype=np.float32)
+        sin_t = np.ascontiguousarray(sin_t, dtype=np.float32)
+        pos = np.ascontiguousarray(pos, dtype=np.uint32)
+        self.lib.ref_rope_rows(_p(x), x.shape[0], x.shape[1], _p(cos_t), _p(sin_t), cos_t.shape[1], _p(pos), style)
+        return x
+
+    def kl_rows(self, base_logprobs, trial_logits):
+        b = np.ascontiguousarray(base_logprobs, dtype=np.float32)
+        t = np.ascontiguousarray(trial_logits, dtype=np.float32)
+        return np.array([self.lib.ref_kl_row(_p(b[i]), _p(t[i]), b.shape[1]) for i in range(b.shape[0])])
+
+    def edit_delta(self, w, v, weight):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        k = v.shape[0]
+        a = np.empty((k, w.cols), dtype=np.float32)
+        b = np.empty((w.rows, k), dtype=np.float32)
+        self._check(self.lib.ref_edit_delta(_p(a), _p(b), w.ref(), _p(v), k, weight, self.threads))
+        return a, b
+
+    def fill_rope(self, spec):
+        cfg = spec.config_struct()
+        half = spec.config["rotary_dim"] // 2
+        cos_t = np.zeros((spec.config["rope_len"], half), dtype=np.float32)
+        sin_t = np.zeros_like(cos_t)
+        self.lib.ref_fill_rope(ctypes.byref(cfg), _p(cos_t), _p(sin_t))
+        return cos_t, sin_t
+
+
+class RefModel:
+    """The oracle's model.forward over a ModelSpec."""
+
+    def __init__(self, spec, path=LIB, threads=8):
+        self.lib = load(path)
+        self.spec = spec
+        self.cfg = spec.config_struct()
+        self.h = self.lib.ref_model_create(ctypes.byref(self.cfg))
+        self.lib.ref_set_threads(self.h, threads)
+        for (layer, slot, expert), w in spec.tensors.items():
+            if self.lib.ref_model_set(self.h, layer, slot, expert, w.ref()) != 0:
+                raise OracleError(self.lib.ref_last_error().decode())
+
+    def free(self):
+        if self.h:
+            self.lib.ref_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    def limit_layers(self, first, count):
+        self.lib.ref_model_limit_layers(self.h, first, count)
+
+    def set_delta(self, layer, slot, expert, a, b):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        if self.lib.ref_model_set_delta(self.h, layer, slot, expert, a.shape[0], _p(a), _p(b)) != 0:
+            raise OracleError(self.lib.ref_last_error().decode())
+
+    def edit(self, layer, slot, expert, v, weight):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        if self.lib.ref_model_edit(self.h, layer, slot, expert, _p(v), v.shape[0], weight) != 0:
+            raise OracleError(self.lib.ref_last_error().decode())
+
+    def forward(self, tokens, rows, capture_rows=(), logit_rows=()):
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        rows_a = np.ascontiguousarray(rows, dtype=np.uint32).reshape(-1, 2)
+        cap = np.ascontiguousarray(capture_rows, dtype=np.uint64)
+        lr = np.ascontiguousarray(logit_rows, dtype=np.uint64)
+        c = self.spec.config
+        res = np.empty((c["layers"] + 1, cap.size, c["hidden"]), dtype=np.float32)
+        logits = np.empty((lr.size, c["vocab"]), dtype=np.float32)
+        rc = self.lib.ref_forward(self.h, _p(tokens), _p(rows_a), tokens.size, _p(cap) if cap.size else None,
+                                  cap.size, _p(res) if cap.size else None, _p(lr) if lr.size else None, lr.size,
+                                  _p(logits) if lr.size else None)
+        if rc != 0:
+            raise OracleError(self.lib.ref_last_error().decode())
+        return res, logits
