@@ -119,7 +119,9 @@ int32_t ditch_hip_matmulT(ditch_hip *h, float *out, const float *x, uint64_t n, 
         std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
         Tmp dx(n * w->cols * 4), dout(n * w->rows * 4);
         h2d(dx.p, x, n * w->cols * 4, s);
-        launch_matmul(t->v, dout.as<float>(), dx.as<float>(), (int64_t)n, MatmulEpilogue{}, s);
+        MatmulEpilogue ep;
+        ep.exact = 1;
+        launch_matmul(t->v, dout.as<float>(), dx.as<float>(), (int64_t)n, ep, s);
         d2h(out, dout.p, n * w->rows * 4, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
     });

@@ -32,6 +32,10 @@ __device__ __forceinline__ floatx4 mfma_bf16(u32x4 a, u32x4 b, floatx4 c) {
                                                    0, 0, 0);
 }
 
+__device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // high halves of two f32 -> one packed bf16 pair (exact when the values are)
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
     return __builtin_amdgcn_perm(f2u(hi), f2u(lo), 0x07060302u);
@@ -57,6 +61,32 @@ __device__ __forceinline__ void split8(const float (&v)[8], u32x4 &hi, u32x4 &lo
     lo = u32x4{pack_rne(l[0], l[1]), pack_rne(l[2], l[3]), pack_rne(l[4], l[5]), pack_rne(l[6], l[7])};
 }
 
+// The A operand words of 8 activations: XT bf16 terms x = t0 + t1 (+ t2),
+// each the round-to-nearest-even bf16 of the remainder of the previous
+// ones (remainder below 2^-18 |x| for two terms, 2^-27 |x| for three), or
+// for the fp32 MFMA the f32 values themselves in t[0] (0..3) and t[1] (4..7).
+template <bool FP32, int XT>
+__device__ __forceinline__ void a_words(const float (&v)[8], u32x4 (&t)[XT]) {
+    if constexpr (FP32) {
+        t[0] = u32x4{f2u(v[0]), f2u(v[1]), f2u(v[2]), f2u(v[3])};
+        t[1] = u32x4{f2u(v[4]), f2u(v[5]), f2u(v[6]), f2u(v[7])};
+    } else {
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r[j] = v[j];
+#pragma unroll
+        for (int e = 0; e < XT; e++) {
+            float h[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                h[j] = u2f(rne_bits(r[j]));
+                r[j] = __fsub_rn(r[j], h[j]);
+            }
+            t[e] = u32x4{pack_hi(h[0], h[1]), pack_hi(h[2], h[3]), pack_hi(h[4], h[5]), pack_hi(h[6], h[7])};
+        }
+    }
+}
+
 struct GemmParams {
     TileView w;
     float *out;
@@ -69,6 +99,7 @@ struct GemmParams {
     const float *delta_b;
     const float *delta_xa;
     int delta_rank;
+    int delta_stride;  // row stride of delta_xa (>= delta_rank)
     // grouped (routed experts): segment z = blockIdx.z has its own weight,
     // rows [seg[z].off, seg[z].off + seg[z].cnt) of x/out and delta
     const GroupSeg *segs;
@@ -98,8 +129,10 @@ __device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) {
 // Number of k tiles per unit and MFMA terms.
 template <int TF> struct Fmt {
     static constexpr int tiles = TF == TF_Q8 || TF == TF_FP8 ? 2 : (TF == TF_MX4 || TF == TF_INT4) ? 4 : 1;
-    static constexpr bool split_w = TF == TF_F16 || TF == TF_F32;  // weight hi/lo
-    static constexpr bool acc_scale = TF == TF_Q8;                 // block scale on the partial sum
+    // f16 and f32 weights run on the fp32 MFMA with f32 activations: every
+    // product is exact, as in the CPU's f32 fused multiply-adds
+    static constexpr bool fp32 = TF == TF_F16 || TF == TF_F32;
+    static constexpr bool acc_scale = TF == TF_Q8;  // block scale on the partial sum
 };
 
 // Per-unit side data (scales) loaded once per unit.
@@ -126,29 +159,20 @@ __device__ __forceinline__ void decode_tile(const TileView &w, const Raw &raw, c
     if constexpr (TF == TF_BF16) {
         bh = u32x4{raw.a.x, raw.a.y, raw.a.z, raw.a.w};
     } else if constexpr (TF == TF_F16 || TF == TF_F32) {
-        float f[8];
+        // the 8 f32 weights, as bit patterns: bh = values 0..3, bl = 4..7
         if constexpr (TF == TF_F16) {
+            float f[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 uint32_t wd = word_of(raw.a, j / 2);
-                uint16_t hb = (uint16_t)((j & 1) ? (wd >> 16) : (wd & 0xffffu));
-                f[j] = f16_to_f32(hb);
+                f[j] = f16_to_f32((uint16_t)((j & 1) ? (wd >> 16) : (wd & 0xffffu)));
             }
+            bh = u32x4{f2u(f[0]), f2u(f[1]), f2u(f[2]), f2u(f[3])};
+            bl = u32x4{f2u(f[4]), f2u(f[5]), f2u(f[6]), f2u(f[7])};
         } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                f[j] = u2f(word_of(raw.a, j));
-                f[4 + j] = u2f(word_of(raw.b, j));
-            }
+            bh = u32x4{raw.a.x, raw.a.y, raw.a.z, raw.a.w};
+            bl = u32x4{raw.b.x, raw.b.y, raw.b.z, raw.b.w};
         }
-        float h[8], l[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            h[j] = u2f(f2u(f[j]) & 0xffff0000u);
-            l[j] = __fsub_rn(f[j], h[j]);
-        }
-        bh = u32x4{pack_hi(h[0], h[1]), pack_hi(h[2], h[3]), pack_hi(h[4], h[5]), pack_hi(h[6], h[7])};
-        bl = u32x4{pack_rne(l[0], l[1]), pack_rne(l[2], l[3]), pack_rne(l[4], l[5]), pack_rne(l[6], l[7])};
     } else if constexpr (TF == TF_Q8) {
         uint32_t w0 = word_of(raw.a, 2 * t), w1 = word_of(raw.a, 2 * t + 1);
         float f[8];
@@ -208,23 +232,26 @@ __device__ __forceinline__ void decode_tile(const TileView &w, const Raw &raw, c
     }
 }
 
-// acc += x_frag (hi, lo) . B (with the format's term structure)
-template <int TF>
-__device__ __forceinline__ void mac(floatx4 &acc, const u32x4 &xh, const u32x4 &xl, const u32x4 &bh, const u32x4 &bl,
+// acc += (sum of the activation terms) . B, with the format's structure
+template <int TF, int XT>
+__device__ __forceinline__ void mac(floatx4 &acc, const u32x4 (&x)[XT], const u32x4 &bh, const u32x4 &bl,
                                     float tile_scale) {
     if constexpr (Fmt<TF>::acc_scale) {
         floatx4 t = {0.f, 0.f, 0.f, 0.f};
-        t = mfma_bf16(xh, bh, t);
-        t = mfma_bf16(xl, bh, t);
+#pragma unroll
+        for (int e = 0; e < XT; e++) t = mfma_bf16(x[e], bh, t);
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(tile_scale, t[r], acc[r]);
-    } else if constexpr (Fmt<TF>::split_w) {
-        acc = mfma_bf16(xh, bh, acc);
-        acc = mfma_bf16(xl, bh, acc);
-        acc = mfma_bf16(xh, bl, acc);
+    } else if constexpr (Fmt<TF>::fp32) {
+        // 8 rank-4 steps over k = 8 * (lane / 16) + s: A and B hold the same
+        // k in the same register, so the 32 products of the tile are summed
+#pragma unroll
+        for (int s = 0; s < 4; s++) acc = mfma_f32(u2f(x[0][s]), u2f(bh[s]), acc);
+#pragma unroll
+        for (int s = 0; s < 4; s++) acc = mfma_f32(u2f(x[1][s]), u2f(bl[s]), acc);
     } else {
-        acc = mfma_bf16(xh, bh, acc);
-        acc = mfma_bf16(xl, bh, acc);
+#pragma unroll
+        for (int e = 0; e < XT; e++) acc = mfma_bf16(x[e], bh, acc);
     }
 }
 
@@ -254,7 +281,7 @@ __device__ __forceinline__ void store_out(const GemmParams &p, int64_t tok, int6
     if (p.delta_rank > 0) {
         float d = 0.f;
         for (int j = 0; j < p.delta_rank; j++)
-            d = __fadd_rn(d, __fmul_rn(p.delta_b[row * p.delta_rank + j], p.delta_xa[tok * p.delta_rank + j]));
+            d = __fadd_rn(d, __fmul_rn(p.delta_b[row * p.delta_rank + j], p.delta_xa[tok * p.delta_stride + j]));
         v = __fadd_rn(v, d);
     }
     if (p.bias) v = __fadd_rn(v, p.bias[row]);
@@ -278,7 +305,7 @@ __device__ __forceinline__ bool select_segment(GemmParams &p, int64_t m0) {
     p.ldx = s.w.cols;
     p.delta_rank = s.delta_rank;
     p.delta_b = s.delta_b;
-    p.delta_xa = s.delta_rank ? p.delta_xa + (int64_t)s.off * s.delta_rank : nullptr;
+    p.delta_xa = s.delta_rank ? p.delta_xa + (int64_t)s.off * p.delta_stride : nullptr;
     return true;
 }
 
@@ -286,7 +313,7 @@ __device__ __forceinline__ bool select_segment(GemmParams &p, int64_t m0) {
 // GEMV regime (n <= 16): one 16-token fragment, NT 16-row groups per block,
 // K split over the 4 waves and reduced through LDS.
 
-template <int TF, int NT>
+template <int TF, int NT, int XT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemmParams p) {
     if (!select_segment(p, 0)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -320,14 +347,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmParams p) {
             int64_t k0 = u * UK + 32 * t + 8 * kq;
             float xv[8];
             load_x8(p, tok, k0, xv, vec_ok);
-            u32x4 xh, xl;
-            split8(xv, xh, xl);
+            u32x4 xt[XT];
+            a_words<Fmt<TF>::fp32, XT>(xv, xt);
 #pragma unroll
             for (int i = 0; i < NT; i++) {
                 u32x4 bh, bl = u32x4{0, 0, 0, 0};
                 float ts = 1.f;
                 decode_tile<TF>(p.w, raw[i], side[i], t, (g0 + i) * 16 + lane % 16, k0, bh, bl, ts);
-                mac<TF>(acc[i], xh, xl, bh, bl, ts);
+                mac<TF, XT>(acc[i], xt, bh, bl, ts);
             }
         }
     }
@@ -359,13 +386,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmParams p) {
 // one unit is staged in LDS as hi/lo fragments, each wave streams its own
 // 16*NT weight rows straight from HBM into registers.
 
-template <int TF, int MT, int NT>
+template <int TF, int MT, int NT, int XT>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     constexpr int UK = TF == TF_Q8 || TF == TF_FP8 ? 64 : (TF == TF_MX4 || TF == TF_INT4) ? 128 : 32;
     constexpr int TILES = UK / 32;
     constexpr int BM = 16 * MT;
-    // [mt][t][hi/lo][lane] 16-byte words
-    __shared__ u32x4 xs[MT][TILES][2][64];
+    // [mt][t][term][lane] 16-byte words
+    __shared__ u32x4 xs[MT][TILES][XT][64];
 
     const int64_t m0 = (int64_t)blockIdx.y * BM;
     if (!select_segment(p, m0)) return;
@@ -402,11 +429,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
                 int i = q % BM, g8 = q / BM;
                 float xv[8];
                 load_x8(p, m0 + i, u * UK + 8 * g8, xv, vec_ok);
-                u32x4 xh, xl;
-                split8(xv, xh, xl);
+                u32x4 xt[XT];
+                a_words<Fmt<TF>::fp32, XT>(xv, xt);
                 int t = g8 / 4, sl = (i % 16) + 16 * (g8 % 4);
-                xs[i / 16][t][0][sl] = xh;
-                xs[i / 16][t][1][sl] = xl;
+#pragma unroll
+                for (int e = 0; e < XT; e++) xs[i / 16][t][e][sl] = xt[e];
             }
         }
         __syncthreads();
@@ -423,9 +450,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             }
 #pragma unroll
             for (int m = 0; m < MT; m++) {
-                u32x4 xh = xs[m][t][0][lane], xl = xs[m][t][1][lane];
+                u32x4 xt[XT];
 #pragma unroll
-                for (int i = 0; i < NT; i++) mac<TF>(acc[m][i], xh, xl, bh[i], bl[i], ts[i]);
+                for (int e = 0; e < XT; e++) xt[e] = xs[m][t][e][lane];
+#pragma unroll
+                for (int i = 0; i < NT; i++) mac<TF, XT>(acc[m][i], xt, bh[i], bl[i], ts[i]);
             }
         }
     }
@@ -441,33 +470,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 
 // ---------------------------------------------------------------------------
 
-template <int TF>
+template <int TF, int XT>
 static void dispatch(const GemmParams &p, int64_t max_rows, int64_t n_for_shape, unsigned nseg, hipStream_t s) {
     int64_t groups = (max_rows + 15) / 16;
     if (n_for_shape <= 16) {
         constexpr int NT = 1;
         dim3 grid((unsigned)((groups + NT - 1) / NT), 1, nseg);
-        hipLaunchKernelGGL((gemv_kernel<TF, NT>), grid, dim3(256), 0, s, p);
-    } else if (n_for_shape <= 64) {
+        hipLaunchKernelGGL((gemv_kernel<TF, NT, XT>), grid, dim3(256), 0, s, p);
+    } else if (n_for_shape <= 64 || XT > 2) {
         constexpr int MT = 4, NT = 2;
         dim3 grid((unsigned)((groups + 4 * NT - 1) / (4 * NT)), (unsigned)((n_for_shape + 16 * MT - 1) / (16 * MT)), nseg);
-        hipLaunchKernelGGL((gemm_kernel<TF, MT, NT>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((gemm_kernel<TF, MT, NT, XT>), grid, dim3(256), 0, s, p);
     } else {
         constexpr int MT = 8, NT = 2;
         dim3 grid((unsigned)((groups + 4 * NT - 1) / (4 * NT)), (unsigned)((n_for_shape + 16 * MT - 1) / (16 * MT)), nseg);
-        hipLaunchKernelGGL((gemm_kernel<TF, MT, NT>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((gemm_kernel<TF, MT, NT, XT>), grid, dim3(256), 0, s, p);
     }
 }
 
-static void dispatch_tf(int tf, const GemmParams &p, int64_t max_rows, int64_t n_for_shape, unsigned nseg, hipStream_t s) {
+template <int TF>
+static void dispatch_xt(const GemmParams &p, int64_t max_rows, int64_t n_for_shape, unsigned nseg, bool exact,
+                        hipStream_t s) {
+    if (Fmt<TF>::fp32) dispatch<TF, 2>(p, max_rows, n_for_shape, nseg, s);  // f32 activations, exact products
+    else if (exact) dispatch<TF, 3>(p, max_rows, n_for_shape, nseg, s);
+    else dispatch<TF, 2>(p, max_rows, n_for_shape, nseg, s);
+}
+
+static void dispatch_tf(int tf, const GemmParams &p, int64_t max_rows, int64_t n_for_shape, unsigned nseg, bool exact,
+                        hipStream_t s) {
     switch (tf) {
-    case TF_BF16: dispatch<TF_BF16>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_F16: dispatch<TF_F16>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_F32: dispatch<TF_F32>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_Q8: dispatch<TF_Q8>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_FP8: dispatch<TF_FP8>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_MX4: dispatch<TF_MX4>(p, max_rows, n_for_shape, nseg, s); break;
-    case TF_INT4: dispatch<TF_INT4>(p, max_rows, n_for_shape, nseg, s); break;
+    case TF_BF16: dispatch_xt<TF_BF16>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_F16: dispatch_xt<TF_F16>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_F32: dispatch_xt<TF_F32>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_Q8: dispatch_xt<TF_Q8>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_FP8: dispatch_xt<TF_FP8>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_MX4: dispatch_xt<TF_MX4>(p, max_rows, n_for_shape, nseg, exact, s); break;
+    case TF_INT4: dispatch_xt<TF_INT4>(p, max_rows, n_for_shape, nseg, exact, s); break;
     default: throw Error{DITCH_UNSUPPORTED, "tile format"};
     }
     DITCH_TRY_HIP(hipGetLastError());
@@ -488,12 +526,14 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     p.delta_b = ep.delta_b;
     p.delta_xa = ep.delta_xa;
     p.delta_rank = ep.delta_rank;
+    p.delta_stride = ep.delta_rank;
     p.segs = nullptr;
-    dispatch_tf(w.tf, p, w.rows, n, 1, s);
+    dispatch_tf(w.tf, p, w.rows, n, 1, ep.exact != 0, s);
 }
 
 void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols, int64_t max_cnt,
-                           float *out, const float *x, const int32_t *row_index, const float *delta_xa, hipStream_t s) {
+                           float *out, const float *x, const int32_t *row_index, const float *delta_xa,
+                           int delta_stride, hipStream_t s) {
     if (nseg == 0 || max_cnt <= 0) return;
     GemmParams p{};
     p.out = out;
@@ -502,10 +542,11 @@ void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_
     p.ldx = cols;
     p.row_index = row_index;
     p.delta_xa = delta_xa;
+    p.delta_stride = delta_stride;
     p.segs = d_segs;
     p.w.rows = rows;
     p.w.cols = cols;
-    dispatch_tf(tf, p, rows, max_cnt, nseg, s);
+    dispatch_tf(tf, p, rows, max_cnt, nseg, false, s);
 }
 
 }  // namespace ditch

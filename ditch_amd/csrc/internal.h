@@ -121,6 +121,10 @@ struct MatmulEpilogue {
     const float *delta_b = nullptr;  // [rows][rank]
     const float *delta_xa = nullptr; // [n][rank]
     int delta_rank = 0;
+    // three bf16 activation terms instead of two: products exact to f32
+    // rounding (the VTable entry point, checked at the reference's
+    // device-contract tolerance); the resident forward uses two
+    int exact = 0;
 };
 void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
                    hipStream_t s, const int32_t *row_index = nullptr);
@@ -136,11 +140,12 @@ struct GroupSeg {
 };
 void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols,
                            int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
-                           const float *delta_xa, hipStream_t s);
+                           const float *delta_xa, int delta_stride, hipStream_t s);
 
 // ops.hip
+// row_index (optional) gathers input rows out of n_src rows
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
-                    float eps, int gemma, hipStream_t s, const int64_t *row_index = nullptr);
+                    float eps, int gemma, hipStream_t s, const int64_t *row_index = nullptr, int64_t n_src = 0);
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
                             int64_t in_stride, int64_t out_stride, float eps, hipStream_t s);
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,

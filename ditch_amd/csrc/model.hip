@@ -29,17 +29,22 @@ __global__ void embed_kernel(float *x, TileView w, const uint32_t *tokens, int64
     int64_t total = n * w.cols;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         int64_t r = i / w.cols, c = i % w.cols;
+        int64_t t = (int64_t)tokens[r];
+        t = t < w.rows ? t : w.rows - 1;  // ids are checked on the host; clamp device-side inputs
         uint16_t b;
-        x[i] = tiled_element_f32(w, (int64_t)tokens[r], c, &b);
+        x[i] = tiled_element_f32(w, t, c, &b);
     }
 }
 
 // residuals[entry][ci] = x[capture_rows[ci]] (model.zig:4856-4862)
-__global__ void capture_kernel(float *res, const float *x, const uint64_t *rows, int64_t n_capture, int64_t hidden) {
+__global__ void capture_kernel(float *res, const float *x, const uint64_t *rows, int64_t n_capture, int64_t hidden,
+                               int64_t n) {
     int64_t total = n_capture * hidden;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         int64_t ci = i / hidden, c = i % hidden;
-        res[i] = x[(int64_t)rows[ci] * hidden + c];
+        int64_t r = (int64_t)rows[ci];
+        r = r < n ? r : n - 1;
+        res[i] = x[r * hidden + c];
     }
 }
 
@@ -367,7 +372,7 @@ __global__ void grouped_delta_xa_kernel(float *xa, const float *x, const int32_t
     float acc = 0.f;
     for (int64_t c = lane; c < cols; c += 64) acc = __builtin_fmaf(s.a[j * cols + c], x[src * cols + c], acc);
     acc = wave_sum64(acc);
-    if (lane == 0) xa[p * s.rank + j] = acc;
+    if (lane == 0) xa[p * max_rank + j] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -660,15 +665,21 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         max_rank = std::max(max_rank, L.ed[e].rank);
     }
     unsigned nseg = (unsigned)sg.size();
+    for (unsigned i = 0; i < nseg; i++)
+        DITCH_CHECK(sg[i].w.tf == sg[0].w.tf && su[i].w.tf == su[0].w.tf && sd[i].w.tf == sd[0].w.tf &&
+                        sg[i].w.rows == inter && sg[i].w.cols == hidden && sd[i].w.rows == hidden &&
+                        sd[i].w.cols == inter,
+                    DITCH_INVALID_ARGUMENT, "experts of one layer must share shape and format");
     GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * nseg);
     DITCH_TRY_HIP(hipMemcpyAsync(dsegs, sg.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
-    const TileView &vg = L.eg[0].t->v, &vd = L.ed[0].t->v;
+    const TileView &vg = sg[0].w, &vd = sd[0].w;
     float *gate = m->e_gate.get<float>(P * inter), *up = m->e_up.get<float>(P * inter);
     float *eo = m->e_out.get<float>(P * hidden);
-    launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, s);
-    launch_matmul_grouped(dsegs + nseg, nseg, L.eu[0].t->v.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, s);
+    launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0, s);
+    launch_matmul_grouped(dsegs + nseg, nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, 0,
+                          s);
     launch_gated_act(0, gate, gate, up, P, inter, inter, inter, s);
     float *dxa = nullptr;
     if (max_rank > 0) {
@@ -679,7 +690,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
         DITCH_TRY_HIP(hipGetLastError());
     }
-    launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, s);
+    launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, max_rank, s);
     float *esh = nullptr;
     if (L.sh_gate.ok()) {
         int64_t si = L.sh_gate.t->v.rows;
@@ -724,7 +735,7 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
     auto capture = [&](int64_t entry) {
         if (!d_res || n_capture == 0) return;
         hipLaunchKernelGGL(capture_kernel, dim3(grid_for(n_capture * hidden)), dim3(256), 0, s,
-                           d_res + entry * n_capture * hidden, x, d_capture, n_capture, hidden);
+                           d_res + entry * n_capture * hidden, x, d_capture, n_capture, hidden, n);
         DITCH_TRY_HIP(hipGetLastError());
     };
     capture(0);
@@ -801,7 +812,7 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
     if (n_logit > 0 && d_logits) {
         float *hl = m->logit_h.get<float>(n_logit * hidden);
         launch_rmsnorm(hl, x, m->final_norm.p, m->final_norm.len, n_logit, hidden, c.rms_eps, 0, s,
-                       (const int64_t *)d_logit_rows);
+                       (const int64_t *)d_logit_rows, n);
         const Mat &lm = m->lm_head.ok() ? m->lm_head : m->embed;
         mm(m, lm, d_logits, hl, n_logit, nullptr, 0, s);
     }

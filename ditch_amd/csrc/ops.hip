@@ -90,10 +90,12 @@ __device__ float act_apply(uint32_t act, float x) {
 // row. `row_index` gathers input rows (the logit rows of model.zig:4798-4852).
 
 __global__ void rmsnorm_kernel(float *out, const float *x, const float *w, int64_t wlen, int64_t len, float eps,
-                               int gemma, const int64_t *row_index, int64_t in_stride, int64_t out_stride) {
+                               int gemma, const int64_t *row_index, int64_t n_src, int64_t in_stride,
+                               int64_t out_stride) {
     __shared__ float sh[8];
     int64_t r = blockIdx.x;
     int64_t src = row_index ? row_index[r] : r;
+    src = src < n_src ? src : n_src - 1;
     const float *xr = x + src * in_stride;
     float ss = 0.f;
     for (int64_t i = threadIdx.x; i < len; i += blockDim.x) ss = __builtin_fmaf(xr[i], xr[i], ss);
@@ -300,16 +302,16 @@ __global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64
 // Launchers
 
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len, float eps,
-                    int gemma, hipStream_t s, const int64_t *row_index) {
+                    int gemma, hipStream_t s, const int64_t *row_index, int64_t n_src) {
     if (n <= 0) return;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, gemma, row_index,
-                       len, len);
+                       row_index ? n_src : n, len, len);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
                             int64_t in_stride, int64_t out_stride, float eps, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, 0, nullptr,
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, 0, nullptr, n,
                        in_stride, out_stride);
     DITCH_TRY_HIP(hipGetLastError());
 }

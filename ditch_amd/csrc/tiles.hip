@@ -400,6 +400,17 @@ static RawSizes raw_sizes(const ditch_weight *w) {
         DITCH_CHECK(scale_elem_bytes(w->scale_dtype) > 0, DITCH_INVALID_ARGUMENT, "FP8 scale dtype");
         z.data = rows * cols;
         z.scale = w->scale_rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
+        {
+            // the grid must cover every row (dequant.zig:471-475) and column block
+            int64_t last = rows - 1, sr;
+            if (w->row_shard == 0) sr = last / (int64_t)w->block_rows;
+            else {
+                int64_t per_shard = ((int64_t)w->row_shard + (int64_t)w->block_rows - 1) / (int64_t)w->block_rows;
+                sr = last / (int64_t)w->row_shard * per_shard + (last % (int64_t)w->row_shard) / (int64_t)w->block_rows;
+            }
+            DITCH_CHECK(sr < (int64_t)w->scale_rows && (cols - 1) / (int64_t)w->block_cols < (int64_t)w->scale_cols,
+                        DITCH_INVALID_ARGUMENT, "FP8 scale grid does not cover the matrix");
+        }
         break;
     case DITCH_MXFP4:
         DITCH_CHECK(cols % 32 == 0 && w->scale, DITCH_INVALID_ARGUMENT, "MXFP4 needs cols % 32 == 0 and scales");
@@ -420,7 +431,15 @@ static RawSizes raw_sizes(const ditch_weight *w) {
         z.data = rows * wpr * 4;
         z.scale = rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
         if (w->zero) z.zero = ((rows * w->bits + 31) / 32) * w->scale_cols * 4;
-        if (w->g_idx) z.gidx = cols * 4;
+        if (w->g_idx) {
+            z.gidx = cols * 4;
+            for (int64_t c = 0; c < cols; c++)
+                DITCH_CHECK(w->g_idx[c] >= 0 && (uint64_t)w->g_idx[c] < w->scale_cols, DITCH_INVALID_ARGUMENT,
+                            "g_idx names a group beyond the scales");
+        } else {
+            DITCH_CHECK((uint64_t)((cols + (int64_t)w->group - 1) / (int64_t)w->group) <= w->scale_cols,
+                        DITCH_INVALID_ARGUMENT, "fewer scale groups than columns need");
+        }
         break;
     }
     default: throw Error{DITCH_UNSUPPORTED, "unsupported weight dtype " + std::to_string(w->dtype)};

@@ -1,0 +1,221 @@
+"""HIP kernels against the CPU oracle, through the C ABI (needs an MI355X).
+
+Bars: decoded weights bit-exact; matrix products within the reference's
+device-contract tolerance (selftest.zig:34-41: abs 1e-4 or rel 1e-3 per
+element for matmul, abs 1e-5 / rel 1e-4 element-wise, abs/rel 1e-4 for
+reductions).
+"""
+import ctypes
+import zlib
+
+import numpy as np
+import pytest
+
+import weights_gen as wg
+from ditch_amd import abi
+
+pytestmark = pytest.mark.gpu
+
+TOL_MATMUL = dict(atol=1e-4, rtol=1e-3)
+TOL_ELEM = dict(atol=1e-5, rtol=1e-4)
+TOL_RED = dict(atol=1e-4, rtol=1e-4)
+
+
+def close(got, want, atol, rtol):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    bad = np.abs(got - want) > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; worst {np.abs(got - want).max():.3e}"
+
+
+def same_bits(got, want):
+    """Bit equality; NaN positions must match (payloads of x86-quieted NaNs
+    are compared too)."""
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.dtype == want.dtype and got.shape == want.shape
+    neq = got != want
+    assert not neq.any(), f"{neq.sum()} of {neq.size} differ; first at {np.argwhere(neq)[0]}: {got[neq][0]:#x} vs {want[neq][0]:#x}"
+
+
+# -- decode --------------------------------------------------------------------
+
+DEQUANT_CASES = [
+    ("f32", lambda r: wg.float_random("f32", 33, 70, r)),
+    ("f16", lambda r: wg.float_random("f16", 33, 70, r)),
+    ("bf16", lambda r: wg.float_random("bf16", 33, 70, r)),
+    ("q8_0", lambda r: wg.gguf_random(abi.Q8_0, 37, 96, r)),
+    ("q4_0", lambda r: wg.gguf_random(abi.Q4_0, 21, 64, r)),
+    ("q4_1", lambda r: wg.gguf_random(abi.Q4_1, 21, 64, r)),
+    ("q5_0", lambda r: wg.gguf_random(abi.Q5_0, 21, 64, r)),
+    ("q5_1", lambda r: wg.gguf_random(abi.Q5_1, 21, 64, r)),
+    ("q4_k", lambda r: wg.gguf_random(abi.Q4_K, 9, 512, r)),
+    ("q6_k", lambda r: wg.gguf_random(abi.Q6_K, 9, 512, r)),
+    ("q8_k", lambda r: wg.gguf_random(abi.Q8_K, 9, 512, r)),
+    ("fp8_e4m3_all_codes", lambda r: wg.fp8_random(256, 256, r, all_codes=True)),
+    ("fp8_e5m2_all_codes", lambda r: wg.fp8_random(256, 256, r, e5m2=True, all_codes=True)),
+    ("fp8_16x8_bf16_scale", lambda r: wg.fp8_random(48, 40, r, block=(16, 8), scale_kind="bf16")),
+    ("fp8_f16_scale", lambda r: wg.fp8_random(130, 200, r, scale_kind="f16")),
+    ("fp8_e8m0_scale", lambda r: wg.fp8_random(64, 96, r, block=(1, 32), scale_kind="e8m0", all_codes=True)),
+    ("fp8_row_shard", lambda r: wg.fp8_random(96, 64, r, block=(16, 16), row_shard=48)),
+    ("mxfp4_all_scales", lambda r: wg.mxfp4_random(256, 64, r, scale_lo=0, scale_hi=256)),
+    ("mxfp4", lambda r: wg.mxfp4_random(40, 256, r)),
+    ("mxfp4_t", lambda r: wg.mxfp4_t_random(64, 48, r)),
+    ("int4_g128", lambda r: wg.int_random(37, 256, r)),
+    ("int4_g16_bf16", lambda r: wg.int_random(37, 48, r, group=16, scale_kind="bf16")),
+    ("int4_sym", lambda r: wg.int_random(20, 128, r, zero=False, scale_kind="f32")),
+    ("int4_actorder", lambda r: wg.int_random(32, 64, r, group=16, actorder=True)),
+    ("int3", lambda r: wg.int_random(33, 40, r, bits=3, group=8)),
+    ("int8", lambda r: wg.int_random(17, 64, r, bits=8, group=32)),
+]
+
+
+@pytest.mark.parametrize("name,gen", DEQUANT_CASES, ids=[c[0] for c in DEQUANT_CASES])
+def test_dequant_bit_exact(dev, ref, name, gen):
+    from ditch_amd.hipmem import Buffer
+    w = gen(np.random.default_rng(zlib.crc32(name.encode())))
+    want = ref.dequant(w)
+    got = dev.dequant(w)  # raw-layout decode
+    same_bits(got.view(np.uint32) if got.dtype == np.float32 else got,
+              want.view(np.uint32) if want.dtype == np.float32 else want)
+    # the re-tiled HBM layout decodes to the same bits
+    t = dev.upload(w)
+    try:
+        buf = Buffer(want.nbytes)
+        t.dequant_device(buf.ptr, 0, w.rows)
+        dev.sync()
+        tiled = buf.download(want.dtype, want.shape)
+        buf.free()
+    finally:
+        t.free()
+    same_bits(tiled.view(np.uint32) if tiled.dtype == np.float32 else tiled,
+              want.view(np.uint32) if want.dtype == np.float32 else want)
+
+
+# -- matmulT -------------------------------------------------------------------
+
+MM_KINDS = ["f32", "f16", "bf16", "q8_0", "q4_0", "q4_k", "q6_k", "fp8", "fp8_16x8", "mxfp4", "mxfp4_t", "int4",
+            "int4_g16", "int4_sym", "int4_actorder", "int8"]
+MM_SHAPES = [(1, 48, 256), (3, 100, 384), (16, 64, 512), (17, 80, 256), (64, 200, 512), (100, 96, 1024)]
+
+
+@pytest.mark.parametrize("kind", MM_KINDS)
+@pytest.mark.parametrize("n,rows,cols", MM_SHAPES)
+def test_matmulT_matches_oracle(dev, ref, kind, n, rows, cols):
+    rng = np.random.default_rng(n * 7919 + rows * 31 + cols)
+    if kind.startswith(("q4_k", "q6_k")) and cols % 256:
+        pytest.skip("k-quants need 256-column rows")
+    w = wg.make(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    want = ref.matmulT(x, w)
+    got = dev.matmulT(x, w)
+    close(got, want, **TOL_MATMUL)
+
+
+def test_matmulT_odd_k(dev, ref):
+    """K not a multiple of 8 takes the guarded activation loads."""
+    rng = np.random.default_rng(11)
+    for n, rows, cols in [(1, 5, 12), (20, 7, 20), (70, 33, 44)]:
+        w = wg.float_random("bf16", rows, cols, rng)
+        x = rng.standard_normal((n, cols)).astype(np.float32)
+        close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
+
+
+# -- VTable element-wise ops ------------------------------------------------------
+
+def test_rmsnorm_layernorm_softmax(dev, ref):
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((7, 300)).astype(np.float32)
+    w = rng.standard_normal(300).astype(np.float32)
+    close(dev.rmsnormRows(x, w, 1e-6), ref.rmsnorm_rows(x, w, 1e-6), **TOL_ELEM)
+    close(dev.rmsnormRows(x, None, 1e-5), ref.rmsnorm_rows(x, None, 1e-5), **TOL_ELEM)
+    close(dev.softmaxRows(x * 4), ref.softmax_rows(x * 4), **TOL_ELEM)
+    close(dev.logSoftmaxRows(x * 4), ref.log_softmax_rows(x * 4), **TOL_ELEM)
+
+
+@pytest.mark.parametrize("act", range(6))
+def test_gated_activation(dev, ref, act):
+    rng = np.random.default_rng(13 + act)
+    n, length, stride = 5, 70, 80
+    g = rng.standard_normal(n * stride).astype(np.float32) * 3
+    u = rng.standard_normal(n * stride).astype(np.float32)
+    close(dev.gatedActivation(act, g, u, n, length, stride, length),
+          ref.gated(act, g, u, n, length, stride, length), **TOL_ELEM)
+
+
+def test_rope_rows(dev, ref):
+    rng = np.random.default_rng(14)
+    ang = rng.uniform(0, 6, (10, 8))
+    cos_t, sin_t = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    x = rng.standard_normal((6, 16)).astype(np.float32)
+    pos = [0, 3, 9, 2, 2, 5]
+    for style in (0, 1):
+        close(dev.ropeRows(x, cos_t, sin_t, pos, style), ref.rope_rows(x, cos_t, sin_t, pos, style), **TOL_ELEM)
+
+
+def test_attention_scores_values(dev, ref):
+    rng = np.random.default_rng(15)
+    hd, stride, nk = 64, 128, 37
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal(nk * stride).astype(np.float32)
+    s = dev.attentionScores(q, k, nk, stride, 0.125)
+    want = np.array([np.dot(q.astype(np.float64), k[p * stride:p * stride + hd]) for p in range(nk)]) * 0.125
+    close(s, want, **TOL_RED)
+    p = np.exp(want - want.max()).astype(np.float32)
+    p /= p.sum()
+    out = dev.attentionValues(p, k, hd, stride)
+    wv = sum(p[i] * k[i * stride:i * stride + hd].astype(np.float64) for i in range(nk))
+    close(out, wv, **TOL_RED)
+
+
+def test_rownorms_matvecT(dev, ref):
+    rng = np.random.default_rng(16)
+    for kind in ("bf16", "q8_0", "mxfp4", "int4", "fp8"):
+        w = wg.make(kind, 70, 256, rng)
+        close(dev.rowNorms(w), ref.rowNorms(w), **TOL_RED)
+        y = rng.standard_normal((2, 70)).astype(np.float32)
+        close(dev.matvecTMulti(w, y), ref.matvecTMulti(w, y), **TOL_MATMUL)
+
+
+def test_kl_rows(dev, ref):
+    rng = np.random.default_rng(17)
+    base = rng.standard_normal((4, 5000)).astype(np.float32) * 2
+    lb = ref.log_softmax_rows(base)
+    trial = base + rng.standard_normal(base.shape).astype(np.float32) * 0.05
+    close(dev.klRows(lb, trial), ref.kl_rows(lb, trial), atol=1e-9, rtol=1e-5)
+    assert np.abs(dev.klRows(lb, base)).max() < 1e-6
+
+
+def test_edit_delta(dev, ref):
+    rng = np.random.default_rng(18)
+    for kind in ("bf16", "int4", "mxfp4"):
+        w = wg.make(kind, 96, 256, rng)
+        v, _ = np.linalg.qr(rng.standard_normal((96, 2)))
+        v = v.T.astype(np.float32)
+        a, b = dev.edit_delta(w, v, 1.0)
+        ra, rb = ref.edit_delta(w, v, 1.0)
+        close(a, ra, **TOL_MATMUL)
+        np.testing.assert_array_equal(b, rb)
+
+
+def test_errors_are_reported_not_raised(dev):
+    """Bad arguments come back as status codes with a message."""
+    from ditch_amd.hip import DeviceError
+    from ditch_amd.weights import HostWeight
+    bad = HostWeight.fp8(np.zeros((64, 64), np.uint8), np.ones((1, 1), np.float32), 128, 128)
+    bad.struct.scale_rows = 0
+    with pytest.raises(DeviceError):
+        dev.matmulT(np.zeros((1, 64), np.float32), bad)
+
+
+# the reference's device-contract sweep (selftest.zig:121-134, 159-177):
+# N(0,1) weights stored as f32/f16/bf16, N(0,1) activations
+SELFTEST_SHAPES = [(1, 1, 1), (1, 1, 16), (1, 3, 17), (1, 16, 16), (1, 64, 128), (2, 17, 33), (4, 32, 64),
+                   (5, 65, 31), (8, 128, 256), (13, 37, 48)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_selftest_matmul_sweep(dev, ref, dtype):
+    rng = np.random.default_rng(99)
+    for n, rows, cols in SELFTEST_SHAPES:
+        w = wg.float_random(dtype, rows, cols, rng, scale=1.0)
+        x = rng.standard_normal((n, cols)).astype(np.float32)
+        close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
