@@ -1,0 +1,137 @@
+"""The resident forward pass on the GPU against the oracle and the
+reference's goldens (needs an MI355X).
+
+Bars: logits within 1e-3 relative to the CPU
+logits (max |dlogit| <= 1e-3 * max |logit|), per-prompt KL(CPU || GPU) <=
+1e-4 with scorers.zig:387-394's formula, residuals within 1e-3 relative;
+against the fixture goldens, the reference's own 2e-3 absolute
+(model_test.zig:58-75).
+"""
+import numpy as np
+import pytest
+
+import fixture_io as fx
+import model_gen as mg
+from ditch_amd import abi
+from ditch_amd.hip import Model
+from oracle.ref import RefModel
+
+pytestmark = pytest.mark.gpu
+
+HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "deepseek_v3"]
+GGUF = ["qwen2_gguf", "llama_gguf"]
+
+
+def check_parity(ref, res_g, log_g, res_c, log_c, tag=""):
+    scale = np.abs(log_c).max()
+    err = np.abs(log_g - log_c).max()
+    assert err <= 1e-3 * scale, f"{tag} logits: max err {err:.3e} vs scale {scale:.3e}"
+    if res_c.size:
+        rs = np.abs(res_c).max(axis=-1, keepdims=True)
+        assert (np.abs(res_g - res_c) <= 1e-3 * rs + 1e-6).all(), f"{tag} residuals"
+    lb = ref.log_softmax_rows(log_c)
+    kl = ref.kl_rows(lb, log_g)
+    assert kl.max() <= 1e-4, f"{tag} KL {kl.max():.3e}"
+    return err / scale, kl.max()
+
+
+@pytest.mark.parametrize("name", HF + GGUF)
+def test_fixture_forward_matches_goldens_and_oracle(dev, ref, name):
+    spec = fx.spec_from_gguf(name) if name in GGUF else fx.spec_from_hf(name)
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        for case in fx.golden(name)["cases"]:
+            ids = case["ids"]
+            n = len(ids)
+            res, logits = gm.forward(ids, fx.case_rows(ids), capture_rows=[n - 1], logit_rows=[n - 1])
+            np.testing.assert_allclose(logits[0], case["last_logits"], atol=2e-3, rtol=0)
+            np.testing.assert_allclose(res[:, 0, :], case["last_hidden"], atol=2e-3, rtol=0)
+            assert int(np.argmax(logits[0])) == case["argmax"]
+            rc, lc = cm.forward(ids, fx.case_rows(ids), capture_rows=[n - 1], logit_rows=[n - 1])
+            check_parity(ref, res, logits, rc, lc, name)
+    finally:
+        gm.free()
+        cm.free()
+
+
+def test_fixture_batch_of_prompts(dev, ref):
+    """All cases of a fixture as one batch (rows {b, pos}): each prompt's
+    logits equal its single-prompt run."""
+    spec = fx.spec_from_hf("qwen3_moe")
+    cases = fx.golden("qwen3_moe")["cases"]
+    tokens, rows, last = [], [], []
+    for b, c in enumerate(cases):
+        for p, t in enumerate(c["ids"]):
+            tokens.append(t)
+            rows.append((b, p))
+        last.append(len(tokens) - 1)
+    gm = Model(dev, spec)
+    try:
+        res, logits = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+    for i, c in enumerate(cases):
+        np.testing.assert_allclose(logits[i], c["last_logits"], atol=2e-3, rtol=0)
+        np.testing.assert_allclose(res[:, i, :], c["last_hidden"], atol=2e-3, rtol=0)
+
+
+SYNTH = {
+    "dense_bf16": lambda: mg.dense("bf16", qkv_bias=True),
+    "dense_f32": lambda: mg.dense("f32", embed_fmt="f32"),
+    "dense_mxfp4": lambda: mg.dense("mxfp4", tie=False),
+    "dense_fp8": lambda: mg.dense("fp8", qk_norm=True),
+    "dense_int4": lambda: mg.dense("int4"),
+    "dense_q8_0": lambda: mg.dense("q8_0"),
+    "moe_int4_softmax": lambda: mg.moe("int4"),
+    "moe_fp8_sigmoid_groups": lambda: mg.moe("fp8", sigmoid=True, n_group=4, topk_group=2, shared=128, scaling=2.5,
+                                             dense_first=1),
+    "mla_fp8": lambda: mg.mla("fp8"),
+}
+
+
+@pytest.mark.parametrize("name", list(SYNTH))
+def test_synthetic_forward_matches_oracle(dev, ref, name):
+    spec = SYNTH[name]()
+    tokens, rows, last = mg.batch(6, [17, 64, 1, 40], spec.config["vocab"], seed=len(name))
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    check_parity(ref, rg, lg, rc, lc, name)
+
+
+def test_edit_then_forward(dev, ref):
+    """Rank-2 none-mode edit (abliterate.zig:264-280) of o_proj, down_proj and
+    every expert down_proj, applied in the matmul epilogue, against the
+    oracle doing the same edit."""
+    spec = mg.moe("int4", dense_first=1)
+    rng = np.random.default_rng(3)
+    v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+    v = v.T.astype(np.float32)
+    tokens, rows, last = mg.batch(4, [30, 12], spec.config["vocab"], seed=5)
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        for li in range(spec.config["layers"]):
+            for m in (gm, cm):
+                m.edit(li, abi.SLOT["O"], -1, v, 1.0)
+                if spec.moe_layers[li]:
+                    for e in range(spec.config["n_experts"]):
+                        m.edit(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0)
+                else:
+                    m.edit(li, abi.SLOT["DOWN"], -1, v, 1.0)
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        check_parity(ref, rg, lg, rc, lc, "edited")
+        # the edit changed the model
+        gm.reset_deltas()
+        _, l0 = gm.forward(tokens, rows, logit_rows=last)
+        assert np.abs(l0 - lg).max() > 1e-4
+    finally:
+        gm.free()
+        cm.free()
