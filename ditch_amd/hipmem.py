@@ -14,19 +14,30 @@ from . import load_library
 _hip = None
 
 
+def _mapped_hip_runtimes():
+    """Paths of the libamdhip64 files mapped into this process."""
+    paths = []
+    with open("/proc/self/maps") as f:
+        for line in f:
+            p = line.split()[-1] if len(line.split()) >= 6 else ""
+            if "libamdhip64" in os.path.basename(p) and p not in paths:
+                paths.append(p)
+    return paths
+
+
 def hip():
+    """The HIP runtime libditch_hip.so runs on (the ROCm installation's
+    libamdhip64.so.N). Torch's wheel maps a second copy under its own lib
+    directory for itself; binding by path to the library's copy keeps device
+    pointers of this module valid for the library."""
     global _hip
     if _hip is not None:
         return _hip
-    load_library()  # brings in libamdhip64 through its DT_NEEDED entry
-    for name in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
-        try:
-            lib = ctypes.CDLL(name, mode=ctypes.RTLD_GLOBAL)
-            break
-        except OSError:
-            lib = None
-    if lib is None:
-        raise OSError("libamdhip64.so not found")
+    load_library()
+    mapped = [p for p in _mapped_hip_runtimes() if "/torch/lib/" not in p]
+    if len(mapped) != 1:
+        raise RuntimeError(f"cannot tell which HIP runtime libditch_hip.so uses: {_mapped_hip_runtimes()}")
+    lib = ctypes.CDLL(mapped[0], mode=ctypes.RTLD_GLOBAL)
     P, S = ctypes.c_void_p, ctypes.c_size_t
     proto = {
         "hipMalloc": [ctypes.POINTER(P), S],

@@ -55,8 +55,9 @@ def mxfp4_quantize(w: torch.Tensor) -> HostWeight:
     amax = x.abs().amax(dim=2, keepdim=True).clamp_min(1e-30)
     e = torch.ceil(torch.log2(amax / 6.0)).clamp(-127, 127)
     y = x / torch.exp2(e)
-    grid = E2M1.to(w.device)
-    idx = (y.abs().unsqueeze(-1) - grid).abs().argmin(dim=-1)
+    # nearest E2M1 magnitude through the midpoints between grid values
+    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], device=w.device)
+    idx = torch.bucketize(y.abs(), mids)
     code = idx | ((y < 0).to(torch.int64) << 3)
     code = code.reshape(rows, cols // 2, 2)
     packed = (code[..., 0] | (code[..., 1] << 4)).to(torch.uint8)
