@@ -184,6 +184,30 @@ def gemv_leg(dev, reps):
     return out
 
 
+def copy_leg(dev, reps):
+    """A plain streaming kernel of known size for calibrating the HBM
+    counters: the decode of a 64 MiB bf16 tensor to f32 (reads 64 MiB of
+    tiles, writes 128 MiB)."""
+    from ditch_amd import hipmem
+    from ditch_amd.weights import HostWeight
+    rows, cols = 8192, 4096
+    w = HostWeight.bf16(np.random.default_rng(5).integers(0, 1 << 15, (rows, cols)).astype(np.uint16))
+    t = dev.upload(w)
+    out = hipmem.Buffer(rows * cols * 4)  # plain bf16 weights decode to f32
+    e0, e1 = hipmem.Event(), hipmem.Event()
+    t.dequant_device(out.ptr, out.nbytes, 0, rows)
+    dev.sync()
+    e0.record(dev.stream)
+    for _ in range(reps):
+        t.dequant_device(out.ptr, out.nbytes, 0, rows)
+    e1.record(dev.stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    t.free()
+    return {"bytes_read": rows * cols * 2, "bytes_written": rows * cols * 4, "avg_launch_us": round(ms * 1e3, 2),
+            "GB_s": round(6 * rows * cols / (ms * 1e-3) / 1e9, 1)}
+
+
 def traffic_for(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE), when the summary has been recorded under profiles/."""
@@ -257,7 +281,7 @@ def main():
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (quick runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
-    ap.add_argument("--kernel-only", choices=["gemm", "gemv"], default=None,
+    ap.add_argument("--kernel-only", choices=["gemm", "gemv", "copy"], default=None,
                     help="run only the roofline kernel (for rocprofv3 runs)")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
@@ -280,6 +304,9 @@ def main():
         return
     if args.kernel_only == "gemv":
         print(json.dumps({"kernel_only": "gemv", "gemv": gemv_leg(dev, args.reps)}))
+        return
+    if args.kernel_only == "copy":
+        print(json.dumps({"kernel_only": "copy", "copy": copy_leg(dev, args.reps)}))
         return
 
     t0 = time.time()

@@ -148,7 +148,7 @@ PROTOTYPES = {
     "ditch_hip_upload": (P, [P, P]),
     "ditch_hip_tensor_free": (None, [P, P]),
     "ditch_hip_tensor_bytes": (U64, [P]),
-    "ditch_hip_tensor_dequant": (I32, [P, P, P, U64, U64]),
+    "ditch_hip_tensor_dequant": (I32, [P, P, U64, P, U64, U64]),
     "ditch_hip_matmulT_device": (I32, [P, P, P, U64, P, P, I32, P]),
     "ditch_hip_model_create": (P, [P, P]),
     "ditch_hip_model_free": (None, [P]),

@@ -303,10 +303,13 @@ void ditch_hip_tensor_free(ditch_hip *h, ditch_hip_tensor *t) {
 
 uint64_t ditch_hip_tensor_bytes(const ditch_hip_tensor *t) { return t ? t->bytes : 0; }
 
-int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, const ditch_hip_tensor *t, uint64_t row0,
-                                 uint64_t nrows) {
+int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, uint64_t out_bytes, const ditch_hip_tensor *t,
+                                 uint64_t row0, uint64_t nrows) {
     return guarded(h, [&] {
         DITCH_CHECK(t && d_out && row0 + nrows <= (uint64_t)t->v.rows, DITCH_INVALID_ARGUMENT, "tensor_dequant range");
+        uint64_t elem = is_bf16_virtual(t->v.orig_dtype) ? 2 : 4;
+        DITCH_CHECK(nrows * (uint64_t)t->v.cols * elem <= out_bytes, DITCH_INVALID_ARGUMENT,
+                    "tensor_dequant: output buffer too small");
         launch_dequant(t->v, d_out, (int64_t)row0, (int64_t)nrows, h->stream);
     });
 }

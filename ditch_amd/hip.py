@@ -193,8 +193,8 @@ class Tensor:
         self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, d_x, n, self.handle, d_bias,
                                                              int(accumulate), stream))
 
-    def dequant_device(self, d_out, row0, nrows):
-        self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, self.handle, row0, nrows))
+    def dequant_device(self, d_out, out_bytes, row0, nrows):
+        self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, out_bytes, self.handle, row0, nrows))
 
 
 class Model:

@@ -191,9 +191,11 @@ ditch_hip_tensor *ditch_hip_upload(ditch_hip *h, const ditch_weight *w);
 void ditch_hip_tensor_free(ditch_hip *h, ditch_hip_tensor *t);
 /* HBM bytes the tensor occupies (codes + scales).                          */
 uint64_t ditch_hip_tensor_bytes(const ditch_hip_tensor *t);
-/* Decode of a resident tensor into device memory (`d_out`), same output
- * types as ditch_hip_dequant. Runs on the context stream.                   */
-int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out,
+/* Decode of a resident tensor into device memory (`d_out`, `out_bytes`
+ * long), same output types as ditch_hip_dequant: 2 bytes per element for the
+ * virtual-bf16 formats, 4 otherwise. A buffer shorter than nrows * cols
+ * elements is refused. Runs on the context stream.                         */
+int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, uint64_t out_bytes,
                                  const ditch_hip_tensor *t, uint64_t row0,
                                  uint64_t nrows);
 /* d_out[n][rows] (=|+=) d_x[n][cols] @ W^T (+ d_bias[rows]) on device

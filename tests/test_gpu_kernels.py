@@ -80,7 +80,7 @@ def test_dequant_bit_exact(dev, ref, name, gen):
     t = dev.upload(w)
     try:
         buf = Buffer(want.nbytes)
-        t.dequant_device(buf.ptr, 0, w.rows)
+        t.dequant_device(buf.ptr, buf.nbytes, 0, w.rows)
         dev.sync()
         tiled = buf.download(want.dtype, want.shape)
         buf.free()
@@ -219,3 +219,19 @@ def test_selftest_matmul_sweep(dev, ref, dtype):
         w = wg.float_random(dtype, rows, cols, rng, scale=1.0)
         x = rng.standard_normal((n, cols)).astype(np.float32)
         close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
+
+
+def test_tensor_dequant_refuses_a_short_buffer(dev):
+    """The decode of plain bf16 weights writes f32: a buffer sized for bf16
+    output is refused on the host before any kernel runs."""
+    from ditch_amd.hip import DeviceError
+    from ditch_amd.hipmem import Buffer
+    w = wg.float_random("bf16", 64, 128, np.random.default_rng(1))
+    t = dev.upload(w)
+    short = Buffer(64 * 128 * 2)
+    try:
+        with pytest.raises(DeviceError):
+            t.dequant_device(short.ptr, short.nbytes, 0, 64)
+    finally:
+        short.free()
+        t.free()
