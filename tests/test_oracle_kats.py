@@ -308,3 +308,72 @@ def test_edit_removes_the_directions(ref):
     a, b = ref.edit_delta(HostWeight.f32(wf), v, 1.0)
     wp = wf.astype(np.float64) + b.astype(np.float64) @ a.astype(np.float64)
     assert np.abs(v.astype(np.float64) @ wp).max() < 1e-4
+
+
+# -- closed forms for the per-op kernels (float64 / torch restatements) ----------
+
+def test_matvecT_and_row_norms_against_float64(ref):
+    rng = np.random.default_rng(7)
+    for q, rows, cols in [(1, 9, 31), (3, 70, 129), (8, 300, 64)]:
+        wf = rng.standard_normal((rows, cols)).astype(np.float32)
+        y = rng.standard_normal((q, rows)).astype(np.float32)
+        y[0, ::3] = 0  # zero entries are skipped by the reference (tensor.zig:1056-1094)
+        w = HostWeight.f32(wf)
+        want = y.astype(np.float64) @ wf.astype(np.float64)
+        np.testing.assert_allclose(ref.matvecTMulti(w, y), want, rtol=1e-5, atol=1e-4)
+        np.testing.assert_allclose(ref.rowNorms(w), np.linalg.norm(wf.astype(np.float64), axis=1), rtol=1e-6)
+
+
+def test_attention_scores_and_values_against_float64(ref):
+    rng = np.random.default_rng(8)
+    hd, n_keys, stride = 64, 37, 96
+    q = rng.standard_normal(hd).astype(np.float32)
+    kv = rng.standard_normal(n_keys * stride).astype(np.float32)
+    scores = np.empty(n_keys, np.float32)
+    ref.lib.ref_attention_scores(scores.ctypes.data, n_keys, q.ctypes.data, hd, kv.ctypes.data, stride, 0.125)
+    kmat = kv.reshape(n_keys, stride)[:, :hd].astype(np.float64)
+    np.testing.assert_allclose(scores, 0.125 * (kmat @ q.astype(np.float64)), rtol=1e-5, atol=1e-5)
+    p = rng.random(n_keys).astype(np.float32)
+    vd = 48
+    out = np.empty(vd, np.float32)
+    ref.lib.ref_attention_values(out.ctypes.data, vd, p.ctypes.data, n_keys, kv.ctypes.data, stride)
+    want = p.astype(np.float64) @ kv.reshape(n_keys, stride)[:, :vd].astype(np.float64)
+    np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("one_plus", [0, 1])
+def test_layernorm_and_gemma_rmsnorm_against_float64(ref, one_plus):
+    rng = np.random.default_rng(9)
+    n = 200
+    x = (rng.standard_normal(n) * 3 + 1).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    out = np.empty(n, np.float32)
+    ref.lib.ref_layernorm(out.ctypes.data, x.ctypes.data, w.ctypes.data, n, b.ctypes.data, n, 1e-5, one_plus)
+    xd = x.astype(np.float64)
+    scale = (1 + w.astype(np.float64)) if one_plus else w.astype(np.float64)
+    want = (xd - xd.mean()) / np.sqrt(xd.var() + 1e-5) * scale + b
+    np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-5)
+    got = ref.rmsnorm_rows(x[None], w, 1e-6, gemma=bool(one_plus))[0]
+    want = xd / np.sqrt((xd * xd).mean() + 1e-6) * scale
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_gated_activations_against_torch(ref):
+    """Activation order of tensor.Activation (compute.zig:81-83): silu,
+    gelu_tanh, gelu (erf), relu, relu2, quick_gelu (x * sigmoid(1.702 x))."""
+    import torch.nn.functional as F
+    g = torch.linspace(-9, 9, 601, dtype=torch.float64)
+    u = torch.linspace(2, -1, 601, dtype=torch.float64)
+    want = [F.silu(g), F.gelu(g, approximate="tanh"), F.gelu(g), F.relu(g), F.relu(g) ** 2,
+            g * torch.sigmoid(1.702 * g)]
+    for act, a in enumerate(want):
+        got = ref.gated(act, g.float().numpy(), u.float().numpy(), 1, g.numel(), g.numel(), g.numel())
+        np.testing.assert_allclose(got, (a * u).numpy(), rtol=2e-5, atol=2e-6, err_msg=f"act {act}")
+
+
+def test_softmax_against_scipy(ref):
+    from scipy.special import softmax
+    rng = np.random.default_rng(10)
+    x = (rng.standard_normal((4, 77)) * 5).astype(np.float32)
+    np.testing.assert_allclose(ref.softmax_rows(x), softmax(x.astype(np.float64), axis=1), rtol=2e-6, atol=1e-9)
