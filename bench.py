@@ -221,10 +221,11 @@ def traffic_for(name):
 # CPU baseline (oracle, bounded sample)
 
 
-def cpu_leg(spec, cfg, batch, gpu_res, prompts=2):
-    """The oracle on `prompts` prompts of the benchmark batch through the
-    first one and two layers of the same model (+ embedding, final norm and
-    lm_head); the per-layer time is extrapolated to the full depth. Also
+def cpu_leg(spec, cfg, batch, gpu_res, prompts=None):
+    """The oracle on the benchmark batch (all of its prompts unless `prompts`
+    says fewer) through the first one and two layers of the same model (+
+    embedding, final norm and lm_head); the per-layer time is extrapolated to
+    the full depth (about 10 s of CPU work at the C3 shape on 16 cores). Also
     returns how far the GPU's residuals at those layer entries are from the
     oracle's."""
     from ditch_amd.spec import ModelSpec
@@ -236,6 +237,7 @@ def cpu_leg(spec, cfg, batch, gpu_res, prompts=2):
             small.tensors[(layer, slot, expert)] = w
     tokens, rows, last = batch
     T = cfg["tokens"]
+    prompts = cfg["prompts"] if prompts is None else prompts
     n = prompts * T
     with tempfile.TemporaryDirectory() as d:
         so = os.path.join(d, "libcpu_ref_native.so")
