@@ -121,7 +121,7 @@ int32_t ditch_hip_matmulT(ditch_hip *h, float *out, const float *x, uint64_t n, 
         h2d(dx.p, x, n * w->cols * 4, s);
         MatmulEpilogue ep;
         ep.exact = 1;
-        launch_matmul(t->v, dout.as<float>(), dx.as<float>(), (int64_t)n, ep, s);
+        launch_matmul(t->v, dout.as<float>(), dx.as<float>(), (int64_t)n, ep, s, nullptr, &h->split);
         d2h(out, dout.p, n * w->rows * 4, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
     });
@@ -321,7 +321,7 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x, u
         MatmulEpilogue ep;
         ep.bias = d_bias;
         ep.accumulate = accumulate;
-        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream);
+        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream, nullptr, &h->split);
     });
 }
 

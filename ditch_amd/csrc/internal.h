@@ -76,6 +76,35 @@ struct TileView {
     int64_t group;          // INT4 group size
     int32_t e5m2;
     int32_t orig_dtype;     // ditch_weight dtype the tensor came from
+    // 1 when the gfx950 conversion instructions decode every element of this
+    // tensor exactly as the reference does: no E8M0 scale byte 255 (MXFP4),
+    // no NaN/Inf codes and finite scales (FP8), finite scales (INT4), and
+    // scale blocks that cover whole 64-column stages (FP8 block_cols and
+    // INT4 group multiples of 64). Set at upload; the tiled GEMM requires it.
+    int32_t fast;
+};
+
+// Device memory helpers (all on the context stream).
+void *dev_alloc(size_t bytes);
+void dev_free(void *p);
+
+// A device buffer that grows on demand (contents are not kept on growth).
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    ~DevBuf() { dev_free(p); }
+    template <typename T>
+    T *get(size_t count) {
+        size_t need = count * sizeof(T);
+        if (need > bytes) {
+            dev_free(p);
+            p = nullptr;
+            bytes = 0;
+            p = dev_alloc(need < 256 ? 256 : need);
+            bytes = need;
+        }
+        return (T *)p;
+    }
 };
 
 }  // namespace ditch
@@ -98,14 +127,11 @@ struct ditch_hip {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     int cu_count = 0;
+    // activation fragments of the tiled GEMM for the context's own products
+    ditch::DevBuf split;
 };
 
 namespace ditch {
-
-// Device memory helpers (all on the context stream).
-void *dev_alloc(size_t bytes);
-void dev_free(void *p);
-void *ctx_scratch(ditch_hip *h, size_t bytes);
 
 // tiles.hip
 ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s);
@@ -126,8 +152,19 @@ struct MatmulEpilogue {
     // device-contract tolerance); the resident forward uses two
     int exact = 0;
 };
+// `ws` (optional) holds the split activations of the tiled GEMM; without it
+// the product runs on the small-batch kernels.
 void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
-                   hipStream_t s, const int32_t *row_index = nullptr);
+                   hipStream_t s, const int32_t *row_index = nullptr, DevBuf *ws = nullptr);
+
+// gemm_tile.hip: large-batch product on pre-split activation fragments
+bool tile_gemm_takes(const TileView &w, int64_t n);
+int64_t split_k_tiles(const TileView &w);  // k tiles of the fragments (even)
+size_t split_bytes(const TileView &w, int64_t n, int xt);
+void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
+                  int64_t kt_total, int xt, hipStream_t s);
+void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t n, int xt,
+                      const MatmulEpilogue &ep, hipStream_t s);
 // One product per segment (routed experts): segment z multiplies rows
 // [off, off + cnt) of x (through row_index when given) by its own weight
 // into rows [off, off + cnt) of out. Every segment has rows x cols weights

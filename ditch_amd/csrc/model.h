@@ -6,24 +6,6 @@
 
 namespace ditch {
 
-struct DevBuf {
-    void *p = nullptr;
-    size_t bytes = 0;
-    ~DevBuf() { dev_free(p); }
-    template <typename T>
-    T *get(size_t count) {
-        size_t need = count * sizeof(T);
-        if (need > bytes) {
-            dev_free(p);
-            p = nullptr;
-            bytes = 0;
-            p = dev_alloc(need < 256 ? 256 : need);
-            bytes = need;
-        }
-        return (T *)p;
-    }
-};
-
 struct Mat {
     ditch_hip_tensor *t = nullptr;
     float *da = nullptr, *db = nullptr;  // delta A [rank][cols], B [rows][rank]
@@ -72,5 +54,6 @@ struct ditch_hip_model {
     ditch::DevBuf x, hbuf, q, k, v, att, o, g, u, kc, vc, rowsb, xa, logit_h, mla_a, mla_b, mla_c;
     ditch::DevBuf r_logits, r_sel, r_selw, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
         segs, segd, e_xa;
+    ditch::DevBuf xsplit;  // split activations of the tiled GEMM
     ~ditch_hip_model();
 };

@@ -613,7 +613,7 @@ static void mm(ditch_hip_model *m, const Mat &mt, float *out, const float *x, in
         ep.delta_xa = xa;
         ep.delta_rank = mt.rank;
     }
-    launch_matmul(mt.t->v, out, x, n, ep, s);
+    launch_matmul(mt.t->v, out, x, n, ep, s, nullptr, &m->xsplit);
 }
 
 // Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).

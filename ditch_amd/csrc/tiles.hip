@@ -6,6 +6,7 @@
 // 477-673). Fused formats (TF_Q8/FP8/MX4/INT4/BF16/F16/F32) keep their codes
 // and are re-tiled for the matmul kernels; the others are decoded once at
 // upload to the reference's virtual dtype (bf16, or f32 for GGUF blocks).
+#include <string.h>
 #include "decode.h"
 #include "internal.h"
 #include "tiled.h"
@@ -447,6 +448,71 @@ static RawSizes raw_sizes(const ditch_weight *w) {
     return z;
 }
 
+// Whether the gfx950 conversion instructions decode every element of `w`
+// (stored as tile format `tf`) exactly as the reference does; see
+// TileView::fast. Scans the host copy of the codes and scales.
+static bool has_byte(const uint8_t *p, size_t n, uint8_t mask, uint8_t value) {
+    // any byte with (b & mask) == value, eight bytes at a time
+    const uint64_t M = 0x0101010101010101ull * mask, V = 0x0101010101010101ull * value;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        uint64_t w;
+        memcpy(&w, p + i, 8);
+        uint64_t v = (w & M) ^ V;  // zero bytes where the pattern matches
+        if ((v - 0x0101010101010101ull) & ~v & 0x8080808080808080ull) return true;
+    }
+    for (; i < n; i++)
+        if ((p[i] & mask) == value) return true;
+    return false;
+}
+
+static bool finite_scales(const void *p, size_t count, int32_t dtype) {
+    for (size_t i = 0; i < count; i++) {
+        switch (dtype) {
+        case DITCH_F32: {
+            uint32_t b;
+            memcpy(&b, (const uint8_t *)p + 4 * i, 4);
+            if ((b & 0x7f800000u) == 0x7f800000u) return false;
+            break;
+        }
+        case DITCH_BF16: {
+            uint16_t b;
+            memcpy(&b, (const uint8_t *)p + 2 * i, 2);
+            if ((b & 0x7f80u) == 0x7f80u) return false;
+            break;
+        }
+        case DITCH_F16: {
+            uint16_t b;
+            memcpy(&b, (const uint8_t *)p + 2 * i, 2);
+            if ((b & 0x7c00u) == 0x7c00u) return false;
+            break;
+        }
+        case DITCH_E8M0:
+            if (((const uint8_t *)p)[i] == 255u) return false;
+            break;
+        default: return false;
+        }
+    }
+    return true;
+}
+
+static int fast_decode_ok(const ditch_weight *w, int tf) {
+    switch (tf) {
+    case TF_BF16: case TF_Q8: return 1;  // nothing decoded by conversion instructions
+    case TF_MX4: return has_byte((const uint8_t *)w->scale, w->rows * w->cols / 32, 0xffu, 0xffu) ? 0 : 1;
+    case TF_FP8: {
+        if (w->block_cols % 64 != 0 || w->fp8_e5m2) return 0;  // E5M2 stays on the exact decoder
+        bool special = w->fp8_e5m2 ? has_byte((const uint8_t *)w->data, w->rows * w->cols, 0x7cu, 0x7cu)
+                                   : has_byte((const uint8_t *)w->data, w->rows * w->cols, 0x7fu, 0x7fu);
+        return !special && finite_scales(w->scale, w->scale_rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
+    }
+    case TF_INT4:
+        if (w->group % 64 != 0) return 0;
+        return finite_scales(w->scale, w->rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
+    default: return 0;
+    }
+}
+
 // Copies the raw pieces of `w` to one device staging buffer.
 struct Staged {
     void *buf = nullptr;
@@ -574,6 +640,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             launch_raw_dequant(st.v, dense, 0, v.rows, dense_f32 ? 0 : 1, s);
         }
         v.tf = tf;
+        v.fast = decode_first ? (tf == TF_BF16 ? 1 : 0) : fast_decode_ok(w, tf);
         int uk = unit_k_of(tf);
         int64_t rows_pad = pad_to(v.rows, 16), cols_pad = pad_to(v.cols, uk);
         v.units_k = cols_pad / uk;

@@ -1,11 +1,14 @@
-"""Device buffers and events through the HIP runtime libditch_hip.so links.
+"""Device buffers and events through the HIP runtime libditch_hip.so runs on.
 
 Callers that hand device pointers to the C ABI (tests, bench.py) allocate them
-here. Torch is not used on the device in the same process: its wheel carries
-its own HIP runtime, and two runtimes in one process do not share devices.
+here. Torch's wheel carries its own copy of the HIP runtime under the same
+soname (libamdhip64.so.7) as the ROCm installation's; whichever copy is
+loaded first in a process is the one libditch_hip.so binds to. The functions
+below are therefore looked up through the library's own handle (dlsym
+searches its dependencies), so buffers and events always live in the runtime
+the library uses.
 """
 import ctypes
-import os
 
 import numpy as np
 
@@ -14,30 +17,12 @@ from . import load_library
 _hip = None
 
 
-def _mapped_hip_runtimes():
-    """Paths of the libamdhip64 files mapped into this process."""
-    paths = []
-    with open("/proc/self/maps") as f:
-        for line in f:
-            p = line.split()[-1] if len(line.split()) >= 6 else ""
-            if "libamdhip64" in os.path.basename(p) and p not in paths:
-                paths.append(p)
-    return paths
-
-
 def hip():
-    """The HIP runtime libditch_hip.so runs on (the ROCm installation's
-    libamdhip64.so.N). Torch's wheel maps a second copy under its own lib
-    directory for itself; binding by path to the library's copy keeps device
-    pointers of this module valid for the library."""
+    """The HIP runtime functions libditch_hip.so resolves to."""
     global _hip
     if _hip is not None:
         return _hip
-    load_library()
-    mapped = [p for p in _mapped_hip_runtimes() if "/torch/lib/" not in p]
-    if len(mapped) != 1:
-        raise RuntimeError(f"cannot tell which HIP runtime libditch_hip.so uses: {_mapped_hip_runtimes()}")
-    lib = ctypes.CDLL(mapped[0], mode=ctypes.RTLD_GLOBAL)
+    lib = load_library()
     P, S = ctypes.c_void_p, ctypes.c_size_t
     proto = {
         "hipMalloc": [ctypes.POINTER(P), S],

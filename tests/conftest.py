@@ -10,6 +10,17 @@ for p in (ROOT, TESTS):
         sys.path.insert(0, p)
 
 
+# Load libditch_hip.so before any test module imports torch, so that it binds
+# the ROCm installation's HIP runtime (the one it is built against) rather
+# than the copy inside the torch wheel, which has the same soname.
+try:
+    import ditch_amd
+
+    ditch_amd.load_library()
+except Exception:  # not built: the ABI tests report it
+    pass
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library)")
 

@@ -113,7 +113,7 @@ def test_edit_then_forward(dev, ref):
     rng = np.random.default_rng(3)
     v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
     v = v.T.astype(np.float32)
-    tokens, rows, last = mg.batch(4, [30, 12], spec.config["vocab"], seed=5)
+    tokens, rows, last = mg.batch(6, [30, 12, 64], spec.config["vocab"], seed=5)  # 212 rows: the tiled product
     gm = Model(dev, spec)
     cm = RefModel(spec)
     try:

@@ -235,3 +235,64 @@ def test_tensor_dequant_refuses_a_short_buffer(dev):
     finally:
         short.free()
         t.free()
+
+
+# -- the large-batch tiled product (n >= 128): split activations + LDS-staged MFMA ----------
+
+TILE_KINDS = ["bf16", "fp8", "mxfp4", "int4", "int4_sym", "mxfp4_t", "int8", "fp8_16x8", "q8_0", "f32"]
+TILE_SHAPES = [(128, 256, 512), (200, 300, 640), (257, 48, 1024), (130, 1000, 384), (300, 17, 128)]
+
+
+@pytest.mark.parametrize("kind", TILE_KINDS)
+@pytest.mark.parametrize("n,rows,cols", TILE_SHAPES)
+def test_matmulT_large_batch_matches_oracle(dev, ref, kind, n, rows, cols):
+    """Shapes that reach the tiled kernel (ragged tokens, rows and k stages
+    included); formats it does not take run on the small-batch kernels."""
+    rng = np.random.default_rng(n * 131 + rows * 7 + cols)
+    w = wg.make(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "mxfp4", "int4"])
+def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
+    """The forward's product (two activation terms) on a resident tensor,
+    with the bias and accumulate epilogue, against the oracle."""
+    from ditch_amd import hipmem
+    rng = np.random.default_rng(77)
+    n, rows, cols = 384, 520, 1024
+    w = wg.make(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    prior = rng.standard_normal((n, rows)).astype(np.float32)
+    t = dev.upload(w)
+    try:
+        bx, bb, bo = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias), hipmem.Buffer.from_array(prior)
+        t.matmul_device(bo.ptr, bx.ptr, n, d_bias=bb.ptr, accumulate=True)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    want = (prior.astype(np.float64) + ref.matmulT(x, w).astype(np.float64) + bias)
+    # two bf16 terms leave |x - t0 - t1| <= 2^-18 |x| per activation, so the
+    # product may differ by up to 2^-18 * sum_k |x||w| (bounded here with a
+    # factor 4 of margin) beyond the exact path's tolerance
+    wd = ref.dequant(w)
+    wf = (wd.astype(np.uint32) << 16).view(np.float32) if wd.dtype == np.uint16 else wd
+    split = 2.0 ** -16 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    bad = np.abs(got - want) > TOL_MATMUL["atol"] + TOL_MATMUL["rtol"] * np.abs(want) + split
+    assert not bad.any(), f"{bad.sum()} outside the two-term bound"
+    assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
+
+
+def test_matmulT_large_batch_nan_scale_takes_the_exact_decoder(dev, ref):
+    """An E8M0 scale byte 255 (NaN block, dequant.zig:259-261) keeps the
+    tensor off the conversion instructions; the NaN rows match the oracle."""
+    rng = np.random.default_rng(5)
+    w = wg.mxfp4_random(64, 256, rng)
+    w.arrays[1][3, 2] = 255  # the scale array the weight struct points at
+    x = rng.standard_normal((160, 256)).astype(np.float32)
+    got, want = dev.matmulT(x, w), ref.matmulT(x, w)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    close(got[fin], want[fin], **TOL_MATMUL)
