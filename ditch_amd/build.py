@@ -27,13 +27,19 @@ FLAGS = [
 ]
 
 
+# per-source additions: the tiled GEMM keeps its MFMA accumulators in the
+# architectural VGPRs (with them in AGPRs the register allocator copies every
+# accumulator between the two files once per k stage)
+EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src, build_dir):
     obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

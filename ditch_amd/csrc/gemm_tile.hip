@@ -2,7 +2,7 @@
 //
 // out[n][rows] = x[n][cols] @ W^T (tensor.matmulT, tensor.zig:1023-1045) for
 // weights whose decode the gfx950 conversion instructions do exactly
-// (TileView::fast): bf16, MXFP4, FP8, INT4, Q8_0.
+// (TileView::fast): bf16, MXFP4, FP8, INT4.
 //
 // Two kernels:
 //
@@ -12,18 +12,20 @@
 //     xs[m16][kt][term][lane] (16 B each), lane l = token 16*m16 + l%16,
 //     k = 32*kt + 8*(l/16) .. +8
 // so every A fragment is one contiguous KiB. k tiles past the matrix are
-// zero up to an even count.
+// zero up to a whole number of pipeline stages.
 //
-// tile_gemm_kernel: a workgroup of WAVES waves computes BM = 16*WM tokens x
-// BN = 16*WN*WAVES weight rows. The A fragments of a 64-wide k stage are
-// staged in LDS (double buffered, each wave copies whole fragments with
-// 16-byte loads) and read by every wave; each wave owns WN row groups of
-// the weight and streams their tiles from HBM straight into registers two
-// stages ahead, decoding them with v_cvt_scalef32_pk_bf16_fp4 (MXFP4),
-// v_cvt_pk_f32_fp8 + f32 scale + v_cvt_pk_bf16_f32 (FP8), or integer
-// unpacking (INT4, Q8_0). The block index is remapped so that the
-// workgroups an XCD runs at the same time cover an 8 x (few) patch of output
-// tiles: they share A and W tiles in that XCD's L2.
+// tile_gemm_kernel: a workgroup of waves side by side computes 64 tokens x
+// 64 rows per wave (64 accumulator registers, two waves per SIMD). A stage
+// covers 64 or 128 k: its A fragments, each wave's weight codes (1 KiB units
+// of 16 rows) and per-row side words (scales) are copied global -> LDS with
+// global_load_lds (no registers, double buffered), then every wave decodes
+// its weight tiles with v_cvt_scalef32_pk_bf16_fp4 (MXFP4), v_cvt_pk_f32_fp8
+// + f32 scale + v_cvt_pk_bf16_f32 (FP8) or integer unpacking (INT4) and
+// issues the MFMAs. The block index is remapped so that the workgroups an
+// XCD runs at the same time cover an 8 x (few) patch of output tiles: they
+// share A and W tiles in that XCD's L2.
+#include <type_traits>
+
 #include "gemm_common.h"
 
 namespace ditch {
@@ -84,103 +86,75 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int TF> struct BSt;
-template <> struct BSt<TF_BF16> { uint4 a, b; };
-template <> struct BSt<TF_MX4> { uint2 c; uint32_t sw; };
-template <> struct BSt<TF_FP8> { uint4 c; float sc; };
-template <> struct BSt<TF_INT4> { uint2 c; float sc; int32_t zf; };
-template <> struct BSt<TF_Q8> { uint4 c; uint32_t sw; };
+// Per-format pipeline geometry: TPS k tiles (32 wide) per stage, NU weight
+// units (1 KiB per 16-row group) and NS side words per row per stage.
+template <int TF> struct TileCfg;
+template <> struct TileCfg<TF_BF16> { static constexpr int TPS = 2, NU = 2, NS = 0; };  // units 2s, 2s+1
+template <> struct TileCfg<TF_FP8> { static constexpr int TPS = 2, NU = 1, NS = 1; };   // unit s; f32 scale
+template <> struct TileCfg<TF_MX4> { static constexpr int TPS = 4, NU = 1, NS = 1; };   // unit s; 4 E8M0 bytes
+template <> struct TileCfg<TF_INT4> { static constexpr int TPS = 4, NU = 1, NS = 2; };  // unit s; two 64-col groups
 
-// Per-lane constants of one row group.
-struct RowCtx {
-    int64_t g;    // row group (clamped to the matrix)
-    int64_t row;  // weight row of this lane (clamped)
-    int64_t srow; // FP8: row of the scale grid
-};
+// Side word of stage s, entry j, for a row whose side row starts at `base`.
+template <int TF>
+__device__ __forceinline__ const uint32_t *side_word(const TileView &w, int64_t base, int64_t s, int j) {
+    if constexpr (TF == TF_MX4) return w.side + base + s;
+    else if constexpr (TF == TF_FP8) return w.side + base + (s * 64) / w.block_cols;
+    else return w.side + base + (s * 128 + 64 * j) / w.group;
+}
 
-__device__ __forceinline__ RowCtx row_ctx(const TileView &w, int64_t g, int lane) {
-    RowCtx c;
-    c.g = g;
+// Side row of this lane's weight row (FP8: its row of the scale grid).
+__device__ __forceinline__ int64_t side_row(const TileView &w, int64_t g, int lane) {
     int64_t r = g * 16 + (lane & 15);
-    c.row = r < w.rows ? r : w.rows - 1;
-    c.srow = 0;
+    r = r < w.rows ? r : w.rows - 1;
     if (w.tf == TF_FP8) {
-        if (w.row_shard == 0) c.srow = c.row / w.block_rows;
+        if (w.row_shard == 0) r = r / w.block_rows;
         else {
             int64_t per_shard = (w.row_shard + w.block_rows - 1) / w.block_rows;
-            c.srow = c.row / w.row_shard * per_shard + (c.row % w.row_shard) / w.block_rows;
+            r = r / w.row_shard * per_shard + (r % w.row_shard) / w.block_rows;
         }
     }
-    return c;
+    return r * w.side_cols;
 }
 
+// B fragment of k tile t of a stage from its codes (NU x 16 bytes) and side
+// words. `second` is false when a bf16 stage's second unit lies past the
+// matrix (its codes are a repeat of the first and must read as zero).
 template <int TF>
-__device__ __forceinline__ void load_stage(const TileView &w, const RowCtx &rc, int64_t s, int lane, BSt<TF> &b) {
-    const uint8_t *grp = w.codes + rc.g * w.units_k * 1024;
+__device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 (&c)[TileCfg<TF>::NU],
+                                                 const uint32_t *sd, int t, bool second) {
+    u32x4 f;
     if constexpr (TF == TF_BF16) {
-        // units 2s and 2s + 1 (the second is absent past an odd unit count)
-        b.a = *(const uint4 *)(grp + (2 * s) * 1024 + lane * 16);
-        if (2 * s + 1 < w.units_k) b.b = *(const uint4 *)(grp + (2 * s + 1) * 1024 + lane * 16);
-        else b.b = make_uint4(0, 0, 0, 0);
+        f = t == 0 ? c[0] : (second ? c[1] : u32x4{0, 0, 0, 0});
     } else if constexpr (TF == TF_MX4) {
-        int64_t u = s >> 1;
-        b.c = *(const uint2 *)(grp + u * 1024 + lane * 16 + 8 * (s & 1));
-        b.sw = *(const uint32_t *)((const uint8_t *)w.scale + rc.row * w.scale_cols + u * 4);
-    } else if constexpr (TF == TF_FP8) {
-        b.c = *(const uint4 *)(grp + s * 1024 + lane * 16);
-        b.sc = load_scale(w.scale, rc.srow * w.scale_cols + (s * 64) / w.block_cols, w.scale_type);
-    } else if constexpr (TF == TF_INT4) {
-        int64_t u = s >> 1;
-        b.c = *(const uint2 *)(grp + u * 1024 + lane * 16 + 8 * (s & 1));
-        int64_t gi = rc.row * w.scale_cols + (s * 64) / w.group;
-        b.sc = load_scale(w.scale, gi, w.scale_type);
-        b.zf = w.zero ? (int32_t)w.zero[gi] : 8;
-    } else if constexpr (TF == TF_Q8) {
-        b.c = *(const uint4 *)(grp + s * 1024 + lane * 16);
-        b.sw = *(const uint32_t *)((const uint16_t *)w.scale + rc.row * w.scale_cols + 2 * s);
-    }
-}
-
-// B fragment of tile t (0, 1) of stage s; `ts` is the partial-sum scale (Q8_0).
-template <int TF>
-__device__ __forceinline__ void decode_stage(const BSt<TF> &b, int64_t s, int t, u32x4 &f, float &ts) {
-    ts = 1.f;
-    if constexpr (TF == TF_BF16) {
-        const uint4 &v = t ? b.b : b.a;
-        f = u32x4{v.x, v.y, v.z, v.w};
-    } else if constexpr (TF == TF_MX4) {
-        uint32_t wd = t ? b.c.y : b.c.x;
-        uint32_t sb = (b.sw >> (8 * (2 * (uint32_t)(s & 1) + t))) & 0xffu;
-        float sc = u2f(sb ? (sb << 23) : 0x00400000u);  // 2^(b-127); byte 0 is the subnormal 2^-127
+        const uint32_t wd = c[0][t];
+        const uint32_t sb = (sd[0] >> (8 * t)) & 0xffu;
+        const float sc = u2f(sb ? (sb << 23) : 0x00400000u);  // 2^(b-127); byte 0 is the subnormal 2^-127
         f[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 0));
         f[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 1));
         f[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 2));
         f[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 3));
     } else if constexpr (TF == TF_FP8) {
-        uint32_t w0 = t ? b.c.z : b.c.x, w1 = t ? b.c.w : b.c.y;
+        const float sc = u2f(sd[0]);
+        const uint32_t w0 = c[0][2 * t], w1 = c[0][2 * t + 1];
         floatx2 p0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false), p1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
         floatx2 p2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false), p3 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
-        f[0] = cvt_pk_bf16(__fmul_rn(p0.x, b.sc), __fmul_rn(p0.y, b.sc));
-        f[1] = cvt_pk_bf16(__fmul_rn(p1.x, b.sc), __fmul_rn(p1.y, b.sc));
-        f[2] = cvt_pk_bf16(__fmul_rn(p2.x, b.sc), __fmul_rn(p2.y, b.sc));
-        f[3] = cvt_pk_bf16(__fmul_rn(p3.x, b.sc), __fmul_rn(p3.y, b.sc));
+        f[0] = cvt_pk_bf16(__fmul_rn(p0.x, sc), __fmul_rn(p0.y, sc));
+        f[1] = cvt_pk_bf16(__fmul_rn(p1.x, sc), __fmul_rn(p1.y, sc));
+        f[2] = cvt_pk_bf16(__fmul_rn(p2.x, sc), __fmul_rn(p2.y, sc));
+        f[3] = cvt_pk_bf16(__fmul_rn(p3.x, sc), __fmul_rn(p3.y, sc));
     } else if constexpr (TF == TF_INT4) {
-        uint32_t wd = t ? b.c.y : b.c.x;
+        const uint32_t word = sd[t >> 1];
+        const uint32_t bits = word & 0xffffu;
+        // the scale's own dtype, widened exactly
+        const float sc = w.scale_type == SC_BF16 ? u2f(bits << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+        const int32_t zf = (int32_t)(word >> 16);
+        const uint32_t wd = c[0][t];
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = __fmul_rn((float)((int32_t)((wd >> (4 * j)) & 0xfu) - b.zf), b.sc);
+        for (int j = 0; j < 8; j++) v[j] = __fmul_rn((float)((int32_t)((wd >> (4 * j)) & 0xfu) - zf), sc);
         f = u32x4{cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]), cvt_pk_bf16(v[4], v[5]), cvt_pk_bf16(v[6], v[7])};
-    } else if constexpr (TF == TF_Q8) {
-        uint32_t w0 = t ? b.c.z : b.c.x, w1 = t ? b.c.w : b.c.y;
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[j] = (float)(int8_t)((w0 >> (8 * j)) & 0xffu);
-            v[4 + j] = (float)(int8_t)((w1 >> (8 * j)) & 0xffu);
-        }
-        f = u32x4{pack_hi(v[0], v[1]), pack_hi(v[2], v[3]), pack_hi(v[4], v[5]), pack_hi(v[6], v[7])};
-        ts = f16_to_f32((uint16_t)((b.sw >> (16 * t)) & 0xffffu));
     }
+    return f;
 }
 
 // ---------------------------------------------------------------------------
@@ -232,39 +206,88 @@ __device__ __forceinline__ void tile_store(const TileGemmParams &p, int64_t tok,
     *o = v;
 }
 
-template <int TF, int XT, int WAVES, int WN, int WM>
-__global__ __launch_bounds__(WAVES * 64) void tile_gemm_kernel(TileGemmParams p) {
-    constexpr int FR = WM * 2 * XT;   // A fragments per stage: [m][t][term]
-    constexpr int PER = FR / WAVES;   // fragments each wave copies per stage
-    static_assert(FR % WAVES == 0, "stage fragments must split evenly over the waves");
-    __shared__ u32x4 As[2][FR][64];
+// s_waitcnt operand: wait until at most n vector memory loads are in flight
+// (expcnt and lgkmcnt left at their no-wait maxima).
+__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Every operand of a stage travels global -> LDS by DMA (global_load_lds:
+// lane l's bytes land at the destination + l * size), two stage buffers:
+// stage s + 1 is copied while stage s is computed, and a stage ends with
+// this wave's copies drained plus a barrier. No global load writes a
+// register inside the loop.
+template <int TF, int XT, int WGM, int WGN, int WM, int WN>
+__global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParams p) {
+    constexpr int WAVES = WGM * WGN;
+    constexpr int TPS = TileCfg<TF>::TPS, NU = TileCfg<TF>::NU, NS = TileCfg<TF>::NS;
+    constexpr int NS1 = NS ? NS : 1;
+    constexpr int FR = WGM * WM * TPS * XT;  // A fragments per stage: [m][t][term]
+    constexpr int PER = FR / WAVES;          // fragments each wave copies per stage
+    static_assert(FR % WAVES == 0, "stage fragments must split evenly over the waves");
+    // two stage buffers as distinct LDS objects, so that the compiler can
+    // tell the DMA into one from the reads of the other (with one array it
+    // waits for every copy in flight before any LDS read)
+    __shared__ u32x4 As0[FR * 64], As1[FR * 64];                            // [fragment][lane]
+    __shared__ u32x4 Bs0[WAVES * WN * NU * 64], Bs1[WAVES * WN * NU * 64];  // [wave][group][unit][lane]
+    __shared__ uint32_t Ss0[WAVES * WN * NS1 * 16], Ss1[WAVES * WN * NS1 * 16];  // [wave][group][entry][row]
+
+    const TileView &w = p.w;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_m = wave / WGN, wave_n = wave % WGN;
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
-    const int64_t groups = (p.w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)nt * (WN * WAVES) + wave * WN;
-    const int64_t m16_0 = (int64_t)mt * WM, m16_n = (p.n + 15) / 16;
-    const int64_t S = p.kt_total / 2;
+    const int64_t groups = (w.rows + 15) / 16;
+    const int64_t g0 = (int64_t)nt * (WN * WGN) + wave_n * WN;
+    const int64_t m16_0 = (int64_t)mt * (WGM * WM), m16_n = (p.n + 15) / 16;
+    const int64_t S = p.kt_total / TPS;
+    const int64_t units = w.units_k;
 
-    RowCtx rc[WN];
+    // this wave's share of a stage's A fragments (whole KiB fragments)
+    const u32x4 *asrc[PER];
 #pragma unroll
-    for (int i = 0; i < WN; i++) rc[i] = row_ctx(p.w, g0 + i < groups ? g0 + i : groups - 1, lane);
+    for (int j = 0; j < PER; j++) {
+        const int f = wave + WAVES * j;
+        const int m = f / (TPS * XT), t = (f / XT) % TPS, e = f % XT;
+        int64_t mb = m16_0 + m;
+        mb = mb < m16_n ? mb : m16_n - 1;
+        asrc[j] = p.xs + ((mb * p.kt_total + t) * XT + e) * 64 + lane;
+    }
+    // this wave's weight row groups: code bases and side rows
+    const uint8_t *gb[WN];
+    int64_t srow[WN];
+#pragma unroll
+    for (int i = 0; i < WN; i++) {
+        const int64_t g = g0 + i < groups ? g0 + i : groups - 1;
+        gb[i] = w.codes + g * units * 1024;
+        srow[i] = NS ? side_row(w, g, lane) : 0;
+    }
 
-    u32x4 ar[PER];
-    auto load_a = [&](int64_t s) {
+    auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
 #pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int f = wave + WAVES * j;
-            const int m = f / (2 * XT), t = (f / XT) % 2, e = f % XT;
-            int64_t mb = m16_0 + m;
-            mb = mb < m16_n ? mb : m16_n - 1;
-            ar[j] = p.xs[((mb * p.kt_total + 2 * s + t) * XT + e) * 64 + lane];
+        for (int j = 0; j < PER; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + TPS * s * XT * 64),
+                                             (lds_void *)&As[(wave + WAVES * j) * 64], 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < WN; i++)
+#pragma unroll
+            for (int u = 0; u < NU; u++) {
+                int64_t un = s * NU + u;
+                un = un < units ? un : units - 1;  // a bf16 stage's missing second unit: decoded as zero
+                __builtin_amdgcn_global_load_lds((const void *)(gb[i] + un * 1024 + lane * 16),
+                                                 (lds_void *)&Bs[((wave * WN + i) * NU + u) * 64], 16, 0, 0);
+            }
+        if constexpr (NS > 0) {
+            if (lane < 16) {  // four lanes share a row: copy each row's word once
+#pragma unroll
+                for (int i = 0; i < WN; i++)
+#pragma unroll
+                    for (int j = 0; j < NS; j++)
+                        __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, srow[i], s, j),
+                                                         (lds_void *)&Ss[((wave * WN + i) * NS + j) * 16], 4, 0, 0);
+            }
         }
-    };
-    auto store_a = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < PER; j++) As[buf][wave + WAVES * j][lane] = ar[j];
     };
 
     floatx4 acc[WM][WN];
@@ -273,55 +296,85 @@ __global__ __launch_bounds__(WAVES * 64) void tile_gemm_kernel(TileGemmParams p)
 #pragma unroll
         for (int i = 0; i < WN; i++) acc[m][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    BSt<TF> bs[2][WN];
-    auto load_b = [&](int slot, int64_t s) {
+    copy_stage(0, As0, Bs0, Ss0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The last k tile of each stage is computed across the barrier: its A
+    // fragments and decoded weights are read into registers before the
+    // barrier (after it, other waves may overwrite the stage's buffers), and
+    // its MFMAs are issued after the next stage's first LDS reads, covering
+    // their latency.
+    u32x4 a_last[WM][XT], b_last[WN];
+    auto mfma_last = [&]() {
 #pragma unroll
-        for (int i = 0; i < WN; i++) load_stage<TF>(p.w, rc[i], s, lane, bs[slot][i]);
+        for (int m = 0; m < WM; m++)
+#pragma unroll
+            for (int e = 0; e < XT; e++)
+#pragma unroll
+                for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a_last[m][e], b_last[i], acc[m][i]);
     };
-    auto compute = [&](int buf, int slot, int64_t s) {
+    // one stage: copy stage s + 1 into the other buffers (every wave finished
+    // reading them in stage s - 1; the last stage repeats itself into the
+    // idle buffers), compute stage s, drain the copies, barrier
+    auto step = [&](int64_t s, const u32x4 *As, const u32x4 *Bs, const uint32_t *Ss, u32x4 *An, u32x4 *Bn,
+                    uint32_t *Sn, bool pending) {
+        copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
+        u32x4 c[WN][NU];
+        uint32_t sd[WN][NS1];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int i = 0; i < WN; i++) {
+#pragma unroll
+            for (int u = 0; u < NU; u++) c[i][u] = Bs[((wave * WN + i) * NU + u) * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < NS1; j++) sd[i][j] = NS ? Ss[((wave * WN + i) * NS1 + j) * 16 + (lane & 15)] : 0u;
+        }
+        const bool second = TF != TF_BF16 || 2 * s + 1 < units;
+        const u32x4 *A = As + wave_m * WM * TPS * XT * 64 + lane;
+        if (pending) mfma_last();  // the previous stage's last tile
+#pragma unroll
+        for (int t = 0; t < TPS - 1; t++) {
             u32x4 bf[WN];
-            float ts[WN];
 #pragma unroll
-            for (int i = 0; i < WN; i++) decode_stage<TF>(bs[slot][i], s, t, bf[i], ts[i]);
+            for (int i = 0; i < WN; i++) bf[i] = decode_tile_lds<TF>(w, c[i], sd[i], t, second);
+            // the activation terms of one A fragment go to WN different
+            // accumulators back to back
 #pragma unroll
             for (int m = 0; m < WM; m++) {
                 u32x4 a[XT];
 #pragma unroll
-                for (int e = 0; e < XT; e++) a[e] = As[buf][(m * 2 + t) * XT + e][lane];
+                for (int e = 0; e < XT; e++) a[e] = A[((m * TPS + t) * XT + e) * 64];
 #pragma unroll
-                for (int i = 0; i < WN; i++) mac<TF, XT>(acc[m][i], a, bf[i], bf[i], ts[i]);
+                for (int e = 0; e < XT; e++)
+#pragma unroll
+                    for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[e], bf[i], acc[m][i]);
             }
         }
+#pragma unroll
+        for (int i = 0; i < WN; i++) b_last[i] = decode_tile_lds<TF>(w, c[i], sd[i], TPS - 1, second);
+#pragma unroll
+        for (int m = 0; m < WM; m++)
+#pragma unroll
+            for (int e = 0; e < XT; e++) a_last[m][e] = A[((m * TPS + TPS - 1) * XT + e) * 64];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0);   // the last tile's LDS reads and this wave's copies of stage s + 1
+        __builtin_amdgcn_s_barrier();    // ... and every other wave's copies
+        __builtin_amdgcn_sched_barrier(0);
     };
-
-    load_a(0);
-    load_b(0, 0);
-    store_a(0);
-    if (S > 1) {
-        load_a(1);
-        load_b(1, 1);
+    int64_t s = 0;
+    bool pending = false;
+    for (; s + 1 < S; s += 2) {
+        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1, pending);
+        step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0, true);
+        pending = true;
     }
-    __syncthreads();
-    for (int64_t s = 0; s < S; s += 2) {
-        compute(0, 0, s);
-        if (s + 1 < S) store_a(1);
-        if (s + 2 < S) {
-            load_a(s + 2);
-            load_b(0, s + 2);
-        }
-        __syncthreads();
-        if (s + 1 < S) {
-            compute(1, 1, s + 1);
-            if (s + 2 < S) store_a(0);
-            if (s + 3 < S) {
-                load_a(s + 3);
-                load_b(1, s + 3);
-            }
-            __syncthreads();
-        }
+    if (s < S) {
+        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1, pending);
+        pending = true;
     }
+    if (pending) mfma_last();
 
     const int kq = lane >> 4;
 #pragma unroll
@@ -330,15 +383,17 @@ __global__ __launch_bounds__(WAVES * 64) void tile_gemm_kernel(TileGemmParams p)
         for (int i = 0; i < WN; i++) {
             int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+            for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
         }
 }
 
 // ---------------------------------------------------------------------------
 
 int64_t split_k_tiles(const TileView &w) {
+    // a whole number of pipeline stages (4 k tiles; 2 for bf16 and FP8 weights)
+    const int64_t tps = (w.tf == TF_BF16 || w.tf == TF_FP8) ? 2 : 4;
     int64_t kt = w.units_k * (unit_k_of(w.tf) / 32);
-    return (kt + 1) & ~(int64_t)1;
+    return (kt + tps - 1) / tps * tps;
 }
 
 bool tile_gemm_takes(const TileView &w, int64_t n) {
@@ -360,18 +415,22 @@ void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n,
     DITCH_TRY_HIP(hipGetLastError());
 }
 
-template <int TF, int XT, int WAVES, int WN, int WM>
+template <int TF, int XT, int WGM, int WGN, int WM, int WN>
 static void launch_tile(TileGemmParams &p, hipStream_t s) {
-    constexpr int BM = 16 * WM, BN = 16 * WN * WAVES;
+    constexpr int BM = 16 * WM * WGM, BN = 16 * WN * WGN;
     p.tiles_m = (int)((p.n + BM - 1) / BM);
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-    hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WAVES, WN, WM>), grid, dim3(WAVES * 64), 0, s, p);
+    hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WGM, WGN, WM, WN>), grid, dim3(WGM * WGN * 64), 0, s, p);
 }
 
 template <int TF, int XT>
 static void launch_tile_tf(TileGemmParams &p, hipStream_t s) {
-    launch_tile<TF, XT, 4, 4, 8>(p, s);
+    // waves side by side, each 64 tokens x 64 rows with 64 accumulator
+    // registers: 8 waves (two per SIMD, a 64 x 512 tile) where the stage
+    // buffers fit in LDS, 4 otherwise
+    if constexpr (TF == TF_BF16 || XT == 3) launch_tile<TF, XT, 1, 4, 4, 4>(p, s);
+    else launch_tile<TF, XT, 1, 8, 4, 4>(p, s);
 }
 
 void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t n, int xt,

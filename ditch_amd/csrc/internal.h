@@ -82,6 +82,12 @@ struct TileView {
     // scale blocks that cover whole 64-column stages (FP8 block_cols and
     // INT4 group multiples of 64). Set at upload; the tiled GEMM requires it.
     int32_t fast;
+    // per-row side words of the tiled GEMM (fast tensors), one 32-bit word
+    // per (row, stage entry): MXFP4 the unit's four E8M0 bytes (aliases
+    // `scale`), FP8 the scale grid as f32, INT4 the 16-bit scale bits | the
+    // zero field << 16 per group
+    const uint32_t *side;
+    int64_t side_cols;
 };
 
 // Device memory helpers (all on the context stream).
@@ -114,6 +120,7 @@ struct ditch_hip_tensor {
     void *codes = nullptr;
     void *scale = nullptr;
     void *zero = nullptr;
+    void *side = nullptr;  // owned side words (FP8, INT4); MXFP4 aliases scale
     uint64_t bytes = 0;
 };
 

@@ -339,6 +339,19 @@ __global__ void int_zero_kernel(const uint32_t *zw, uint8_t *out, int64_t rows, 
     }
 }
 
+// Side words of the tiled GEMM (TileView::side). FP8: the scale grid as f32
+// (exact for f32, f16, bf16 and finite E8M0 scales).
+__global__ void fp8_side_kernel(const void *scale, int32_t scale_type, uint32_t *out, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = f2u(load_scale(scale, i, scale_type));
+}
+
+// INT4: the 16-bit scale (f16 or bf16 bits) | zero field << 16 per (row, group).
+__global__ void int4_side_kernel(const uint16_t *scale, const uint8_t *zero, uint32_t *out, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (uint32_t)scale[i] | ((uint32_t)(zero ? zero[i] : 8u) << 16);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 
@@ -507,7 +520,8 @@ static int fast_decode_ok(const ditch_weight *w, int tf) {
         return !special && finite_scales(w->scale, w->scale_rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
     }
     case TF_INT4:
-        if (w->group % 64 != 0) return 0;
+        // the tiled GEMM's side word holds a 16-bit scale
+        if (w->group % 64 != 0 || (w->scale_dtype != DITCH_F16 && w->scale_dtype != DITCH_BF16)) return 0;
         return finite_scales(w->scale, w->rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
     default: return 0;
     }
@@ -600,6 +614,7 @@ void free_tensor(ditch_hip_tensor *t) {
     dev_free(t->codes);
     dev_free(t->scale);
     dev_free(t->zero);
+    dev_free(t->side);
     delete t;
 }
 
@@ -729,6 +744,28 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             break;
         }
         default: break;
+        }
+        DITCH_TRY_HIP(hipGetLastError());
+        // side words of the tiled GEMM
+        if (v.fast && tf == TF_MX4) {
+            v.side = (const uint32_t *)t->scale;
+            v.side_cols = v.scale_cols / 4;
+        } else if (v.fast && tf == TF_FP8) {
+            int64_t total = ((int64_t)w->scale_rows + 1) * v.scale_cols;
+            t->side = dev_alloc(total * 4);
+            t->bytes += total * 4;
+            hipLaunchKernelGGL(fp8_side_kernel, dim3(grid_for(total)), dim3(256), 0, s, t->scale, v.scale_type,
+                               (uint32_t *)t->side, total);
+            v.side = (const uint32_t *)t->side;
+            v.side_cols = v.scale_cols;
+        } else if (v.fast && tf == TF_INT4) {
+            int64_t total = pad_to(v.rows, 16) * v.scale_cols;
+            t->side = dev_alloc(total * 4);
+            t->bytes += total * 4;
+            hipLaunchKernelGGL(int4_side_kernel, dim3(grid_for(total)), dim3(256), 0, s, (const uint16_t *)t->scale,
+                               (const uint8_t *)t->zero, (uint32_t *)t->side, total);
+            v.side = (const uint32_t *)t->side;
+            v.side_cols = v.scale_cols;
         }
         DITCH_TRY_HIP(hipGetLastError());
         v.codes = (const uint8_t *)t->codes;
