@@ -302,25 +302,11 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    // The last k tile of each stage is computed across the barrier: its A
-    // fragments and decoded weights are read into registers before the
-    // barrier (after it, other waves may overwrite the stage's buffers), and
-    // its MFMAs are issued after the next stage's first LDS reads, covering
-    // their latency.
-    u32x4 a_last[WM][XT], b_last[WN];
-    auto mfma_last = [&]() {
-#pragma unroll
-        for (int m = 0; m < WM; m++)
-#pragma unroll
-            for (int e = 0; e < XT; e++)
-#pragma unroll
-                for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a_last[m][e], b_last[i], acc[m][i]);
-    };
     // one stage: copy stage s + 1 into the other buffers (every wave finished
     // reading them in stage s - 1; the last stage repeats itself into the
     // idle buffers), compute stage s, drain the copies, barrier
     auto step = [&](int64_t s, const u32x4 *As, const u32x4 *Bs, const uint32_t *Ss, u32x4 *An, u32x4 *Bn,
-                    uint32_t *Sn, bool pending) {
+                    uint32_t *Sn) {
         copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
         u32x4 c[WN][NU];
         uint32_t sd[WN][NS1];
@@ -333,9 +319,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         }
         const bool second = TF != TF_BF16 || 2 * s + 1 < units;
         const u32x4 *A = As + wave_m * WM * TPS * XT * 64 + lane;
-        if (pending) mfma_last();  // the previous stage's last tile
 #pragma unroll
-        for (int t = 0; t < TPS - 1; t++) {
+        for (int t = 0; t < TPS; t++) {
             u32x4 bf[WN];
 #pragma unroll
             for (int i = 0; i < WN; i++) bf[i] = decode_tile_lds<TF>(w, c[i], sd[i], t, second);
@@ -352,29 +337,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                     for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[e], bf[i], acc[m][i]);
             }
         }
-#pragma unroll
-        for (int i = 0; i < WN; i++) b_last[i] = decode_tile_lds<TF>(w, c[i], sd[i], TPS - 1, second);
-#pragma unroll
-        for (int m = 0; m < WM; m++)
-#pragma unroll
-            for (int e = 0; e < XT; e++) a_last[m][e] = A[((m * TPS + TPS - 1) * XT + e) * 64];
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0);   // the last tile's LDS reads and this wave's copies of stage s + 1
-        __builtin_amdgcn_s_barrier();    // ... and every other wave's copies
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's copies of stage s + 1 landed
+        __builtin_amdgcn_s_barrier();              // ... and every other wave's
         __builtin_amdgcn_sched_barrier(0);
     };
     int64_t s = 0;
-    bool pending = false;
     for (; s + 1 < S; s += 2) {
-        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1, pending);
-        step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0, true);
-        pending = true;
+        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
+        step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0);
     }
-    if (s < S) {
-        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1, pending);
-        pending = true;
-    }
-    if (pending) mfma_last();
+    if (s < S) step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
 
     const int kq = lane >> 4;
 #pragma unroll

@@ -186,6 +186,19 @@ void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_
                            int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
                            const float *delta_xa, int delta_stride, hipStream_t s);
 
+// attention.hip: prompt attention (model.zig:2935-2986) on the fp32 MFMA for
+// the head shapes it takes; q [n][heads][hd], caches [prompt][T][kvd], out
+// [n][heads][vd]
+struct AttnArgs {
+    const float *q, *kc, *vc;
+    float *out;
+    const ditch_row *rows;
+    int64_t n, heads, groups, hd, vd, T, kvd;
+    float scale;
+};
+bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups);
+void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
+
 // ops.hip
 // row_index (optional) gathers input rows out of n_src rows
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,

@@ -131,14 +131,6 @@ __global__ void qk_rope_cache_kernel(RopeArgs a) {
 // for keys 0..pos of the row's prompt, softmax (Cephes exp, tensor.zig:
 // 1181-1200), then the weighted sum of values. Output compacted to
 // [n][heads][vd] (model.zig:4338-4345).
-struct AttnArgs {
-    const float *q, *kc, *vc;
-    float *out;
-    const ditch_row *rows;
-    int64_t n, heads, groups, hd, vd, T, kvd;
-    float scale;
-};
-
 constexpr int ATT_MAXK = 1024;  // keys per row held in LDS
 
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
@@ -793,7 +785,8 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
         DITCH_TRY_HIP(hipGetLastError());
         AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale};
-        hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);
+        if (attention_mfma_takes(hd, vd, nh / nkv)) launch_attention_mfma(aa, nkv, s);
+        else hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);
         DITCH_TRY_HIP(hipGetLastError());
         mm(m, L.o, x, att, n, nullptr, 1, s);  // x += o(att)
         launch_rmsnorm(h, x, L.ffn_norm.p, L.ffn_norm.len, n, hidden, c.rms_eps, 0, s);

@@ -135,3 +135,34 @@ def test_edit_then_forward(dev, ref):
     finally:
         gm.free()
         cm.free()
+
+
+# Shapes that take the MFMA attention kernel (head dims 64/128, and MLA's
+# 192/128): several 64-key chunks, prompts that share 16-row blocks, GQA
+# groups of 4, and one query head per KV head.
+ATTN_CASES = {
+    "gqa4_hd128": (lambda: mg.dense("bf16", hidden=512, inter=512, heads=8, kv_heads=2, head_dim=128, seed=3),
+                   [130, 7, 70, 16]),
+    "gqa1_hd64": (lambda: mg.dense("mxfp4", hidden=256, inter=512, heads=4, kv_heads=4, head_dim=64, seed=4),
+                  [65, 3, 129]),
+    "mla_hd192": (lambda: mg.mla("bf16", hidden=256, heads=2, q_lora=64, kv_lora=64, nope=128, rope=64, v_dim=128,
+                                 seed=5), [100, 33]),
+}
+
+
+@pytest.mark.parametrize("name", list(ATTN_CASES))
+def test_long_prompt_attention_matches_oracle(dev, ref, name):
+    make, lens = ATTN_CASES[name]
+    spec = make()
+    tokens, rows, last = mg.batch(len(lens), lens, spec.config["vocab"], seed=11)
+    # capture every row of the last prompt as well: attention of early positions
+    cap = sorted(set(last) | set(range(len(tokens) - lens[-1], len(tokens))))
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        rg, lg = gm.forward(tokens, rows, capture_rows=cap, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=cap, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    check_parity(ref, rg, lg, rc, lc, name)
