@@ -16,6 +16,7 @@
 // 1/sum at the end. Rows of the block that belong to different prompts are
 // processed one prompt at a time.
 #include "decode.h"
+#include "gemm_common.h"
 #include "internal.h"
 
 namespace ditch {
@@ -45,7 +46,7 @@ constexpr int AK = 32;  // keys per LDS chunk
 // The k index of step j is assigned per lane group g = l/16: QK^T steps over
 // head dims g*HD/4 + j, PV steps over keys (AK/4) g + j, so every lane reads
 // contiguous runs (ds_read_b128) from padded, bank-conflict-free rows.
-template <int HD, int VD, int NW>
+template <int HD, int VD, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     constexpr int KS = HD + 4;  // K row stride (floats)
     constexpr int VS = AK + 4;  // transposed V row stride
@@ -57,6 +58,9 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     __shared__ float Vt[VD * VS];
     __shared__ float Ps[NW][16 * PS];
     __shared__ int32_t rb[16], rp[16];
+    // SPLIT: the block's finished output rows per wave, for the fragments
+    constexpr int OS = VD + 4;
+    __shared__ float Ot[SPLIT ? NW : 1][SPLIT ? 16 * OS : 1];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
@@ -69,6 +73,9 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
         int64_t r = r0 + threadIdx.x;
         rb[threadIdx.x] = r < a.n ? (int32_t)a.rows[r].b : -1;
         rp[threadIdx.x] = r < a.n ? (int32_t)a.rows[r].pos : -1;
+    }
+    if constexpr (SPLIT) {
+        for (int i = lane; i < 16 * OS; i += 64) Ot[wave][i] = 0.f;
     }
     __syncthreads();
 
@@ -227,7 +234,30 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
                 if (pos[r] < 0) continue;
                 float *orow = a.out + ((r0 + 4 * g + r) * a.heads + h) * a.vd;
 #pragma unroll
-                for (int db = 0; db < VB; db++) orow[db * 16 + c16] = __fmul_rn(o[db][r], inv[r]);
+                for (int db = 0; db < VB; db++) {
+                    const float y = __fmul_rn(o[db][r], inv[r]);
+                    orow[db * 16 + c16] = y;
+                    if constexpr (SPLIT) Ot[wave][(4 * g + r) * OS + db * 16 + c16] = y;
+                }
+            }
+        }
+    }
+    if constexpr (SPLIT) {
+        // this head's k tiles (k = h * vd + dim) of the block's 16 rows
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        if (head_ok) {
+            u32x4 *xs = (u32x4 *)a.xs;
+#pragma unroll
+            for (int kt = 0; kt < VD / 32; kt++) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = Ot[wave][c16 * OS + kt * 32 + 8 * g + j];
+                u32x4 words[2];
+                a_words<false, 2>(v, words);
+                const int64_t ktg = (h * VD) / 32 + kt;
+#pragma unroll
+                for (int e = 0; e < 2; e++) xs[(((int64_t)blockIdx.x * a.ldk + ktg) * 2 + e) * 64 + lane] = words[e];
             }
         }
     }
@@ -240,7 +270,13 @@ bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups) {
 template <int HD, int VD, int NW>
 static void launch_attn_nw(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
     dim3 grid((unsigned)((a.n + 15) / 16), (unsigned)kv_heads, (unsigned)((a.groups + NW - 1) / NW));
-    hipLaunchKernelGGL((attn_mfma_kernel<HD, VD, NW>), grid, dim3(NW * 64), 0, s, a);
+    if (a.xs) {
+        DITCH_CHECK((a.heads * VD) % 128 == 0 && a.ldk * 32 >= a.heads * VD, DITCH_INVALID_ARGUMENT,
+                    "attention: fragment output needs heads * v_head_dim a multiple of 128");
+        hipLaunchKernelGGL((attn_mfma_kernel<HD, VD, NW, true>), grid, dim3(NW * 64), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((attn_mfma_kernel<HD, VD, NW, false>), grid, dim3(NW * 64), 0, s, a);
+    }
 }
 
 // one wave per query head of the group, up to four per workgroup

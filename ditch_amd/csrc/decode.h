@@ -122,4 +122,32 @@ __device__ __forceinline__ float exp_cephes(float x_in) {
     return __fmul_rn(y, u2f((uint32_t)(e + 127) << 23));
 }
 
+// Activation.applyVec (tensor.zig:1257-1274); gelu (2) has no vector form
+// and uses Abramowitz-Stegun erf (tensor.zig:1220-1225).
+__device__ __forceinline__ float act_apply(uint32_t act, float x) {
+    switch (act) {
+    case 0: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(-x)));
+    case 1: {
+        float u = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
+        float t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(exp_cephes(__fadd_rn(u, u)), 1.0f)));
+        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, t));
+    }
+    case 2: {
+        float z = __fdiv_rn(x, 1.41421356237309504880f);
+        float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, fabsf(z))));
+        float p = __fsub_rn(__fmul_rn(1.061405429f, t), 1.453152027f);
+        p = __fadd_rn(__fmul_rn(p, t), 1.421413741f);
+        p = __fsub_rn(__fmul_rn(p, t), 0.284496736f);
+        p = __fadd_rn(__fmul_rn(p, t), 0.254829592f);
+        float y = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(p, t), expf(-__fmul_rn(z, z))));
+        float erf_v = z >= 0 ? y : -y;
+        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erf_v));
+    }
+    case 3: return fmaxf(x, 0.0f);
+    case 4: { float r = fmaxf(x, 0.0f); return __fmul_rn(r, r); }
+    case 5: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(__fmul_rn(-1.702f, x))));
+    default: return x;
+    }
+}
+
 }  // namespace ditch

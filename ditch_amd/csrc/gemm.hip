@@ -211,9 +211,10 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     if (n <= 0 || w.rows <= 0) return;
     if (ws && tile_gemm_takes(w, n)) {
         const int xt = ep.exact ? 3 : 2;
-        void *xs = ws->get<uint8_t>(split_bytes(w, n, xt));
-        launch_split(xs, x, row_index, n, w.cols, w.cols, split_k_tiles(w), xt, s);
-        launch_tile_gemm(w, out, w.rows, xs, n, xt, ep, s);
+        const int64_t ldk = split_k_tiles(w);
+        void *xs = ws->get<uint8_t>(split_bytes_ldk(n, ldk, xt));
+        launch_split(xs, x, row_index, n, w.cols, w.cols, ldk, xt, s);
+        launch_tile_gemm(w, out, w.rows, xs, ldk, n, xt, ep, s);
         return;
     }
     GemmParams p{};
@@ -231,6 +232,17 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     p.delta_stride = ep.delta_rank;
     p.segs = nullptr;
     dispatch_tf(w.tf, p, w.rows, n, 1, ep.exact != 0, s);
+}
+
+void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, const MatmulEpilogue &ep,
+                       hipStream_t s, DevBuf *ws) {
+    if (n <= 0 || w.rows <= 0) return;
+    if (x.xs && !ep.exact && tile_gemm_takes(w, n) && x.ldk >= split_k_tiles(w)) {
+        launch_tile_gemm(w, out, w.rows, x.xs, x.ldk, n, 2, ep, s);
+        return;
+    }
+    DITCH_CHECK(x.f32 != nullptr, DITCH_INVALID_ARGUMENT, "product: no f32 rows for a weight the tiled kernel does not take");
+    launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
 }
 
 void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols, int64_t max_cnt,

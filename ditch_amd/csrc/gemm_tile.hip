@@ -41,7 +41,7 @@ struct SplitParams {
     const float *x;
     const int32_t *row_index;  // optional gather of x rows
     int64_t n, ldx, K;
-    int64_t kt_total;  // k tiles per 16-token block (even)
+    int64_t kt_total;  // k tiles per 16-token block (the fragments' ldk)
     int64_t m16;       // 16-token blocks
 };
 
@@ -96,10 +96,11 @@ template <> struct TileCfg<TF_INT4> { static constexpr int TPS = 4, NU = 1, NS =
 
 // Side word of stage s, entry j, for a row whose side row starts at `base`.
 template <int TF>
-__device__ __forceinline__ const uint32_t *side_word(const TileView &w, int64_t base, int64_t s, int j) {
-    if constexpr (TF == TF_MX4) return w.side + base + s;
-    else if constexpr (TF == TF_FP8) return w.side + base + (s * 64) / w.block_cols;
-    else return w.side + base + (s * 128 + 64 * j) / w.group;
+__device__ __forceinline__ const uint32_t *side_word(const TileView &w, const uint32_t *side, int64_t base, int64_t s,
+                                                     int j) {
+    if constexpr (TF == TF_MX4) return side + base + s;
+    else if constexpr (TF == TF_FP8) return side + base + (s * 64) / w.block_cols;
+    else return side + base + (s * 128 + 64 * j) / w.group;
 }
 
 // Side row of this lane's weight row (FP8: its row of the scale grid).
@@ -161,8 +162,13 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
 
 struct TileGemmParams {
     TileView w;
+    TileView w2;            // GLU: the up projection (w is the gate)
     const u32x4 *xs;
-    int64_t kt_total;
+    int64_t kt_total;       // k tiles the product runs over
+    int64_t ldk;            // k tiles per 16-token block in xs (>= kt_total)
+    uint32_t act;           // GLU: activation code (tensor.Activation order)
+    u32x4 *xs_out;          // GLU: act(gate) * up as A fragments of the next product
+    int64_t ldk_out;
     float *out;
     int64_t ldo;
     int64_t n;
@@ -217,7 +223,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 // stage s + 1 is copied while stage s is computed, and a stage ends with
 // this wave's copies drained plus a barrier. No global load writes a
 // register inside the loop.
-template <int TF, int XT, int WGM, int WGN, int WM, int WN>
+template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU>
 __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParams p) {
     constexpr int WAVES = WGM * WGN;
     constexpr int TPS = TileCfg<TF>::TPS, NU = TileCfg<TF>::NU, NS = TileCfg<TF>::NS;
@@ -238,8 +244,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     const int wave_m = wave / WGN, wave_n = wave % WGN;
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
+    // row groups of this wave: WN of w, or (GLU) the same WN/2 output groups
+    // of the gate (w) and of the up projection (w2)
+    constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
+    static_assert(!GLU || WN % 4 == 0, "a GLU wave covers whole 32-column k tiles of its output");
     const int64_t groups = (w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)nt * (WN * WGN) + wave_n * WN;
+    const int64_t g0 = (int64_t)nt * (OG * WGN) + wave_n * OG;
     const int64_t m16_0 = (int64_t)mt * (WGM * WM), m16_n = (p.n + 15) / 16;
     const int64_t S = p.kt_total / TPS;
     const int64_t units = w.units_k;
@@ -252,16 +262,20 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         const int m = f / (TPS * XT), t = (f / XT) % TPS, e = f % XT;
         int64_t mb = m16_0 + m;
         mb = mb < m16_n ? mb : m16_n - 1;
-        asrc[j] = p.xs + ((mb * p.kt_total + t) * XT + e) * 64 + lane;
+        asrc[j] = p.xs + ((mb * p.ldk + t) * XT + e) * 64 + lane;
     }
-    // this wave's weight row groups: code bases and side rows
+    // this wave's weight row groups: code bases, side arrays and side rows
     const uint8_t *gb[WN];
+    const uint32_t *sbase[WN];
     int64_t srow[WN];
 #pragma unroll
     for (int i = 0; i < WN; i++) {
-        const int64_t g = g0 + i < groups ? g0 + i : groups - 1;
-        gb[i] = w.codes + g * units * 1024;
-        srow[i] = NS ? side_row(w, g, lane) : 0;
+        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        const int64_t gi = g0 + (i % OG);
+        const int64_t g = gi < groups ? gi : groups - 1;
+        gb[i] = wi.codes + g * units * 1024;
+        sbase[i] = wi.side;
+        srow[i] = NS ? side_row(wi, g, lane) : 0;
     }
 
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
@@ -284,7 +298,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                 for (int i = 0; i < WN; i++)
 #pragma unroll
                     for (int j = 0; j < NS; j++)
-                        __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, srow[i], s, j),
+                        __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, sbase[i], srow[i], s, j),
                                                          (lds_void *)&Ss[((wave * WN + i) * NS + j) * 16], 4, 0, 0);
             }
         }
@@ -350,14 +364,53 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     if (s < S) step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
 
     const int kq = lane >> 4;
+    if constexpr (!GLU) {
 #pragma unroll
-    for (int m = 0; m < WM; m++)
+        for (int m = 0; m < WM; m++)
 #pragma unroll
-        for (int i = 0; i < WN; i++) {
-            int64_t row = (g0 + i) * 16 + (lane & 15);
+            for (int i = 0; i < WN; i++) {
+                int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+                for (int r = 0; r < 4; r++)
+                    tile_store(p, (m16_0 + wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+            }
+    } else {
+        // act(gate) * up (tensor.gatedActivation), as f32 rows and/or as the
+        // A fragments of the next product: each 16-token block of the wave's
+        // 32-column k tile goes through a per-wave LDS patch [16][32] (the
+        // stage buffers are idle: the last stage ended with a barrier)
+        float *patch = (float *)As0 + wave * 16 * 32;
+#pragma unroll
+        for (int m = 0; m < WM; m++) {
+            const int64_t mblk = m16_0 + wave_m * WM + m;
+#pragma unroll
+            for (int i = 0; i < OG; i++) {
+                const int64_t col = (g0 + i) * 16 + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int64_t tok = mblk * 16 + 4 * kq + r;
+                    float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
+                    if (tok >= p.n || col >= w.rows) y = 0.f;
+                    else if (p.out) p.out[tok * p.ldo + col] = y;
+                    patch[(4 * kq + r) * 32 + (i & 1) * 16 + (lane & 15)] = y;
+                }
+                if ((i & 1) && p.xs_out && mblk < m16_n && ((g0 + i - 1) * 16) / 32 < p.ldk_out) {
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) v[j] = patch[(lane & 15) * 32 + 8 * kq + j];
+                    u32x4 words[2];
+                    a_words<false, 2>(v, words);
+                    const int64_t kt = ((g0 + i - 1) * 16) / 32;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) p.xs_out[((mblk * p.ldk_out + kt) * 2 + e) * 64 + lane] = words[e];
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                }
+            }
         }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -374,10 +427,6 @@ bool tile_gemm_takes(const TileView &w, int64_t n) {
     return w.tf == TF_BF16 || w.tf == TF_MX4 || w.tf == TF_FP8 || w.tf == TF_INT4;
 }
 
-size_t split_bytes(const TileView &w, int64_t n, int xt) {
-    return (size_t)((n + 15) / 16) * split_k_tiles(w) * xt * 1024;
-}
-
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
                   int64_t kt_total, int xt, hipStream_t s) {
     SplitParams sp{(u32x4 *)xs, x, row_index, n, ldx, K, kt_total, (n + 15) / 16};
@@ -388,30 +437,56 @@ void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n,
     DITCH_TRY_HIP(hipGetLastError());
 }
 
-template <int TF, int XT, int WGM, int WGN, int WM, int WN>
+template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU>
 static void launch_tile(TileGemmParams &p, hipStream_t s) {
-    constexpr int BM = 16 * WM * WGM, BN = 16 * WN * WGN;
+    constexpr int BM = 16 * WM * WGM, BN = 16 * (GLU ? WN / 2 : WN) * WGN;
     p.tiles_m = (int)((p.n + BM - 1) / BM);
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-    hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WGM, WGN, WM, WN>), grid, dim3(WGM * WGN * 64), 0, s, p);
+    hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WGM, WGN, WM, WN, GLU>), grid, dim3(WGM * WGN * 64), 0, s, p);
 }
 
-template <int TF, int XT>
+template <int TF, int XT, bool GLU>
 static void launch_tile_tf(TileGemmParams &p, hipStream_t s) {
     // waves side by side, each 64 tokens x 64 rows with 64 accumulator
     // registers: 8 waves (two per SIMD, a 64 x 512 tile) where the stage
     // buffers fit in LDS, 4 otherwise
-    if constexpr (TF == TF_BF16 || XT == 3) launch_tile<TF, XT, 1, 4, 4, 4>(p, s);
-    else launch_tile<TF, XT, 1, 8, 4, 4>(p, s);
+    if constexpr (TF == TF_BF16 || XT == 3) launch_tile<TF, XT, 1, 4, 4, 4, GLU>(p, s);
+    else launch_tile<TF, XT, 1, 8, 4, 4, GLU>(p, s);
 }
 
-void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t n, int xt,
+template <bool GLU>
+static void launch_tile_any(TileGemmParams &p, int xt, hipStream_t s) {
+    if constexpr (GLU) {  // the forward's two activation terms only
+        switch (p.w.tf) {
+        case TF_BF16: launch_tile_tf<TF_BF16, 2, true>(p, s); break;
+        case TF_MX4: launch_tile_tf<TF_MX4, 2, true>(p, s); break;
+        case TF_FP8: launch_tile_tf<TF_FP8, 2, true>(p, s); break;
+        case TF_INT4: launch_tile_tf<TF_INT4, 2, true>(p, s); break;
+        default: throw Error{DITCH_UNSUPPORTED, "tiled GLU: tile format"};
+        }
+        DITCH_TRY_HIP(hipGetLastError());
+    } else {
+        const bool x3 = xt == 3;
+        switch (p.w.tf) {
+        case TF_BF16: x3 ? launch_tile_tf<TF_BF16, 3, false>(p, s) : launch_tile_tf<TF_BF16, 2, false>(p, s); break;
+        case TF_MX4: x3 ? launch_tile_tf<TF_MX4, 3, false>(p, s) : launch_tile_tf<TF_MX4, 2, false>(p, s); break;
+        case TF_FP8: x3 ? launch_tile_tf<TF_FP8, 3, false>(p, s) : launch_tile_tf<TF_FP8, 2, false>(p, s); break;
+        case TF_INT4: x3 ? launch_tile_tf<TF_INT4, 3, false>(p, s) : launch_tile_tf<TF_INT4, 2, false>(p, s); break;
+        default: throw Error{DITCH_UNSUPPORTED, "tiled GEMM: tile format"};
+        }
+        DITCH_TRY_HIP(hipGetLastError());
+    }
+}
+
+void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t ldk, int64_t n, int xt,
                       const MatmulEpilogue &ep, hipStream_t s) {
     TileGemmParams p{};
     p.w = w;
     p.xs = (const u32x4 *)xs;
     p.kt_total = split_k_tiles(w);
+    p.ldk = ldk;
+    DITCH_CHECK(ldk >= p.kt_total, DITCH_INVALID_ARGUMENT, "tiled GEMM: activation fragments shorter than K");
     p.out = out;
     p.ldo = ldo;
     p.n = n;
@@ -421,15 +496,33 @@ void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs
     p.delta_xa = ep.delta_xa;
     p.delta_rank = ep.delta_rank;
     p.delta_stride = ep.delta_rank;
-    const bool x3 = xt == 3;
-    switch (w.tf) {
-    case TF_BF16: x3 ? launch_tile_tf<TF_BF16, 3>(p, s) : launch_tile_tf<TF_BF16, 2>(p, s); break;
-    case TF_MX4: x3 ? launch_tile_tf<TF_MX4, 3>(p, s) : launch_tile_tf<TF_MX4, 2>(p, s); break;
-    case TF_FP8: x3 ? launch_tile_tf<TF_FP8, 3>(p, s) : launch_tile_tf<TF_FP8, 2>(p, s); break;
-    case TF_INT4: x3 ? launch_tile_tf<TF_INT4, 3>(p, s) : launch_tile_tf<TF_INT4, 2>(p, s); break;
-    default: throw Error{DITCH_UNSUPPORTED, "tiled GEMM: tile format"};
-    }
-    DITCH_TRY_HIP(hipGetLastError());
+    launch_tile_any<false>(p, xt, s);
+}
+
+bool tile_glu_takes(const TileView &g, const TileView &u, int64_t n) {
+    if (!tile_gemm_takes(g, n) || !tile_gemm_takes(u, n)) return false;
+    return g.tf == u.tf && g.rows == u.rows && g.cols == u.cols && g.units_k == u.units_k &&
+           g.scale_type == u.scale_type && g.block_rows == u.block_rows && g.block_cols == u.block_cols &&
+           g.row_shard == u.row_shard && g.group == u.group && g.side_cols == u.side_cols;
+}
+
+void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xs_out,
+                     int64_t ldk_out, const void *xs, int64_t ldk, int64_t n, hipStream_t s) {
+    TileGemmParams p{};
+    p.w = gate;
+    p.w2 = up;
+    p.act = act;
+    p.xs = (const u32x4 *)xs;
+    p.kt_total = split_k_tiles(gate);
+    p.ldk = ldk;
+    DITCH_CHECK(ldk >= p.kt_total, DITCH_INVALID_ARGUMENT, "tiled GLU: activation fragments shorter than K");
+    DITCH_CHECK(!xs_out || ldk_out * 32 >= gate.rows, DITCH_INVALID_ARGUMENT, "tiled GLU: output fragments too short");
+    p.xs_out = (u32x4 *)xs_out;
+    p.ldk_out = ldk_out;
+    p.out = out;
+    p.ldo = gate.rows;
+    p.n = n;
+    launch_tile_any<true>(p, 2, s);
 }
 
 }  // namespace ditch

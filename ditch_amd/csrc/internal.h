@@ -164,14 +164,33 @@ struct MatmulEpilogue {
 void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
                    hipStream_t s, const int32_t *row_index = nullptr, DevBuf *ws = nullptr);
 
-// gemm_tile.hip: large-batch product on pre-split activation fragments
+// gemm_tile.hip: large-batch product on pre-split activation fragments.
+// Fragments of an activation [n][K] are stored [n/16][ldk][xt][64 lanes] x
+// 16 bytes; split_ldk(K) tiles per block serve every weight format with K
+// columns.
 bool tile_gemm_takes(const TileView &w, int64_t n);
-int64_t split_k_tiles(const TileView &w);  // k tiles of the fragments (even)
-size_t split_bytes(const TileView &w, int64_t n, int xt);
+int64_t split_k_tiles(const TileView &w);  // k tiles a product over w runs
+inline int64_t split_ldk(int64_t K) { return (K + 127) / 128 * 4; }
+inline size_t split_bytes_ldk(int64_t n, int64_t ldk, int xt) { return (size_t)((n + 15) / 16) * ldk * xt * 1024; }
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
-                  int64_t kt_total, int xt, hipStream_t s);
-void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t n, int xt,
+                  int64_t ldk, int xt, hipStream_t s);
+void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t ldk, int64_t n, int xt,
                       const MatmulEpilogue &ep, hipStream_t s);
+// gate/up in one product: act(x gate^T) * (x up^T) into f32 rows [n][rows]
+// (out, may be NULL) and/or the A fragments of the next product (xs_out)
+bool tile_glu_takes(const TileView &gate, const TileView &up, int64_t n);
+void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xs_out,
+                     int64_t ldk_out, const void *xs, int64_t ldk, int64_t n, hipStream_t s);
+
+// An activation [n][K] handed to a product: f32 rows, pre-split fragments
+// (xt = 2 terms, stride ldk), or both.
+struct Act {
+    const float *f32 = nullptr;
+    const void *xs = nullptr;
+    int64_t ldk = 0;
+};
+void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, const MatmulEpilogue &ep,
+                       hipStream_t s, DevBuf *ws);
 // One product per segment (routed experts): segment z multiplies rows
 // [off, off + cnt) of x (through row_index when given) by its own weight
 // into rows [off, off + cnt) of out. Every segment has rows x cols weights
@@ -195,6 +214,10 @@ struct AttnArgs {
     const ditch_row *rows;
     int64_t n, heads, groups, hd, vd, T, kvd;
     float scale;
+    // optional: the output also as the tiled GEMM's A fragments (k = head *
+    // vd + dim; heads * vd a multiple of 128)
+    void *xs;
+    int64_t ldk;
 };
 bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups);
 void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
@@ -203,6 +226,9 @@ void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
 // row_index (optional) gathers input rows out of n_src rows
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
                     float eps, int gemma, hipStream_t s, const int64_t *row_index = nullptr, int64_t n_src = 0);
+// RMS norm into the tiled GEMM's A fragments (and f32 rows when out != NULL)
+void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, const float *w, int64_t wlen, int64_t n,
+                          int64_t len, float eps, int gemma, hipStream_t s);
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
                             int64_t in_stride, int64_t out_stride, float eps, hipStream_t s);
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,

@@ -55,5 +55,6 @@ struct ditch_hip_model {
     ditch::DevBuf r_logits, r_sel, r_selw, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
         segs, segd, e_xa;
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
+    ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     ~ditch_hip_model();
 };

@@ -608,6 +608,28 @@ static void mm(ditch_hip_model *m, const Mat &mt, float *out, const float *x, in
     launch_matmul(mt.t->v, out, x, n, ep, s, nullptr, &m->xsplit);
 }
 
+// The same on an activation that may come as pre-split A fragments (the
+// delta's x A^T needs the f32 rows).
+static void mm_act(ditch_hip_model *m, const Mat &mt, float *out, const Act &x, int64_t n, const float *bias,
+                   int accumulate, hipStream_t s) {
+    DITCH_CHECK(mt.ok(), DITCH_INVALID_ARGUMENT, "forward: a weight slot is empty");
+    MatmulEpilogue ep;
+    ep.bias = bias;
+    ep.accumulate = accumulate;
+    if (mt.rank > 0) {
+        DITCH_CHECK(x.f32, DITCH_INVALID_ARGUMENT, "forward: a delta needs the f32 activation");
+        float *xa = m->xa.get<float>((size_t)n * mt.rank);
+        launch_delta_xa(xa, x.f32, mt.da, n, mt.t->v.cols, mt.rank, s);
+        ep.delta_b = mt.db;
+        ep.delta_xa = xa;
+        ep.delta_rank = mt.rank;
+    }
+    launch_matmul_act(mt.t->v, out, x, n, ep, s, &m->xsplit);
+}
+
+// Whether the tiled product takes `mt` with fragments alone (no f32 rows).
+static bool frag_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && tile_gemm_takes(mt.t->v, n); }
+
 // Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).
 static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, int64_t n, hipStream_t s) {
     const ditch_model_config &c = m->c;
@@ -731,9 +753,23 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         DITCH_TRY_HIP(hipGetLastError());
     };
     capture(0);
+    // Large batches hand the products pre-split A fragments written by the
+    // producing kernel (RMS norm, attention, the gate/up product); f32 rows
+    // are kept only for consumers that need them.
+    const bool frags = n >= 128;
+    const int64_t ldk_h = split_ldk(hidden);
     for (int64_t li = 0; li < (int64_t)c.layers; li++) {
         Layer &L = m->layers[li];
-        launch_rmsnorm(h, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
+        Act hact{h, nullptr, 0};
+        if (frags) {
+            const bool f32_needed = c.mla || !frag_only(L.q, n) || !frag_only(L.k, n) || !frag_only(L.v, n);
+            void *hs = m->hs.get<uint8_t>(split_bytes_ldk(n, ldk_h, 2));
+            launch_rmsnorm_split(hs, ldk_h, f32_needed ? h : nullptr, x, L.attn_norm.p, L.attn_norm.len, n, hidden,
+                                 c.rms_eps, 0, s);
+            hact = Act{f32_needed ? h : nullptr, hs, ldk_h};
+        } else {
+            launch_rmsnorm(h, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
+        }
         if (c.mla) {
             int64_t nope = (int64_t)c.qk_nope_dim, rd = (int64_t)c.qk_rope_dim, kvl = (int64_t)c.kv_lora_rank;
             if (L.q_a.ok()) {
@@ -755,9 +791,9 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
                                nh, hd, nope, rd, vd, kvl);
             DITCH_TRY_HIP(hipGetLastError());
         } else {
-            mm(m, L.q, q, h, n, L.q_bias.p, 0, s);
-            mm(m, L.k, kk, h, n, L.k_bias.p, 0, s);
-            mm(m, L.v, vv, h, n, L.v_bias.p, 0, s);
+            mm_act(m, L.q, q, hact, n, L.q_bias.p, 0, s);
+            mm_act(m, L.k, kk, hact, n, L.k_bias.p, 0, s);
+            mm_act(m, L.v, vv, hact, n, L.v_bias.p, 0, s);
         }
         RopeArgs ra{};
         ra.q = q;
@@ -784,13 +820,35 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         ra.style = c.rope_style;
         hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
         DITCH_TRY_HIP(hipGetLastError());
-        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale};
-        if (attention_mfma_takes(hd, vd, nh / nkv)) launch_attention_mfma(aa, nkv, s);
+        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0};
+        const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
+        Act aact{att, nullptr, 0};
+        if (frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n)) {
+            aa.ldk = split_ldk(nh * vd);
+            aa.xs = m->atts.get<uint8_t>(split_bytes_ldk(n, aa.ldk, 2));
+            aact = Act{att, aa.xs, aa.ldk};
+        }
+        if (mfma_attn) launch_attention_mfma(aa, nkv, s);
         else hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);
         DITCH_TRY_HIP(hipGetLastError());
-        mm(m, L.o, x, att, n, nullptr, 1, s);  // x += o(att)
+        mm_act(m, L.o, x, aact, n, nullptr, 1, s);  // x += o(att)
+        const bool moe_layer = c.n_experts && m->moe_layers[li];
+        // gate and up in one tiled product whose epilogue applies the
+        // activation and writes the down projection's fragments
+        const bool glu = frags && !moe_layer && L.gate.ok() && L.up.ok() && L.gate.rank == 0 && L.up.rank == 0 &&
+                         tile_glu_takes(L.gate.t->v, L.up.t->v, n) && frag_only(L.down, n);
+        if (glu) {
+            void *hs = m->hs.get<uint8_t>(split_bytes_ldk(n, ldk_h, 2));
+            launch_rmsnorm_split(hs, ldk_h, nullptr, x, L.ffn_norm.p, L.ffn_norm.len, n, hidden, c.rms_eps, 0, s);
+            const int64_t inter = L.gate.t->v.rows, ldk_i = split_ldk(inter);
+            void *as = m->acts.get<uint8_t>(split_bytes_ldk(n, ldk_i, 2));
+            launch_tile_glu(L.gate.t->v, L.up.t->v, 0, nullptr, as, ldk_i, hs, ldk_h, n, s);
+            mm_act(m, L.down, x, Act{nullptr, as, ldk_i}, n, nullptr, 1, s);  // x += down(act)
+            capture(li + 1);
+            continue;
+        }
         launch_rmsnorm(h, x, L.ffn_norm.p, L.ffn_norm.len, n, hidden, c.rms_eps, 0, s);
-        if (c.n_experts && m->moe_layers[li]) {
+        if (moe_layer) {
             moe_forward(m, L, x, h, n, s);
         } else {
             int64_t inter = L.gate.t ? L.gate.t->v.rows : 0;

@@ -3,6 +3,7 @@
 // W^T y over resident weights (tensor.zig:1056-1122).
 #include "decode.h"
 #include "internal.h"
+#include "gemm_common.h"
 #include "tiled.h"
 
 namespace ditch {
@@ -56,34 +57,6 @@ __device__ __forceinline__ float block_max(float v, float *sh) {
     return block_reduce(v, [](float a, float b) { return fmaxf(a, b); }, sh);
 }
 
-// ---------------------------------------------------------------------------
-// Activation.applyVec (tensor.zig:1257-1274); gelu (2) has no vector form
-// and uses Abramowitz-Stegun erf (tensor.zig:1220-1225).
-__device__ float act_apply(uint32_t act, float x) {
-    switch (act) {
-    case 0: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(-x)));
-    case 1: {
-        float u = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
-        float t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(exp_cephes(__fadd_rn(u, u)), 1.0f)));
-        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, t));
-    }
-    case 2: {
-        float z = __fdiv_rn(x, 1.41421356237309504880f);
-        float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, fabsf(z))));
-        float p = __fsub_rn(__fmul_rn(1.061405429f, t), 1.453152027f);
-        p = __fadd_rn(__fmul_rn(p, t), 1.421413741f);
-        p = __fsub_rn(__fmul_rn(p, t), 0.284496736f);
-        p = __fadd_rn(__fmul_rn(p, t), 0.254829592f);
-        float y = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(p, t), expf(-__fmul_rn(z, z))));
-        float erf_v = z >= 0 ? y : -y;
-        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erf_v));
-    }
-    case 3: return fmaxf(x, 0.0f);
-    case 4: { float r = fmaxf(x, 0.0f); return __fmul_rn(r, r); }
-    case 5: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(__fmul_rn(-1.702f, x))));
-    default: return x;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm / LayerNorm rows (tensor.zig:1167-1179, 1343-1358): one block per
@@ -106,6 +79,90 @@ __global__ void rmsnorm_kernel(float *out, const float *x, const float *w, int64
         float v = __fmul_rn(xr[i], inv);
         if (wlen > 0) v = __fmul_rn(v, gemma ? __fadd_rn(1.0f, w[i]) : w[i]);
         o[i] = v;
+    }
+}
+
+// RMS norm of rows (tensor.zig:1167-1179) written straight into the tiled
+// GEMM's two-term bf16 A fragments ([n/16][ldk][2][64 lanes] x 16 bytes,
+// columns past len are zero) and, when `out` is given, as f32 rows too. One
+// block per 16 rows: the inverse RMS of each row first (a wave per 4 rows),
+// then one (k tile, lane) fragment word pair per thread step.
+__global__ __launch_bounds__(256) void rmsnorm_split_kernel(u32x4 *xs, int64_t ldk, float *out, const float *x,
+                                                            const float *w, int64_t wlen, int64_t len, float eps,
+                                                            int gemma, int64_t n) {
+    __shared__ float inv_s[16];
+    const int64_t m16 = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool vec = (len % 4) == 0;  // rows of whole float4s (the bases are 16-byte aligned)
+    for (int rr = 0; rr < 4; rr++) {
+        const int row = wave * 4 + rr;
+        const int64_t r = m16 * 16 + row;
+        float ss = 0.f;
+        if (r < n) {
+            const float *xr = x + r * len;
+            if (vec) {
+                for (int64_t i = 4 * lane; i < len; i += 256) {
+                    float4 v = *(const float4 *)(xr + i);
+                    ss = __builtin_fmaf(v.x, v.x, ss);
+                    ss = __builtin_fmaf(v.y, v.y, ss);
+                    ss = __builtin_fmaf(v.z, v.z, ss);
+                    ss = __builtin_fmaf(v.w, v.w, ss);
+                }
+            } else {
+                for (int64_t i = lane; i < len; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+        if (lane == 0)
+            inv_s[row] = r < n ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps))) : 0.f;
+    }
+    __syncthreads();
+    for (int64_t q = threadIdx.x; q < ldk * 64; q += 256) {
+        const int64_t kt = q >> 6;
+        const int l = (int)(q & 63), row = l & 15;
+        const int64_t r = m16 * 16 + row;
+        const int64_t k0 = kt * 32 + 8 * (l >> 4);
+        const float inv = inv_s[row];
+        float xv[8], wv[8];
+        if (r < n && vec && k0 + 8 <= len) {
+            float4 a = *(const float4 *)(x + r * len + k0), b = *(const float4 *)(x + r * len + k0 + 4);
+            xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = (r < n && k0 + j < len) ? x[r * len + k0 + j] : 0.f;
+        }
+        if (wlen > 0 && (wlen % 4) == 0 && k0 + 8 <= wlen) {
+            float4 a = *(const float4 *)(w + k0), b = *(const float4 *)(w + k0 + 4);
+            wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w; wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) wv[j] = (wlen > 0 && k0 + j < wlen) ? w[k0 + j] : 1.f;
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float y = 0.f;
+            if (r < n && k0 + j < len) {
+                y = __fmul_rn(xv[j], inv);
+                if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wv[j]) : wv[j]);
+            }
+            v[j] = y;
+        }
+        if (out && r < n) {
+            if (vec && k0 + 8 <= len) {
+                *(float4 *)(out + r * len + k0) = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(out + r * len + k0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (k0 + j < len) out[r * len + k0 + j] = v[j];
+            }
+        }
+        u32x4 words[2];
+        a_words<false, 2>(v, words);
+        xs[((m16 * ldk + kt) * 2 + 0) * 64 + l] = words[0];
+        xs[((m16 * ldk + kt) * 2 + 1) * 64 + l] = words[1];
     }
 }
 
@@ -306,6 +363,14 @@ void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, in
     if (n <= 0) return;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, gemma, row_index,
                        row_index ? n_src : n, len, len);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, const float *w, int64_t wlen, int64_t n,
+                          int64_t len, float eps, int gemma, hipStream_t s) {
+    if (n <= 0) return;
+    DITCH_CHECK(ldk * 32 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split: fragments shorter than the row");
+    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (u32x4 *)xs, ldk, out, x,
+                       w, wlen, len, eps, gemma, n);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
