@@ -325,6 +325,35 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x, u
     });
 }
 
+uint64_t ditch_hip_frag_bytes(uint64_t n, uint64_t k) { return split_bytes_ldk((int64_t)n, split_ldk((int64_t)k), 2); }
+
+int32_t ditch_hip_split_device(ditch_hip *h, void *d_frags, uint64_t frag_bytes, const float *d_x, uint64_t n,
+                               uint64_t k, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_frags && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0) return;
+        DITCH_CHECK(frag_bytes >= ditch_hip_frag_bytes(n, k), DITCH_INVALID_ARGUMENT, "split: fragment buffer too small");
+        launch_split(d_frags, d_x, nullptr, (int64_t)n, (int64_t)k, (int64_t)k, split_ldk((int64_t)k), 2,
+                     stream ? (hipStream_t)stream : h->stream);
+    });
+}
+
+int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, const void *d_frags, uint64_t n,
+                                       const ditch_hip_tensor *w, const float *d_bias, int32_t accumulate,
+                                       void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && d_out && d_frags, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0) return;
+        DITCH_CHECK(tile_gemm_takes(w->v, (int64_t)n), DITCH_UNSUPPORTED,
+                    "matmulT_frags: the large-batch product does not take this weight or batch");
+        MatmulEpilogue ep;
+        ep.bias = d_bias;
+        ep.accumulate = accumulate;
+        launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep,
+                         stream ? (hipStream_t)stream : h->stream);
+    });
+}
+
 // ---------------------------------------------------------------------------
 // Model
 

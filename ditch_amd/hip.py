@@ -146,6 +146,13 @@ class Device:
         self.check(self.lib.ditch_hip_dequant(self.h, _p(out), w.ref(), row0, nrows))
         return out
 
+    def frag_bytes(self, n, k):
+        return self.lib.ditch_hip_frag_bytes(n, k)
+
+    def split_device(self, d_frags, frag_bytes, d_x, n, k, stream=None):
+        """Writes the activation fragments of d_x [n][k] (device f32)."""
+        self.check(self.lib.ditch_hip_split_device(self.h, d_frags, frag_bytes, d_x, n, k, stream))
+
     def upload(self, w: HostWeight):
         t = self.lib.ditch_hip_upload(self.h, w.ref())
         if not t:
@@ -192,6 +199,11 @@ class Tensor:
     def matmul_device(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None):
         self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, d_x, n, self.handle, d_bias,
                                                              int(accumulate), stream))
+
+    def matmul_frags_device(self, d_out, d_frags, n, d_bias=None, accumulate=False, stream=None):
+        """The large-batch product on activation fragments (ditch_hip_split_device)."""
+        self.dev.check(self.dev.lib.ditch_hip_matmulT_frags_device(self.dev.h, d_out, d_frags, n, self.handle, d_bias,
+                                                                   int(accumulate), stream))
 
     def dequant_device(self, d_out, out_bytes, row0, nrows):
         self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, out_bytes, self.handle, row0, nrows))

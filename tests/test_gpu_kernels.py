@@ -285,6 +285,41 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("kind,n,rows,cols", [("bf16", 200, 136, 576), ("fp8", 130, 520, 576),
+                                               ("mxfp4", 256, 520, 640), ("int4", 321, 72, 1024)])
+def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
+    """ditch_hip_split_device + ditch_hip_matmulT_frags_device run the same
+    tiled product as ditch_hip_matmulT_device on large batches: bit-identical
+    outputs, bias and accumulate included (K padded past the product's own
+    stage count, ragged token count)."""
+    from ditch_amd import hipmem
+    from ditch_amd.hip import DeviceError
+    rng = np.random.default_rng(13)
+    w = wg.make(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    prior = rng.standard_normal((n, rows)).astype(np.float32)
+    fb = dev.frag_bytes(n, cols)
+    assert fb == -(-n // 16) * (-(-cols // 128) * 4) * 2 * 1024
+    t = dev.upload(w)
+    try:
+        bx, bb = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias)
+        o1, o2 = hipmem.Buffer.from_array(prior), hipmem.Buffer.from_array(prior)
+        xs = hipmem.Buffer(fb)
+        t.matmul_device(o1.ptr, bx.ptr, n, d_bias=bb.ptr, accumulate=True)
+        dev.split_device(xs.ptr, fb, bx.ptr, n, cols)
+        t.matmul_frags_device(o2.ptr, xs.ptr, n, d_bias=bb.ptr, accumulate=True)
+        dev.sync()
+        a, b = o1.download(np.float32, (n, rows)), o2.download(np.float32, (n, rows))
+        with pytest.raises(DeviceError, match="too small"):
+            dev.split_device(xs.ptr, fb - 1, bx.ptr, n, cols)
+        with pytest.raises(DeviceError, match="Unsupported"):
+            t.matmul_frags_device(o2.ptr, xs.ptr, 64)
+    finally:
+        t.free()
+    assert np.array_equal(a, b)
+
+
 def test_matmulT_large_batch_nan_scale_takes_the_exact_decoder(dev, ref):
     """An E8M0 scale byte 255 (NaN block, dequant.zig:259-261) keeps the
     tensor off the conversion instructions; the NaN rows match the oracle."""
