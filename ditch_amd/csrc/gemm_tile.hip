@@ -18,12 +18,15 @@
 // 64 rows per wave (64 accumulator registers, two waves per SIMD). A stage
 // covers 64 or 128 k: its A fragments, each wave's weight codes (1 KiB units
 // of 16 rows) and per-row side words (scales) are copied global -> LDS with
-// global_load_lds (no registers, double buffered), then every wave decodes
+// global_load_lds (no registers, double buffered; with two waves per SIMD
+// only the younger wave of each SIMD issues them), then every wave decodes
 // its weight tiles with v_cvt_scalef32_pk_bf16_fp4 (MXFP4), v_cvt_pk_f32_fp8
 // + f32 scale + v_cvt_pk_bf16_f32 (FP8) or integer unpacking (INT4) and
-// issues the MFMAs. The block index is remapped so that the workgroups an
-// XCD runs at the same time cover an 8 x (few) patch of output tiles: they
-// share A and W tiles in that XCD's L2.
+// issues the MFMAs, reading k tile t + 1's A fragments and decoding its
+// weights between k tile t's MFMAs (the order is fixed with
+// sched_group_barrier). The block index is remapped so that the workgroups
+// an XCD runs at the same time cover an 8 x (few) patch of output tiles:
+// they share A and W tiles in that XCD's L2.
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -146,8 +149,10 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
     } else if constexpr (TF == TF_INT4) {
         const uint32_t word = sd[t >> 1];
         const uint32_t bits = word & 0xffffu;
-        // the scale's own dtype, widened exactly
-        const float sc = w.scale_type == SC_BF16 ? u2f(bits << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+        // the scale's own dtype, widened exactly (both widenings, then a
+        // select: no branch inside the product loop)
+        const float sc_bf = u2f(bits << 16), sc_h = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+        const float sc = w.scale_type == SC_BF16 ? sc_bf : sc_h;
         const int32_t zf = (int32_t)(word >> 16);
         const uint32_t wd = c[0][t];
         float v[8];
@@ -229,14 +234,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     constexpr int TPS = TileCfg<TF>::TPS, NU = TileCfg<TF>::NU, NS = TileCfg<TF>::NS;
     constexpr int NS1 = NS ? NS : 1;
     constexpr int FR = WGM * WM * TPS * XT;  // A fragments per stage: [m][t][term]
-    constexpr int PER = FR / WAVES;          // fragments each wave copies per stage
-    static_assert(FR % WAVES == 0, "stage fragments must split evenly over the waves");
     // two stage buffers as distinct LDS objects, so that the compiler can
     // tell the DMA into one from the reads of the other (with one array it
     // waits for every copy in flight before any LDS read)
     __shared__ u32x4 As0[FR * 64], As1[FR * 64];                            // [fragment][lane]
     __shared__ u32x4 Bs0[WAVES * WN * NU * 64], Bs1[WAVES * WN * NU * 64];  // [wave][group][unit][lane]
-    __shared__ uint32_t Ss0[WAVES * WN * NS1 * 16], Ss1[WAVES * WN * NS1 * 16];  // [wave][group][entry][row]
+    __shared__ uint32_t Ss0[WAVES * NS1 * 64], Ss1[WAVES * NS1 * 64];        // [wave][entry][group][row]
 
     const TileView &w = p.w;
     const int lane = threadIdx.x & 63;
@@ -254,52 +257,64 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     const int64_t S = p.kt_total / TPS;
     const int64_t units = w.units_k;
 
-    // this wave's share of a stage's A fragments (whole KiB fragments)
-    const u32x4 *asrc[PER];
+    // Copies: a global_load_lds stalls the issuing wave while the texture
+    // unit's queue is full, so with two waves per SIMD only the younger one
+    // (waves WAVES/2.., which the issue arbiter serves after the older one)
+    // issues the copies of a stage, and the older waves run their products
+    // undisturbed. With one wave per SIMD every wave copies its share.
+    constexpr int CW = WAVES >= 8 ? WAVES / 2 : WAVES;  // copying waves
+    constexpr int CA = FR / CW, CB = WAVES * WN * NU / CW, CS = NS ? WAVES * NS / CW : 0;
+    static_assert(FR % CW == 0 && (WAVES * WN * NU) % CW == 0 && (WAVES * NS) % CW == 0, "copies split evenly");
+    static_assert(WN == 4, "one side-word copy covers a wave's four row groups");
+    const bool copier = wave >= WAVES - CW;
+    const int ck = copier ? wave - (WAVES - CW) : 0;
+    const u32x4 *asrc[CA];
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int f = wave + WAVES * j;
+    for (int j = 0; j < CA; j++) {
+        const int f = ck + CW * j;
         const int m = f / (TPS * XT), t = (f / XT) % TPS, e = f % XT;
         int64_t mb = m16_0 + m;
         mb = mb < m16_n ? mb : m16_n - 1;
         asrc[j] = p.xs + ((mb * p.ldk + t) * XT + e) * 64 + lane;
     }
-    // this wave's weight row groups: code bases, side arrays and side rows
-    const uint8_t *gb[WN];
-    const uint32_t *sbase[WN];
-    int64_t srow[WN];
+    auto group_of = [&](int wq, int i) {
+        const int64_t gi = (int64_t)nt * (OG * WGN) + (wq % WGN) * OG + (i % OG);
+        return gi < groups ? gi : groups - 1;
+    };
+    const uint8_t *bsrc[CB];
 #pragma unroll
-    for (int i = 0; i < WN; i++) {
+    for (int j = 0; j < CB; j++) {
+        const int q = ck + CW * j, wq = q / (WN * NU), i = (q / NU) % WN;
         const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
-        const int64_t gi = g0 + (i % OG);
-        const int64_t g = gi < groups ? gi : groups - 1;
-        gb[i] = wi.codes + g * units * 1024;
-        sbase[i] = wi.side;
-        srow[i] = NS ? side_row(wi, g, lane) : 0;
+        bsrc[j] = wi.codes + group_of(wq, i) * units * 1024 + lane * 16;
+    }
+    const uint32_t *ssrc[CS > 0 ? CS : 1];
+#pragma unroll
+    for (int j = 0; j < CS; j++) {
+        const int q = ck + CW * j, wq = q / NS1, i = lane >> 4;  // lane l: row l % 16 of row group l / 16
+        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        ssrc[j] = wi.side + side_row(wi, group_of(wq, i), lane);
     }
 
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
+        if (!copier) return;
 #pragma unroll
-        for (int j = 0; j < PER; j++)
+        for (int j = 0; j < CA; j++)
             __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + TPS * s * XT * 64),
-                                             (lds_void *)&As[(wave + WAVES * j) * 64], 16, 0, 0);
+                                             (lds_void *)&As[(ck + CW * j) * 64], 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < WN; i++)
-#pragma unroll
-            for (int u = 0; u < NU; u++) {
-                int64_t un = s * NU + u;
-                un = un < units ? un : units - 1;  // a bf16 stage's missing second unit: decoded as zero
-                __builtin_amdgcn_global_load_lds((const void *)(gb[i] + un * 1024 + lane * 16),
-                                                 (lds_void *)&Bs[((wave * WN + i) * NU + u) * 64], 16, 0, 0);
-            }
+        for (int j = 0; j < CB; j++) {
+            const int q = ck + CW * j, u = q % NU;
+            int64_t un = s * NU + u;
+            un = un < units ? un : units - 1;  // a bf16 stage's missing second unit: decoded as zero
+            __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + un * 1024), (lds_void *)&Bs[q * 64], 16, 0, 0);
+        }
         if constexpr (NS > 0) {
-            if (lane < 16) {  // four lanes share a row: copy each row's word once
 #pragma unroll
-                for (int i = 0; i < WN; i++)
-#pragma unroll
-                    for (int j = 0; j < NS; j++)
-                        __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, sbase[i], srow[i], s, j),
-                                                         (lds_void *)&Ss[((wave * WN + i) * NS + j) * 16], 4, 0, 0);
+            for (int j = 0; j < CS; j++) {
+                const int q = ck + CW * j;
+                __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, ssrc[j], 0, s, q % NS1),
+                                                 (lds_void *)&Ss[q * 64], 4, 0, 0);
             }
         }
     };
@@ -316,12 +331,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    // one stage: copy stage s + 1 into the other buffers (every wave finished
-    // reading them in stage s - 1; the last stage repeats itself into the
-    // idle buffers), compute stage s, drain the copies, barrier
+    // one stage: the copying waves copy stage s + 1 into the other buffers
+    // (every wave finished reading them in stage s - 1; the last stage
+    // repeats itself into the idle buffers), every wave computes stage s,
+    // drains its copies and meets the others at the barrier
     auto step = [&](int64_t s, const u32x4 *As, const u32x4 *Bs, const uint32_t *Ss, u32x4 *An, u32x4 *Bn,
                     uint32_t *Sn) {
         copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 c[WN][NU];
         uint32_t sd[WN][NS1];
 #pragma unroll
@@ -329,26 +346,61 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
             for (int u = 0; u < NU; u++) c[i][u] = Bs[((wave * WN + i) * NU + u) * 64 + lane];
 #pragma unroll
-            for (int j = 0; j < NS1; j++) sd[i][j] = NS ? Ss[((wave * WN + i) * NS1 + j) * 16 + (lane & 15)] : 0u;
+            for (int j = 0; j < NS1; j++) sd[i][j] = NS ? Ss[(wave * NS1 + j) * 64 + i * 16 + (lane & 15)] : 0u;
         }
         const bool second = TF != TF_BF16 || 2 * s + 1 < units;
         const u32x4 *A = As + wave_m * WM * TPS * XT * 64 + lane;
+        // k tile t + 1's A fragments are read and its weight tiles decoded
+        // while k tile t's products issue (two register sets)
+        u32x4 a[2][WM][XT], bf[2][WN];
+#pragma unroll
+        for (int m = 0; m < WM; m++)
+#pragma unroll
+            for (int e = 0; e < XT; e++) a[0][m][e] = A[(m * TPS * XT + e) * 64];
+#pragma unroll
+        for (int i = 0; i < WN; i++) bf[0][i] = decode_tile_lds<TF>(w, c[i], sd[i], 0, second);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < TPS; t++) {
-            u32x4 bf[WN];
+            const int cu = t & 1, nx = cu ^ 1;
+            if (t + 1 < TPS) {
 #pragma unroll
-            for (int i = 0; i < WN; i++) bf[i] = decode_tile_lds<TF>(w, c[i], sd[i], t, second);
-            // the activation terms of one A fragment go to WN different
-            // accumulators back to back
+                for (int m = 0; m < WM; m++)
 #pragma unroll
-            for (int m = 0; m < WM; m++) {
-                u32x4 a[XT];
+                    for (int e = 0; e < XT; e++) a[nx][m][e] = A[((m * TPS + t + 1) * XT + e) * 64];
+            }
 #pragma unroll
-                for (int e = 0; e < XT; e++) a[e] = A[((m * TPS + t) * XT + e) * 64];
+            for (int m = 0; m < WM; m++)
 #pragma unroll
                 for (int e = 0; e < XT; e++)
 #pragma unroll
-                    for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[e], bf[i], acc[m][i]);
+                    for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[cu][m][e], bf[cu][i], acc[m][i]);
+            if (t + 1 < TPS) {
+#pragma unroll
+                for (int i = 0; i < WN; i++) bf[nx][i] = decode_tile_lds<TF>(w, c[i], sd[i], t + 1, second);
+            }
+        }
+        // issue order: each k tile's products interleaved with the next k
+        // tile's A reads (one per product), then with its weight decode
+        // VALU per product: roughly the decode's instruction count per k tile
+        // over the products left after the A reads
+        constexpr int NA = WM * XT, NM = WM * XT * WN, NV = NM - NA;
+        constexpr int VPM = TF == TF_BF16 ? 1 : TF == TF_MX4 ? 2 : TF == TF_FP8 ? 3 : 4;
+#pragma unroll
+        for (int t = 0; t < TPS; t++) {
+            if (t + 1 < TPS) {
+#pragma unroll
+                for (int j = 0; j < NA; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < NV; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
