@@ -134,9 +134,9 @@ def time_matmul(dev, tensor, n, k, reps, frags=False):
     x = hipmem.Buffer.from_array(rng.standard_normal((n, k)).astype(np.float32))
     out = hipmem.Buffer(n * tensor.rows * 4)
     if frags:
-        fb = dev.frag_bytes(n, k)
+        fb = tensor.frag_bytes(n)
         xs = hipmem.Buffer(fb)
-        dev.split_device(xs.ptr, fb, x.ptr, n, k)
+        tensor.split_device(xs.ptr, fb, x.ptr, n)
 
         def launch():
             tensor.matmul_frags_device(out.ptr, xs.ptr, n)

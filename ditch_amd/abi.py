@@ -150,8 +150,8 @@ PROTOTYPES = {
     "ditch_hip_tensor_bytes": (U64, [P]),
     "ditch_hip_tensor_dequant": (I32, [P, P, U64, P, U64, U64]),
     "ditch_hip_matmulT_device": (I32, [P, P, P, U64, P, P, I32, P]),
-    "ditch_hip_frag_bytes": (U64, [U64, U64]),
-    "ditch_hip_split_device": (I32, [P, P, U64, P, U64, U64, P]),
+    "ditch_hip_frag_bytes": (U64, [P, U64]),
+    "ditch_hip_split_device": (I32, [P, P, U64, P, U64, P, P]),
     "ditch_hip_matmulT_frags_device": (I32, [P, P, P, U64, P, P, I32, P]),
     "ditch_hip_model_create": (P, [P, P]),
     "ditch_hip_model_free": (None, [P]),

@@ -325,16 +325,37 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x, u
     });
 }
 
-uint64_t ditch_hip_frag_bytes(uint64_t n, uint64_t k) { return split_bytes_ldk((int64_t)n, split_ldk((int64_t)k), 2); }
+// fragment layout of the large-batch product over w: 2 = bf16 terms, 1 = MX
+// fp6 terms, 0 = none
+static int frag_kind(const TileView &w, int64_t n) {
+    if (mx_gemm_takes(w, n)) return 1;
+    if (tile_gemm_takes(w, n)) return 2;
+    return 0;
+}
+
+uint64_t ditch_hip_frag_bytes(const ditch_hip_tensor *w, uint64_t n) {
+    if (!w || n == 0) return 0;
+    switch (frag_kind(w->v, (int64_t)n)) {
+    case 1: return mx_frag_bytes((int64_t)n, w->v.units_k);
+    case 2: return split_bytes_ldk((int64_t)n, split_ldk(w->v.cols), 2);
+    default: return 0;
+    }
+}
 
 int32_t ditch_hip_split_device(ditch_hip *h, void *d_frags, uint64_t frag_bytes, const float *d_x, uint64_t n,
-                               uint64_t k, void *stream) {
+                               const ditch_hip_tensor *w, void *stream) {
     return guarded(h, [&] {
-        DITCH_CHECK(d_frags && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        DITCH_CHECK(d_frags && d_x && w, DITCH_INVALID_ARGUMENT, "NULL argument");
         if (n == 0) return;
-        DITCH_CHECK(frag_bytes >= ditch_hip_frag_bytes(n, k), DITCH_INVALID_ARGUMENT, "split: fragment buffer too small");
-        launch_split(d_frags, d_x, nullptr, (int64_t)n, (int64_t)k, (int64_t)k, split_ldk((int64_t)k), 2,
-                     stream ? (hipStream_t)stream : h->stream);
+        const uint64_t need = ditch_hip_frag_bytes(w, n);
+        DITCH_CHECK(need > 0, DITCH_UNSUPPORTED, "split: the large-batch product does not take this weight or batch");
+        DITCH_CHECK(frag_bytes >= need, DITCH_INVALID_ARGUMENT, "split: fragment buffer too small");
+        const TileView &v = w->v;
+        hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+        if (frag_kind(v, (int64_t)n) == 1)
+            launch_split_mx(d_frags, d_x, nullptr, (int64_t)n, v.cols, v.cols, v.units_k, s);
+        else
+            launch_split(d_frags, d_x, nullptr, (int64_t)n, v.cols, v.cols, split_ldk(v.cols), 2, s);
     });
 }
 
@@ -344,13 +365,17 @@ int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, const void *d
     return guarded(h, [&] {
         DITCH_CHECK(w && d_out && d_frags, DITCH_INVALID_ARGUMENT, "NULL argument");
         if (n == 0) return;
-        DITCH_CHECK(tile_gemm_takes(w->v, (int64_t)n), DITCH_UNSUPPORTED,
+        const int kind = frag_kind(w->v, (int64_t)n);
+        DITCH_CHECK(kind != 0, DITCH_UNSUPPORTED,
                     "matmulT_frags: the large-batch product does not take this weight or batch");
         MatmulEpilogue ep;
         ep.bias = d_bias;
         ep.accumulate = accumulate;
-        launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep,
-                         stream ? (hipStream_t)stream : h->stream);
+        hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+        if (kind == 1)
+            launch_mx_gemm(w->v, d_out, w->v.rows, d_frags, w->v.units_k, (int64_t)n, ep, s);
+        else
+            launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep, s);
     });
 }
 

@@ -209,6 +209,13 @@ static void dispatch_tf(int tf, const GemmParams &p, int64_t max_rows, int64_t n
 void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep, hipStream_t s,
                    const int32_t *row_index, DevBuf *ws) {
     if (n <= 0 || w.rows <= 0) return;
+    if (ws && !ep.exact && mx_gemm_takes(w, n)) {
+        const int64_t ldst = w.units_k;
+        void *xm = ws->get<uint8_t>(mx_frag_bytes(n, ldst));
+        launch_split_mx(xm, x, row_index, n, w.cols, w.cols, ldst, s);
+        launch_mx_gemm(w, out, w.rows, xm, ldst, n, ep, s);
+        return;
+    }
     if (ws && tile_gemm_takes(w, n)) {
         const int xt = ep.exact ? 3 : 2;
         const int64_t ldk = split_k_tiles(w);
@@ -237,6 +244,10 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
 void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, const MatmulEpilogue &ep,
                        hipStream_t s, DevBuf *ws) {
     if (n <= 0 || w.rows <= 0) return;
+    if (x.f32 && !ep.exact && mx_gemm_takes(w, n)) {
+        launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
+        return;
+    }
     if (x.xs && !ep.exact && tile_gemm_takes(w, n) && x.ldk >= split_k_tiles(w)) {
         launch_tile_gemm(w, out, w.rows, x.xs, x.ldk, n, 2, ep, s);
         return;

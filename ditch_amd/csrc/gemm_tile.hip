@@ -466,6 +466,302 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 }
 
 // ---------------------------------------------------------------------------
+// MXFP4 weights on the scaled MFMA
+//
+// v_mfma_scale_f32_16x16x128_f8f6f4 multiplies a 16 x 128 A block by a 128 x 16
+// B block where each lane supplies 32 consecutive k of one row / column with
+// one E8M0 scale: lane l holds row l % 16, k = 32 (l / 16) .. +32. With B =
+// the MXFP4 codes (e2m1) and their own E8M0 block scales, the weights enter
+// exactly (the e2m1 value times 2^k is what the reference's bf16 decode
+// yields). The activations enter as MX_TERMS fp6 (e2m3) terms with their own
+// E8M0 scale per 32-k block: x = sum_e code_e * 2^s_e + r, each term the
+// round-to-nearest-even e2m3 value of the remainder over the scale that puts
+// the remainder's block maximum in (3.75, 7.5]; every subtraction is exact,
+// so |r| <= 2^-3.9 of the previous remainder's block maximum, i.e. after four
+// terms |r| <= 15^-4 * max|x over the block| ~ 2^-15.6 max|x|. The fp6 x fp4
+// MFMA runs at four times the bf16 rate: four terms cost what one bf16 term
+// does, against two bf16 terms on the bf16 path.
+//
+// Activation fragments: xm[m16][stage][term][half][lane] x 16 B (2 KiB per
+// term): lane l, token 16 m16 + l % 16, k = 128 stage + 32 (l / 16) .. +32;
+// dwords 0..5 the 32 codes (code j at bits 6j..6j+5), dword 6 zero, dword 7
+// the E8M0 byte (apart from the codes, so that the codes load into one
+// six-register operand).
+
+constexpr int MX_TERMS = 4;
+
+struct MxSplitParams {
+    u32x4 *xm;
+    const float *x;
+    const int32_t *row_index;
+    int64_t n, ldx, K, ldst, m16;
+};
+
+// |v| <= 7.5 to the nearest e2m3 value (ties to even); returns the code
+// magnitude bits and sets q to the value
+__device__ __forceinline__ uint32_t e2m3_rne(float a, float &q) {
+    q = a < 2.f ? __builtin_rintf(a * 8.f) * 0.125f : a < 4.f ? __builtin_rintf(a * 4.f) * 0.25f
+                                                                : __builtin_rintf(a * 2.f) * 0.5f;
+    uint32_t c;
+    if (q < 1.f) c = (uint32_t)(q * 8.f);
+    else if (q < 2.f) c = 8u | (uint32_t)((q - 1.f) * 8.f);
+    else if (q < 4.f) c = 16u | (uint32_t)((q * 0.5f - 1.f) * 8.f);
+    else c = 24u | (uint32_t)((q * 0.25f - 1.f) * 8.f);
+    return c;
+}
+
+__global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= p.m16 * p.ldst * 64) return;
+    const int lane = (int)(t & 63);
+    const int64_t f = t >> 6;  // m16 * ldst + stage
+    const int64_t st = f % p.ldst, mb = f / p.ldst;
+    const int64_t tok = mb * 16 + (lane & 15);
+    const int64_t k0 = st * 128 + 32 * (lane >> 4);
+    float r[32];
+    if (tok < p.n) {
+        const int64_t src = p.row_index ? (int64_t)p.row_index[tok] : tok;
+        const float *xr = p.x + src * p.ldx;
+        if (k0 + 32 <= p.K && ((((uintptr_t)(xr + k0)) & 15) == 0)) {
+#pragma unroll
+            for (int j = 0; j < 32; j += 4) {
+                const float4 v = *(const float4 *)(xr + k0 + j);
+                r[j] = v.x; r[j + 1] = v.y; r[j + 2] = v.z; r[j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; j++) r[j] = (k0 + j < p.K) ? xr[k0 + j] : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) r[j] = 0.f;
+    }
+    u32x4 *out = p.xm + f * (MX_TERMS * 2 * 64) + lane;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 32; j++) finite = finite && __builtin_isfinite(r[j]);
+    if (!finite) {
+        // a NaN or infinity in the block: E8M0 255 (NaN) makes every product
+        // that reads it NaN
+#pragma unroll
+        for (int e = 0; e < MX_TERMS; e++) {
+            out[(e * 2 + 0) * 64] = u32x4{0, 0, 0, 0};
+            out[(e * 2 + 1) * 64] = u32x4{0, 0, 0, 255u};
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < MX_TERMS; e++) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(r[j]));
+        // scale 2^x with m / 2^x in (3.75, 7.5]: m = f 2^E, f in [1, 2)
+        int x = -127;
+        if (m > 0.f) {
+            const uint32_t b = __builtin_bit_cast(uint32_t, m);
+            const int E = (int)(b >> 23) - 127;  // m is normal past the first term's subnormal-free range
+            const uint32_t frac = b & 0x7fffffu;
+            x = E - 2 + (frac > 0x700000u ? 1 : 0);  // f > 1.875
+            x = x < -127 ? -127 : x;
+        }
+        const float sc = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(x + 127) << 23) : __builtin_bit_cast(float, 0x00400000u);
+        const float inv = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(127 - x) << 23) : 0.f;
+        uint32_t d[8] = {0, 0, 0, 0, 0, 0, 0, (uint32_t)(x + 127)};
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            float q;
+            const float a = x >= -126 && x <= 126 ? fabsf(r[j]) * inv : 0.f;
+            const uint32_t mag = e2m3_rne(a, q);
+            const uint32_t sgn = r[j] < 0.f ? 32u : 0u;
+            const uint32_t code = q > 0.f ? (mag | sgn) : 0u;
+            r[j] = __fsub_rn(r[j], copysignf(q, r[j]) * sc);
+            const int bit = 6 * j;
+            d[bit >> 5] |= code << (bit & 31);
+            if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
+        }
+        out[(e * 2 + 0) * 64] = u32x4{d[0], d[1], d[2], d[3]};
+        out[(e * 2 + 1) * 64] = u32x4{d[4], d[5], d[6], d[7]};
+    }
+}
+
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+
+// One A operand: the six code dwords of a fragment lane and its E8M0 word
+// (dword 7), read as 128-, 64- and 32-bit LDS loads.
+struct MxA {
+    v4i_t lo;
+    v2i_t hi;
+    int sc;
+};
+
+__device__ __forceinline__ floatx4 mfma_mx(const MxA &a, const u32x4 &b, int sb, floatx4 c) {
+    // A: fp6 e2m3 (format 2, six dwords read); B: fp4 e2m1 (format 4, four
+    // dwords read)
+    const v4i_t b0 = __builtin_bit_cast(v4i_t, b);
+    const v4i_t h4 = __builtin_shufflevector(a.hi, a.hi, 0, 1, -1, -1);
+    const v8i_t av = __builtin_shufflevector(a.lo, h4, 0, 1, 2, 3, 4, 5, -1, -1);
+    const v8i_t bv = __builtin_shufflevector(b0, b0, 0, 1, 2, 3, -1, -1, -1, -1);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 2, 4, 0, a.sc, 0, sb);
+}
+
+// The scaled-MFMA product: the pipeline of tile_gemm_kernel (copies by the
+// younger wave of each SIMD, two stage buffers, one barrier a stage) with a
+// stage of 128 k: A = WM x MX_TERMS fragments of 2 KiB, B = one 1 KiB unit
+// per row group (MXFP4 codes in MFMA order) and the side word of each row.
+template <int WGN, int WM, int WN>
+__global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
+    constexpr int WAVES = WGN, NT = MX_TERMS;
+    constexpr int FR = WM * NT * 2;  // A KiB per stage
+    __shared__ u32x4 As0[FR * 64], As1[FR * 64];                // [m][term][half][lane]
+    __shared__ u32x4 Bs0[WAVES * WN * 64], Bs1[WAVES * WN * 64];  // [wave][group][lane]
+    __shared__ uint32_t Ss0[WAVES * 64], Ss1[WAVES * 64];        // [wave][group][row]
+    const TileView &w = p.w;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int mt, nt;
+    map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
+    const int64_t groups = (w.rows + 15) / 16;
+    const int64_t g0 = (int64_t)nt * (WN * WGN) + wave * WN;
+    const int64_t m16_0 = (int64_t)mt * WM, m16_n = (p.n + 15) / 16;
+    const int64_t S = w.units_k;  // stages: one 128-column unit each
+
+    constexpr int CW = WAVES >= 8 ? WAVES / 2 : WAVES;
+    constexpr int CA = FR / CW, CB = WAVES * WN / CW, CS = WAVES / CW;
+    static_assert(FR % CW == 0 && (WAVES * WN) % CW == 0 && WAVES % CW == 0, "copies split evenly");
+    static_assert(WN == 4, "one side-word copy covers a wave's four row groups");
+    const bool copier = wave >= WAVES - CW;
+    const int ck = copier ? wave - (WAVES - CW) : 0;
+    // copy sources: wave-uniform bases (+ the lane's 16 bytes at the copy)
+    int64_t asrc[CA];
+#pragma unroll
+    for (int j = 0; j < CA; j++) {
+        const int f = ck + CW * j;  // [m][term][half]
+        const int m = f / (NT * 2), eh = f % (NT * 2);
+        int64_t mb = m16_0 + m;
+        mb = mb < m16_n ? mb : m16_n - 1;
+        asrc[j] = (mb * p.ldk * NT * 2 + eh) * 64;
+    }
+    auto group_of = [&](int wq, int i) {
+        const int64_t gi = (int64_t)nt * (WN * WGN) + wq * WN + i;
+        return gi < groups ? gi : groups - 1;
+    };
+    int64_t bsrc[CB];
+#pragma unroll
+    for (int j = 0; j < CB; j++) {
+        const int q = ck + CW * j;
+        bsrc[j] = group_of(q / WN, q % WN) * S * 64;
+    }
+    const uint32_t *ssrc[CS];
+#pragma unroll
+    for (int j = 0; j < CS; j++)  // lane l: row l % 16 of row group l / 16
+        ssrc[j] = w.side + side_row(w, group_of(ck + CW * j, lane >> 4), lane);
+
+    auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
+        if (!copier) return;
+#pragma unroll
+        for (int j = 0; j < CA; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(p.xs + asrc[j] + s * NT * 2 * 64 + lane),
+                                             (lds_void *)&As[(ck + CW * j) * 64], 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < CB; j++)
+            __builtin_amdgcn_global_load_lds((const void *)((const u32x4 *)w.mx + bsrc[j] + s * 64 + lane),
+                                             (lds_void *)&Bs[(ck + CW * j) * 64], 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < CS; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(ssrc[j] + s), (lds_void *)&Ss[(ck + CW * j) * 64], 4, 0, 0);
+    };
+
+    floatx4 acc[WM][WN];
+#pragma unroll
+    for (int m = 0; m < WM; m++)
+#pragma unroll
+        for (int i = 0; i < WN; i++) acc[m][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    copy_stage(0, As0, Bs0, Ss0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto step = [&](int64_t s, const u32x4 *As, const u32x4 *Bs, const uint32_t *Ss, u32x4 *An, u32x4 *Bn,
+                    uint32_t *Sn) {
+        copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 b[WN];
+        int sb[WN];
+#pragma unroll
+        for (int i = 0; i < WN; i++) {
+            b[i] = Bs[(wave * WN + i) * 64 + lane];
+            // this lane's E8M0 byte (its 32-column block) in bits 0..7
+            sb[i] = (int)(Ss[wave * 64 + i * 16 + (lane & 15)] >> (8 * (lane >> 4)));
+        }
+        const u32x4 *A = As + lane;
+        auto read_a = [&](int m, int e) {
+            MxA r;
+            r.lo = __builtin_bit_cast(v4i_t, A[((m * NT + e) * 2 + 0) * 64]);
+            const int *h = (const int *)&A[((m * NT + e) * 2 + 1) * 64];
+            r.hi = *(const v2i_t *)h;
+            r.sc = h[3];
+            return r;
+        };
+        // term e + 1's fragments are read while term e's products issue
+        MxA a[2][WM];
+#pragma unroll
+        for (int m = 0; m < WM; m++) a[0][m] = read_a(m, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < NT; e++) {
+            const int cu = e & 1, nx = cu ^ 1;
+            if (e + 1 < NT) {
+#pragma unroll
+                for (int m = 0; m < WM; m++) a[nx][m] = read_a(m, e + 1);
+            }
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int i = 0; i < WN; i++) acc[m][i] = mfma_mx(a[cu][m], b[i], sb[i], acc[m][i]);
+        }
+        constexpr int NA = WM * 2, NM = WM * WN;
+#pragma unroll
+        for (int e = 0; e < NT; e++) {
+            if (e + 1 < NT) {
+#pragma unroll
+                for (int j = 0; j < NA; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NM - NA, 0);
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int64_t s = 0;
+    for (; s + 1 < S; s += 2) {
+        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
+        step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0);
+    }
+    if (s < S) step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
+
+    const int kq = lane >> 4;
+#pragma unroll
+    for (int m = 0; m < WM; m++)
+#pragma unroll
+        for (int i = 0; i < WN; i++) {
+            const int64_t row = (g0 + i) * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+        }
+}
+
+// ---------------------------------------------------------------------------
 
 int64_t split_k_tiles(const TileView &w) {
     // a whole number of pipeline stages (4 k tiles; 2 for bf16 and FP8 weights)
@@ -575,6 +871,47 @@ void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, flo
     p.ldo = gate.rows;
     p.n = n;
     launch_tile_any<true>(p, 2, s);
+}
+
+// ---------------------------------------------------------------------------
+// MXFP4 on the scaled MFMA: host side
+
+bool mx_gemm_takes(const TileView &w, int64_t n) { return w.tf == TF_MX4 && w.fast && w.mx && n >= 128; }
+
+size_t mx_frag_bytes(int64_t n, int64_t ldst) { return (size_t)((n + 15) / 16) * ldst * MX_TERMS * 2048; }
+
+void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
+                     int64_t ldst, hipStream_t s) {
+    DITCH_CHECK(ldst * 128 >= K, DITCH_INVALID_ARGUMENT, "MX fragments shorter than K");
+    MxSplitParams sp{(u32x4 *)xm, x, row_index, n, ldx, K, ldst, (n + 15) / 16};
+    const int64_t total = sp.m16 * ldst * 64;
+    hipLaunchKernelGGL(split_mx_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+void launch_mx_gemm(const TileView &w, float *out, int64_t ldo, const void *xm, int64_t ldst, int64_t n,
+                    const MatmulEpilogue &ep, hipStream_t s) {
+    DITCH_CHECK(mx_gemm_takes(w, n), DITCH_INVALID_ARGUMENT, "scaled-MFMA product: not an MXFP4 tensor it takes");
+    DITCH_CHECK(ldst >= w.units_k, DITCH_INVALID_ARGUMENT, "MX fragments shorter than K");
+    TileGemmParams p{};
+    p.w = w;
+    p.xs = (const u32x4 *)xm;
+    p.kt_total = w.units_k;
+    p.ldk = ldst;
+    p.out = out;
+    p.ldo = ldo;
+    p.n = n;
+    p.bias = ep.bias;
+    p.accumulate = ep.accumulate;
+    p.delta_b = ep.delta_b;
+    p.delta_xa = ep.delta_xa;
+    p.delta_rank = ep.delta_rank;
+    p.delta_stride = ep.delta_rank;
+    constexpr int WGN = 8, WM = 4, WN = 4;
+    p.tiles_m = (int)((n + 16 * WM - 1) / (16 * WM));
+    p.tiles_n = (int)((w.rows + 16 * WN * WGN - 1) / (16 * WN * WGN));
+    hipLaunchKernelGGL((mx_gemm_kernel<WGN, WM, WN>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(WGN * 64), 0, s, p);
+    DITCH_TRY_HIP(hipGetLastError());
 }
 
 }  // namespace ditch

@@ -88,6 +88,11 @@ struct TileView {
     // zero field << 16 per group
     const uint32_t *side;
     int64_t side_cols;
+    // MXFP4 (fast tensors): the codes once more in the operand order of the
+    // scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4): per 16-row group and
+    // 128-column unit, lane l holds the 16 source bytes of row l % 16,
+    // columns 32 * (l / 16) .. +32 (one E8M0 block)
+    const uint8_t *mx;
 };
 
 // Device memory helpers (all on the context stream).
@@ -121,6 +126,7 @@ struct ditch_hip_tensor {
     void *scale = nullptr;
     void *zero = nullptr;
     void *side = nullptr;  // owned side words (FP8, INT4); MXFP4 aliases scale
+    void *mx = nullptr;    // MXFP4 codes in scaled-MFMA order
     uint64_t bytes = 0;
 };
 
@@ -178,6 +184,14 @@ void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs
                       const MatmulEpilogue &ep, hipStream_t s);
 // gate/up in one product: act(x gate^T) * (x up^T) into f32 rows [n][rows]
 // (out, may be NULL) and/or the A fragments of the next product (xs_out)
+// MXFP4 large batches on the scaled MFMA (fp6 activation terms x the fp4
+// codes): fragments [ceil(n/16)][ldst][4 terms] x 2 KiB, ldst >= cols / 128.
+bool mx_gemm_takes(const TileView &w, int64_t n);
+size_t mx_frag_bytes(int64_t n, int64_t ldst);
+void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
+                     int64_t ldst, hipStream_t s);
+void launch_mx_gemm(const TileView &w, float *out, int64_t ldo, const void *xm, int64_t ldst, int64_t n,
+                    const MatmulEpilogue &ep, hipStream_t s);
 bool tile_glu_takes(const TileView &gate, const TileView &up, int64_t n);
 void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xs_out,
                      int64_t ldk_out, const void *xs, int64_t ldk, int64_t n, hipStream_t s);

@@ -628,6 +628,9 @@ static void mm_act(ditch_hip_model *m, const Mat &mt, float *out, const Act &x, 
 }
 
 // Whether the tiled product takes `mt` with fragments alone (no f32 rows).
+// A product whose input may come as bf16-term fragments alone (no f32 rows):
+// the bf16 tiled kernel takes it (MXFP4 included: its producers write bf16
+// terms; given f32 rows an MXFP4 product takes the scaled-MFMA path).
 static bool frag_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && tile_gemm_takes(mt.t->v, n); }
 
 // Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).

@@ -339,6 +339,27 @@ __global__ void int_zero_kernel(const uint32_t *zw, uint8_t *out, int64_t rows, 
     }
 }
 
+// MXFP4 codes in the B operand order of the scaled MFMA: unit (g, u), lane l
+// = the 16 source bytes of row 16 g + l % 16, columns 128 u + 32 (l / 16) ..
+// +32 (two codes a byte, the lower column in the low nibble: the order the
+// MFMA reads e2m1 codes); zero past the matrix.
+__global__ void mx_native_kernel(const uint8_t *src, int64_t rows, int64_t cols, uint8_t *out, int64_t groups,
+                                 int64_t units) {
+    const int64_t total = groups * units * 64;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i % 64);
+        const int64_t unit = i / 64, g = unit / units, u = unit % units;
+        const int64_t n = g * 16 + lane % 16, k0 = u * 128 + 32 * (lane / 16);
+        uint32_t w[4] = {0, 0, 0, 0};
+        if (n < rows && k0 < cols) {
+            const uint8_t *row = src + n * (cols / 2) + k0 / 2;  // MXFP4 columns come in whole 32-blocks
+#pragma unroll
+            for (int j = 0; j < 16; j++) w[j / 4] |= (uint32_t)row[j] << (8 * (j % 4));
+        }
+        *(uint4 *)(out + i * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // Side words of the tiled GEMM (TileView::side). FP8: the scale grid as f32
 // (exact for f32, f16, bf16 and finite E8M0 scales).
 __global__ void fp8_side_kernel(const void *scale, int32_t scale_type, uint32_t *out, int64_t total) {
@@ -615,6 +636,7 @@ void free_tensor(ditch_hip_tensor *t) {
     dev_free(t->scale);
     dev_free(t->zero);
     dev_free(t->side);
+    dev_free(t->mx);
     delete t;
 }
 
@@ -750,6 +772,12 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
         if (v.fast && tf == TF_MX4) {
             v.side = (const uint32_t *)t->scale;
             v.side_cols = v.scale_cols / 4;
+            t->mx = dev_alloc(code_bytes);
+            t->bytes += code_bytes;
+            const int64_t total_mx = a.groups_n * v.units_k * 64;
+            hipLaunchKernelGGL(mx_native_kernel, dim3(grid_for(total_mx)), dim3(256), 0, s, st.v.data, v.rows, v.cols,
+                               (uint8_t *)t->mx, a.groups_n, v.units_k);
+            v.mx = (const uint8_t *)t->mx;
         } else if (v.fast && tf == TF_FP8) {
             int64_t total = ((int64_t)w->scale_rows + 1) * v.scale_cols;
             t->side = dev_alloc(total * 4);

@@ -146,13 +146,6 @@ class Device:
         self.check(self.lib.ditch_hip_dequant(self.h, _p(out), w.ref(), row0, nrows))
         return out
 
-    def frag_bytes(self, n, k):
-        return self.lib.ditch_hip_frag_bytes(n, k)
-
-    def split_device(self, d_frags, frag_bytes, d_x, n, k, stream=None):
-        """Writes the activation fragments of d_x [n][k] (device f32)."""
-        self.check(self.lib.ditch_hip_split_device(self.h, d_frags, frag_bytes, d_x, n, k, stream))
-
     def upload(self, w: HostWeight):
         t = self.lib.ditch_hip_upload(self.h, w.ref())
         if not t:
@@ -199,6 +192,16 @@ class Tensor:
     def matmul_device(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None):
         self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, d_x, n, self.handle, d_bias,
                                                              int(accumulate), stream))
+
+    def frag_bytes(self, n):
+        """Bytes of the activation fragments of n rows for products over this
+        tensor (0: the large-batch product does not take it)."""
+        return self.dev.lib.ditch_hip_frag_bytes(self.handle, n)
+
+    def split_device(self, d_frags, frag_bytes, d_x, n, stream=None):
+        """Writes the fragments of d_x [n][cols] (device f32) for this tensor."""
+        self.dev.check(self.dev.lib.ditch_hip_split_device(self.dev.h, d_frags, frag_bytes, d_x, n, self.handle,
+                                                           stream))
 
     def matmul_frags_device(self, d_out, d_frags, n, d_bias=None, accumulate=False, stream=None):
         """The large-batch product on activation fragments (ditch_hip_split_device)."""

@@ -206,23 +206,26 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x,
                                  const float *d_bias, int32_t accumulate,
                                  void *stream);
 
-/* Activation fragments: the layout the large-batch product reads, for
- * callers that keep activations resident between products (the resident
- * forward's own producers write it). An activation [n][k] is stored as
- * [ceil(n/16)][ldk][2][64 lanes] x 16 bytes, ldk = ceil(k/128) * 4: two
- * bf16 terms per value (hi = bf16(x), lo = bf16(x - hi)); lane l of a
- * fragment holds token l % 16 of its 16-token block and k = 32 * tile +
- * 8 * (l / 16) .. +8. Columns past k are zero. No reference counterpart:
- * matmulT (compute.zig:100) takes f32 rows.                               */
-uint64_t ditch_hip_frag_bytes(uint64_t n, uint64_t k);
-/* Writes the fragments of d_x [n][k] (f32) into d_frags (frag_bytes long),
- * on `stream` (NULL = the context stream).                                 */
+/* Activation fragments: the activations already in the layout the
+ * large-batch product over a given tensor reads, for callers that multiply
+ * the same activations by several tensors or keep them resident (the
+ * resident forward's own producers write them). The layout depends on the
+ * tensor's format: two bf16 terms per value in MFMA operand order for BF16,
+ * FP8 and INT4 tensors, four fp6 (e2m3) terms with E8M0 block scales for
+ * MXFP4 tensors (the operands of the scaled MFMA). No reference
+ * counterpart: matmulT (compute.zig:100) takes f32 rows.
+ * ditch_hip_frag_bytes: bytes for n rows of activations against w, or 0
+ * when the large-batch product does not take w (n < 128, or a format it does
+ * not decode exactly); the f32 entry point then applies.                  */
+uint64_t ditch_hip_frag_bytes(const ditch_hip_tensor *w, uint64_t n);
+/* Writes the fragments of d_x [n][cols of w] (f32) for products over w into
+ * d_frags (frag_bytes long), on `stream` (NULL = the context stream).     */
 int32_t ditch_hip_split_device(ditch_hip *h, void *d_frags, uint64_t frag_bytes,
-                               const float *d_x, uint64_t n, uint64_t k,
-                               void *stream);
-/* ditch_hip_matmulT_device on fragments (k = w's cols). Unsupported when the
- * large-batch product does not take w (n < 128, or a format it does not
- * decode exactly); the f32 entry point then applies.                      */
+                               const float *d_x, uint64_t n,
+                               const ditch_hip_tensor *w, void *stream);
+/* ditch_hip_matmulT_device on fragments that ditch_hip_split_device wrote
+ * for w (or for a tensor of the same format and cols). Unsupported where
+ * ditch_hip_frag_bytes is 0.                                               */
 int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out,
                                        const void *d_frags, uint64_t n,
                                        const ditch_hip_tensor *w,

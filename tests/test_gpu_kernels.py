@@ -254,10 +254,32 @@ def test_matmulT_large_batch_matches_oracle(dev, ref, kind, n, rows, cols):
     close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
 
 
+def split_bound(kind, x, wf):
+    """Bound on |product - exact product| from the activation split of the
+    large-batch products: two bf16 terms leave |x - t0 - t1| <= 2^-18 |x|
+    per activation (bounded with a factor 4 of margin: 2^-16 sum_k |x||w|);
+    four fp6 terms over E8M0 block scales (MXFP4) leave at most 15^-4 of the
+    block's max |x| (bounded by 2^-15 sum_blocks max|x| sum_k |w|)."""
+    x64, w64 = np.abs(x).astype(np.float64), np.abs(wf).astype(np.float64)
+    if kind != "mxfp4":
+        return 2.0 ** -16 * (x64 @ w64.T)
+    n, cols = x.shape
+    pad = -cols % 32
+    xm = np.pad(x64, ((0, 0), (0, pad))).reshape(n, -1, 32).max(-1)
+    ws = np.pad(w64, ((0, 0), (0, pad))).reshape(w64.shape[0], -1, 32).sum(-1)
+    return 2.0 ** -15 * (xm @ ws.T)
+
+
+def dequant_f32(ref, w):
+    wd = ref.dequant(w)
+    return (wd.astype(np.uint32) << 16).view(np.float32) if wd.dtype == np.uint16 else wd
+
+
 @pytest.mark.parametrize("kind", ["bf16", "fp8", "mxfp4", "int4"])
 def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
-    """The forward's product (two activation terms) on a resident tensor,
-    with the bias and accumulate epilogue, against the oracle."""
+    """The forward's product (activations split into two bf16 terms, or four
+    fp6 terms for MXFP4 weights) on a resident tensor, with the bias and
+    accumulate epilogue, against the oracle."""
     from ditch_amd import hipmem
     rng = np.random.default_rng(77)
     n, rows, cols = 384, 520, 1024
@@ -274,14 +296,9 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
     finally:
         t.free()
     want = (prior.astype(np.float64) + ref.matmulT(x, w).astype(np.float64) + bias)
-    # two bf16 terms leave |x - t0 - t1| <= 2^-18 |x| per activation, so the
-    # product may differ by up to 2^-18 * sum_k |x||w| (bounded here with a
-    # factor 4 of margin) beyond the exact path's tolerance
-    wd = ref.dequant(w)
-    wf = (wd.astype(np.uint32) << 16).view(np.float32) if wd.dtype == np.uint16 else wd
-    split = 2.0 ** -16 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    split = split_bound(kind, x, dequant_f32(ref, w))
     bad = np.abs(got - want) > TOL_MATMUL["atol"] + TOL_MATMUL["rtol"] * np.abs(want) + split
-    assert not bad.any(), f"{bad.sum()} outside the two-term bound"
+    assert not bad.any(), f"{bad.sum()} outside the split bound"
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
 
 
@@ -289,9 +306,10 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
                                                ("mxfp4", 256, 520, 640), ("int4", 321, 72, 1024)])
 def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
     """ditch_hip_split_device + ditch_hip_matmulT_frags_device run the same
-    tiled product as ditch_hip_matmulT_device on large batches: bit-identical
-    outputs, bias and accumulate included (K padded past the product's own
-    stage count, ragged token count)."""
+    large-batch product as ditch_hip_matmulT_device: bit-identical outputs,
+    bias and accumulate included (K padded past the product's own stage
+    count, ragged token count); the fragment size follows the tensor's
+    format (bf16 terms, or fp6 terms for MXFP4)."""
     from ditch_amd import hipmem
     from ditch_amd.hip import DeviceError
     rng = np.random.default_rng(13)
@@ -299,25 +317,93 @@ def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
     x = rng.standard_normal((n, cols)).astype(np.float32)
     bias = rng.standard_normal(rows).astype(np.float32)
     prior = rng.standard_normal((n, rows)).astype(np.float32)
-    fb = dev.frag_bytes(n, cols)
-    assert fb == -(-n // 16) * (-(-cols // 128) * 4) * 2 * 1024
     t = dev.upload(w)
     try:
+        fb = t.frag_bytes(n)
+        if kind == "mxfp4":  # [n/16][cols/128][4 terms] x 2 KiB
+            assert fb == -(-n // 16) * -(-cols // 128) * 4 * 2048
+        else:  # [n/16][cols/128 * 4 k tiles][2 terms] x 1 KiB
+            assert fb == -(-n // 16) * (-(-cols // 128) * 4) * 2 * 1024
+        assert t.frag_bytes(64) == 0
         bx, bb = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias)
         o1, o2 = hipmem.Buffer.from_array(prior), hipmem.Buffer.from_array(prior)
         xs = hipmem.Buffer(fb)
         t.matmul_device(o1.ptr, bx.ptr, n, d_bias=bb.ptr, accumulate=True)
-        dev.split_device(xs.ptr, fb, bx.ptr, n, cols)
+        t.split_device(xs.ptr, fb, bx.ptr, n)
         t.matmul_frags_device(o2.ptr, xs.ptr, n, d_bias=bb.ptr, accumulate=True)
         dev.sync()
         a, b = o1.download(np.float32, (n, rows)), o2.download(np.float32, (n, rows))
         with pytest.raises(DeviceError, match="too small"):
-            dev.split_device(xs.ptr, fb - 1, bx.ptr, n, cols)
+            t.split_device(xs.ptr, fb - 1, bx.ptr, n)
+        with pytest.raises(DeviceError, match="Unsupported"):
+            t.split_device(xs.ptr, fb, bx.ptr, 64)
         with pytest.raises(DeviceError, match="Unsupported"):
             t.matmul_frags_device(o2.ptr, xs.ptr, 64)
     finally:
         t.free()
     assert np.array_equal(a, b)
+
+
+MX_CASES = {
+    # n, rows, cols, activation generator
+    "ragged": (131, 72, 576, lambda rng, n, c: rng.standard_normal((n, c))),
+    "outliers": (256, 136, 1024, lambda rng, n, c: rng.standard_normal((n, c)) * np.where(
+        rng.random((n, c)) < 0.01, 300.0, 1.0)),
+    "wide_range": (128, 64, 512, lambda rng, n, c: rng.standard_normal((n, c)) * 2.0 ** rng.integers(-60, 60, (n, c))),
+    "zero_blocks": (160, 48, 384, lambda rng, n, c: rng.standard_normal((n, c)) * (np.arange(c) // 32 % 3 != 0)),
+}
+
+
+@pytest.mark.parametrize("case", sorted(MX_CASES))
+def test_mxfp4_scaled_mfma_product(dev, ref, case):
+    """MXFP4 on the scaled MFMA (fp6 activation terms x the fp4 codes with
+    both E8M0 scales) against the oracle, within the four-term split bound:
+    ragged tokens and K, outlier channels, activations over 2^+-60, all-zero
+    32-blocks."""
+    from ditch_amd import hipmem
+    n, rows, cols, gen = MX_CASES[case]
+    rng = np.random.default_rng(sum(map(ord, case)))
+    w = wg.make("mxfp4", rows, cols, rng)
+    x = gen(rng, n, cols).astype(np.float32)
+    t = dev.upload(w)
+    try:
+        assert t.frag_bytes(n) > 0
+        bx, bo = hipmem.Buffer.from_array(x), hipmem.Buffer(n * rows * 4)
+        t.matmul_device(bo.ptr, bx.ptr, n)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    want = ref.matmulT(x, w).astype(np.float64)
+    wf = dequant_f32(ref, w)
+    bound = split_bound("mxfp4", x, wf) + 1e-5 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    bad = np.abs(got - want) > bound + 1e-30
+    assert not bad.any(), f"{bad.sum()} outside the MX split bound (max excess {(np.abs(got - want) - bound).max():.3g})"
+
+
+def test_mxfp4_scaled_mfma_non_finite_activation_gives_nan_rows(dev, ref):
+    """A NaN or infinity among an activation block's 32 values makes that
+    token's outputs NaN on the scaled-MFMA path (E8M0 255); other tokens are
+    unaffected."""
+    from ditch_amd import hipmem
+    rng = np.random.default_rng(3)
+    n, rows, cols = 128, 32, 256
+    w = wg.make("mxfp4", rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    x[5, 77] = np.nan
+    x[9, 200] = np.inf
+    t = dev.upload(w)
+    try:
+        bx, bo = hipmem.Buffer.from_array(x), hipmem.Buffer(n * rows * 4)
+        t.matmul_device(bo.ptr, bx.ptr, n)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    assert np.isnan(got[5]).all() and np.isnan(got[9]).all()
+    keep = np.ones(n, bool)
+    keep[[5, 9]] = False
+    assert np.isfinite(got[keep]).all()
 
 
 def test_matmulT_large_batch_nan_scale_takes_the_exact_decoder(dev, ref):
