@@ -482,13 +482,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 // MFMA runs at four times the bf16 rate: four terms cost what one bf16 term
 // does, against two bf16 terms on the bf16 path.
 //
-// Activation fragments: xm[m16][stage][term][half][lane] x 16 B (2 KiB per
-// term): lane l, token 16 m16 + l % 16, k = 128 stage + 32 (l / 16) .. +32;
-// dwords 0..5 the 32 codes (code j at bits 6j..6j+5), dword 6 zero, dword 7
-// the E8M0 byte (apart from the codes, so that the codes load into one
-// six-register operand).
+// Activation fragments: per 16-token block and 128-k stage a 6400-byte block
+// (lane l: token 16 m16 + l % 16, k = 128 stage + 32 (l / 16) .. +32; the
+// 32 fp6 codes of a term are 6 dwords, code j at bits 6j..6j+5):
+//     [term][lane] 16 B   dwords 0..3 of each term       4 x 1 KiB
+//     [term][lane] 8 B    dwords 4..5                    4 x 512 B
+//     [lane] 4 B          E8M0 byte of term e in byte e  256 B
+// so that every part is read with one conflict-free LDS load per lane and
+// copied in whole KiB (the last 256 B apart).
 
 constexpr int MX_TERMS = 4;
+constexpr int MX_BLOCK = 6400;  // bytes per 16 tokens x 128 k
 
 struct MxSplitParams {
     u32x4 *xm;
@@ -536,7 +540,10 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
 #pragma unroll
         for (int j = 0; j < 32; j++) r[j] = 0.f;
     }
-    u32x4 *out = p.xm + f * (MX_TERMS * 2 * 64) + lane;
+    uint8_t *blk = (uint8_t *)p.xm + f * MX_BLOCK;
+    u32x4 *lo = (u32x4 *)blk + lane;                 // + 64 e
+    uint2 *hi = (uint2 *)(blk + 4096) + lane;         // + 64 e
+    uint32_t *scw = (uint32_t *)(blk + 6144) + lane;
     bool finite = true;
 #pragma unroll
     for (int j = 0; j < 32; j++) finite = finite && __builtin_isfinite(r[j]);
@@ -545,11 +552,13 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
         // that reads it NaN
 #pragma unroll
         for (int e = 0; e < MX_TERMS; e++) {
-            out[(e * 2 + 0) * 64] = u32x4{0, 0, 0, 0};
-            out[(e * 2 + 1) * 64] = u32x4{0, 0, 0, 255u};
+            lo[64 * e] = u32x4{0, 0, 0, 0};
+            hi[64 * e] = make_uint2(0, 0);
         }
+        *scw = 0xffffffffu;
         return;
     }
+    uint32_t scales = 0;
 #pragma unroll
     for (int e = 0; e < MX_TERMS; e++) {
         float m = 0.f;
@@ -566,7 +575,8 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
         }
         const float sc = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(x + 127) << 23) : __builtin_bit_cast(float, 0x00400000u);
         const float inv = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(127 - x) << 23) : 0.f;
-        uint32_t d[8] = {0, 0, 0, 0, 0, 0, 0, (uint32_t)(x + 127)};
+        uint32_t d[6] = {0, 0, 0, 0, 0, 0};
+        scales |= (uint32_t)(x + 127) << (8 * e);
 #pragma unroll
         for (int j = 0; j < 32; j++) {
             float q;
@@ -579,9 +589,10 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
             d[bit >> 5] |= code << (bit & 31);
             if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
         }
-        out[(e * 2 + 0) * 64] = u32x4{d[0], d[1], d[2], d[3]};
-        out[(e * 2 + 1) * 64] = u32x4{d[4], d[5], d[6], d[7]};
+        lo[64 * e] = u32x4{d[0], d[1], d[2], d[3]};
+        hi[64 * e] = make_uint2(d[4], d[5]);
     }
+    *scw = scales;
 }
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
@@ -589,35 +600,35 @@ typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 
-// One A operand: the six code dwords of a fragment lane and its E8M0 word
-// (dword 7), read as 128-, 64- and 32-bit LDS loads.
+// One A operand: the six code dwords of a fragment lane (128- and 64-bit LDS
+// loads); its scale is byte E of the lane's scale word.
 struct MxA {
     v4i_t lo;
     v2i_t hi;
-    int sc;
 };
 
-__device__ __forceinline__ floatx4 mfma_mx(const MxA &a, const u32x4 &b, int sb, floatx4 c) {
+template <int E>
+__device__ __forceinline__ floatx4 mfma_mx(const MxA &a, int sa, const u32x4 &b, int sb, floatx4 c) {
     // A: fp6 e2m3 (format 2, six dwords read); B: fp4 e2m1 (format 4, four
     // dwords read)
     const v4i_t b0 = __builtin_bit_cast(v4i_t, b);
     const v4i_t h4 = __builtin_shufflevector(a.hi, a.hi, 0, 1, -1, -1);
     const v8i_t av = __builtin_shufflevector(a.lo, h4, 0, 1, 2, 3, 4, 5, -1, -1);
     const v8i_t bv = __builtin_shufflevector(b0, b0, 0, 1, 2, 3, -1, -1, -1, -1);
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 2, 4, 0, a.sc, 0, sb);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 2, 4, E, sa, 0, sb);
 }
 
 // The scaled-MFMA product: the pipeline of tile_gemm_kernel (copies by the
 // younger wave of each SIMD, two stage buffers, one barrier a stage) with a
-// stage of 128 k: A = WM x MX_TERMS fragments of 2 KiB, B = one 1 KiB unit
-// per row group (MXFP4 codes in MFMA order) and the side word of each row.
+// stage of 128 k: A = WM fragment blocks of 6400 B, B = one 1 KiB unit per
+// row group (MXFP4 codes in MFMA order) and its 64 scale bytes.
 template <int WGN, int WM, int WN>
 __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     constexpr int WAVES = WGN, NT = MX_TERMS;
-    constexpr int FR = WM * NT * 2;  // A KiB per stage
-    __shared__ u32x4 As0[FR * 64], As1[FR * 64];                // [m][term][half][lane]
+    constexpr int AQ = MX_BLOCK / 16;                            // u32x4 per A block
+    __shared__ u32x4 As0[WM * AQ], As1[WM * AQ];                  // [m][block]
     __shared__ u32x4 Bs0[WAVES * WN * 64], Bs1[WAVES * WN * 64];  // [wave][group][lane]
-    __shared__ uint32_t Ss0[WAVES * 64], Ss1[WAVES * 64];        // [wave][group][row]
+    __shared__ uint32_t Ss0[WAVES * 64], Ss1[WAVES * 64];        // [wave][group][lane] bytes
     const TileView &w = p.w;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -628,22 +639,29 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     const int64_t m16_0 = (int64_t)mt * WM, m16_n = (p.n + 15) / 16;
     const int64_t S = w.units_k;  // stages: one 128-column unit each
 
+    // copies of a stage: six KiB pieces and one 256 B piece per A block, one
+    // KiB per row group, 256 B of B scales per wave (four groups)
+    constexpr int NAK = WM * 6, NAS = WM, NB = WAVES * WN, NBS = WAVES;
     constexpr int CW = WAVES >= 8 ? WAVES / 2 : WAVES;
-    constexpr int CA = FR / CW, CB = WAVES * WN / CW, CS = WAVES / CW;
-    static_assert(FR % CW == 0 && (WAVES * WN) % CW == 0 && WAVES % CW == 0, "copies split evenly");
-    static_assert(WN == 4, "one side-word copy covers a wave's four row groups");
+    constexpr int CAK = NAK / CW, CAS = (NAS + CW - 1) / CW, CB = NB / CW, CBS = NBS / CW;
+    static_assert(NAK % CW == 0 && NB % CW == 0 && NBS % CW == 0, "copies split evenly");
+    static_assert(WN == 4, "one scale copy covers a wave's four row groups");
     const bool copier = wave >= WAVES - CW;
     const int ck = copier ? wave - (WAVES - CW) : 0;
-    // copy sources: wave-uniform bases (+ the lane's 16 bytes at the copy)
-    int64_t asrc[CA];
-#pragma unroll
-    for (int j = 0; j < CA; j++) {
-        const int f = ck + CW * j;  // [m][term][half]
-        const int m = f / (NT * 2), eh = f % (NT * 2);
+    auto a_block = [&](int m) {
         int64_t mb = m16_0 + m;
         mb = mb < m16_n ? mb : m16_n - 1;
-        asrc[j] = (mb * p.ldk * NT * 2 + eh) * 64;
+        return mb * p.ldk * AQ;  // u32x4 offset of block (mb, stage 0)
+    };
+    int64_t ak[CAK];
+#pragma unroll
+    for (int j = 0; j < CAK; j++) {
+        const int q = ck + CW * j;  // [m][piece 0..5]
+        ak[j] = a_block(q / 6) + (q % 6) * 64;
     }
+    int64_t as_[CAS];
+#pragma unroll
+    for (int j = 0; j < CAS; j++) as_[j] = a_block((ck + CW * j) % WM) + 384;
     auto group_of = [&](int wq, int i) {
         const int64_t gi = (int64_t)nt * (WN * WGN) + wq * WN + i;
         return gi < groups ? gi : groups - 1;
@@ -654,24 +672,35 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
         const int q = ck + CW * j;
         bsrc[j] = group_of(q / WN, q % WN) * S * 64;
     }
-    const uint32_t *ssrc[CS];
+    const uint32_t *bss[CBS];
 #pragma unroll
-    for (int j = 0; j < CS; j++)  // lane l: row l % 16 of row group l / 16
-        ssrc[j] = w.side + side_row(w, group_of(ck + CW * j, lane >> 4), lane);
+    for (int j = 0; j < CBS; j++)  // lane l: dword l % 16 of group l / 16's 64 bytes
+        bss[j] = (const uint32_t *)(w.mx_scales + group_of(ck + CW * j, lane >> 4) * S * 64) + (lane & 15);
 
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
         if (!copier) return;
+        const u32x4 *xs = p.xs + s * AQ;
 #pragma unroll
-        for (int j = 0; j < CA; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(p.xs + asrc[j] + s * NT * 2 * 64 + lane),
-                                             (lds_void *)&As[(ck + CW * j) * 64], 16, 0, 0);
+        for (int j = 0; j < CAK; j++) {
+            const int q = ck + CW * j;
+            __builtin_amdgcn_global_load_lds((const void *)(xs + ak[j] + lane),
+                                             (lds_void *)&As[(q / 6) * AQ + (q % 6) * 64], 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < CAS; j++) {
+            const int q = ck + CW * j;
+            if (q < NAS)
+                __builtin_amdgcn_global_load_lds((const void *)((const uint32_t *)(xs + as_[j]) + lane),
+                                                 (lds_void *)&As[q * AQ + 384], 4, 0, 0);
+        }
 #pragma unroll
         for (int j = 0; j < CB; j++)
             __builtin_amdgcn_global_load_lds((const void *)((const u32x4 *)w.mx + bsrc[j] + s * 64 + lane),
                                              (lds_void *)&Bs[(ck + CW * j) * 64], 16, 0, 0);
 #pragma unroll
-        for (int j = 0; j < CS; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(ssrc[j] + s), (lds_void *)&Ss[(ck + CW * j) * 64], 4, 0, 0);
+        for (int j = 0; j < CBS; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(bss[j] + s * 16), (lds_void *)&Ss[(ck + CW * j) * 64], 4,
+                                             0, 0);
     };
 
     floatx4 acc[WM][WN];
@@ -691,40 +720,44 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
         copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
         __builtin_amdgcn_sched_barrier(0);
         u32x4 b[WN];
-        int sb[WN];
+        int sb[WN], sa[WM];
 #pragma unroll
         for (int i = 0; i < WN; i++) {
             b[i] = Bs[(wave * WN + i) * 64 + lane];
-            // this lane's E8M0 byte (its 32-column block) in bits 0..7
-            sb[i] = (int)(Ss[wave * 64 + i * 16 + (lane & 15)] >> (8 * (lane >> 4)));
+            sb[i] = ((const uint8_t *)Ss)[wave * 256 + i * 64 + lane];
         }
-        const u32x4 *A = As + lane;
+#pragma unroll
+        for (int m = 0; m < WM; m++) sa[m] = (int)((const uint32_t *)(As + m * AQ + 384))[lane];
         auto read_a = [&](int m, int e) {
             MxA r;
-            r.lo = __builtin_bit_cast(v4i_t, A[((m * NT + e) * 2 + 0) * 64]);
-            const int *h = (const int *)&A[((m * NT + e) * 2 + 1) * 64];
-            r.hi = *(const v2i_t *)h;
-            r.sc = h[3];
+            r.lo = __builtin_bit_cast(v4i_t, As[m * AQ + e * 64 + lane]);
+            r.hi = ((const v2i_t *)(As + m * AQ + 256))[e * 64 + lane];
             return r;
         };
-        // term e + 1's fragments are read while term e's products issue
+        auto mma_term = [&](auto ec, const MxA (&at)[WM]) {
+            constexpr int E = decltype(ec)::value;
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int i = 0; i < WN; i++) acc[m][i] = mfma_mx<E>(at[m], sa[m], b[i], sb[i], acc[m][i]);
+        };
+        // term e + 1's operands are read while term e's products issue
+        static_assert(NT == 4, "the term sequence below is written out for four terms");
         MxA a[2][WM];
 #pragma unroll
         for (int m = 0; m < WM; m++) a[0][m] = read_a(m, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int e = 0; e < NT; e++) {
-            const int cu = e & 1, nx = cu ^ 1;
-            if (e + 1 < NT) {
+        for (int m = 0; m < WM; m++) a[1][m] = read_a(m, 1);
+        mma_term(std::integral_constant<int, 0>{}, a[0]);
 #pragma unroll
-                for (int m = 0; m < WM; m++) a[nx][m] = read_a(m, e + 1);
-            }
+        for (int m = 0; m < WM; m++) a[0][m] = read_a(m, 2);
+        mma_term(std::integral_constant<int, 1>{}, a[1]);
 #pragma unroll
-            for (int m = 0; m < WM; m++)
-#pragma unroll
-                for (int i = 0; i < WN; i++) acc[m][i] = mfma_mx(a[cu][m], b[i], sb[i], acc[m][i]);
-        }
-        constexpr int NA = WM * 2, NM = WM * WN;
+        for (int m = 0; m < WM; m++) a[1][m] = read_a(m, 3);
+        mma_term(std::integral_constant<int, 2>{}, a[0]);
+        mma_term(std::integral_constant<int, 3>{}, a[1]);
+        constexpr int NA = WM * 2, NM = WM * WN;  // two LDS reads per A operand
 #pragma unroll
         for (int e = 0; e < NT; e++) {
             if (e + 1 < NT) {
@@ -878,7 +911,7 @@ void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, flo
 
 bool mx_gemm_takes(const TileView &w, int64_t n) { return w.tf == TF_MX4 && w.fast && w.mx && n >= 128; }
 
-size_t mx_frag_bytes(int64_t n, int64_t ldst) { return (size_t)((n + 15) / 16) * ldst * MX_TERMS * 2048; }
+size_t mx_frag_bytes(int64_t n, int64_t ldst) { return (size_t)((n + 15) / 16) * ldst * MX_BLOCK; }
 
 void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
                      int64_t ldst, hipStream_t s) {

@@ -91,8 +91,11 @@ struct TileView {
     // MXFP4 (fast tensors): the codes once more in the operand order of the
     // scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4): per 16-row group and
     // 128-column unit, lane l holds the 16 source bytes of row l % 16,
-    // columns 32 * (l / 16) .. +32 (one E8M0 block)
+    // columns 32 * (l / 16) .. +32 (one E8M0 block), followed by the scales in
+    // the same order: per group and unit 64 bytes, byte l = the E8M0 of that
+    // lane's block (mx_scales)
     const uint8_t *mx;
+    const uint8_t *mx_scales;
 };
 
 // Device memory helpers (all on the context stream).
@@ -127,6 +130,7 @@ struct ditch_hip_tensor {
     void *zero = nullptr;
     void *side = nullptr;  // owned side words (FP8, INT4); MXFP4 aliases scale
     void *mx = nullptr;    // MXFP4 codes in scaled-MFMA order
+    void *mx_scales = nullptr;
     uint64_t bytes = 0;
 };
 
@@ -185,7 +189,7 @@ void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs
 // gate/up in one product: act(x gate^T) * (x up^T) into f32 rows [n][rows]
 // (out, may be NULL) and/or the A fragments of the next product (xs_out)
 // MXFP4 large batches on the scaled MFMA (fp6 activation terms x the fp4
-// codes): fragments [ceil(n/16)][ldst][4 terms] x 2 KiB, ldst >= cols / 128.
+// codes): fragments [ceil(n/16)][ldst] x 6400 B, ldst >= cols / 128.
 bool mx_gemm_takes(const TileView &w, int64_t n);
 size_t mx_frag_bytes(int64_t n, int64_t ldst);
 void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,

@@ -360,6 +360,19 @@ __global__ void mx_native_kernel(const uint8_t *src, int64_t rows, int64_t cols,
     }
 }
 
+// Their E8M0 scales in the same order: (g, u) -> 64 bytes, byte l = the scale
+// of row 16 g + l % 16, column block 4 u + l / 16 (zero past the matrix).
+__global__ void mx_scales_kernel(const uint8_t *scale, int64_t rows, int64_t kt, uint8_t *out, int64_t groups,
+                                 int64_t units) {
+    const int64_t total = groups * units * 64;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i % 64);
+        const int64_t unit = i / 64, g = unit / units, u = unit % units;
+        const int64_t n = g * 16 + lane % 16, b = u * 4 + lane / 16;
+        out[i] = (n < rows && b < kt) ? scale[n * kt + b] : 0;
+    }
+}
+
 // Side words of the tiled GEMM (TileView::side). FP8: the scale grid as f32
 // (exact for f32, f16, bf16 and finite E8M0 scales).
 __global__ void fp8_side_kernel(const void *scale, int32_t scale_type, uint32_t *out, int64_t total) {
@@ -637,6 +650,7 @@ void free_tensor(ditch_hip_tensor *t) {
     dev_free(t->zero);
     dev_free(t->side);
     dev_free(t->mx);
+    dev_free(t->mx_scales);
     delete t;
 }
 
@@ -777,7 +791,12 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             const int64_t total_mx = a.groups_n * v.units_k * 64;
             hipLaunchKernelGGL(mx_native_kernel, dim3(grid_for(total_mx)), dim3(256), 0, s, st.v.data, v.rows, v.cols,
                                (uint8_t *)t->mx, a.groups_n, v.units_k);
+            t->mx_scales = dev_alloc(total_mx);
+            t->bytes += total_mx;
+            hipLaunchKernelGGL(mx_scales_kernel, dim3(grid_for(total_mx)), dim3(256), 0, s, (const uint8_t *)st.v.scale,
+                               v.rows, v.cols / 32, (uint8_t *)t->mx_scales, a.groups_n, v.units_k);
             v.mx = (const uint8_t *)t->mx;
+            v.mx_scales = (const uint8_t *)t->mx_scales;
         } else if (v.fast && tf == TF_FP8) {
             int64_t total = ((int64_t)w->scale_rows + 1) * v.scale_cols;
             t->side = dev_alloc(total * 4);

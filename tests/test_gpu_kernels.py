@@ -320,8 +320,8 @@ def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
     t = dev.upload(w)
     try:
         fb = t.frag_bytes(n)
-        if kind == "mxfp4":  # [n/16][cols/128][4 terms] x 2 KiB
-            assert fb == -(-n // 16) * -(-cols // 128) * 4 * 2048
+        if kind == "mxfp4":  # [n/16][cols/128] x 6400 B (four fp6 terms + scales)
+            assert fb == -(-n // 16) * -(-cols // 128) * 6400
         else:  # [n/16][cols/128 * 4 k tiles][2 terms] x 1 KiB
             assert fb == -(-n // 16) * (-(-cols // 128) * 4) * 2 * 1024
         assert t.frag_bytes(64) == 0
