@@ -244,15 +244,21 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
 void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, const MatmulEpilogue &ep,
                        hipStream_t s, DevBuf *ws) {
     if (n <= 0 || w.rows <= 0) return;
-    if (x.f32 && !ep.exact && mx_gemm_takes(w, n)) {
-        launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
-        return;
+    if (!ep.exact && mx_gemm_takes(w, n)) {
+        if (x.xm && x.ldst >= w.units_k) {
+            launch_mx_gemm(w, out, w.rows, x.xm, x.ldst, n, ep, s);
+            return;
+        }
+        if (x.f32) {
+            launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
+            return;
+        }
     }
     if (x.xs && !ep.exact && tile_gemm_takes(w, n) && x.ldk >= split_k_tiles(w)) {
         launch_tile_gemm(w, out, w.rows, x.xs, x.ldk, n, 2, ep, s);
         return;
     }
-    DITCH_CHECK(x.f32 != nullptr, DITCH_INVALID_ARGUMENT, "product: no f32 rows for a weight the tiled kernel does not take");
+    DITCH_CHECK(x.f32 != nullptr, DITCH_INVALID_ARGUMENT, "product: no activation form the weight's product takes");
     launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
 }
 

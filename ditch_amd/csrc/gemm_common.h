@@ -312,4 +312,75 @@ __device__ __forceinline__ bool select_segment(GemmParams &p, int64_t m0) {
 }
 
 
+// ---------------------------------------------------------------------------
+// MX (scaled-MFMA) activation fragments
+
+// Activation fragments: per 16-token block and 128-k stage a 6400-byte block
+// (lane l: token 16 m16 + l % 16, k = 128 stage + 32 (l / 16) .. +32; the
+// 32 fp6 codes of a term are 6 dwords, code j at bits 6j..6j+5):
+//     [term][lane] 16 B   dwords 0..3 of each term       4 x 1 KiB
+//     [term][lane] 8 B    dwords 4..5                    4 x 512 B
+//     [lane] 4 B          E8M0 byte of term e in byte e  256 B
+// so that every part is read with one conflict-free LDS load per lane and
+// copied in whole KiB (the last 256 B apart).
+
+constexpr int MX_TERMS = 4;
+constexpr int MX_BLOCK = 6400;  // bytes per 16 tokens x 128 k
+
+// Writes the MX_TERMS fp6 terms of the 32 values r (one E8M0 block) into lane
+// slot `slot` of a fragment block (slot = token % 16 + 16 * block within the
+// stage); r is left holding the remainder. A NaN or infinity among the 32
+// values gives the slot E8M0 255 (NaN) in every term, so that every product
+// reading it is NaN.
+__device__ __forceinline__ void mx_write_slot(float (&r)[32], uint8_t *blk, int slot) {
+    typedef float v16f_t __attribute__((ext_vector_type(16)));
+    u32x4 *lo = (u32x4 *)blk + slot;                // + 64 e
+    uint2 *hi = (uint2 *)(blk + 4096) + slot;        // + 64 e
+    uint32_t *scw = (uint32_t *)(blk + 6144) + slot;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 32; j++) finite = finite && __builtin_isfinite(r[j]);
+    if (!finite) {
+#pragma unroll
+        for (int e = 0; e < MX_TERMS; e++) {
+            lo[64 * e] = u32x4{0, 0, 0, 0};
+            hi[64 * e] = make_uint2(0, 0);
+        }
+        *scw = 0xffffffffu;
+        return;
+    }
+    uint32_t scales = 0;
+#pragma unroll
+    for (int e = 0; e < MX_TERMS; e++) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(r[j]));
+        // scale 2^x with m / 2^x in (3.75, 7.5]: m = f 2^E, f in [1, 2)
+        const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+        int x = (int)(mb >> 23) - 129 + ((mb & 0x7fffffu) > 0x700000u ? 1 : 0);  // E - 2 (+1 when f > 1.875)
+        const bool live = m > 0.f && x >= -126;  // remainders under 7.5 * 2^-127 stay in r: codes 0
+        x = live ? x : -127;
+        scales |= (uint32_t)(x + 127) << (8 * e);
+        const float sc = __builtin_bit_cast(float, (uint32_t)(live ? x + 127 : 127) << 23);
+        // v_cvt_scalef32_2xpk16_fp6_f32: round-to-nearest-even e2m3 of v / sc,
+        // code 2j from the first operand's element j and 2j + 1 from the
+        // second's; the reverse conversion gives code * sc exactly, so the
+        // subtraction below is exact (the value and its rounding are within
+        // a factor of two, or the code is zero)
+        v16f_t ev, od;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            ev[j] = live ? r[2 * j] : 0.f;
+            od[j] = live ? r[2 * j + 1] : 0.f;
+        }
+        const auto d = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc);
+        const auto back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(d, sc);
+#pragma unroll
+        for (int j = 0; j < 32; j++) r[j] = __fsub_rn(r[j], back[j]);
+        lo[64 * e] = u32x4{(uint32_t)d[0], (uint32_t)d[1], (uint32_t)d[2], (uint32_t)d[3]};
+        hi[64 * e] = make_uint2((uint32_t)d[4], (uint32_t)d[5]);
+    }
+    *scw = scales;
+}
+
 }  // namespace ditch

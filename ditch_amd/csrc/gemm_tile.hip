@@ -482,37 +482,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 // MFMA runs at four times the bf16 rate: four terms cost what one bf16 term
 // does, against two bf16 terms on the bf16 path.
 //
-// Activation fragments: per 16-token block and 128-k stage a 6400-byte block
-// (lane l: token 16 m16 + l % 16, k = 128 stage + 32 (l / 16) .. +32; the
-// 32 fp6 codes of a term are 6 dwords, code j at bits 6j..6j+5):
-//     [term][lane] 16 B   dwords 0..3 of each term       4 x 1 KiB
-//     [term][lane] 8 B    dwords 4..5                    4 x 512 B
-//     [lane] 4 B          E8M0 byte of term e in byte e  256 B
-// so that every part is read with one conflict-free LDS load per lane and
-// copied in whole KiB (the last 256 B apart).
-
-constexpr int MX_TERMS = 4;
-constexpr int MX_BLOCK = 6400;  // bytes per 16 tokens x 128 k
-
 struct MxSplitParams {
     u32x4 *xm;
     const float *x;
     const int32_t *row_index;
     int64_t n, ldx, K, ldst, m16;
 };
-
-// |v| <= 7.5 to the nearest e2m3 value (ties to even); returns the code
-// magnitude bits and sets q to the value
-__device__ __forceinline__ uint32_t e2m3_rne(float a, float &q) {
-    q = a < 2.f ? __builtin_rintf(a * 8.f) * 0.125f : a < 4.f ? __builtin_rintf(a * 4.f) * 0.25f
-                                                                : __builtin_rintf(a * 2.f) * 0.5f;
-    uint32_t c;
-    if (q < 1.f) c = (uint32_t)(q * 8.f);
-    else if (q < 2.f) c = 8u | (uint32_t)((q - 1.f) * 8.f);
-    else if (q < 4.f) c = 16u | (uint32_t)((q * 0.5f - 1.f) * 8.f);
-    else c = 24u | (uint32_t)((q * 0.25f - 1.f) * 8.f);
-    return c;
-}
 
 __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -540,59 +515,7 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
 #pragma unroll
         for (int j = 0; j < 32; j++) r[j] = 0.f;
     }
-    uint8_t *blk = (uint8_t *)p.xm + f * MX_BLOCK;
-    u32x4 *lo = (u32x4 *)blk + lane;                 // + 64 e
-    uint2 *hi = (uint2 *)(blk + 4096) + lane;         // + 64 e
-    uint32_t *scw = (uint32_t *)(blk + 6144) + lane;
-    bool finite = true;
-#pragma unroll
-    for (int j = 0; j < 32; j++) finite = finite && __builtin_isfinite(r[j]);
-    if (!finite) {
-        // a NaN or infinity in the block: E8M0 255 (NaN) makes every product
-        // that reads it NaN
-#pragma unroll
-        for (int e = 0; e < MX_TERMS; e++) {
-            lo[64 * e] = u32x4{0, 0, 0, 0};
-            hi[64 * e] = make_uint2(0, 0);
-        }
-        *scw = 0xffffffffu;
-        return;
-    }
-    uint32_t scales = 0;
-#pragma unroll
-    for (int e = 0; e < MX_TERMS; e++) {
-        float m = 0.f;
-#pragma unroll
-        for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(r[j]));
-        // scale 2^x with m / 2^x in (3.75, 7.5]: m = f 2^E, f in [1, 2)
-        int x = -127;
-        if (m > 0.f) {
-            const uint32_t b = __builtin_bit_cast(uint32_t, m);
-            const int E = (int)(b >> 23) - 127;  // m is normal past the first term's subnormal-free range
-            const uint32_t frac = b & 0x7fffffu;
-            x = E - 2 + (frac > 0x700000u ? 1 : 0);  // f > 1.875
-            x = x < -127 ? -127 : x;
-        }
-        const float sc = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(x + 127) << 23) : __builtin_bit_cast(float, 0x00400000u);
-        const float inv = x >= -126 ? __builtin_bit_cast(float, (uint32_t)(127 - x) << 23) : 0.f;
-        uint32_t d[6] = {0, 0, 0, 0, 0, 0};
-        scales |= (uint32_t)(x + 127) << (8 * e);
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-            float q;
-            const float a = x >= -126 && x <= 126 ? fabsf(r[j]) * inv : 0.f;
-            const uint32_t mag = e2m3_rne(a, q);
-            const uint32_t sgn = r[j] < 0.f ? 32u : 0u;
-            const uint32_t code = q > 0.f ? (mag | sgn) : 0u;
-            r[j] = __fsub_rn(r[j], copysignf(q, r[j]) * sc);
-            const int bit = 6 * j;
-            d[bit >> 5] |= code << (bit & 31);
-            if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
-        }
-        lo[64 * e] = u32x4{d[0], d[1], d[2], d[3]};
-        hi[64 * e] = make_uint2(d[4], d[5]);
-    }
-    *scw = scales;
+    mx_write_slot(r, (uint8_t *)p.xm + f * MX_BLOCK, lane);
 }
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
@@ -621,10 +544,14 @@ __device__ __forceinline__ floatx4 mfma_mx(const MxA &a, int sa, const u32x4 &b,
 // The scaled-MFMA product: the pipeline of tile_gemm_kernel (copies by the
 // younger wave of each SIMD, two stage buffers, one barrier a stage) with a
 // stage of 128 k: A = WM fragment blocks of 6400 B, B = one 1 KiB unit per
-// row group (MXFP4 codes in MFMA order) and its 64 scale bytes.
-template <int WGN, int WM, int WN>
+// row group (MXFP4 codes in MFMA order) and its 64 scale bytes. GLU: a wave's
+// first WN/2 row groups are gate rows (w), the others the same rows of the up
+// projection (w2); the epilogue writes act(gate) * up as f32 rows and/or as
+// the MX fragments of the next product.
+template <int WGN, int WM, int WN, bool GLU>
 __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     constexpr int WAVES = WGN, NT = MX_TERMS;
+    constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
     constexpr int AQ = MX_BLOCK / 16;                            // u32x4 per A block
     __shared__ u32x4 As0[WM * AQ], As1[WM * AQ];                  // [m][block]
     __shared__ u32x4 Bs0[WAVES * WN * 64], Bs1[WAVES * WN * 64];  // [wave][group][lane]
@@ -635,7 +562,7 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
     const int64_t groups = (w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)nt * (WN * WGN) + wave * WN;
+    const int64_t g0 = (int64_t)nt * (OG * WGN) + wave * OG;
     const int64_t m16_0 = (int64_t)mt * WM, m16_n = (p.n + 15) / 16;
     const int64_t S = w.units_k;  // stages: one 128-column unit each
 
@@ -663,19 +590,23 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
 #pragma unroll
     for (int j = 0; j < CAS; j++) as_[j] = a_block((ck + CW * j) % WM) + 384;
     auto group_of = [&](int wq, int i) {
-        const int64_t gi = (int64_t)nt * (WN * WGN) + wq * WN + i;
+        const int64_t gi = (int64_t)nt * (OG * WGN) + wq * OG + (i % OG);
         return gi < groups ? gi : groups - 1;
     };
-    int64_t bsrc[CB];
+    const u32x4 *bsrc[CB];
 #pragma unroll
     for (int j = 0; j < CB; j++) {
-        const int q = ck + CW * j;
-        bsrc[j] = group_of(q / WN, q % WN) * S * 64;
+        const int q = ck + CW * j, i = q % WN;
+        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        bsrc[j] = (const u32x4 *)wi.mx + group_of(q / WN, i) * S * 64;
     }
     const uint32_t *bss[CBS];
 #pragma unroll
-    for (int j = 0; j < CBS; j++)  // lane l: dword l % 16 of group l / 16's 64 bytes
-        bss[j] = (const uint32_t *)(w.mx_scales + group_of(ck + CW * j, lane >> 4) * S * 64) + (lane & 15);
+    for (int j = 0; j < CBS; j++) {  // lane l: dword l % 16 of group l / 16's 64 bytes
+        const int i = lane >> 4;
+        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        bss[j] = (const uint32_t *)(wi.mx_scales + group_of(ck + CW * j, i) * S * 64) + (lane & 15);
+    }
 
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
         if (!copier) return;
@@ -695,7 +626,7 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
         }
 #pragma unroll
         for (int j = 0; j < CB; j++)
-            __builtin_amdgcn_global_load_lds((const void *)((const u32x4 *)w.mx + bsrc[j] + s * 64 + lane),
+            __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + s * 64 + lane),
                                              (lds_void *)&Bs[(ck + CW * j) * 64], 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < CBS; j++)
@@ -784,14 +715,51 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     if (s < S) step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
 
     const int kq = lane >> 4;
+    if constexpr (!GLU) {
 #pragma unroll
-    for (int m = 0; m < WM; m++)
+        for (int m = 0; m < WM; m++)
 #pragma unroll
-        for (int i = 0; i < WN; i++) {
-            const int64_t row = (g0 + i) * 16 + (lane & 15);
+            for (int i = 0; i < WN; i++) {
+                const int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+                for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+            }
+    } else {
+        // y = act(gate) * up (tensor.gatedActivation) for the wave's 32
+        // columns (one E8M0 block of the next product's k) and 16 WM tokens,
+        // through a per-wave LDS patch [m][16 tokens][32 columns] (the B
+        // stage buffers are idle: the last stage ended with a barrier); then
+        // lane l splits token l % 16 of block m = l / 16 into its slot
+        static_assert(OG == 2 && WM * 16 == 64 && WAVES <= 8, "one 32-column block per wave, a token block per lane group");
+        float *patch = (float *)(wave < 4 ? Bs0 : Bs1) + (wave % 4) * (WM * 16 * 32);
+#pragma unroll
+        for (int m = 0; m < WM; m++) {
+#pragma unroll
+            for (int i = 0; i < OG; i++) {
+                const int64_t col = (g0 + i) * 16 + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int64_t tok = (m16_0 + m) * 16 + 4 * kq + r;
+                    float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
+                    if (tok >= p.n || col >= w.rows) y = 0.f;
+                    else if (p.out) p.out[tok * p.ldo + col] = y;
+                    patch[(m * 16 + 4 * kq + r) * 32 + i * 16 + (lane & 15)] = y;
+                }
+            }
         }
+        const int64_t kb = (g0 * 16) / 32;  // the next product's E8M0 block of these columns
+        const int64_t mblk = m16_0 + (lane >> 4);
+        if (p.xs_out && kb / 4 < p.ldk_out) {
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            float r[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) r[j] = patch[(lane >> 4) * 512 + (lane & 15) * 32 + j];
+            if (mblk < m16_n)
+                mx_write_slot(r, (uint8_t *)p.xs_out + (mblk * p.ldk_out + kb / 4) * MX_BLOCK,
+                              (lane & 15) + 16 * (int)(kb % 4));
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -922,6 +890,16 @@ void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t
     DITCH_TRY_HIP(hipGetLastError());
 }
 
+template <bool GLU>
+static void launch_mx(TileGemmParams &p, hipStream_t s) {
+    constexpr int WGN = 8, WM = 4, WN = 4, OG = GLU ? WN / 2 : WN;
+    p.tiles_m = (int)((p.n + 16 * WM - 1) / (16 * WM));
+    p.tiles_n = (int)((p.w.rows + 16 * OG * WGN - 1) / (16 * OG * WGN));
+    hipLaunchKernelGGL((mx_gemm_kernel<WGN, WM, WN, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(WGN * 64), 0, s,
+                       p);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
 void launch_mx_gemm(const TileView &w, float *out, int64_t ldo, const void *xm, int64_t ldst, int64_t n,
                     const MatmulEpilogue &ep, hipStream_t s) {
     DITCH_CHECK(mx_gemm_takes(w, n), DITCH_INVALID_ARGUMENT, "scaled-MFMA product: not an MXFP4 tensor it takes");
@@ -940,11 +918,31 @@ void launch_mx_gemm(const TileView &w, float *out, int64_t ldo, const void *xm, 
     p.delta_xa = ep.delta_xa;
     p.delta_rank = ep.delta_rank;
     p.delta_stride = ep.delta_rank;
-    constexpr int WGN = 8, WM = 4, WN = 4;
-    p.tiles_m = (int)((n + 16 * WM - 1) / (16 * WM));
-    p.tiles_n = (int)((w.rows + 16 * WN * WGN - 1) / (16 * WN * WGN));
-    hipLaunchKernelGGL((mx_gemm_kernel<WGN, WM, WN>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(WGN * 64), 0, s, p);
-    DITCH_TRY_HIP(hipGetLastError());
+    launch_mx<false>(p, s);
+}
+
+bool mx_glu_takes(const TileView &g, const TileView &u, int64_t n) {
+    return mx_gemm_takes(g, n) && mx_gemm_takes(u, n) && g.rows == u.rows && g.cols == u.cols && g.rows % 32 == 0;
+}
+
+void launch_mx_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xm_out, int64_t ldst_out,
+                   const void *xm, int64_t ldst, int64_t n, hipStream_t s) {
+    DITCH_CHECK(mx_glu_takes(gate, up, n), DITCH_INVALID_ARGUMENT, "scaled-MFMA gate/up: shapes or formats it does not take");
+    DITCH_CHECK(ldst >= gate.units_k, DITCH_INVALID_ARGUMENT, "MX fragments shorter than K");
+    DITCH_CHECK(!xm_out || ldst_out * 128 >= gate.rows, DITCH_INVALID_ARGUMENT, "MX output fragments shorter than the rows");
+    TileGemmParams p{};
+    p.w = gate;
+    p.w2 = up;
+    p.act = act;
+    p.xs = (const u32x4 *)xm;
+    p.kt_total = gate.units_k;
+    p.ldk = ldst;
+    p.xs_out = (u32x4 *)xm_out;
+    p.ldk_out = ldst_out;
+    p.out = out;
+    p.ldo = gate.rows;
+    p.n = n;
+    launch_mx<true>(p, s);
 }
 
 }  // namespace ditch

@@ -196,6 +196,12 @@ void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t
                      int64_t ldst, hipStream_t s);
 void launch_mx_gemm(const TileView &w, float *out, int64_t ldo, const void *xm, int64_t ldst, int64_t n,
                     const MatmulEpilogue &ep, hipStream_t s);
+// act(x gate^T) * (x up^T) in one scaled-MFMA pass: f32 rows [n][rows] (out,
+// optional) and/or the MX fragments of a product over them (xm_out, ldst_out
+// stages of 128 columns; optional).
+bool mx_glu_takes(const TileView &gate, const TileView &up, int64_t n);
+void launch_mx_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xm_out, int64_t ldst_out,
+                   const void *xm, int64_t ldst, int64_t n, hipStream_t s);
 bool tile_glu_takes(const TileView &gate, const TileView &up, int64_t n);
 void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, float *out, void *xs_out,
                      int64_t ldk_out, const void *xs, int64_t ldk, int64_t n, hipStream_t s);
@@ -204,8 +210,10 @@ void launch_tile_glu(const TileView &gate, const TileView &up, uint32_t act, flo
 // (xt = 2 terms, stride ldk), or both.
 struct Act {
     const float *f32 = nullptr;
-    const void *xs = nullptr;
+    const void *xs = nullptr;  // bf16-term fragments, ldk k tiles per 16 tokens
     int64_t ldk = 0;
+    const void *xm = nullptr;  // MX fragments, ldst stages per 16 tokens
+    int64_t ldst = 0;
 };
 void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, const MatmulEpilogue &ep,
                        hipStream_t s, DevBuf *ws);
@@ -245,6 +253,8 @@ void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
                     float eps, int gemma, hipStream_t s, const int64_t *row_index = nullptr, int64_t n_src = 0);
 // RMS norm into the tiled GEMM's A fragments (and f32 rows when out != NULL)
+void launch_rmsnorm_split_mx(void *xm, int64_t ldst, float *out, const float *x, const float *w, int64_t wlen,
+                             int64_t n, int64_t len, float eps, int gemma, hipStream_t s);
 void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, const float *w, int64_t wlen, int64_t n,
                           int64_t len, float eps, int gemma, hipStream_t s);
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,

@@ -632,6 +632,8 @@ static void mm_act(ditch_hip_model *m, const Mat &mt, float *out, const Act &x, 
 // the bf16 tiled kernel takes it (MXFP4 included: its producers write bf16
 // terms; given f32 rows an MXFP4 product takes the scaled-MFMA path).
 static bool frag_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && tile_gemm_takes(mt.t->v, n); }
+// A product that reads MX fragments alone (MXFP4 on the scaled MFMA).
+static bool mx_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && mx_gemm_takes(mt.t->v, n); }
 
 // Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).
 static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, int64_t n, hipStream_t s) {
@@ -764,7 +766,14 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
     for (int64_t li = 0; li < (int64_t)c.layers; li++) {
         Layer &L = m->layers[li];
         Act hact{h, nullptr, 0};
-        if (frags) {
+        const bool mx_qkv = frags && !c.mla && mx_only(L.q, n) && mx_only(L.k, n) && mx_only(L.v, n) &&
+                            L.q.t->v.units_k == L.k.t->v.units_k && L.q.t->v.units_k == L.v.t->v.units_k;
+        if (mx_qkv) {
+            const int64_t ldst = L.q.t->v.units_k;
+            void *hm = m->hs.get<uint8_t>(mx_frag_bytes(n, ldst));
+            launch_rmsnorm_split_mx(hm, ldst, nullptr, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
+            hact = Act{nullptr, nullptr, 0, hm, ldst};
+        } else if (frags) {
             const bool f32_needed = c.mla || !frag_only(L.q, n) || !frag_only(L.k, n) || !frag_only(L.v, n);
             void *hs = m->hs.get<uint8_t>(split_bytes_ldk(n, ldk_h, 2));
             launch_rmsnorm_split(hs, ldk_h, f32_needed ? h : nullptr, x, L.attn_norm.p, L.attn_norm.len, n, hidden,
@@ -826,7 +835,7 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0};
         const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
         Act aact{att, nullptr, 0};
-        if (frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n)) {
+        if (frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n) && !mx_only(L.o, n)) {
             aa.ldk = split_ldk(nh * vd);
             aa.xs = m->atts.get<uint8_t>(split_bytes_ldk(n, aa.ldk, 2));
             aact = Act{att, aa.xs, aa.ldk};
@@ -836,6 +845,21 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         DITCH_TRY_HIP(hipGetLastError());
         mm_act(m, L.o, x, aact, n, nullptr, 1, s);  // x += o(att)
         const bool moe_layer = c.n_experts && m->moe_layers[li];
+        // MXFP4 gate/up in one scaled-MFMA product whose epilogue applies the
+        // activation and writes the down projection's MX fragments
+        const bool mx_glu = frags && !moe_layer && L.gate.ok() && L.up.ok() && L.gate.rank == 0 && L.up.rank == 0 &&
+                            mx_glu_takes(L.gate.t->v, L.up.t->v, n) && L.gate.t->v.rows % 128 == 0 &&
+                            mx_only(L.down, n) && L.down.t->v.units_k * 128 == L.gate.t->v.rows;
+        if (mx_glu) {
+            const int64_t ldst = L.gate.t->v.units_k, ldst_i = L.down.t->v.units_k;
+            void *hm = m->hs.get<uint8_t>(mx_frag_bytes(n, ldst));
+            launch_rmsnorm_split_mx(hm, ldst, nullptr, x, L.ffn_norm.p, L.ffn_norm.len, n, hidden, c.rms_eps, 0, s);
+            void *am = m->acts.get<uint8_t>(mx_frag_bytes(n, ldst_i));
+            launch_mx_glu(L.gate.t->v, L.up.t->v, 0, nullptr, am, ldst_i, hm, ldst, n, s);
+            mm_act(m, L.down, x, Act{nullptr, nullptr, 0, am, ldst_i}, n, nullptr, 1, s);  // x += down(act)
+            capture(li + 1);
+            continue;
+        }
         // gate and up in one tiled product whose epilogue applies the
         // activation and writes the down projection's fragments
         const bool glu = frags && !moe_layer && L.gate.ok() && L.up.ok() && L.gate.rank == 0 && L.up.rank == 0 &&

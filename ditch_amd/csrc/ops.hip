@@ -166,6 +166,90 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(u32x4 *xs, int64_t l
     }
 }
 
+// RMSNorm of 16 rows per block written as the MX fragments of a scaled-MFMA
+// product (and, when `out`, as f32 rows): one thread per lane slot (a
+// token's 32-column E8M0 block).
+__global__ __launch_bounds__(256) void rmsnorm_split_mx_kernel(uint8_t *xm, int64_t ldst, float *out, const float *x,
+                                                               const float *w, int64_t wlen, int64_t len, float eps,
+                                                               int gemma, int64_t n) {
+    __shared__ float inv_s[16];
+    const int64_t m16 = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool vec = (len % 4) == 0;
+    for (int rr = 0; rr < 4; rr++) {
+        const int row = wave * 4 + rr;
+        const int64_t r = m16 * 16 + row;
+        float ss = 0.f;
+        if (r < n) {
+            const float *xr = x + r * len;
+            if (vec) {
+                for (int64_t i = 4 * lane; i < len; i += 256) {
+                    float4 v = *(const float4 *)(xr + i);
+                    ss = __builtin_fmaf(v.x, v.x, ss);
+                    ss = __builtin_fmaf(v.y, v.y, ss);
+                    ss = __builtin_fmaf(v.z, v.z, ss);
+                    ss = __builtin_fmaf(v.w, v.w, ss);
+                }
+            } else {
+                for (int64_t i = lane; i < len; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+        if (lane == 0)
+            inv_s[row] = r < n ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps))) : 0.f;
+    }
+    __syncthreads();
+    for (int64_t q = threadIdx.x; q < ldst * 64; q += 256) {
+        const int64_t st = q >> 6;
+        const int l = (int)(q & 63), row = l & 15;
+        const int64_t r = m16 * 16 + row;
+        const int64_t k0 = st * 128 + 32 * (l >> 4);
+        const float inv = inv_s[row];
+        float v[32];
+        const bool full = r < n && vec && k0 + 32 <= len;
+#pragma unroll
+        for (int j = 0; j < 32; j += 4) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (full) a = *(const float4 *)(x + r * len + k0 + j);
+            else {
+                float t[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) t[u] = (r < n && k0 + j + u < len) ? x[r * len + k0 + j + u] : 0.f;
+                a = make_float4(t[0], t[1], t[2], t[3]);
+            }
+            if (wlen > 0 && (wlen % 4) == 0 && k0 + j + 4 <= wlen) b = *(const float4 *)(w + k0 + j);
+            else if (wlen > 0) {
+                float t[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) t[u] = k0 + j + u < wlen ? w[k0 + j + u] : 1.f;
+                b = make_float4(t[0], t[1], t[2], t[3]);
+            }
+            const float xa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float y = 0.f;
+                if (r < n && k0 + j + u < len) {
+                    y = __fmul_rn(xa[u], inv);
+                    if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wb[u]) : wb[u]);
+                }
+                v[j + u] = y;
+            }
+        }
+        if (out && r < n) {
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) *(float4 *)(out + r * len + k0 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 32; j++)
+                    if (k0 + j < len) out[r * len + k0 + j] = v[j];
+            }
+        }
+        mx_write_slot(v, xm + (m16 * ldst + st) * MX_BLOCK, l);
+    }
+}
+
 __global__ void layernorm_kernel(float *out, const float *x, const float *w, int64_t wlen, const float *bias,
                                  int64_t len, float eps, int one_plus) {
     __shared__ float sh[8];
@@ -371,6 +455,14 @@ void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, con
     DITCH_CHECK(ldk * 32 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split: fragments shorter than the row");
     hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (u32x4 *)xs, ldk, out, x,
                        w, wlen, len, eps, gemma, n);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_rmsnorm_split_mx(void *xm, int64_t ldst, float *out, const float *x, const float *w, int64_t wlen,
+                             int64_t n, int64_t len, float eps, int gemma, hipStream_t s) {
+    if (n <= 0) return;
+    DITCH_CHECK(ldst * 128 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split_mx: fragments shorter than the row");
+    hipLaunchKernelGGL(rmsnorm_split_mx_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (uint8_t *)xm, ldst,
+                       out, x, w, wlen, len, eps, gemma, n);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,

@@ -105,6 +105,27 @@ def test_synthetic_forward_matches_oracle(dev, ref, name):
     check_parity(ref, rg, lg, rc, lc, name)
 
 
+LARGE = ["dense_mxfp4", "dense_fp8", "dense_int4", "dense_bf16"]
+
+
+@pytest.mark.parametrize("name", LARGE)
+def test_synthetic_forward_large_batch_matches_oracle(dev, ref, name):
+    """294 rows: every product on the large-batch kernels, with the fused
+    producers (RMSNorm and the gate/up epilogue writing the next product's
+    fragments; fp6 terms and the scaled MFMA for MXFP4)."""
+    spec = SYNTH[name]()
+    tokens, rows, last = mg.batch(3, [130, 64, 100], spec.config["vocab"], seed=len(name) + 7)
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    check_parity(ref, rg, lg, rc, lc, name)
+
+
 def test_edit_then_forward(dev, ref):
     """Rank-2 none-mode edit (abliterate.zig:264-280) of o_proj, down_proj and
     every expert down_proj, applied in the matmul epilogue, against the
