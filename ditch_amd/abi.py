@@ -119,6 +119,12 @@ class Row(C.Structure):
     _fields_ = [("b", C.c_uint32), ("pos", C.c_uint32)]
 
 
+class ExpertCacheStats(C.Structure):
+    """`ditch_expert_cache_stats` (expert_cache.Stats)."""
+    _fields_ = [(n, C.c_uint64) for n in ("capacity", "slots", "resident", "hits", "misses", "prefetched",
+                                          "bytes_read", "evictions", "slot_bytes")]
+
+
 P = C.c_void_p
 U64 = C.c_uint64
 I32 = C.c_int32
@@ -157,6 +163,8 @@ PROTOTYPES = {
     "ditch_hip_model_free": (None, [P]),
     "ditch_hip_model_set": (I32, [P, I32, I32, I32, P]),
     "ditch_hip_model_set_delta": (I32, [P, I32, I32, I32, U64, P, P]),
+    "ditch_hip_model_set_expert_cache": (I32, [P, U64]),
+    "ditch_hip_model_expert_cache_stats": (I32, [P, P]),
     "ditch_hip_model_reset_deltas": (I32, [P]),
     "ditch_hip_model_bytes": (U64, [P]),
     "ditch_hip_forward": (I32, [P, P, P, U64, P, U64, P, P, U64, P]),

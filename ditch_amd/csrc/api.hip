@@ -414,6 +414,35 @@ int32_t ditch_hip_model_set_delta(ditch_hip_model *m, int32_t layer, int32_t slo
     });
 }
 
+int32_t ditch_hip_model_set_expert_cache(ditch_hip_model *m, uint64_t bytes) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        for (const auto &L : m->layers)
+            for (const auto *vec : {&L.eg, &L.eu, &L.ed})
+                for (const auto &mt : *vec)
+                    DITCH_CHECK(!mt.ok(), DITCH_INVALID_ARGUMENT, "expert cache: experts were registered before");
+        DITCH_CHECK(!m->cache, DITCH_INVALID_ARGUMENT, "expert cache already built");
+        m->expert_budget = bytes;
+    });
+}
+
+int32_t ditch_hip_model_expert_cache_stats(const ditch_hip_model *m, ditch_expert_cache_stats *out) {
+    if (!m || !out) return DITCH_INVALID_ARGUMENT;
+    *out = ditch_expert_cache_stats{};
+    out->capacity = m->expert_budget;
+    if (const ditch::ExpertCache *c = m->cache) {
+        out->slots = c->slots.size();
+        for (const auto &sl : c->slots) out->resident += sl.layer >= 0;
+        out->hits = c->hits;
+        out->misses = c->misses;
+        out->prefetched = c->prefetches;
+        out->bytes_read = c->bytes_read;
+        out->evictions = c->evictions;
+        out->slot_bytes = c->slot_bytes;
+    }
+    return DITCH_OK;
+}
+
 int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m) {
     if (!m) return DITCH_INVALID_ARGUMENT;
     return guarded(m->h, [&] { model_reset_deltas(m); });

@@ -1,0 +1,260 @@
+// experts.hip — routed-expert streaming (expert_cache.zig:108-607).
+//
+// With a budget set on the model (ditch_hip_model_set_expert_cache) every
+// routed expert matrix is re-tiled on the device at registration as usual,
+// then copied to pinned host memory (one blob per matrix) and its device
+// memory freed. The forward keeps a device cache of fixed-size slots (one
+// slot = an expert's gate, up and down blobs) within the budget; after a
+// layer's router has picked its experts, the missing ones are copied host ->
+// slot on the cache's own stream, the compute stream waits on those copies,
+// and the grouped products run on views into the slots. A layer whose
+// experts do not all fit runs in chunks that do. The experts the next routed
+// layer used in the previous forward are copied ahead while this layer
+// computes (prompts of a search share their routing from trial to trial).
+#include <algorithm>
+#include <cstring>
+
+#include "model.h"
+
+namespace ditch {
+
+void host_mat_free(HostMat &hm) {
+    if (hm.host) (void)hipHostFree(hm.host);
+    hm.host = nullptr;
+    hm.bytes = 0;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+void stream_out(Mat &mt) {
+    ditch_hip_tensor *t = mt.t;
+    DITCH_CHECK(t, DITCH_INVALID_ARGUMENT, "stream_out of an empty slot");
+    void *parts[6] = {t->codes, t->scale, t->zero, t->side, t->mx, t->mx_scales};
+    size_t off[6], total = 0;
+    for (int i = 0; i < 6; i++) {
+        off[i] = total;
+        if (parts[i]) total += align256(t->part_bytes[i]);
+    }
+    HostMat hm;
+    DITCH_TRY_HIP(hipHostMalloc((void **)&hm.host, total ? total : 256, hipHostMallocDefault));
+    hm.bytes = total;
+    for (int i = 0; i < 6; i++)
+        if (parts[i] && t->part_bytes[i]) DITCH_TRY_HIP(hipMemcpy(hm.host + off[i], parts[i], t->part_bytes[i], hipMemcpyDeviceToHost));
+    // where each TileView pointer lands: inside one of the parts (MXFP4's side
+    // words alias its scale array)
+    const TileView &v = t->v;
+    const void *fields[6] = {v.codes, v.scale, v.zero, v.side, v.mx, v.mx_scales};
+    for (int f = 0; f < 6; f++) {
+        hm.field_off[f] = -1;
+        if (!fields[f]) continue;
+        for (int i = 0; i < 6; i++) {
+            const uint8_t *b = (const uint8_t *)parts[i];
+            if (b && (const uint8_t *)fields[f] >= b && (const uint8_t *)fields[f] < b + t->part_bytes[i]) {
+                hm.field_off[f] = (int64_t)(off[i] + ((const uint8_t *)fields[f] - b));
+                break;
+            }
+        }
+        DITCH_CHECK(hm.field_off[f] >= 0, DITCH_DEVICE_FAILED, "stream_out: a view pointer outside the tensor's parts");
+    }
+    for (int i = 0; i < 6; i++) dev_free(parts[i]);
+    t->codes = t->scale = t->zero = t->side = t->mx = t->mx_scales = nullptr;
+    t->v.codes = nullptr;
+    t->v.scale = nullptr;
+    t->v.zero = nullptr;
+    t->v.side = nullptr;
+    t->v.mx = nullptr;
+    t->v.mx_scales = nullptr;
+    host_mat_free(mt.hm);
+    mt.hm = hm;
+}
+
+TileView view_at(const Mat &mt, const uint8_t *base) {
+    TileView v = mt.t->v;
+    auto at = [&](int f) { return mt.hm.field_off[f] < 0 ? nullptr : base + mt.hm.field_off[f]; };
+    v.codes = at(0);
+    v.scale = at(1);
+    v.zero = at(2);
+    v.side = (const uint32_t *)at(3);
+    v.mx = at(4);
+    v.mx_scales = at(5);
+    return v;
+}
+
+ExpertCache::~ExpertCache() {
+    if (copy) (void)hipStreamSynchronize(copy);
+    for (Slot &sl : slots) {
+        if (sl.used) (void)hipEventDestroy(sl.used);
+        if (sl.loaded) (void)hipEventDestroy(sl.loaded);
+    }
+    dev_free(arena);
+    if (copy) (void)hipStreamDestroy(copy);
+}
+
+// Slot layout: gate blob, up blob, down blob (256-byte aligned).
+static uint64_t expert_bytes(const Layer &L, int64_t e) {
+    return align256(L.eg[e].hm.bytes) + align256(L.eu[e].hm.bytes) + align256(L.ed[e].hm.bytes);
+}
+
+// Builds the cache at the first forward: the slot size is the largest
+// expert of the model, the slot count what the budget holds.
+static ExpertCache &cache_of(ditch_hip_model *m) {
+    if (m->cache) return *m->cache;
+    uint64_t slot = 0, count = 0;
+    for (const Layer &L : m->layers)
+        for (size_t e = 0; e < L.eg.size(); e++)
+            if (L.eg[e].streamed() && L.eu[e].streamed() && L.ed[e].streamed()) {
+                slot = std::max(slot, expert_bytes(L, (int64_t)e));
+                count++;
+            }
+    DITCH_CHECK(slot > 0, DITCH_INVALID_ARGUMENT, "expert cache: no streamed experts");
+    const uint64_t n = std::min(m->expert_budget / slot, count);  // no more slots than experts
+    DITCH_CHECK(n >= 1, DITCH_INVALID_ARGUMENT, "expert cache budget below one expert's gate + up + down");
+    auto *c = new ExpertCache();
+    try {
+        c->capacity = m->expert_budget;
+        c->slot_bytes = slot;
+        c->arena = (uint8_t *)dev_alloc(n * slot);
+        c->slots.resize(n);
+        for (auto &sl : c->slots) {
+            DITCH_TRY_HIP(hipEventCreateWithFlags(&sl.used, hipEventDisableTiming));
+            DITCH_TRY_HIP(hipEventCreateWithFlags(&sl.loaded, hipEventDisableTiming));
+        }
+        DITCH_TRY_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking));
+        c->last_used.resize(m->layers.size());
+    } catch (...) {
+        delete c;
+        throw;
+    }
+    m->cache = c;
+    return *c;
+}
+
+static int find_slot(const ExpertCache &c, int64_t layer, int64_t e) {
+    for (size_t i = 0; i < c.slots.size(); i++)
+        if (c.slots[i].layer == layer && c.slots[i].expert == e) return (int)i;
+    return -1;
+}
+
+// Victim for a fill during layer `cur`: an unpinned slot, empty first, then
+// the one whose layer the forward reaches last from `cur` (the layers just
+// computed), then the least recently used.
+static int victim(const ExpertCache &c, int64_t cur, int64_t nlayers) {
+    int best = -1;
+    int64_t best_d = -1;
+    uint64_t best_stamp = 0;
+    for (size_t i = 0; i < c.slots.size(); i++) {
+        const auto &sl = c.slots[i];
+        if (sl.pins > 0) continue;
+        if (sl.layer < 0) return (int)i;
+        const int64_t d = ((sl.layer - cur - 1) % nlayers + nlayers) % nlayers;
+        if (d > best_d || (d == best_d && sl.stamp < best_stamp)) {
+            best = (int)i;
+            best_d = d;
+            best_stamp = sl.stamp;
+        }
+    }
+    return best;
+}
+
+// Fills slot `i` with expert (layer, e): the copy stream waits for the
+// compute stream's last use of the slot, then copies the three blobs.
+static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64_t e) {
+    auto &sl = c.slots[i];
+    if (sl.layer >= 0) c.evictions++;
+    if (sl.used_pending) DITCH_TRY_HIP(hipStreamWaitEvent(c.copy, sl.used, 0));
+    const Layer &L = m->layers[layer];
+    uint8_t *base = c.arena + (uint64_t)i * c.slot_bytes;
+    uint64_t off = 0;
+    for (const Mat *mt : {&L.eg[e], &L.eu[e], &L.ed[e]}) {
+        DITCH_TRY_HIP(hipMemcpyAsync(base + off, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, c.copy));
+        c.bytes_read += mt->hm.bytes;
+        off += align256(mt->hm.bytes);
+    }
+    DITCH_TRY_HIP(hipEventRecord(sl.loaded, c.copy));
+    sl.layer = layer;
+    sl.expert = e;
+    sl.used_pending = false;
+    sl.stamp = ++c.clock;
+}
+
+void expert_views(ExpertCache &c, int i, const Layer &L, int64_t e, TileView &g, TileView &u, TileView &d) {
+    const uint8_t *base = c.arena + (uint64_t)i * c.slot_bytes;
+    g = view_at(L.eg[e], base);
+    u = view_at(L.eu[e], base + align256(L.eg[e].hm.bytes));
+    d = view_at(L.ed[e], base + align256(L.eg[e].hm.bytes) + align256(L.eu[e].hm.bytes));
+}
+
+// Makes as many of `experts` (from `from` on) resident and pinned as the
+// slots allow; the compute stream `s` waits for their copies. Returns the
+// slots in the order of `experts` (chunk = the prefix that fits).
+std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts, size_t from,
+                               hipStream_t s) {
+    ExpertCache &c = cache_of(m);
+    std::vector<int> got;
+    const int64_t nl = (int64_t)m->layers.size();
+    for (size_t k = from; k < experts.size(); k++) {
+        const int64_t e = experts[k];
+        int i = find_slot(c, layer, e);
+        if (i >= 0) {
+            c.hits++;
+        } else {
+            i = victim(c, layer, nl);
+            if (i < 0) break;  // every slot pinned by this chunk
+            fill(c, m, i, layer, e);
+            c.misses++;
+        }
+        auto &sl = c.slots[i];
+        sl.pins++;
+        sl.stamp = ++c.clock;
+        DITCH_TRY_HIP(hipStreamWaitEvent(s, sl.loaded, 0));
+        got.push_back(i);
+    }
+    DITCH_CHECK(!got.empty(), DITCH_DEVICE_FAILED, "expert cache: no slot free for a chunk");
+    return got;
+}
+
+// The chunk's products are enqueued on `s`: the slots may be refilled once
+// the stream has passed this point.
+void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_t s) {
+    ExpertCache &c = *m->cache;
+    for (int i : slots) {
+        auto &sl = c.slots[i];
+        DITCH_TRY_HIP(hipEventRecord(sl.used, s));
+        sl.used_pending = true;
+        sl.pins--;
+    }
+}
+
+// After layer `layer`: copy ahead the experts the next routed layer used in
+// the previous forward, into slots that hold nothing nearer in the cycle.
+void cache_prefetch_next(ditch_hip_model *m, int64_t layer) {
+    if (!m->cache) return;
+    ExpertCache &c = *m->cache;
+    const int64_t nl = (int64_t)m->layers.size();
+    int64_t next = -1;
+    for (int64_t d = 1; d < nl; d++) {
+        const int64_t l = (layer + d) % nl;
+        if (!m->layers[l].eg.empty() && m->moe_layers[l] && m->layers[l].eg[0].streamed()) {
+            next = l;
+            break;
+        }
+    }
+    if (next < 0 || (size_t)next >= c.last_used.size()) return;
+    const int64_t dist_next = ((next - layer - 1) % nl + nl) % nl;
+    for (int32_t e : c.last_used[next]) {
+        if (find_slot(c, next, e) >= 0) continue;
+        const int i = victim(c, layer, nl);
+        if (i < 0) return;
+        const auto &sl = c.slots[i];
+        // never displace an expert the forward needs before `next`
+        if (sl.layer >= 0 && ((sl.layer - layer - 1) % nl + nl) % nl <= dist_next) return;
+        fill(c, m, i, next, e);
+        c.prefetches++;
+    }
+}
+
+void cache_note_layer(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts) {
+    if (m->cache && (size_t)layer < m->cache->last_used.size()) m->cache->last_used[layer] = experts;
+}
+
+}  // namespace ditch

@@ -131,6 +131,8 @@ struct ditch_hip_tensor {
     void *side = nullptr;  // owned side words (FP8, INT4); MXFP4 aliases scale
     void *mx = nullptr;    // MXFP4 codes in scaled-MFMA order
     void *mx_scales = nullptr;
+    // bytes of codes, scale, zero, side, mx, mx_scales (the owned allocations)
+    size_t part_bytes[6] = {0, 0, 0, 0, 0, 0};
     uint64_t bytes = 0;
 };
 

@@ -1,15 +1,30 @@
 // model.h — host-side state of a resident model (not part of the ABI).
 #pragma once
+#include <cstdint>
 #include <vector>
 
 #include "internal.h"
 
+struct ditch_hip_model;
+
 namespace ditch {
+
+// A routed expert matrix kept in pinned host memory (expert streaming): its
+// re-tiled parts back to back, and where each device pointer of its TileView
+// lands in that blob (field_off: codes, scale, zero, side, mx, mx_scales; -1
+// for none). `t` keeps the tensor's metadata with no device memory.
+struct HostMat {
+    uint8_t *host = nullptr;
+    size_t bytes = 0;
+    int64_t field_off[6] = {-1, -1, -1, -1, -1, -1};
+};
+void host_mat_free(HostMat &hm);
 
 struct Mat {
     ditch_hip_tensor *t = nullptr;
     float *da = nullptr, *db = nullptr;  // delta A [rank][cols], B [rows][rank]
     int rank = 0;
+    HostMat hm;
     void clear_delta() {
         dev_free(da);
         dev_free(db);
@@ -19,9 +34,11 @@ struct Mat {
     void release() {
         free_tensor(t);
         t = nullptr;
+        host_mat_free(hm);
         clear_delta();
     }
     bool ok() const { return t != nullptr; }
+    bool streamed() const { return hm.host != nullptr; }
 };
 
 struct Vec {
@@ -33,6 +50,44 @@ struct Vec {
         len = 0;
     }
 };
+
+// Moves an uploaded matrix to pinned host memory (frees its device parts).
+void stream_out(Mat &mt);
+// The matrix's TileView with its device pointers inside a copy of its host
+// blob at `base`.
+TileView view_at(const Mat &mt, const uint8_t *base);
+
+// Device cache of routed experts (expert_cache.zig:108-607): fixed-size
+// slots holding an expert's gate, up and down blobs, filled from pinned host
+// memory by hipMemcpyAsync on a copy stream of its own. Keyed by (layer,
+// expert); pinned while a chunk of a layer computes with them; victims are
+// the unpinned entries whose layer comes back last in the layer cycle (the
+// forward visits layers in order), least recently used among equals.
+struct ExpertCache {
+    struct Slot {
+        int64_t layer = -1, expert = -1;
+        int pins = 0;
+        uint64_t stamp = 0;
+        bool used_pending = false;  // `used` recorded since the last load
+        hipEvent_t used = nullptr;   // the compute stream's last use
+        hipEvent_t loaded = nullptr; // the copy stream's last fill
+    };
+    uint64_t capacity = 0, slot_bytes = 0, clock = 0;
+    uint8_t *arena = nullptr;
+    std::vector<Slot> slots;
+    hipStream_t copy = nullptr;
+    uint64_t hits = 0, misses = 0, prefetches = 0, bytes_read = 0, evictions = 0;
+    std::vector<std::vector<int32_t>> last_used;  // per layer: experts routed by the last forward
+    ~ExpertCache();
+};
+
+struct Layer;
+std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts, size_t from,
+                               hipStream_t s);
+void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_t s);
+void cache_note_layer(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts);
+void cache_prefetch_next(ditch_hip_model *m, int64_t layer);
+void expert_views(ExpertCache &c, int slot, const Layer &L, int64_t e, TileView &g, TileView &u, TileView &d);
 
 struct Layer {
     Vec attn_norm, q_bias, k_bias, v_bias, q_norm, k_norm, ffn_norm, corr, q_a_norm, kv_a_norm;
@@ -56,5 +111,7 @@ struct ditch_hip_model {
         segs, segd, e_xa;
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
+    uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
+    ditch::ExpertCache *cache = nullptr;
     ~ditch_hip_model();
 };

@@ -519,6 +519,11 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
     ditch_hip_tensor *t = upload_weight(m->h, w, s);
     mt->release();
     mt->t = t;
+    if (m->expert_budget > 0 &&
+        (slot == DITCH_SLOT_EXPERT_GATE || slot == DITCH_SLOT_EXPERT_UP || slot == DITCH_SLOT_EXPERT_DOWN)) {
+        DITCH_CHECK(!m->cache, DITCH_INVALID_ARGUMENT, "expert registered after the expert cache was built");
+        stream_out(*mt);
+    }
 }
 
 void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64_t rank, const float *a,
@@ -544,8 +549,13 @@ void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float
     Mat *mt = mat_slot(m, layer, slot, expert);
     DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "edit of an empty slot");
     hipStream_t s = m->h->stream;
-    const TileView &w = mt->t->v;
-    DevBuf dv, part;
+    DevBuf dv, part, staged;
+    TileView w = mt->t->v;
+    if (mt->streamed()) {  // a streamed expert: the edit reads a device copy of its blob
+        uint8_t *d = staged.get<uint8_t>(mt->hm.bytes);
+        DITCH_TRY_HIP(hipMemcpyAsync(d, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, s));
+        w = view_at(*mt, d);
+    }
     float *d_v = dv.get<float>(k * w.rows + k * w.cols);
     float *d_a = d_v + k * w.rows;
     DITCH_TRY_HIP(hipMemcpyAsync(d_v, v, k * w.rows * 4, hipMemcpyHostToDevice, s));
@@ -667,49 +677,83 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
     hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(256), 0, s, sel, n, k, offsets, pair_token, pair_of);
     DITCH_TRY_HIP(hipGetLastError());
-    // segments (experts with tokens), in index order
-    std::vector<GroupSeg> sg, su, sd;
-    std::vector<SegDelta> dd;
-    int max_rank = 0;
+    // segments (experts with tokens), in index order; with expert streaming
+    // in chunks of experts resident together in the cache
+    std::vector<int32_t> used;
     for (int64_t e = 0; e < E; e++) {
         if (hc[e] == 0) continue;
         DITCH_CHECK(L.eg[e].ok() && L.eu[e].ok() && L.ed[e].ok(), DITCH_INVALID_ARGUMENT, "forward: expert weights missing");
-        GroupSeg g{L.eg[e].t->v, ho[e], hc[e], nullptr, 0};
-        GroupSeg u{L.eu[e].t->v, ho[e], hc[e], nullptr, 0};
-        GroupSeg d{L.ed[e].t->v, ho[e], hc[e], L.ed[e].db, L.ed[e].rank};
-        sg.push_back(g);
-        su.push_back(u);
-        sd.push_back(d);
-        dd.push_back(SegDelta{L.ed[e].da, ho[e], hc[e], L.ed[e].rank});
-        max_rank = std::max(max_rank, L.ed[e].rank);
+        used.push_back((int32_t)e);
     }
-    unsigned nseg = (unsigned)sg.size();
-    for (unsigned i = 0; i < nseg; i++)
-        DITCH_CHECK(sg[i].w.tf == sg[0].w.tf && su[i].w.tf == su[0].w.tf && sd[i].w.tf == sd[0].w.tf &&
-                        sg[i].w.rows == inter && sg[i].w.cols == hidden && sd[i].w.rows == hidden &&
-                        sd[i].w.cols == inter,
-                    DITCH_INVALID_ARGUMENT, "experts of one layer must share shape and format");
-    GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * nseg);
-    DITCH_TRY_HIP(hipMemcpyAsync(dsegs, sg.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
-    DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
-    DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
-    const TileView &vg = sg[0].w, &vd = sd[0].w;
+    const bool streamed = !used.empty() && L.eg[used[0]].streamed();
+    const int64_t li = &L - m->layers.data();
     float *gate = m->e_gate.get<float>(P * inter), *up = m->e_up.get<float>(P * inter);
     float *eo = m->e_out.get<float>(P * hidden);
-    launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0, s);
-    launch_matmul_grouped(dsegs + nseg, nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, 0,
-                          s);
-    launch_gated_act(0, gate, gate, up, P, inter, inter, inter, s);
-    float *dxa = nullptr;
-    if (max_rank > 0) {
-        SegDelta *dsd = m->segd.get<SegDelta>(nseg);
-        DITCH_TRY_HIP(hipMemcpyAsync(dsd, dd.data(), nseg * sizeof(SegDelta), hipMemcpyHostToDevice, s));
-        dxa = m->e_xa.get<float>(P * max_rank);
-        dim3 grid((unsigned)((max_cnt * max_rank + 3) / 4), nseg);
-        hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
-        DITCH_TRY_HIP(hipGetLastError());
+    size_t from = 0;
+    while (from < used.size()) {
+        std::vector<int> slots;
+        size_t cnt = used.size() - from;
+        if (streamed) {
+            slots = cache_acquire(m, li, used, from, s);
+            cnt = slots.size();
+        }
+        std::vector<GroupSeg> sg, su, sd;
+        std::vector<SegDelta> dd;
+        int max_rank = 0;
+        int32_t max_cnt = 0;
+        for (size_t q = 0; q < cnt; q++) {
+            const int64_t e = used[from + q];
+            TileView vg = L.eg[e].t->v, vu = L.eu[e].t->v, vdn = L.ed[e].t->v;
+            if (streamed) expert_views(*m->cache, slots[q], L, e, vg, vu, vdn);
+            sg.push_back(GroupSeg{vg, ho[e], hc[e], nullptr, 0});
+            su.push_back(GroupSeg{vu, ho[e], hc[e], nullptr, 0});
+            sd.push_back(GroupSeg{vdn, ho[e], hc[e], L.ed[e].db, L.ed[e].rank});
+            dd.push_back(SegDelta{L.ed[e].da, ho[e], hc[e], L.ed[e].rank});
+            max_rank = std::max(max_rank, L.ed[e].rank);
+            max_cnt = std::max(max_cnt, hc[e]);
+        }
+        unsigned nseg = (unsigned)sg.size();
+        for (unsigned i = 0; i < nseg; i++)
+            DITCH_CHECK(sg[i].w.tf == sg[0].w.tf && su[i].w.tf == su[0].w.tf && sd[i].w.tf == sd[0].w.tf &&
+                            sg[i].w.rows == inter && sg[i].w.cols == hidden && sd[i].w.rows == hidden &&
+                            sd[i].w.cols == inter,
+                        DITCH_INVALID_ARGUMENT, "experts of one layer must share shape and format");
+        GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * nseg);
+        DITCH_TRY_HIP(hipMemcpyAsync(dsegs, sg.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+        DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+        DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+        const TileView &vg = sg[0].w, &vd = sd[0].w;
+        launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0, s);
+        launch_matmul_grouped(dsegs + nseg, nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, 0,
+                              s);
+        {  // act(gate) * up on this chunk's pairs (consecutive experts: one run of pairs)
+            const int64_t p0 = sg[0].off, p1 = (int64_t)sg[nseg - 1].off + sg[nseg - 1].cnt;
+            launch_gated_act(0, gate + p0 * inter, gate + p0 * inter, up + p0 * inter, p1 - p0, inter, inter, inter, s);
+        }
+        float *dxa = nullptr;
+        if (max_rank > 0) {
+            SegDelta *dsd = m->segd.get<SegDelta>(nseg);
+            DITCH_TRY_HIP(hipMemcpyAsync(dsd, dd.data(), nseg * sizeof(SegDelta), hipMemcpyHostToDevice, s));
+            dxa = m->e_xa.get<float>(P * max_rank);
+            dim3 grid((unsigned)((max_cnt * max_rank + 3) / 4), nseg);
+            hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
+            DITCH_TRY_HIP(hipGetLastError());
+        }
+        launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, max_rank,
+                              s);
+        if (streamed) {
+            cache_release(m, slots, s);
+            // a layer in several chunks: the host tables of this chunk go out
+            // of scope before the next is built (the degraded case, when the
+            // cache holds fewer experts than the layer routes to)
+            if (from + cnt < used.size()) DITCH_TRY_HIP(hipStreamSynchronize(s));
+        }
+        from += cnt;
     }
-    launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, max_rank, s);
+    if (streamed) {
+        cache_note_layer(m, li, used);
+        cache_prefetch_next(m, li);
+    }
     float *esh = nullptr;
     if (L.sh_gate.ok()) {
         int64_t si = L.sh_gate.t->v.rows;
@@ -957,6 +1001,8 @@ static void host_fill_rope(const ditch_model_config &c, std::vector<float> &cos_
 }  // namespace ditch
 
 ditch_hip_model::~ditch_hip_model() {
+    delete cache;  // drains its copy stream before the host blobs go
+    cache = nullptr;
     for (auto &L : layers) {
         for (ditch::Vec *v : {&L.attn_norm, &L.q_bias, &L.k_bias, &L.v_bias, &L.q_norm, &L.k_norm, &L.ffn_norm,
                               &L.corr, &L.q_a_norm, &L.kv_a_norm})

@@ -697,6 +697,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
         v.units_k = cols_pad / uk;
         size_t code_bytes = (size_t)(rows_pad / 16) * v.units_k * unit_bytes_of(tf);
         t->codes = dev_alloc(code_bytes);
+        t->part_bytes[0] = code_bytes;
         t->bytes = code_bytes;
         RetileArgs a{};
         a.src = st.v;
@@ -717,6 +718,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             int64_t kt_src = v.cols / 32, kt_pad = cols_pad / 32;
             size_t b = rows_pad * kt_pad * 2;
             t->scale = dev_alloc(b);
+            t->part_bytes[1] = b;
             t->bytes += b;
             hipLaunchKernelGGL(q8_scales_kernel, dim3(grid_for(rows_pad * kt_pad)), dim3(256), 0, s, st.v,
                                (uint16_t *)t->scale, v.rows, kt_src, kt_pad, rows_pad);
@@ -728,6 +730,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             int64_t kt_src = v.cols / 32, kt_pad = cols_pad / 32;
             size_t b = rows_pad * kt_pad;
             t->scale = dev_alloc(b);
+            t->part_bytes[1] = b;
             t->bytes += b;
             hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(rows_pad * kt_pad)), dim3(256), 0, s, st.v.scale,
                                (uint8_t *)t->scale, v.rows, kt_src, rows_pad, kt_pad);
@@ -742,6 +745,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             if (sc_pad < (int64_t)w->scale_cols) sc_pad = (int64_t)w->scale_cols;
             size_t b = sr_pad * sc_pad * eb;
             t->scale = dev_alloc(b);
+            t->part_bytes[1] = b;
             t->bytes += b;
             DITCH_TRY_HIP(hipMemsetAsync(t->scale, 0, b, s));
             hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(sr_pad * sc_pad * eb)), dim3(256), 0, s, st.v.scale,
@@ -762,6 +766,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             if (groups_pad < groups) groups_pad = groups;
             size_t b = rows_pad * groups_pad * eb;
             t->scale = dev_alloc(b);
+            t->part_bytes[1] = b;
             t->bytes += b;
             hipLaunchKernelGGL(pad_copy_kernel, dim3(grid_for(rows_pad * groups_pad * eb)), dim3(256), 0, s,
                                st.v.scale, (uint8_t *)t->scale, v.rows, (int64_t)(groups * eb), rows_pad,
@@ -769,6 +774,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             if (w->zero) {
                 size_t zb = rows_pad * groups_pad;
                 t->zero = dev_alloc(zb);
+                t->part_bytes[2] = zb;
                 t->bytes += zb;
                 hipLaunchKernelGGL(int_zero_kernel, dim3(grid_for(rows_pad * groups_pad)), dim3(256), 0, s,
                                    (const uint32_t *)st.v.zero, (uint8_t *)t->zero, v.rows, groups, rows_pad,
@@ -787,11 +793,13 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
             v.side = (const uint32_t *)t->scale;
             v.side_cols = v.scale_cols / 4;
             t->mx = dev_alloc(code_bytes);
+            t->part_bytes[4] = code_bytes;
             t->bytes += code_bytes;
             const int64_t total_mx = a.groups_n * v.units_k * 64;
             hipLaunchKernelGGL(mx_native_kernel, dim3(grid_for(total_mx)), dim3(256), 0, s, st.v.data, v.rows, v.cols,
                                (uint8_t *)t->mx, a.groups_n, v.units_k);
             t->mx_scales = dev_alloc(total_mx);
+            t->part_bytes[5] = total_mx;
             t->bytes += total_mx;
             hipLaunchKernelGGL(mx_scales_kernel, dim3(grid_for(total_mx)), dim3(256), 0, s, (const uint8_t *)st.v.scale,
                                v.rows, v.cols / 32, (uint8_t *)t->mx_scales, a.groups_n, v.units_k);
@@ -800,6 +808,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
         } else if (v.fast && tf == TF_FP8) {
             int64_t total = ((int64_t)w->scale_rows + 1) * v.scale_cols;
             t->side = dev_alloc(total * 4);
+            t->part_bytes[3] = total * 4;
             t->bytes += total * 4;
             hipLaunchKernelGGL(fp8_side_kernel, dim3(grid_for(total)), dim3(256), 0, s, t->scale, v.scale_type,
                                (uint32_t *)t->side, total);
@@ -808,6 +817,7 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
         } else if (v.fast && tf == TF_INT4) {
             int64_t total = pad_to(v.rows, 16) * v.scale_cols;
             t->side = dev_alloc(total * 4);
+            t->part_bytes[3] = total * 4;
             t->bytes += total * 4;
             hipLaunchKernelGGL(int4_side_kernel, dim3(grid_for(total)), dim3(256), 0, s, (const uint16_t *)t->scale,
                                (const uint8_t *)t->zero, (uint32_t *)t->side, total);

@@ -215,15 +215,24 @@ class Tensor:
 class Model:
     """A resident model (ditch_hip_model) built from a ModelSpec."""
 
-    def __init__(self, dev: Device, spec):
+    def __init__(self, dev: Device, spec, expert_cache_bytes=0):
+        """expert_cache_bytes > 0: routed experts stream from pinned host memory
+        through a device cache of that many bytes (ditch_hip_model_set_expert_cache)."""
         self.dev = dev
         self.spec = spec
         self.cfg = spec.config_struct()
         self.h = dev.lib.ditch_hip_model_create(dev.h, ctypes.byref(self.cfg))
         if not self.h:
             raise DeviceError(abi.DEVICE_FAILED, dev.lib.ditch_hip_last_error(dev.h).decode())
+        if expert_cache_bytes:
+            dev.check(dev.lib.ditch_hip_model_set_expert_cache(self.h, int(expert_cache_bytes)))
         for (layer, slot, expert), w in spec.tensors.items():
             dev.check(dev.lib.ditch_hip_model_set(self.h, layer, slot, expert, w.ref()))
+
+    def expert_cache_stats(self):
+        st = abi.ExpertCacheStats()
+        self.dev.check(self.dev.lib.ditch_hip_model_expert_cache_stats(self.h, ctypes.byref(st)))
+        return {name: getattr(st, name) for name, _ in st._fields_}
 
     def free(self):
         if self.h:

@@ -354,6 +354,31 @@ int32_t ditch_hip_model_set_delta(ditch_hip_model *m, int32_t layer,
                                   int32_t slot, int32_t expert, uint64_t rank,
                                   const float *a, const float *b);
 /* model.resetDeltas (model.zig:2348).                                      */
+/* Routed-expert streaming (the reference's ExpertCache, expert_cache.zig:
+ * 108-607). Call before registering experts: each routed expert matrix set
+ * afterwards is re-tiled on the device, kept in pinned host memory and freed
+ * from HBM; the forward keeps a device cache of `bytes` (whole experts: gate
+ * + up + down) and copies a layer's routed experts in on a copy stream of
+ * its own once the router has picked them, evicting the experts whose layer
+ * comes back last; a layer whose experts do not fit runs in chunks that do.
+ * InvalidArgument when experts were registered before, or at the first
+ * forward when `bytes` holds less than one expert.                         */
+int32_t ditch_hip_model_set_expert_cache(ditch_hip_model *m, uint64_t bytes);
+
+typedef struct ditch_expert_cache_stats {
+    uint64_t capacity;    /* bytes given                                     */
+    uint64_t slots;       /* experts the cache holds at once                  */
+    uint64_t resident;    /* experts resident now                             */
+    uint64_t hits;        /* routed experts found resident                    */
+    uint64_t misses;      /* routed experts copied in on demand               */
+    uint64_t prefetched;  /* experts copied ahead for the next routed layer   */
+    uint64_t bytes_read;  /* host -> device bytes                             */
+    uint64_t evictions;
+    uint64_t slot_bytes;  /* bytes of one expert's slot                       */
+} ditch_expert_cache_stats;
+/* Zeros before the first forward of a streaming model.                    */
+int32_t ditch_hip_model_expert_cache_stats(const ditch_hip_model *m, ditch_expert_cache_stats *out);
+
 int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m);
 /* HBM bytes held by the model's weights.                                   */
 uint64_t ditch_hip_model_bytes(const ditch_hip_model *m);

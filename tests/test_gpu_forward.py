@@ -187,3 +187,96 @@ def test_long_prompt_attention_matches_oracle(dev, ref, name):
         gm.free()
         cm.free()
     check_parity(ref, rg, lg, rc, lc, name)
+
+
+# ---------------------------------------------------------------------------
+# Routed-expert streaming (expert_cache.zig:108-607)
+
+
+def _moe_forward(gm, cm, tokens, rows, last):
+    rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    return rg, lg, rc, lc
+
+
+def _cache_geometry(dev, spec, tokens, rows, last):
+    """(slot bytes, slot count) of a cache whose budget holds every expert."""
+    probe = Model(dev, spec, expert_cache_bytes=1 << 40)
+    try:
+        probe.forward(tokens, rows, logit_rows=last)
+        st = probe.expert_cache_stats()
+        assert st["misses"] > 0 and st["bytes_read"] > 0 and st["resident"] == st["misses"]
+        return st["slot_bytes"], st["slots"]
+    finally:
+        probe.free()
+
+
+@pytest.mark.parametrize("fraction", [1.0, 0.4, 0.0])
+def test_streamed_experts_match_oracle(dev, ref, fraction):
+    """Experts kept in pinned host memory and copied into a device cache that
+    holds every expert (fraction 1), 40 % of them (layers run in chunks) or
+    exactly one (fraction 0): the forward equals the oracle's, twice in a
+    row; a cache as large as the model misses each expert once and then
+    only hits."""
+    spec = mg.moe("int4", layers=3, dense_first=1, experts=16, top_k=4, seed=21)
+    tokens, rows, last = mg.batch(3, [40, 17, 64], spec.config["vocab"], seed=9)
+    slot, total = _cache_geometry(dev, spec, tokens, rows, last)
+    assert total == 2 * 16
+    budget = max(slot, int(fraction * total) * slot)
+    gm = Model(dev, spec, expert_cache_bytes=budget)
+    cm = RefModel(spec)
+    try:
+        for it in range(2):
+            rg, lg, rc, lc = _moe_forward(gm, cm, tokens, rows, last)
+            check_parity(ref, rg, lg, rc, lc, f"streamed {fraction} pass {it}")
+        st = gm.expert_cache_stats()
+        assert st["slots"] == budget // slot
+        if fraction == 1.0:
+            assert st["evictions"] == 0 and st["hits"] == st["misses"]  # second pass: every expert resident
+        else:
+            assert st["evictions"] > 0
+    finally:
+        gm.free()
+        cm.free()
+
+
+def test_streamed_expert_edit_matches_oracle(dev, ref):
+    """The rank-2 edit of streamed experts' down projections (the edit reads a
+    device copy of each expert's blob) against the oracle doing the same."""
+    spec = mg.moe("int4", dense_first=1, seed=4)
+    rng = np.random.default_rng(8)
+    v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+    v = v.T.astype(np.float32)
+    tokens, rows, last = mg.batch(3, [30, 12, 64], spec.config["vocab"], seed=6)
+    slot, _ = _cache_geometry(dev, spec, tokens, rows, last)
+    gm = Model(dev, spec, expert_cache_bytes=3 * slot)
+    cm = RefModel(spec)
+    try:
+        for li in range(spec.config["layers"]):
+            if spec.moe_layers[li]:
+                for e in range(spec.config["n_experts"]):
+                    for m in (gm, cm):
+                        m.edit(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0)
+        rg, lg, rc, lc = _moe_forward(gm, cm, tokens, rows, last)
+        check_parity(ref, rg, lg, rc, lc, "streamed edit")
+    finally:
+        gm.free()
+        cm.free()
+
+
+def test_expert_cache_rejects_late_budget_and_tiny_budget(dev):
+    from ditch_amd.hip import DeviceError
+    spec = mg.moe("int4", dense_first=1, seed=2)
+    gm = Model(dev, spec)
+    try:
+        with pytest.raises(DeviceError, match="registered before"):
+            dev.check(dev.lib.ditch_hip_model_set_expert_cache(gm.h, 1 << 30))
+    finally:
+        gm.free()
+    tokens, rows, last = mg.batch(2, [5, 7], spec.config["vocab"], seed=1)
+    gm = Model(dev, spec, expert_cache_bytes=1024)
+    try:
+        with pytest.raises(DeviceError, match="below one expert"):
+            gm.forward(tokens, rows, logit_rows=last)
+    finally:
+        gm.free()
