@@ -29,8 +29,11 @@ FLAGS = [
 
 # per-source additions: the tiled GEMM keeps its MFMA accumulators in the
 # architectural VGPRs (with them in AGPRs the register allocator copies every
-# accumulator between the two files once per k stage)
-EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# accumulator between the two files once per k stage); the GEMV's register
+# ring of in-flight units is unrolled whatever its size (indexed at run time
+# it would live in scratch memory)
+EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=1000000"]}
 
 
 def sources():

@@ -17,6 +17,22 @@
 
 namespace ditch {
 
+// A load from global memory (address space 1): the compiler then issues
+// global_load rather than flat_load, whose completion it can only track
+// together with LDS and scalar traffic.
+template <typename T>
+__device__ __forceinline__ T gload(const void *p) {
+    if constexpr (sizeof(T) == 16) {
+        typedef uint32_t v4_t __attribute__((ext_vector_type(4)));
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) v4_t *)p);
+    } else if constexpr (sizeof(T) == 8) {
+        typedef uint32_t v2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) v2_t *)p);
+    } else {
+        return *(const __attribute__((address_space(1))) T *)p;
+    }
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 
@@ -27,6 +43,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
     return (uint16_t)((bits + 0x7fffu + lsb) >> 16);
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return u2f((uint32_t)v << 16); }
+
+// f16 -> f32 by the hardware conversion: the same value for every finite
+// f16 and infinity; a NaN stays a NaN, its payload not kept (for scales of
+// products, where the payload does not matter).
+__device__ __forceinline__ float f16_to_f32_hw(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
@@ -99,10 +120,10 @@ enum ScaleType : int32_t { SC_F32 = 0, SC_F16 = 1, SC_BF16 = 2, SC_E8M0 = 40 };
 
 __device__ __forceinline__ float load_scale(const void *base, size_t idx, int32_t st) {
     switch (st) {
-    case SC_F16: return f16_to_f32(((const uint16_t *)base)[idx]);
-    case SC_BF16: return bf16_to_f32(((const uint16_t *)base)[idx]);
-    case SC_E8M0: return e8m0_value(((const uint8_t *)base)[idx]);
-    default: return ((const float *)base)[idx];
+    case SC_F16: return f16_to_f32(gload<uint16_t>((const uint16_t *)base + idx));
+    case SC_BF16: return bf16_to_f32(gload<uint16_t>((const uint16_t *)base + idx));
+    case SC_E8M0: return e8m0_value(gload<uint8_t>((const uint8_t *)base + idx));
+    default: return gload<float>((const float *)base + idx);
     }
 }
 

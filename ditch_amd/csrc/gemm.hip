@@ -1,80 +1,9 @@
-// gemm.hip — dequant-fused products for the GEMV regime and for formats
-// and shapes the tiled kernel (gemm_tile.hip) does not take.
+// gemm.hip — dequant-fused products for the formats and shapes the tiled
+// kernel (gemm_tile.hip) does not take, and the launchers of every product
+// (the GEMV regime lives in gemv.hip).
 #include "gemm_common.h"
 
 namespace ditch {
-
-// ---------------------------------------------------------------------------
-// GEMV regime (n <= 16): one 16-token fragment, NT 16-row groups per block,
-// K split over the 4 waves and reduced through LDS.
-
-template <int TF, int NT, int XT>
-__global__ __launch_bounds__(256) void gemv_kernel(GemmParams p) {
-    if (!select_segment(p, 0)) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t groups = (p.w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)blockIdx.x * NT;
-    if (g0 >= groups) return;
-    const int64_t units = p.w.units_k;
-    const int64_t per = (units + 3) / 4;
-    const int64_t u0 = wave * per;
-    const int64_t u1 = u0 + per < units ? u0 + per : units;
-    const int UK = unit_k_of(TF);
-    const bool vec_ok = (p.ldx % 4 == 0) && (((uintptr_t)p.x & 15) == 0);
-    const int64_t tok = lane % 16;
-    const int kq = lane / 16;
-
-    floatx4 acc[NT];
-#pragma unroll
-    for (int i = 0; i < NT; i++) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    for (int64_t u = u0; u < u1; u++) {
-        Raw raw[NT];
-        UnitSide side[NT];
-#pragma unroll
-        for (int i = 0; i < NT; i++) {
-            int64_t g = g0 + i < groups ? g0 + i : groups - 1;
-            raw[i] = load_raw<TF>(p.w, g, u, lane);
-            side[i] = load_side<TF>(p.w, g * 16 + lane % 16, u);
-        }
-#pragma unroll
-        for (int t = 0; t < Fmt<TF>::tiles; t++) {
-            int64_t k0 = u * UK + 32 * t + 8 * kq;
-            float xv[8];
-            load_x8(p, tok, k0, xv, vec_ok);
-            u32x4 xt[XT];
-            a_words<Fmt<TF>::fp32, XT>(xv, xt);
-#pragma unroll
-            for (int i = 0; i < NT; i++) {
-                u32x4 bh, bl = u32x4{0, 0, 0, 0};
-                float ts = 1.f;
-                decode_tile<TF>(p.w, raw[i], side[i], t, (g0 + i) * 16 + lane % 16, k0, bh, bl, ts);
-                mac<TF, XT>(acc[i], xt, bh, bl, ts);
-            }
-        }
-    }
-    // reduce the four K slices
-    __shared__ floatx4 red[3][NT][64];
-    if (wave > 0) {
-#pragma unroll
-        for (int i = 0; i < NT; i++) red[wave - 1][i][lane] = acc[i];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int i = 0; i < NT; i++) {
-            floatx4 a = acc[i];
-#pragma unroll
-            for (int w = 0; w < 3; w++) {
-                floatx4 b = red[w][i][lane];
-                a[0] += b[0]; a[1] += b[1]; a[2] += b[2]; a[3] += b[3];
-            }
-            int64_t row = (g0 + i) * 16 + lane % 16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) store_out(p, 4 * kq + r, row, a[r]);
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // GEMM regime: block tile 16*MT tokens x 64*NT rows; the activation tile of
@@ -168,11 +97,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 template <int TF, int XT>
 static void dispatch(const GemmParams &p, int64_t max_rows, int64_t n_for_shape, unsigned nseg, hipStream_t s) {
     int64_t groups = (max_rows + 15) / 16;
-    if (n_for_shape <= 16) {
-        constexpr int NT = 1;
-        dim3 grid((unsigned)((groups + NT - 1) / NT), 1, nseg);
-        hipLaunchKernelGGL((gemv_kernel<TF, NT, XT>), grid, dim3(256), 0, s, p);
-    } else if (n_for_shape <= 64 || XT > 2) {
+    if (n_for_shape <= 64 || XT > 2) {
         constexpr int MT = 4, NT = 2;
         dim3 grid((unsigned)((groups + 4 * NT - 1) / (4 * NT)), (unsigned)((n_for_shape + 16 * MT - 1) / (16 * MT)), nseg);
         hipLaunchKernelGGL((gemm_kernel<TF, MT, NT, XT>), grid, dim3(256), 0, s, p);
@@ -238,6 +163,10 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     p.delta_rank = ep.delta_rank;
     p.delta_stride = ep.delta_rank;
     p.segs = nullptr;
+    if (n <= 16) {
+        launch_gemv(p, w.tf, w.rows, w.cols, ep.exact != 0, 1, ws, s);
+        return;
+    }
     dispatch_tf(w.tf, p, w.rows, n, 1, ep.exact != 0, s);
 }
 
@@ -264,7 +193,7 @@ void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, c
 
 void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols, int64_t max_cnt,
                            float *out, const float *x, const int32_t *row_index, const float *delta_xa,
-                           int delta_stride, hipStream_t s) {
+                           int delta_stride, hipStream_t s, DevBuf *ws) {
     if (nseg == 0 || max_cnt <= 0) return;
     GemmParams p{};
     p.out = out;
@@ -277,6 +206,10 @@ void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_
     p.segs = d_segs;
     p.w.rows = rows;
     p.w.cols = cols;
+    if (max_cnt <= 16) {
+        launch_gemv(p, tf, rows, cols, false, nseg, ws, s);
+        return;
+    }
     dispatch_tf(tf, p, rows, max_cnt, nseg, false, s);
 }
 

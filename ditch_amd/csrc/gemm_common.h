@@ -89,6 +89,31 @@ __device__ __forceinline__ void a_words(const float (&v)[8], u32x4 (&t)[XT]) {
     }
 }
 
+// a_words for bf16 terms with the hardware's round-to-nearest-even
+// conversion (v_cvt_pk_bf16_f32, two values per instruction): the same
+// terms as a_words for finite values.
+template <int XT>
+__device__ __forceinline__ void a_words_cvt(const float (&v)[8], u32x4 (&t)[XT]) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) r[j] = v[j];
+#pragma unroll
+    for (int e = 0; e < XT; e++) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            wd[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{r[2 * q], r[2 * q + 1]}, bf16x2_t));
+            if (e + 1 < XT) {
+                r[2 * q] = __fsub_rn(r[2 * q], u2f(wd[q] << 16));
+                r[2 * q + 1] = __fsub_rn(r[2 * q + 1], u2f(wd[q] & 0xffff0000u));
+            }
+        }
+        t[e] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+    }
+}
+
 struct GemmParams {
     TileView w;
     float *out;
@@ -105,7 +130,15 @@ struct GemmParams {
     // grouped (routed experts): segment z = blockIdx.z has its own weight,
     // rows [seg[z].off, seg[z].off + seg[z].cnt) of x/out and delta
     const GroupSeg *segs;
+    // GEMV activation fragments (gv_split_kernel): 16-byte words
+    // [k tile][term][k quarter][xn tokens], segment z at xf + z * xf_seg
+    const uint8_t *xf;
+    int64_t xn, xf_seg;
 };
+
+// The GEMV regime (gemv.hip): n <= 16 tokens, or segments of at most 16.
+void launch_gemv(GemmParams &p, int tf, int64_t rows, int64_t cols, bool exact, unsigned nseg, DevBuf *ws,
+                 hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Per-format B fragments of k tile `t` of a 16-byte (32 for f32) tile word.
@@ -154,6 +187,67 @@ __device__ __forceinline__ UnitSide load_side(const TileView &w, int64_t row, in
     return s;
 }
 
+// The FP8 / INT4 scale (and INT4 zero point) of the k tile starting at k0 of
+// `row`; k beyond the matrix (codes zero there) reads the last column block.
+template <int TF>
+__device__ __forceinline__ float tile_scale_of(const TileView &w, int64_t row, int64_t k0, int *zp_out = nullptr) {
+    const int64_t r = row < w.rows ? row : w.rows - 1;
+    if constexpr (TF == TF_FP8) {
+        int64_t sr;
+        if (w.row_shard == 0) sr = r / w.block_rows;
+        else {
+            int64_t per_shard = (w.row_shard + w.block_rows - 1) / w.block_rows;
+            sr = r / w.row_shard * per_shard + (r % w.row_shard) / w.block_rows;
+        }
+        int64_t kb = k0 / w.block_cols;
+        kb = kb < w.scale_cols ? kb : w.scale_cols - 1;
+        return load_scale(w.scale, sr * w.scale_cols + kb, w.scale_type);
+    } else {
+        int64_t g = k0 / w.group;
+        g = g < w.scale_cols ? g : w.scale_cols - 1;
+        if (zp_out) *zp_out = w.zero ? (int)gload<uint8_t>(w.zero + r * w.scale_cols + g) - 8 : 0;
+        return load_scale(w.scale, r * w.scale_cols + g, w.scale_type);
+    }
+}
+
+// bf16_rne(e4m3/e5m2 code * s) for the 8 codes of tile t.
+__device__ __forceinline__ void decode_fp8(const TileView &w, const Raw &raw, int t, float s, u32x4 &bh) {
+    uint32_t w0 = word_of(raw.a, 2 * t), w1 = word_of(raw.a, 2 * t + 1);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        f[j] = bf16_to_f32(f32_to_bf16(mul_x86(fp8_value((w0 >> (8 * j)) & 0xffu, w.e5m2), s)));
+        f[4 + j] = bf16_to_f32(f32_to_bf16(mul_x86(fp8_value((w1 >> (8 * j)) & 0xffu, w.e5m2), s)));
+    }
+    bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+}
+
+// bf16_rne(e2m1 code * 2^e) for the 8 codes of tile t; byte t of `word` is e.
+// e2m1 * 2^e has at most two significant bits, so the f32 product is the
+// exact bf16 value. E8M0 255 (NaN) multiplies by infinity: every code gives
+// an infinity or a NaN, and every product reading it a NaN or infinity, as
+// with the reference's NaN weights (payloads aside).
+__device__ __forceinline__ void decode_mx4(const Raw &raw, uint32_t word, int t, u32x4 &bh) {
+    const uint32_t wd = word_of(raw.a, t);
+    const float sc = e8m0_scale((word >> (8 * t)) & 0xffu);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) f[j] = __fmul_rn(e2m1_value((wd >> (4 * j)) & 0xfu), sc);
+    bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+}
+
+// bf16_rne((q - zp) * s) for the 8 codes of tile t.
+__device__ __forceinline__ void decode_int4(const Raw &raw, int t, float s, int zp, u32x4 &bh) {
+    uint32_t wd = word_of(raw.a, t);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int q = (int)((wd >> (4 * j)) & 0xfu) - 8;
+        f[j] = bf16_to_f32(f32_to_bf16(mul_x86((float)(q - zp), s)));
+    }
+    bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+}
+
 // B fragment (hi; lo for split formats) of tile t.
 template <int TF>
 __device__ __forceinline__ void decode_tile(const TileView &w, const Raw &raw, const UnitSide &side, int t,
@@ -185,52 +279,15 @@ __device__ __forceinline__ void decode_tile(const TileView &w, const Raw &raw, c
         }
         bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
         uint16_t sb = (uint16_t)((side.word >> (16 * t)) & 0xffffu);
-        tile_scale = f16_to_f32(sb);
+        tile_scale = f16_to_f32_hw(sb);
     } else if constexpr (TF == TF_FP8) {
-        int64_t r = row < w.rows ? row : w.rows - 1;
-        int64_t sr;
-        if (w.row_shard == 0) sr = r / w.block_rows;
-        else {
-            int64_t per_shard = (w.row_shard + w.block_rows - 1) / w.block_rows;
-            sr = r / w.row_shard * per_shard + (r % w.row_shard) / w.block_rows;
-        }
-        float s = load_scale(w.scale, sr * w.scale_cols + k0 / w.block_cols, w.scale_type);
-        uint32_t w0 = word_of(raw.a, 2 * t), w1 = word_of(raw.a, 2 * t + 1);
-        float f[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            f[j] = bf16_to_f32(f32_to_bf16(mul_x86(fp8_value((w0 >> (8 * j)) & 0xffu, w.e5m2), s)));
-            f[4 + j] = bf16_to_f32(f32_to_bf16(mul_x86(fp8_value((w1 >> (8 * j)) & 0xffu, w.e5m2), s)));
-        }
-        bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+        decode_fp8(w, raw, t, tile_scale_of<TF>(w, row, k0), bh);
     } else if constexpr (TF == TF_MX4) {
-        uint32_t wd = word_of(raw.a, t);
-        uint32_t sb = (side.word >> (8 * t)) & 0xffu;
-        float sc = e8m0_scale(sb);
-        float f[8];
-        if (sb != 255u) {
-            // e2m1 * 2^e has at most two significant bits: the product is the
-            // exact bf16 value, so its high half is the rounded result.
-#pragma unroll
-            for (int j = 0; j < 8; j++) f[j] = __fmul_rn(e2m1_value((wd >> (4 * j)) & 0xfu), sc);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) f[j] = bf16_to_f32(f32_to_bf16(mul_x86(e2m1_value((wd >> (4 * j)) & 0xfu), sc)));
-        }
-        bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+        decode_mx4(raw, side.word, t, bh);
     } else if constexpr (TF == TF_INT4) {
-        int64_t r = row < w.rows ? row : w.rows - 1;
-        int64_t g = k0 / w.group;
-        float s = load_scale(w.scale, r * w.scale_cols + g, w.scale_type);
-        int zp = w.zero ? (int)w.zero[r * w.scale_cols + g] - 8 : 0;
-        uint32_t wd = word_of(raw.a, t);
-        float f[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int q = (int)((wd >> (4 * j)) & 0xfu) - 8;
-            f[j] = bf16_to_f32(f32_to_bf16(mul_x86((float)(q - zp), s)));
-        }
-        bh = u32x4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+        int zp;
+        const float s = tile_scale_of<TF>(w, row, k0, &zp);
+        decode_int4(raw, t, s, zp, bh);
     }
 }
 
@@ -308,6 +365,7 @@ __device__ __forceinline__ bool select_segment(GemmParams &p, int64_t m0) {
     p.delta_rank = s.delta_rank;
     p.delta_b = s.delta_b;
     p.delta_xa = s.delta_rank ? p.delta_xa + (int64_t)s.off * p.delta_stride : nullptr;
+    if (p.xf) p.xf += (int64_t)blockIdx.z * p.xf_seg;
     return true;
 }
 

@@ -231,7 +231,7 @@ struct GroupSeg {
 };
 void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols,
                            int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
-                           const float *delta_xa, int delta_stride, hipStream_t s);
+                           const float *delta_xa, int delta_stride, hipStream_t s, DevBuf *ws);
 
 // attention.hip: prompt attention (model.zig:2935-2986) on the fp32 MFMA for
 // the head shapes it takes; q [n][heads][hd], caches [prompt][T][kvd], out

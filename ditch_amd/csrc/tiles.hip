@@ -380,6 +380,17 @@ __global__ void fp8_side_kernel(const void *scale, int32_t scale_type, uint32_t 
         out[i] = f2u(load_scale(scale, i, scale_type));
 }
 
+// Q8_0 side words of the GEMV: per 16-row group and 64-column unit, the 16
+// rows' two f16 block scales (low half the unit's first block) in one
+// 64-byte run, [group][unit][row % 16], from the [rows_pad][kt_pad] scales.
+__global__ void q8_side_kernel(const uint32_t *scale, uint32_t *out, int64_t groups, int64_t units) {
+    const int64_t total = groups * units * 16;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r16 = i % 16, gu = i / 16, u = gu % units, g = gu / units;
+        out[i] = scale[(g * 16 + r16) * units + u];
+    }
+}
+
 // INT4: the 16-bit scale (f16 or bf16 bits) | zero field << 16 per (row, group).
 __global__ void int4_side_kernel(const uint16_t *scale, const uint8_t *zero, uint32_t *out, int64_t total) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
@@ -788,8 +799,17 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
         default: break;
         }
         DITCH_TRY_HIP(hipGetLastError());
-        // side words of the tiled GEMM
-        if (v.fast && tf == TF_MX4) {
+        // side words of the tiled GEMM (the GEMV for Q8_0)
+        if (tf == TF_Q8) {
+            const int64_t total = a.groups_n * v.units_k * 16;
+            t->side = dev_alloc(total * 4);
+            t->part_bytes[3] = total * 4;
+            t->bytes += total * 4;
+            hipLaunchKernelGGL(q8_side_kernel, dim3(grid_for(total)), dim3(256), 0, s, (const uint32_t *)t->scale,
+                               (uint32_t *)t->side, a.groups_n, v.units_k);
+            v.side = (const uint32_t *)t->side;
+            v.side_cols = v.units_k;
+        } else if (v.fast && tf == TF_MX4) {
             v.side = (const uint32_t *)t->scale;
             v.side_cols = v.scale_cols / 4;
             t->mx = dev_alloc(code_bytes);

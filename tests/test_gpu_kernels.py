@@ -110,6 +110,20 @@ def test_matmulT_matches_oracle(dev, ref, kind, n, rows, cols):
     close(got, want, **TOL_MATMUL)
 
 
+@pytest.mark.parametrize("kind", MM_KINDS)
+@pytest.mark.parametrize("n,rows,cols", [(1, 40, 4096), (7, 33, 2880), (16, 50, 1536)])
+def test_gemv_long_rows_matches_oracle(dev, ref, kind, n, rows, cols):
+    """The GEMV regime over long rows: each wave's share of K runs through
+    its ring of in-flight units several times, with a ragged last round and
+    a ragged last row group."""
+    rng = np.random.default_rng(n * 131 + cols)
+    if kind.startswith(("q4_k", "q6_k")) and cols % 256:
+        pytest.skip("k-quants need 256-column rows")
+    w = wg.make(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
+
+
 def test_matmulT_odd_k(dev, ref):
     """K not a multiple of 8 takes the guarded activation loads."""
     rng = np.random.default_rng(11)
