@@ -103,6 +103,23 @@ def int4_quantize(w: torch.Tensor, group=128) -> HostWeight:
     return HostWeight.int_packed(words32, _np(s.reshape(rows, g)), rows, cols, 4, group, zero=zw32)
 
 
+def int4_random(rows, cols, rng: np.random.Generator, group=128, std=0.02) -> HostWeight:
+    """Random compressed-tensors pack-quantized 4-bit weights drawn in the
+    packed domain (no source matrix: fast at the MoE configurations' sizes):
+    fields uniform in 0..15, zero points in 6..9 packed along rows, f16 group
+    scales around std / 4.6 (the spread of a uniform field about its zero)."""
+    g = -(-cols // group)
+    words = rng.integers(0, 1 << 32, size=(rows, -(-cols * 4 // 32)), dtype=np.uint64).astype(np.uint32)
+    s = (std / 4.6 * rng.uniform(0.5, 1.5, size=(rows, g))).astype(np.float16)
+    zf = rng.integers(6, 10, size=(rows, g), dtype=np.int64)
+    zrows = -(-rows * 4 // 32)
+    zpad = np.zeros((zrows * 8, g), dtype=np.int64)
+    zpad[:rows] = zf
+    zw = (zpad.reshape(zrows, 8, g) << (np.arange(8, dtype=np.int64) * 4).reshape(1, 8, 1)).sum(axis=1)
+    zw32 = (zw & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+    return HostWeight.int_packed(words.view(np.int32), s, rows, cols, 4, group, zero=zw32)
+
+
 QUANTIZERS = {
     "f32": f32_weight,
     "bf16": bf16_weight,

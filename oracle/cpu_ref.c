@@ -1055,6 +1055,15 @@ static rtensor *slot_ptr(ref_model *m, int layer, int slot, int expert) {
     }
 }
 
+/* Rows of a virtual bf16 tensor decoded on the model's threads (each row on
+ * its own: the decode has no cross-row state). */
+typedef struct { const ditch_weight *w; uint16_t *out; int rc; } dq_ctx;
+static void dq_range(void *c, size_t a, size_t b, size_t slot) {
+    dq_ctx *x = (dq_ctx *)c;
+    for (size_t r = a; r < b; r++)
+        if (decode_bf16_row(x->w, r, x->out + r * x->w->cols)) x->rc = -1;
+}
+
 int ref_model_set(ref_model *m, int layer, int slot, int expert, const ditch_weight *w) {
     rtensor *t = slot_ptr(m, layer, slot, expert);
     if (!t) return fail("model_set: bad slot %d layer %d expert %d", slot, layer, expert);
@@ -1072,7 +1081,9 @@ int ref_model_set(ref_model *m, int layer, int slot, int expert, const ditch_wei
     if (is_bf16_virtual(w->dtype)) {
         /* mapped mode: the virtual bf16 tensor decoded once (dequant.zig:841-845) */
         uint16_t *buf = (uint16_t *)malloc(w->rows * w->cols * 2);
-        if (ref_dequant_rows(w, 0, w->rows, buf)) { free(buf); return -1; }
+        dq_ctx c = {w, buf, 0};
+        parallel_for(w->rows, m->threads, dq_range, &c);
+        if (c.rc) { free(buf); return -1; }
         memset(&t->w, 0, sizeof t->w);
         t->w.data = buf;
         t->w.dtype = DITCH_BF16;

@@ -122,6 +122,37 @@ def mla(fmt="fp8", hidden=256, layers=2, heads=4, q_lora=96, kv_lora=64, nope=32
     return spec
 
 
+def moe_c4(layers=2, vocab=8192, seed=0):
+    """Config C4's layer shape (Qwen3-30B-A3B: d=2048, 32/4 heads of 128, q/k
+    head norm, 128 experts top-8 of FFN 768, softmax router with renorm, INT4
+    group-128 asymmetric linear weights, router N(0, 0.02)), a reduced vocab
+    and layer count; the INT4 fields are drawn in the packed domain."""
+    hidden, heads, kv_heads, head_dim, experts, moe_inter = 2048, 32, 4, 128, 128, 768
+    rng = np.random.default_rng(seed)
+    spec = ModelSpec(hidden=hidden, inter=4 * hidden, layers=layers, heads=heads, kv_heads=kv_heads,
+                     head_dim=head_dim, vocab=vocab, rms_eps=1e-6, qk_norm=1, tie_embeddings=0, rope_theta=1e6,
+                     rope_len=512, n_experts=experts, top_k=8, moe_inter=moe_inter, norm_topk_prob=1,
+                     scoring=abi.SCORING_SOFTMAX, moe_layers=[1] * layers)
+    spec.set("EMBED", synth.bf16_weight(torch.from_numpy(rng.normal(0, 0.02, (vocab, hidden)).astype(np.float32))))
+    spec.set("LM_HEAD", synth.int4_random(vocab, hidden, rng))
+    spec.set("FINAL_NORM", 1 + rng.normal(0, 0.02, hidden))
+    for li in range(layers):
+        spec.set("ATTN_NORM", 1 + rng.normal(0, 0.02, hidden), li)
+        spec.set("FFN_NORM", 1 + rng.normal(0, 0.02, hidden), li)
+        for s_, r, c in (("Q", heads * head_dim, hidden), ("K", kv_heads * head_dim, hidden),
+                         ("V", kv_heads * head_dim, hidden), ("O", hidden, heads * head_dim)):
+            spec.set(s_, synth.int4_random(r, c, rng), li)
+        spec.set("Q_NORM", 1 + rng.normal(0, 0.02, head_dim), li)
+        spec.set("K_NORM", 1 + rng.normal(0, 0.02, head_dim), li)
+        spec.set("ROUTER", synth.f32_weight(torch.from_numpy(rng.normal(0, 0.02, (experts, hidden)).astype(np.float32))),
+                 li)
+        for e in range(experts):
+            spec.set("EXPERT_GATE", synth.int4_random(moe_inter, hidden, rng), li, e)
+            spec.set("EXPERT_UP", synth.int4_random(moe_inter, hidden, rng), li, e)
+            spec.set("EXPERT_DOWN", synth.int4_random(hidden, moe_inter, rng), li, e)
+    return spec
+
+
 def batch(prompts, lens, vocab, seed=0):
     """Flattened prompts (engine.zig:395-410): tokens, rows {b, pos}, the last
     row of each prompt (capture + logits)."""

@@ -280,3 +280,50 @@ def test_expert_cache_rejects_late_budget_and_tiny_budget(dev):
             gm.forward(tokens, rows, logit_rows=last)
     finally:
         gm.free()
+
+
+# ---------------------------------------------------------------------------
+# Config C4's layer shape (Qwen3-30B-A3B INT4 MoE + rank-2 edit)
+
+
+def test_c4_shape_moe_forward_edit_and_streaming(dev, ref):
+    """Two layers at C4's width (d 2048, 32/4 heads of 128, 128 experts top-8
+    of FFN 768, INT4 group 128): the forward, then the rank-2 none-mode edit
+    of every o_proj and every expert's down_proj (abliterate.zig:167-188,
+    264-280), resident and with the experts streamed through a cache of a
+    quarter of them, each against the oracle."""
+    spec = mg.moe_c4(layers=2, seed=12)
+    tokens, rows, last = mg.batch(4, [32, 20, 48, 28], spec.config["vocab"], seed=3)
+    rng = np.random.default_rng(14)
+    v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+    v = v.T.astype(np.float32)
+    cm = RefModel(spec)
+    gm = Model(dev, spec)
+    gs = None
+    try:
+        rg, lg, rc, lc = _moe_forward(gm, cm, tokens, rows, last)
+        check_parity(ref, rg, lg, rc, lc, "c4 shape")
+        for li in range(spec.config["layers"]):
+            for m in (gm, cm):
+                m.edit(li, abi.SLOT["O"], -1, v, 1.0)
+                for e in range(spec.config["n_experts"]):
+                    m.edit(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0)
+        rg2, lg2, rc2, lc2 = _moe_forward(gm, cm, tokens, rows, last)
+        check_parity(ref, rg2, lg2, rc2, lc2, "c4 shape edited")
+        assert np.abs(lc2 - lc).max() > 1e-4  # the edit changed the model
+        gm.free()
+        slot, _ = _cache_geometry(dev, spec, tokens, rows, last)
+        gs = Model(dev, spec, expert_cache_bytes=2 * 128 * slot // 4)
+        for li in range(spec.config["layers"]):
+            gs.edit(li, abi.SLOT["O"], -1, v, 1.0)
+            for e in range(spec.config["n_experts"]):
+                gs.edit(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0)
+        rs, ls = gs.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        check_parity(ref, rs, ls, rc2, lc2, "c4 shape edited, streamed")
+        st = gs.expert_cache_stats()
+        assert st["slots"] == 64 and st["evictions"] > 0
+    finally:
+        gm.free()
+        if gs is not None:
+            gs.free()
+        cm.free()
