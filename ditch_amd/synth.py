@@ -120,6 +120,18 @@ def int4_random(rows, cols, rng: np.random.Generator, group=128, std=0.02) -> Ho
     return HostWeight.int_packed(words.view(np.int32), s, rows, cols, 4, group, zero=zw32)
 
 
+def fp8_random(rows, cols, rng: np.random.Generator, block=128, std=0.02) -> HostWeight:
+    """Random E4M3 codes drawn in the code domain (uniform bytes, the two NaN
+    codes replaced by the largest finite ones) with an f32 scale per block x
+    block around std / 100 (the codes' RMS is about 100): fast at the MoE
+    configurations' sizes."""
+    codes = np.frombuffer(rng.bytes(rows * cols), dtype=np.uint8).reshape(rows, cols).copy()
+    codes -= ((codes & 0x7f) == 0x7f).view(np.uint8)
+    sr, sc = -(-rows // block), -(-cols // block)
+    s = (std / 100.0 * rng.uniform(0.5, 1.5, size=(sr, sc))).astype(np.float32)
+    return HostWeight.fp8(codes, s, block, block)
+
+
 QUANTIZERS = {
     "f32": f32_weight,
     "bf16": bf16_weight,

@@ -153,6 +153,57 @@ def moe_c4(layers=2, vocab=8192, seed=0):
     return spec
 
 
+def mla_c5(experts=64, vocab=8192, seed=0):
+    """Config C5's layer shapes (DeepSeek-V3: d=7168, MLA q_lora 1536 /
+    kv_lora 512 / nope 128 / rope 64 / v 128 over 128 heads, a dense first
+    layer of FFN 18432, then routed experts of FFN 2048, top-8 of 8 groups
+    with 4 groups kept, sigmoid router with correction bias 0, scaling 2.5,
+    one shared expert; FP8 E4M3 weights with 128 x 128 f32 block scales):
+    one dense and one routed layer, `experts` routed experts, a reduced vocab;
+    the FP8 codes drawn in the code domain."""
+    hidden, heads, q_lora, kv_lora, nope, rope, v_dim, dense_ff, moe_inter = 7168, 128, 1536, 512, 128, 64, 128, 18432, 2048
+    rng = np.random.default_rng(seed)
+    hd = nope + rope
+    spec = ModelSpec(hidden=hidden, inter=dense_ff, layers=2, heads=heads, kv_heads=heads, head_dim=hd,
+                     v_head_dim=v_dim, vocab=vocab, rms_eps=1e-6, tie_embeddings=0, rope_theta=10000.0, rope_len=512,
+                     rope_style=abi.ROPE_GPTJ, mla=1, q_lora_rank=q_lora, kv_lora_rank=kv_lora, qk_nope_dim=nope,
+                     qk_rope_dim=rope, attn_scale=float(np.float32(1) / np.sqrt(np.float32(hd))),
+                     n_experts=experts, top_k=8, moe_inter=moe_inter, norm_topk_prob=1,
+                     scoring=abi.SCORING_SIGMOID, group_limited=1, n_group=8, topk_group=4, routed_scaling=2.5,
+                     shared_inter=moe_inter, moe_layers=[0, 1])
+    f8 = lambda r, c: synth.fp8_random(r, c, rng)
+    bf = lambda r, c: synth.bf16_weight(torch.from_numpy(rng.normal(0, 0.02, (r, c)).astype(np.float32)))
+    spec.set("EMBED", bf(vocab, hidden))
+    spec.set("LM_HEAD", bf(vocab, hidden))
+    spec.set("FINAL_NORM", 1 + rng.normal(0, 0.02, hidden))
+    for li in range(2):
+        spec.set("ATTN_NORM", 1 + rng.normal(0, 0.02, hidden), li)
+        spec.set("FFN_NORM", 1 + rng.normal(0, 0.02, hidden), li)
+        spec.set("MLA_Q_A", f8(q_lora, hidden), li)
+        spec.set("MLA_Q_A_NORM", 1 + rng.normal(0, 0.02, q_lora), li)
+        spec.set("MLA_Q_B", f8(heads * hd, q_lora), li)
+        spec.set("MLA_KV_A", f8(kv_lora + rope, hidden), li)
+        spec.set("MLA_KV_A_NORM", 1 + rng.normal(0, 0.02, kv_lora), li)
+        spec.set("MLA_KV_B", f8(heads * (nope + v_dim), kv_lora), li)
+        spec.set("O", f8(hidden, heads * v_dim), li)
+        if li == 0:
+            spec.set("GATE", f8(dense_ff, hidden), li)
+            spec.set("UP", f8(dense_ff, hidden), li)
+            spec.set("DOWN", f8(hidden, dense_ff), li)
+        else:
+            spec.set("ROUTER", synth.f32_weight(torch.from_numpy(rng.normal(0, 0.02, (experts, hidden)).astype(np.float32))),
+                     li)
+            spec.set("ROUTER_CORRECTION", np.zeros(experts), li)
+            for e in range(experts):
+                spec.set("EXPERT_GATE", f8(moe_inter, hidden), li, e)
+                spec.set("EXPERT_UP", f8(moe_inter, hidden), li, e)
+                spec.set("EXPERT_DOWN", f8(hidden, moe_inter), li, e)
+            spec.set("SHARED_GATE", f8(moe_inter, hidden), li)
+            spec.set("SHARED_UP", f8(moe_inter, hidden), li)
+            spec.set("SHARED_DOWN", f8(hidden, moe_inter), li)
+    return spec
+
+
 def batch(prompts, lens, vocab, seed=0):
     """Flattened prompts (engine.zig:395-410): tokens, rows {b, pos}, the last
     row of each prompt (capture + logits)."""

@@ -327,3 +327,40 @@ def test_c4_shape_moe_forward_edit_and_streaming(dev, ref):
         if gs is not None:
             gs.free()
         cm.free()
+
+
+# ---------------------------------------------------------------------------
+# Config C5's layer shapes (DeepSeek-V3 FP8, MLA, group-limited routing)
+
+
+def test_c5_shape_mla_moe_streamed(dev, ref):
+    """A dense and a routed layer at C5's width (d 7168, MLA over 128 heads,
+    dense FFN 18432, experts of FFN 2048 top-8 of 8 groups keeping 4,
+    shared expert, FP8 128 x 128): resident, and with the routed experts
+    streamed through a cache of a quarter of them (the C5 configuration's
+    96 GB cache over 101.5 GB of experts, scaled to 64 experts), against the
+    oracle."""
+    spec = mg.mla_c5(experts=64, seed=5)
+    tokens, rows, last = mg.batch(2, [40, 24], spec.config["vocab"], seed=3)
+    cm = RefModel(spec, threads=16)
+    try:
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        gm = Model(dev, spec)
+        try:
+            rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        finally:
+            gm.free()
+        check_parity(ref, rg, lg, rc, lc, "c5 shape")
+        slot, total = _cache_geometry(dev, spec, tokens, rows, last)
+        assert total == 64
+        gs = Model(dev, spec, expert_cache_bytes=16 * slot)
+        try:
+            for it in range(2):
+                rs, ls = gs.forward(tokens, rows, capture_rows=last, logit_rows=last)
+                check_parity(ref, rs, ls, rc, lc, f"c5 shape streamed pass {it}")
+            st = gs.expert_cache_stats()
+            assert st["slots"] == 16 and st["evictions"] > 0
+        finally:
+            gs.free()
+    finally:
+        cm.free()
