@@ -167,86 +167,123 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(u32x4 *xs, int64_t l
 }
 
 // RMSNorm of 16 rows per block written as the MX fragments of a scaled-MFMA
-// product (and, when `out`, as f32 rows): one thread per lane slot (a
-// token's 32-column E8M0 block).
+// product (and, when `out`, as f32 rows). Pass 1: each wave sums the squares
+// of 4 rows with 16 loads in flight. Pass 2: 512 columns at a time, the 16
+// rows are staged in LDS by coalesced loads, then each thread normalises one
+// lane slot (a token's 32-column E8M0 block) of one of the chunk's 4 stages.
+constexpr int RS_CHUNK = 512;  // columns per LDS chunk: 4 stages of 128
 __global__ __launch_bounds__(256) void rmsnorm_split_mx_kernel(uint8_t *xm, int64_t ldst, float *out, const float *x,
                                                                const float *w, int64_t wlen, int64_t len, float eps,
                                                                int gemma, int64_t n) {
     __shared__ float inv_s[16];
+    __shared__ float chunk[16][RS_CHUNK + 4];
     const int64_t m16 = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const bool vec = (len % 4) == 0;
-    for (int rr = 0; rr < 4; rr++) {
-        const int row = wave * 4 + rr;
-        const int64_t r = m16 * 16 + row;
-        float ss = 0.f;
-        if (r < n) {
-            const float *xr = x + r * len;
-            if (vec) {
-                for (int64_t i = 4 * lane; i < len; i += 256) {
-                    float4 v = *(const float4 *)(xr + i);
-                    ss = __builtin_fmaf(v.x, v.x, ss);
-                    ss = __builtin_fmaf(v.y, v.y, ss);
-                    ss = __builtin_fmaf(v.z, v.z, ss);
-                    ss = __builtin_fmaf(v.w, v.w, ss);
-                }
-            } else {
-                for (int64_t i = lane; i < len; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    const bool vec = (len % 4) == 0 && ((uintptr_t)x & 15) == 0;
+    {
+        float ss[4] = {0.f, 0.f, 0.f, 0.f};
+        const int64_t r0 = m16 * 16 + wave * 4;
+        if (vec) {
+            for (int64_t i0 = 4 * lane; i0 < len; i0 += 1024) {
+                float4 v[4][4];
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int64_t i = i0 + 256 * u;
+                        v[rr][u] = (r0 + rr < n && i < len) ? *(const float4 *)(x + (r0 + rr) * len + i)
+                                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        ss[rr] = __builtin_fmaf(v[rr][u].x, v[rr][u].x, ss[rr]);
+                        ss[rr] = __builtin_fmaf(v[rr][u].y, v[rr][u].y, ss[rr]);
+                        ss[rr] = __builtin_fmaf(v[rr][u].z, v[rr][u].z, ss[rr]);
+                        ss[rr] = __builtin_fmaf(v[rr][u].w, v[rr][u].w, ss[rr]);
+                    }
             }
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++)
+                if (r0 + rr < n)
+                    for (int64_t i = lane; i < len; i += 64)
+                        ss[rr] = __builtin_fmaf(x[(r0 + rr) * len + i], x[(r0 + rr) * len + i], ss[rr]);
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
-        if (lane == 0)
-            inv_s[row] = r < n ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps))) : 0.f;
+        for (int rr = 0; rr < 4; rr++) {
+            float t = ss[rr];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) t = __fadd_rn(t, __shfl_xor(t, o, 64));
+            if (lane == 0)
+                inv_s[wave * 4 + rr] =
+                    r0 + rr < n ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(t, (float)len), eps))) : 0.f;
+        }
     }
     __syncthreads();
-    for (int64_t q = threadIdx.x; q < ldst * 64; q += 256) {
-        const int64_t st = q >> 6;
-        const int l = (int)(q & 63), row = l & 15;
-        const int64_t r = m16 * 16 + row;
-        const int64_t k0 = st * 128 + 32 * (l >> 4);
-        const float inv = inv_s[row];
-        float v[32];
-        const bool full = r < n && vec && k0 + 32 <= len;
-#pragma unroll
-        for (int j = 0; j < 32; j += 4) {
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = make_float4(1.f, 1.f, 1.f, 1.f);
-            if (full) a = *(const float4 *)(x + r * len + k0 + j);
-            else {
-                float t[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) t[u] = (r < n && k0 + j + u < len) ? x[r * len + k0 + j + u] : 0.f;
-                a = make_float4(t[0], t[1], t[2], t[3]);
-            }
-            if (wlen > 0 && (wlen % 4) == 0 && k0 + j + 4 <= wlen) b = *(const float4 *)(w + k0 + j);
-            else if (wlen > 0) {
-                float t[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) t[u] = k0 + j + u < wlen ? w[k0 + j + u] : 1.f;
-                b = make_float4(t[0], t[1], t[2], t[3]);
-            }
-            const float xa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                float y = 0.f;
-                if (r < n && k0 + j + u < len) {
-                    y = __fmul_rn(xa[u], inv);
-                    if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wb[u]) : wb[u]);
+    const int st_l = threadIdx.x >> 6, l = lane, row = l & 15, kb = l >> 4;
+    const int64_t r = m16 * 16 + row;
+    const float inv = inv_s[row];
+    for (int64_t c0 = 0; c0 < ldst * 128; c0 += RS_CHUNK) {
+        // the 16 rows' columns c0 .. c0 + 512 (zero past the matrix)
+        for (int q = threadIdx.x; q < 16 * RS_CHUNK / 4; q += 256) {
+            const int qr = q / (RS_CHUNK / 4), qc = (q % (RS_CHUNK / 4)) * 4;
+            const int64_t rq = m16 * 16 + qr, k = c0 + qc;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rq < n) {
+                if (vec && k + 4 <= len) a = *(const float4 *)(x + rq * len + k);
+                else {
+                    a.x = k < len ? x[rq * len + k] : 0.f;
+                    a.y = k + 1 < len ? x[rq * len + k + 1] : 0.f;
+                    a.z = k + 2 < len ? x[rq * len + k + 2] : 0.f;
+                    a.w = k + 3 < len ? x[rq * len + k + 3] : 0.f;
                 }
-                v[j + u] = y;
             }
+            *(float4 *)&chunk[qr][qc] = a;
         }
-        if (out && r < n) {
-            if (full) {
+        __syncthreads();
+        const int64_t st = c0 / 128 + st_l;
+        if (st < ldst) {
+            const int kl = st_l * 128 + kb * 32;
+            const int64_t k0 = c0 + kl;
+            float v[32];
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) *(float4 *)(out + r * len + k0 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
-            } else {
+            for (int j = 0; j < 32; j += 4) {
+                const float4 a = *(const float4 *)&chunk[row][kl + j];
+                float4 b = make_float4(1.f, 1.f, 1.f, 1.f);
+                if (wlen > 0 && (wlen % 4) == 0 && k0 + j + 4 <= wlen) b = *(const float4 *)(w + k0 + j);
+                else if (wlen > 0) {
+                    b.x = k0 + j < wlen ? w[k0 + j] : 1.f;
+                    b.y = k0 + j + 1 < wlen ? w[k0 + j + 1] : 1.f;
+                    b.z = k0 + j + 2 < wlen ? w[k0 + j + 2] : 1.f;
+                    b.w = k0 + j + 3 < wlen ? w[k0 + j + 3] : 1.f;
+                }
+                const float xa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-                for (int j = 0; j < 32; j++)
-                    if (k0 + j < len) out[r * len + k0 + j] = v[j];
+                for (int u = 0; u < 4; u++) {
+                    float y = 0.f;
+                    if (r < n && k0 + j + u < len) {
+                        y = __fmul_rn(xa[u], inv);
+                        if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wb[u]) : wb[u]);
+                    }
+                    v[j + u] = y;
+                }
             }
+            if (out && r < n) {
+                if (vec && k0 + 32 <= len) {
+#pragma unroll
+                    for (int j = 0; j < 32; j += 4)
+                        *(float4 *)(out + r * len + k0 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 32; j++)
+                        if (k0 + j < len) out[r * len + k0 + j] = v[j];
+                }
+            }
+            mx_write_slot(v, xm + (m16 * ldst + st) * MX_BLOCK, l);
         }
-        mx_write_slot(v, xm + (m16 * ldst + st) * MX_BLOCK, l);
+        __syncthreads();
     }
 }
 
