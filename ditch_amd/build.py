@@ -33,7 +33,8 @@ FLAGS = [
 # ring of in-flight units is unrolled whatever its size (indexed at run time
 # it would live in scratch memory)
 EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-         "gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=1000000"]}
+         "gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=1000000"],
+         "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

@@ -1,4 +1,4 @@
-// attention.hip — prompt attention on the fp32 matrix cores.
+// attention.hip — prompt attention on the bf16 matrix cores.
 //
 // For every row (query token) and head: scores[p] = scale * dot(q, k_p) over
 // the keys p <= pos of the row's prompt, softmax (max, Cephes exp of the
@@ -8,11 +8,19 @@
 //
 // A workgroup takes 16 consecutive rows and one KV head; each wave is one
 // query head of that KV head's group. Keys and values are staged in LDS in
-// chunks of 32 positions (shared by the group's waves) and multiplied on
-// v_mfma_f32_16x16x4f32, whose products are exact: only the order of the f32
-// additions differs from the CPU's dot products. The softmax is two-pass in
-// the reference's order: the row maximum over every key first, then
-// exp(s - max), the sum, and the value accumulation; the output is scaled by
+// chunks of 32 positions (shared by the group's waves), each f32 value as
+// two bf16 terms (hi = rne(v), lo = rne(v - hi)), and multiplied on
+// v_mfma_f32_16x16x32_bf16 with three products per pair of operands
+// (hi.hi + hi.lo + lo.hi): each product of two f32 values is taken to within
+// 2^-16 of its magnitude, and the f32 accumulation order differs from the
+// CPU's dot products. The scores are computed transposed (keys x rows), so
+// the lanes that hold a row's scores also hold the A operand of P.V with the
+// k index running over their own keys, and the value operand is read for
+// the same keys: no transposition of P. The softmax is two-pass in the
+// reference's order: the row maximum over every key first (the scores of up
+// to CACHED chunks kept in LDS, each lane its own, longer prompts'
+// recomputed), then
+// exp(s - max), the sum and the value accumulation; the output is scaled by
 // 1/sum at the end. Rows of the block that belong to different prompts are
 // processed one prompt at a time.
 #include "decode.h"
@@ -21,43 +29,53 @@
 
 namespace ditch {
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int AK = 32;      // keys per LDS chunk
+constexpr int CACHED = 4;   // chunks whose scores stay in LDS between the passes
 
-__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+// bf16 terms of two f32 values: hi = rne pair, lo = rne pair of the remainders
+__device__ __forceinline__ uint2 split_pair(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, bf16x2_t));
+    const float ra = __fsub_rn(a, u2f(hi << 16)), rb = __fsub_rn(b, u2f(hi & 0xffff0000u));
+    return make_uint2(hi, __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{ra, rb}, bf16x2_t)));
 }
-
-// max / sum over the 16 lanes that share lane / 16
-__device__ __forceinline__ float max16(float v) {
+// the four pairs of 8 values as the hi and lo words of an MFMA operand
+__device__ __forceinline__ void split8_words(const float (&v)[8], u32x4 &hi, u32x4 &lo) {
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
-    return v;
+    for (int j = 0; j < 4; j++) {
+        const uint2 t = split_pair(v[2 * j], v[2 * j + 1]);
+        hi[j] = t.x;
+        lo[j] = t.y;
+    }
 }
 
-constexpr int AK = 32;  // keys per LDS chunk
+// acc += (ah + al) . (bh + bl) without the al . bl term
+__device__ __forceinline__ floatx4 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, floatx4 acc) {
+    acc = mfma_bf16(ah, bh, acc);
+    acc = mfma_bf16(ah, bl, acc);
+    return mfma_bf16(al, bh, acc);
+}
 
-// MFMA operand layouts (v_mfma_f32_16x16x4f32): A lane l = row l%16, k l/16;
-// B lane l = k l/16, column l%16; D lane l = rows 4*(l/16) + r, column l%16.
-// The k index of step j is assigned per lane group g = l/16: QK^T steps over
-// head dims g*HD/4 + j, PV steps over keys (AK/4) g + j, so every lane reads
-// contiguous runs (ds_read_b128) from padded, bank-conflict-free rows.
+// v_mfma_f32_16x16x32_bf16 layouts: A lane l = row l%16, k 8(l/16)..+8;
+// B lane l = k 8(l/16)..+8, column l%16; D lane l = rows 4(l/16)+r, column
+// l%16. Scores S^T = K Q^T: A = keys (lane: key c16 of a 16-key block, head
+// dims 32 s + 8 g ..), B = the query (dims 32 s + 8 g .., row c16), so lane
+// (g, c16) holds row c16's scores of keys 4 g + r and 16 + 4 g + r of the
+// chunk. P.V: A = P (row c16, k = those 8 keys), B = V (the same 8 keys,
+// dim c16 of a 16-dim block), D = out rows 4 g + r, dim c16.
 template <int HD, int VD, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
-    constexpr int KS = HD + 4;  // K row stride (floats)
-    constexpr int VS = AK + 4;  // transposed V row stride
-    constexpr int PS = AK + 4;  // P row stride
-    constexpr int QJ = HD / 4;  // QK^T k steps
-    constexpr int VB = VD / 16; // output column blocks
-    static_assert(HD % 16 == 0 && VD % 16 == 0, "head dims");
-    __shared__ float Ks[AK * KS];
-    __shared__ float Vt[VD * VS];
-    __shared__ float Ps[NW][16 * PS];
+    constexpr int KRS = HD + 8;  // K row stride (bf16): 16 keys of one read hit distinct banks
+    constexpr int VRS = AK + 8;  // transposed V row stride (bf16)
+    constexpr int QS = HD / 32;  // k steps of the scores
+    constexpr int VB = VD / 16;  // output column blocks
+    constexpr int KB = AK / 16;  // 16-key blocks per chunk
+    static_assert(HD % 32 == 0 && VD % 16 == 0, "head dims");
+    __shared__ __attribute__((aligned(16))) uint16_t Kh[AK * KRS], Kl[AK * KRS];
+    __shared__ __attribute__((aligned(16))) uint16_t Vh[VD * VRS], Vl[VD * VRS];
     __shared__ int32_t rb[16], rp[16];
+    __shared__ floatx4 Sc[NW][CACHED * KB][64];  // pass 1's scores, [wave][chunk, key block][lane]
     // SPLIT: the block's finished output rows per wave, for the fragments
     constexpr int OS = VD + 4;
     __shared__ float Ot[SPLIT ? NW : 1][SPLIT ? 16 * OS : 1];
@@ -79,63 +97,144 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // this lane's query (A operand): row c16, head dims g*QJ .. +QJ
-    float qv[QJ];
+    // this lane's query words (B operand): row c16, head dims 32 s + 8 g .. +8
+    u32x4 qh[QS], ql[QS];
     {
         const int64_t r = r0 + c16;
         const bool ok = head_ok && r < a.n;
-        const float *q = a.q + ((ok ? r : 0) * a.heads + h) * a.hd + g * QJ;
+        const float *q = a.q + ((ok ? r : 0) * a.heads + h) * a.hd + 8 * g;
 #pragma unroll
-        for (int j = 0; j < QJ; j += 4) {
-            float4 v = ok ? *(const float4 *)(q + j) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qv[j] = v.x; qv[j + 1] = v.y; qv[j + 2] = v.z; qv[j + 3] = v.w;
+        for (int st = 0; st < QS; st++) {
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (ok) {
+                v0 = *(const float4 *)(q + 32 * st);
+                v1 = *(const float4 *)(q + 32 * st + 4);
+            }
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            split8_words(v, qh[st], ql[st]);
         }
     }
 
     const int nthreads = NW * 64;
-    auto stage = [&](int64_t b, int64_t c0, int64_t kmax, bool with_v) {
+    // Chunks are staged in two steps so that the next chunk's global loads
+    // are in flight while the current one is multiplied: load_* fetches a
+    // chunk into registers, put_* writes it (as bf16 terms) into LDS.
+    constexpr bool PF = NW >= 4;
+    constexpr int KI = PF ? (AK * (HD / 8) + NW * 64 - 1) / (NW * 64) : 1;        // K items per thread
+    constexpr int VI = PF ? ((AK / 2) * (VD / 4) + NW * 64 - 1) / (NW * 64) : 1;  // V items per thread
+    float4 kr[KI][2], vr[VI][2];
+    // keys c0 .. c0 + AK of prompt b (zero past kmax): item = (key, 8 dims)
+    auto load_k = [&](int64_t b, int64_t c0, int64_t kmax) {
         const float *kb = a.kc + (b * a.T) * a.kvd + hkv * a.hd;
-        const float *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
-        for (int i = threadIdx.x; i < AK * (HD / 4); i += nthreads) {
-            const int key = i / (HD / 4), d = (i % (HD / 4)) * 4;
+#pragma unroll
+        for (int t = 0; t < KI; t++) {
+            const int i = threadIdx.x + t * nthreads;
+            const int key = i / (HD / 8), d = (i % (HD / 8)) * 8;
             const int64_t p = c0 + key;
-            float4 v = p <= kmax ? *(const float4 *)(kb + p * a.kvd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-            *(float4 *)&Ks[key * KS + d] = v;
-        }
-        if (with_v) {
-            for (int i = threadIdx.x; i < AK * (VD / 4); i += nthreads) {
-                const int key = i / (VD / 4), d = (i % (VD / 4)) * 4;
-                const int64_t p = c0 + key;
-                float4 v = p <= kmax ? *(const float4 *)(vb + p * a.kvd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-                Vt[(d + 0) * VS + key] = v.x;
-                Vt[(d + 1) * VS + key] = v.y;
-                Vt[(d + 2) * VS + key] = v.z;
-                Vt[(d + 3) * VS + key] = v.w;
+            kr[t][0] = kr[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < AK * (HD / 8) && p <= kmax) {
+                kr[t][0] = *(const float4 *)(kb + p * a.kvd + d);
+                kr[t][1] = *(const float4 *)(kb + p * a.kvd + d + 4);
             }
         }
     };
-    // scores of the staged chunk's key blocks (16 keys each), D layout,
-    // masked; the blocks' MFMA chains are interleaved
-    constexpr int KB = AK / 16;
-    auto scores = [&](floatx4 (&s)[KB], int64_t c0, const int (&pos)[4]) {
+    auto put_k = [&]() {
 #pragma unroll
-        for (int kb = 0; kb < KB; kb++) s[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < KI; t++) {
+            const int i = threadIdx.x + t * nthreads;
+            if (i >= AK * (HD / 8)) continue;
+            const int key = i / (HD / 8), d = (i % (HD / 8)) * 8;
+            const float v[8] = {kr[t][0].x, kr[t][0].y, kr[t][0].z, kr[t][0].w,
+                                kr[t][1].x, kr[t][1].y, kr[t][1].z, kr[t][1].w};
+            u32x4 hi, lo;
+            split8_words(v, hi, lo);
+            *(u32x4 *)&Kh[key * KRS + d] = hi;
+            *(u32x4 *)&Kl[key * KRS + d] = lo;
+        }
+    };
+    // without prefetch: a chunk loaded and written item by item
+    auto stage_k = [&](int64_t b, int64_t c0, int64_t kmax) {
+        const float *kb = a.kc + (b * a.T) * a.kvd + hkv * a.hd;
+        for (int i = threadIdx.x; i < AK * (HD / 8); i += nthreads) {
+            const int key = i / (HD / 8), d = (i % (HD / 8)) * 8;
+            const int64_t p = c0 + key;
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (p <= kmax) {
+                v0 = *(const float4 *)(kb + p * a.kvd + d);
+                v1 = *(const float4 *)(kb + p * a.kvd + d + 4);
+            }
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            u32x4 hi, lo;
+            split8_words(v, hi, lo);
+            *(u32x4 *)&Kh[key * KRS + d] = hi;
+            *(u32x4 *)&Kl[key * KRS + d] = lo;
+        }
+    };
+    auto stage_v = [&](int64_t b, int64_t c0, int64_t kmax) {
+        const float *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
+        for (int i = threadIdx.x; i < (AK / 2) * (VD / 4); i += nthreads) {
+            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const int64_t p = c0 + 2 * kp;
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (p <= kmax) v0 = *(const float4 *)(vb + p * a.kvd + d);
+            if (p + 1 <= kmax) v1 = *(const float4 *)(vb + (p + 1) * a.kvd + d);
+            const float x0[4] = {v0.x, v0.y, v0.z, v0.w}, x1[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-        for (int j = 0; j < QJ; j += 4) {
-#pragma unroll
-            for (int kb = 0; kb < KB; kb++) {
-                float4 k4 = *(const float4 *)&Ks[(kb * 16 + c16) * KS + g * QJ + j];
-                s[kb] = mfma4(qv[j], k4.x, s[kb]);
-                s[kb] = mfma4(qv[j + 1], k4.y, s[kb]);
-                s[kb] = mfma4(qv[j + 2], k4.z, s[kb]);
-                s[kb] = mfma4(qv[j + 3], k4.w, s[kb]);
+            for (int j = 0; j < 4; j++) {
+                const uint2 w2 = split_pair(x0[j], x1[j]);
+                *(uint32_t *)&Vh[(d + j) * VRS + 2 * kp] = w2.x;
+                *(uint32_t *)&Vl[(d + j) * VRS + 2 * kp] = w2.y;
             }
         }
+    };
+    // values of the same keys: item = (key pair, 4 dims), written transposed [dim][key]
+    auto load_v = [&](int64_t b, int64_t c0, int64_t kmax) {
+        const float *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
+#pragma unroll
+        for (int t = 0; t < VI; t++) {
+            const int i = threadIdx.x + t * nthreads;
+            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const int64_t p = c0 + 2 * kp;
+            vr[t][0] = vr[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < (AK / 2) * (VD / 4)) {
+                if (p <= kmax) vr[t][0] = *(const float4 *)(vb + p * a.kvd + d);
+                if (p + 1 <= kmax) vr[t][1] = *(const float4 *)(vb + (p + 1) * a.kvd + d);
+            }
+        }
+    };
+    auto put_v = [&]() {
+#pragma unroll
+        for (int t = 0; t < VI; t++) {
+            const int i = threadIdx.x + t * nthreads;
+            if (i >= (AK / 2) * (VD / 4)) continue;
+            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const float x0[4] = {vr[t][0].x, vr[t][0].y, vr[t][0].z, vr[t][0].w};
+            const float x1[4] = {vr[t][1].x, vr[t][1].y, vr[t][1].z, vr[t][1].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint2 w2 = split_pair(x0[j], x1[j]);
+                *(uint32_t *)&Vh[(d + j) * VRS + 2 * kp] = w2.x;
+                *(uint32_t *)&Vl[(d + j) * VRS + 2 * kp] = w2.y;
+            }
+        }
+    };
+    // the staged chunk's scores (transposed D layout), scaled and masked for
+    // this lane's row position
+    auto scores = [&](floatx4 (&sc)[KB], int64_t c0, int row_pos) {
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
-            const int64_t key = c0 + kb * 16 + c16;
+            floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; r++) s[kb][r] = key <= pos[r] ? __fmul_rn(s[kb][r], a.scale) : -INFINITY;
+            for (int st = 0; st < QS; st++) {
+                const u32x4 kh = *(const u32x4 *)&Kh[(kb * 16 + c16) * KRS + 32 * st + 8 * g];
+                const u32x4 kl = *(const u32x4 *)&Kl[(kb * 16 + c16) * KRS + 32 * st + 8 * g];
+                acc = mfma3(kh, kl, qh[st], ql[st], acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int64_t key = c0 + kb * 16 + 4 * g + r;
+                sc[kb][r] = key <= row_pos ? __fmul_rn(acc[r], a.scale) : -INFINITY;
+            }
         }
     };
 
@@ -157,75 +256,105 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
                 kmax = rp[i] > kmax ? rp[i] : kmax;
             }
         done |= in_mask;
-        // positions of this lane's four D-layout rows (-1: not in this prompt)
+        // this lane's row (c16) position, and those of its four output rows
+        const int row_pos = ((in_mask >> c16) & 1) ? rp[c16] : -1;
         int pos[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int row = 4 * g + r;
             pos[r] = ((in_mask >> row) & 1) ? rp[row] : -1;
         }
+        const int nch = (kmax + AK) / AK;
+        const bool cached = nch <= CACHED;
 
-        // pass 1: the row maxima
-        float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        for (int64_t c0 = 0; c0 <= kmax; c0 += AK) {
+        // pass 1: the row maximum (scores of the first CACHED chunks kept).
+        // With four waves the next chunk's loads are issued before the
+        // current one is multiplied (PF); smaller groups load just in time
+        // (their threads would need 2-4x the registers).
+        float m = -INFINITY;
+        if constexpr (PF) load_k(b, 0, kmax);
+        for (int c = 0; c < nch; c++) {
             __syncthreads();
-            stage(b, c0, kmax, false);
+            if constexpr (!PF) stage_k(b, (int64_t)c * AK, kmax);
+            else put_k();
             __syncthreads();
+            if constexpr (PF) {
+                if (c + 1 < nch) load_k(b, (int64_t)(c + 1) * AK, kmax);
+                else {
+                    load_v(b, 0, kmax);
+                    if (!cached) load_k(b, 0, kmax);
+                }
+            }
             floatx4 sc[KB];
-            scores(sc, c0, pos);
+            scores(sc, (int64_t)c * AK, row_pos);
 #pragma unroll
             for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) m[r] = fmaxf(m[r], sc[kb][r]);
-        }
+                for (int r = 0; r < 4; r++) m = fmaxf(m, sc[kb][r]);
+            if (cached) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) m[r] = max16(m[r]);
+                for (int kb = 0; kb < KB; kb++) Sc[wave][c * KB + kb][lane] = sc[kb];
+            }
+        }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
 
         // pass 2: exp, sums and P V
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        float sum = 0.f;
         floatx4 o[VB];
 #pragma unroll
         for (int db = 0; db < VB; db++) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-        float *P = Ps[wave];
-        for (int64_t c0 = 0; c0 <= kmax; c0 += AK) {
+        for (int c = 0; c < nch; c++) {
             __syncthreads();
-            stage(b, c0, kmax, true);
+            if constexpr (!PF) {
+                stage_v(b, (int64_t)c * AK, kmax);
+                if (!cached) stage_k(b, (int64_t)c * AK, kmax);
+            } else {
+                if (!cached) put_k();
+                put_v();
+            }
             __syncthreads();
+            if constexpr (PF) {
+                if (c + 1 < nch) {
+                    load_v(b, (int64_t)(c + 1) * AK, kmax);
+                    if (!cached) load_k(b, (int64_t)(c + 1) * AK, kmax);
+                }
+            }
             floatx4 sc[KB];
-            scores(sc, c0, pos);
+            if (cached) {
 #pragma unroll
-            for (int kb = 0; kb < KB; kb++) {
-                const floatx4 &s = sc[kb];
+                for (int kb = 0; kb < KB; kb++) sc[kb] = Sc[wave][c * KB + kb][lane];
+            } else {
+                scores(sc, (int64_t)c * AK, row_pos);
+            }
+            float e[8];
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    float e = pos[r] >= 0 && s[r] != -INFINITY ? exp_cephes(__fsub_rn(s[r], m[r])) : 0.f;
-                    sum[r] = __fadd_rn(sum[r], e);
-                    P[(4 * g + r) * PS + kb * 16 + c16] = e;
+                    const float s = sc[kb][r];
+                    const float v = row_pos >= 0 && s != -INFINITY ? exp_cephes(__fsub_rn(s, m)) : 0.f;
+                    sum = __fadd_rn(sum, v);
+                    e[kb * 4 + r] = v;
                 }
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            // out[row][dim] += sum_key P[row][key] V[key][dim]; keys (AK/4) g + j
-            constexpr int KG = AK / 4;
-            const float *pa = &P[c16 * PS + KG * g];
+            u32x4 ph, pl;
+            split8_words(e, ph, pl);
+            // out[row][dim] += sum over the lane's 8 keys of P[row][key] V[key][dim]
 #pragma unroll
-            for (int j = 0; j < KG; j += 4) {
-                float4 p4 = *(const float4 *)(pa + j);
-#pragma unroll
-                for (int db = 0; db < VB; db++) {
-                    float4 v4 = *(const float4 *)&Vt[(db * 16 + c16) * VS + KG * g + j];
-                    o[db] = mfma4(p4.x, v4.x, o[db]);
-                    o[db] = mfma4(p4.y, v4.y, o[db]);
-                    o[db] = mfma4(p4.z, v4.z, o[db]);
-                    o[db] = mfma4(p4.w, v4.w, o[db]);
-                }
+            for (int db = 0; db < VB; db++) {
+                const uint16_t *vh = &Vh[(db * 16 + c16) * VRS + 4 * g], *vl = &Vl[(db * 16 + c16) * VRS + 4 * g];
+                const uint2 h0 = *(const uint2 *)vh, h1 = *(const uint2 *)(vh + 16);
+                const uint2 l0 = *(const uint2 *)vl, l1 = *(const uint2 *)(vl + 16);
+                o[db] = mfma3(ph, pl, u32x4{h0.x, h0.y, h1.x, h1.y}, u32x4{l0.x, l0.y, l1.x, l1.y}, o[db]);
             }
-            __builtin_amdgcn_wave_barrier();
         }
+        // the row sums over all keys; output row 4 g + r's from lane 4 g + r
+        sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
+        sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
         float inv[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float t = sum16(sum[r]);
+            const float t = __shfl(sum, 4 * g + r, 64);
             inv[r] = t > 0.f ? __fdiv_rn(1.0f, t) : 0.f;
         }
         if (head_ok) {
