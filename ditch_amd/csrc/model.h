@@ -107,7 +107,7 @@ struct ditch_hip_model {
     float *rope_cos = nullptr, *rope_sin = nullptr;
     // workspace
     ditch::DevBuf x, hbuf, q, k, v, att, o, g, u, kc, vc, rowsb, xa, logit_h, mla_a, mla_b, mla_c;
-    ditch::DevBuf r_logits, r_sel, r_selw, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
+    ditch::DevBuf r_logits, r_sel, r_selw, r_ord, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
         segs, segd, e_xa;
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)

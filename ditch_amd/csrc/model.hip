@@ -197,6 +197,7 @@ struct RouteArgs {
     const float *corr;      // [E] or null
     int32_t *sel;           // [n][k]
     float *selw;            // [n][k]
+    int32_t *ord;           // [n][k]: the selections in ascending expert index
     int64_t n, E, k, n_group, topk_group;
     int scoring, group_limited, norm_topk;
     float scaling;
@@ -204,76 +205,149 @@ struct RouteArgs {
 
 constexpr int ROUTE_MAXE = 512;
 constexpr int ROUTE_MAXG = 64;
+constexpr int ROUTE_EJ = ROUTE_MAXE / 64;  // experts per lane
 
-__global__ void route_kernel(RouteArgs a) {
-    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// (value, index) of the better of two candidates of a top-k pass: the
+// larger value, the lower index on ties (moe.zig:971-985: strict > in index
+// order); a candidate that is not above -inf (or NaN) never wins.
+__device__ __forceinline__ void better(float &v, int &i, float v2, int i2) {
+    const bool ok2 = v2 > -INFINITY, ok = v > -INFINITY;
+    if (ok2 && (!ok || v2 > v || (v2 == v && i2 < i))) {
+        v = v2;
+        i = i2;
+    }
+}
+__device__ __forceinline__ int wave_argmax(float v, int i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(v, o, 64);
+        const int i2 = __shfl_xor(i, o, 64);
+        better(v, i, v2, i2);
+    }
+    return v > -INFINITY ? i : 0;  // nothing above -inf: the reference's initial best, index 0
+}
+
+// Router of one token per wave (moe.zig:998-1110): softmax (max, Cephes exp,
+// sum, 1/sum) or sigmoid scores, correction bias for the choice,
+// group-limited selection (a group's score is its best, or with the bias its
+// best two, in index order; kept groups chosen by repeated argmax), top-k by
+// repeated argmax with ties to the lower index, renormalisation and scaling.
+// Lane l holds experts l + 64 j.
+__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+    __shared__ float chs[4][ROUTE_MAXE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t t = (int64_t)blockIdx.x * 4 + wave;
     if (t >= a.n) return;
     float *row = a.logits + t * a.E;
+    float p[ROUTE_EJ], ch[ROUTE_EJ];
+#pragma unroll
+    for (int j = 0; j < ROUTE_EJ; j++) {
+        const int64_t e = lane + 64 * j;
+        p[j] = e < a.E ? row[e] : -INFINITY;
+    }
     if (a.scoring == DITCH_SCORING_SOFTMAX) {
         float m = -INFINITY;
-        for (int64_t e = 0; e < a.E; e++) m = fmaxf(m, row[e]);
-        float s = 0.f;
-        for (int64_t e = 0; e < a.E; e++) {
-            float v = exp_cephes(__fsub_rn(row[e], m));
-            row[e] = v;
-            s = __fadd_rn(s, v);
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) m = fmaxf(m, p[j]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float sm = 0.f;
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) {
+            p[j] = lane + 64 * j < a.E ? exp_cephes(__fsub_rn(p[j], m)) : 0.f;
+            sm = __fadd_rn(sm, p[j]);
         }
-        float inv = __fdiv_rn(1.0f, s);
-        for (int64_t e = 0; e < a.E; e++) row[e] = __fmul_rn(row[e], inv);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sm = __fadd_rn(sm, __shfl_xor(sm, o, 64));
+        const float inv = __fdiv_rn(1.0f, sm);
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) p[j] = __fmul_rn(p[j], inv);
     } else {
-        for (int64_t e = 0; e < a.E; e++) row[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-row[e])));
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) p[j] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-p[j])));
     }
-    float choice[ROUTE_MAXE];
-    for (int64_t e = 0; e < a.E; e++) choice[e] = __fadd_rn(row[e], a.corr ? a.corr[e] : 0.0f);
+#pragma unroll
+    for (int j = 0; j < ROUTE_EJ; j++) {
+        const int64_t e = lane + 64 * j;
+        ch[j] = e < a.E ? __fadd_rn(p[j], a.corr ? a.corr[e] : 0.0f) : -INFINITY;
+        if (e < a.E) chs[wave][e] = ch[j];
+    }
     if (a.group_limited && a.n_group > 1) {
-        int64_t per = a.E / a.n_group;
-        float gs[ROUTE_MAXG];
-        bool kept[ROUTE_MAXG];
-        for (int64_t g = 0; g < a.n_group; g++) {
-            kept[g] = false;
-            const float *s = choice + g * per;
+        // lane g scores group g over its experts in index order
+        const int64_t per = a.E / a.n_group;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float gs = -INFINITY;
+        if (lane < a.n_group) {
+            const float *sg = chs[wave] + lane * per;
             if (a.corr) {
                 float b1 = -INFINITY, b2 = -INFINITY;
                 for (int64_t i = 0; i < per; i++) {
-                    if (s[i] > b1) { b2 = b1; b1 = s[i]; }
-                    else if (s[i] > b2) b2 = s[i];
+                    if (sg[i] > b1) { b2 = b1; b1 = sg[i]; }
+                    else if (sg[i] > b2) b2 = sg[i];
                 }
-                gs[g] = __fadd_rn(b1, per > 1 ? b2 : 0.0f);
+                gs = __fadd_rn(b1, per > 1 ? b2 : 0.0f);
             } else {
                 float best = -INFINITY;
-                for (int64_t i = 0; i < per; i++) best = fmaxf(best, s[i]);
-                gs[g] = best;
+                for (int64_t i = 0; i < per; i++) best = fmaxf(best, sg[i]);
+                gs = best;
             }
         }
-        int64_t keep = a.topk_group < a.n_group ? a.topk_group : a.n_group;
+        // kept groups: repeated argmax; a kept group never wins again
+        bool kept = false;
+        const int64_t keep = a.topk_group < a.n_group ? a.topk_group : a.n_group;
         for (int64_t kk = 0; kk < keep; kk++) {
-            int64_t best = 0;
-            float bv = -INFINITY;
-            for (int64_t g = 0; g < a.n_group; g++)
-                if (!kept[g] && gs[g] > bv) { bv = gs[g]; best = g; }
-            // a group already kept scores NaN in the reference and never wins again
-            kept[best] = true;
-            gs[best] = __uint_as_float(0x7fc00000u);
+            const int best = wave_argmax(lane < a.n_group && !kept ? gs : -INFINITY, lane);
+            if (lane == best) kept = true;
         }
-        for (int64_t g = 0; g < a.n_group; g++)
-            if (!kept[g])
-                for (int64_t i = 0; i < per; i++) choice[g * per + i] = -INFINITY;
+        const uint64_t kept_mask = __ballot(kept);
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) {
+            const int64_t e = lane + 64 * j;
+            if (e < a.E && !((kept_mask >> (e / per)) & 1ull)) ch[j] = -INFINITY;
+        }
     }
+    // top k, in selection order
     float sum = 0.f;
-    for (int64_t j = 0; j < a.k; j++) {
-        int64_t best = 0;
-        float bv = -INFINITY;
-        for (int64_t e = 0; e < a.E; e++)
-            if (choice[e] > bv) { bv = choice[e]; best = e; }
-        a.sel[t * a.k + j] = (int32_t)best;
-        a.selw[t * a.k + j] = row[best];
-        choice[best] = -INFINITY;
-        sum = __fadd_rn(sum, row[best]);
+    int32_t selj[16];
+    for (int64_t jk = 0; jk < a.k; jk++) {
+        float v = -INFINITY;
+        int idx = 0;
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++) better(v, idx, ch[j], lane + 64 * j);
+        const int best = wave_argmax(v, idx);
+        // the winner's probability, from the lane that holds it
+        float pb = 0.f;
+#pragma unroll
+        for (int j = 0; j < ROUTE_EJ; j++)
+            if (lane + 64 * j == best) {
+                pb = p[j];
+                ch[j] = -INFINITY;
+            }
+        pb = __shfl(pb, best % 64, 64);
+        if (jk < 16) selj[jk] = best;
+        if (lane == 0) {
+            a.sel[t * a.k + jk] = best;
+            a.selw[t * a.k + jk] = pb;
+        }
+        sum = __fadd_rn(sum, pb);
     }
-    if (a.norm_topk && sum > 0)
-        for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fdiv_rn(a.selw[t * a.k + j], sum);
-    if (a.scaling != 1.0f)
-        for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fmul_rn(a.selw[t * a.k + j], a.scaling);
+    if (lane == 0) {
+        if (a.norm_topk && sum > 0)
+            for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fdiv_rn(a.selw[t * a.k + j], sum);
+        if (a.scaling != 1.0f)
+            for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fmul_rn(a.selw[t * a.k + j], a.scaling);
+        // the selections in ascending expert index (the combine's order)
+        int32_t order[16];
+        for (int64_t j = 0; j < a.k; j++) order[j] = (int32_t)j;
+        for (int64_t a1 = 1; a1 < a.k; a1++)
+            for (int64_t b1 = a1; b1 > 0 && selj[order[b1]] < selj[order[b1 - 1]]; b1--) {
+                const int32_t tmp = order[b1];
+                order[b1] = order[b1 - 1];
+                order[b1 - 1] = tmp;
+            }
+        for (int64_t j = 0; j < a.k; j++) a.ord[t * a.k + j] = order[j];
+    }
 }
 
 // Per-expert token counts.
@@ -316,28 +390,29 @@ __global__ void expert_list_kernel(const int32_t *sel, int64_t n, int64_t k, con
 }
 
 // out[t] = x[t] + (sum over the token's experts in ascending index of
-// w * eo + shared) (moe.zig:1197-1227 then the residual add).
-__global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared, const int32_t *sel,
+// w * eo + shared) (moe.zig:1197-1227 then the residual add); ord holds each
+// token's selections in that order. Four columns per thread.
+__global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared, const int32_t *ord,
                                    const float *selw, const int32_t *pair_of, int64_t n, int64_t k, int64_t hidden) {
-    int64_t total = n * hidden;
+    const int64_t h4 = (hidden + 3) / 4, total = n * h4;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        int64_t t = i / hidden, c = i % hidden;
-        // experts of this token in ascending index order (k is small)
-        int32_t order[16];
-        for (int64_t j = 0; j < k; j++) order[j] = (int32_t)j;
-        for (int64_t a1 = 1; a1 < k; a1++)
-            for (int64_t b1 = a1; b1 > 0 && sel[t * k + order[b1]] < sel[t * k + order[b1 - 1]]; b1--) {
-                int32_t tmp = order[b1];
-                order[b1] = order[b1 - 1];
-                order[b1 - 1] = tmp;
-            }
-        float m = 0.f;
+        const int64_t t = i / h4, c0 = (i % h4) * 4;
+        float m[4] = {0.f, 0.f, 0.f, 0.f};
         for (int64_t j = 0; j < k; j++) {
-            int64_t s = t * k + order[j];
-            m = __fadd_rn(m, __fmul_rn(selw[s], eo[(int64_t)pair_of[s] * hidden + c]));
+            const int64_t sidx = t * k + ord[t * k + j];
+            const float w = selw[sidx];
+            const float *er = eo + (int64_t)pair_of[sidx] * hidden;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (c0 + u < hidden) m[u] = __fadd_rn(m[u], __fmul_rn(w, er[c0 + u]));
         }
-        if (eo_shared) m = __fadd_rn(m, eo_shared[i]);
-        x[i] = __fadd_rn(x[i], m);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (c0 + u >= hidden) continue;
+            float v = m[u];
+            if (eo_shared) v = __fadd_rn(v, eo_shared[t * hidden + c0 + u]);
+            x[t * hidden + c0 + u] = __fadd_rn(x[t * hidden + c0 + u], v);
+        }
     }
 }
 
@@ -653,9 +728,12 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     mm(m, L.router, logits, h, n, nullptr, 0, s);
     int32_t *sel = m->r_sel.get<int32_t>(n * k);
     float *selw = m->r_selw.get<float>(n * k);
-    RouteArgs ra{logits, L.corr.p, sel, selw, n, E, k, (int64_t)c.n_group, (int64_t)c.topk_group, c.scoring,
+    int32_t *ord = m->r_ord.get<int32_t>(n * k);
+    DITCH_CHECK(E <= ROUTE_MAXE && k <= 16 && (!c.group_limited || c.n_group <= ROUTE_MAXG), DITCH_UNSUPPORTED,
+                "router: more than 512 experts, 16 per token or 64 groups");
+    RouteArgs ra{logits, L.corr.p, sel, selw, ord, n, E, k, (int64_t)c.n_group, (int64_t)c.topk_group, c.scoring,
                  c.group_limited, c.norm_topk_prob, c.routed_scaling};
-    hipLaunchKernelGGL(route_kernel, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, ra);
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, ra);
     DITCH_TRY_HIP(hipGetLastError());
     int32_t *counts = m->r_counts.get<int32_t>(E);
     DITCH_TRY_HIP(hipMemsetAsync(counts, 0, E * 4, s));
@@ -765,8 +843,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         esh = m->e_shared.get<float>(n * hidden);
         mm(m, L.sh_down, esh, sgb, n, nullptr, 0, s);
     }
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(grid_for(n * hidden)), dim3(256), 0, s, x, eo, esh, sel, selw, pair_of,
-                       n, k, hidden);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(grid_for(n * ((hidden + 3) / 4))), dim3(256), 0, s, x, eo, esh, ord,
+                       selw, pair_of, n, k, hidden);
     DITCH_TRY_HIP(hipGetLastError());
 }
 
