@@ -191,10 +191,15 @@ void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, c
     launch_matmul(w, out, x.f32, n, ep, s, nullptr, ws);
 }
 
-void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols, int64_t max_cnt,
-                           float *out, const float *x, const int32_t *row_index, const float *delta_xa,
-                           int delta_stride, hipStream_t s, DevBuf *ws) {
+void launch_matmul_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, int tf, int64_t rows,
+                           int64_t cols, int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
+                           const float *delta_xa, int delta_stride, hipStream_t s, DevBuf *ws, DevBuf *meta) {
     if (nseg == 0 || max_cnt <= 0) return;
+    if (h_segs && ws && meta && tile_grouped_takes(h_segs, nseg, max_cnt)) {
+        launch_tile_gemm_grouped(d_segs, h_segs, nseg, out, rows, x, cols, row_index, delta_xa, delta_stride, ws, meta,
+                                 s);
+        return;
+    }
     GemmParams p{};
     p.out = out;
     p.x = x;

@@ -43,6 +43,7 @@ struct SplitParams {
     u32x4 *xs;
     const float *x;
     const int32_t *row_index;  // optional gather of x rows
+    const int32_t *prow;       // optional: fragment row -> row of the gathered space, -1 for a zero row
     int64_t n, ldx, K;
     int64_t kt_total;  // k tiles per 16-token block (the fragments' ldk)
     int64_t m16;       // 16-token blocks
@@ -58,8 +59,14 @@ __global__ __launch_bounds__(256) void split_kernel(SplitParams p) {
     const int64_t tok = mb * 16 + (lane & 15);
     const int64_t k0 = kt * 32 + 8 * (lane >> 4);
     float v[8];
-    if (tok < p.n) {
-        int64_t src = p.row_index ? (int64_t)p.row_index[tok] : tok;
+    int64_t gi = tok;
+    bool valid = tok < p.n;
+    if (valid && p.prow) {
+        gi = p.prow[tok];
+        valid = gi >= 0;
+    }
+    if (valid) {
+        int64_t src = p.row_index ? (int64_t)p.row_index[gi] : gi;
         const float *xr = p.x + src * p.ldx;
         if (k0 + 8 <= p.K && ((((uintptr_t)(xr + k0)) & 15) == 0)) {
             float4 a = *(const float4 *)(xr + k0), b = *(const float4 *)(xr + k0 + 4);
@@ -184,6 +191,22 @@ struct TileGemmParams {
     int delta_rank;
     int delta_stride;
     int tiles_m, tiles_n;
+    // grouped (routed experts): tile row mt is descriptor gdesc[4 mt ..]:
+    // segment, first 16-token block, the segment's end block, the block's
+    // first token within the segment; the segment's weight, output rows and
+    // delta come from gsegs
+    const GroupSeg *gsegs;
+    const int32_t *gdesc;
+};
+
+// Where a tile's outputs go: a plain product's, or a routed segment's
+struct TileOut {
+    float *out;
+    int64_t ldo, n, rows;
+    const float *bias;
+    int accumulate;
+    const float *delta_b, *delta_xa;
+    int delta_rank, delta_stride;
 };
 
 // Block -> output tile. Consecutive blocks are dispatched round robin over
@@ -203,8 +226,8 @@ __device__ __forceinline__ void map_tile(int g, int G, int tm, int tn, int &mt, 
     nt = r / gs;
 }
 
-__device__ __forceinline__ void tile_store(const TileGemmParams &p, int64_t tok, int64_t row, float v) {
-    if (tok >= p.n || row >= p.w.rows) return;
+__device__ __forceinline__ void tile_store(const TileOut &p, int64_t tok, int64_t row, float v) {
+    if (tok >= p.n || row >= p.rows) return;
     if (p.delta_rank > 0) {
         float d = 0.f;
         for (int j = 0; j < p.delta_rank; j++)
@@ -228,8 +251,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 // stage s + 1 is copied while stage s is computed, and a stage ends with
 // this wave's copies drained plus a barrier. No global load writes a
 // register inside the loop.
-template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU>
+template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU, bool GR = false>
 __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParams p) {
+    static_assert(!(GLU && GR), "grouped products are plain");
     constexpr int WAVES = WGM * WGN;
     constexpr int TPS = TileCfg<TF>::TPS, NU = TileCfg<TF>::NU, NS = TileCfg<TF>::NS;
     constexpr int NS1 = NS ? NS : 1;
@@ -241,19 +265,38 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     __shared__ u32x4 Bs0[WAVES * WN * NU * 64], Bs1[WAVES * WN * NU * 64];  // [wave][group][unit][lane]
     __shared__ uint32_t Ss0[WAVES * NS1 * 64], Ss1[WAVES * NS1 * 64];        // [wave][entry][group][row]
 
-    const TileView &w = p.w;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wave_m = wave / WGN, wave_n = wave % WGN;
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
+    const int32_t *gd = GR ? p.gdesc + 4 * mt : nullptr;
+    const TileView &w = GR ? p.gsegs[gd[0]].w : p.w;
+    TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank, p.delta_stride};
+    int64_t tok0;  // token (within the output rows) of the tile's first block
     // row groups of this wave: WN of w, or (GLU) the same WN/2 output groups
     // of the gate (w) and of the up projection (w2)
     constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
     static_assert(!GLU || WN % 4 == 0, "a GLU wave covers whole 32-column k tiles of its output");
     const int64_t groups = (w.rows + 15) / 16;
     const int64_t g0 = (int64_t)nt * (OG * WGN) + wave_n * OG;
-    const int64_t m16_0 = (int64_t)mt * (WGM * WM), m16_n = (p.n + 15) / 16;
+    int64_t m16_0, m16_n;
+    if constexpr (GR) {
+        const GroupSeg &sg = p.gsegs[gd[0]];
+        m16_0 = gd[1];
+        m16_n = gd[2];
+        tok0 = gd[3];
+        to.out = p.out + sg.off * p.ldo;
+        to.n = sg.cnt;
+        to.bias = nullptr;
+        to.delta_b = sg.delta_b;
+        to.delta_rank = sg.delta_rank;
+        to.delta_xa = sg.delta_rank ? p.delta_xa + sg.off * p.delta_stride : nullptr;
+    } else {
+        m16_0 = (int64_t)mt * (WGM * WM);
+        m16_n = (p.n + 15) / 16;
+        tok0 = m16_0 * 16;
+    }
     const int64_t S = p.kt_total / TPS;
     const int64_t units = w.units_k;
 
@@ -424,7 +467,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                 int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    tile_store(p, (m16_0 + wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+                    tile_store(to, tok0 + (wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
             }
     } else {
         // act(gate) * up (tensor.gatedActivation), as f32 rows and/or as the
@@ -557,6 +600,8 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     __shared__ u32x4 Bs0[WAVES * WN * 64], Bs1[WAVES * WN * 64];  // [wave][group][lane]
     __shared__ uint32_t Ss0[WAVES * 64], Ss1[WAVES * 64];        // [wave][group][lane] bytes
     const TileView &w = p.w;
+    const TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
+                     p.delta_stride};
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int mt, nt;
@@ -722,7 +767,7 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
             for (int i = 0; i < WN; i++) {
                 const int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
-                for (int r = 0; r < 4; r++) tile_store(p, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+                for (int r = 0; r < 4; r++) tile_store(to, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
             }
     } else {
         // y = act(gate) * up (tensor.gatedActivation) for the wave's 32
@@ -778,7 +823,7 @@ bool tile_gemm_takes(const TileView &w, int64_t n) {
 
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
                   int64_t kt_total, int xt, hipStream_t s) {
-    SplitParams sp{(u32x4 *)xs, x, row_index, n, ldx, K, kt_total, (n + 15) / 16};
+    SplitParams sp{(u32x4 *)xs, x, row_index, nullptr, n, ldx, K, kt_total, (n + 15) / 16};
     int64_t total = sp.m16 * kt_total * 64;
     dim3 grid((unsigned)((total + 255) / 256));
     if (xt == 3) hipLaunchKernelGGL(split_kernel<3>, grid, dim3(256), 0, s, sp);
@@ -846,6 +891,87 @@ void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs
     p.delta_rank = ep.delta_rank;
     p.delta_stride = ep.delta_rank;
     launch_tile_any<false>(p, xt, s);
+}
+
+// Routed experts on the tiled product: each segment's rows (gathered by
+// row_index, or consecutive) are split into 16-token blocks of their own, a
+// tile row covers up to 4 blocks of one segment, and the kernel reads the
+// segment's weight, output rows and delta from the device segment table.
+template <int TF>
+static void launch_tile_grouped(TileGemmParams &p, hipStream_t s) {
+    constexpr bool W4 = TF == TF_BF16;  // the stage buffers of the bf16 format need the 4-wave tile
+    constexpr int WGN = W4 ? 4 : 8, BN = 16 * 4 * WGN;
+    p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+    hipLaunchKernelGGL((tile_gemm_kernel<TF, 2, 1, WGN, 4, 4, false, true>), grid, dim3(WGN * 64), 0, s, p);
+}
+
+bool tile_grouped_takes(const GroupSeg *h_segs, unsigned nseg, int64_t max_cnt) {
+    if (nseg == 0 || max_cnt <= 16) return false;
+    for (unsigned i = 0; i < nseg; i++)
+        if (!tile_gemm_takes(h_segs[i].w, 128) || h_segs[i].w.tf != h_segs[0].w.tf ||
+            h_segs[i].w.units_k != h_segs[0].w.units_k)
+            return false;
+    return true;
+}
+
+void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, float *out, int64_t ldo,
+                              const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
+                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s) {
+    const TileView &w0 = h_segs[0].w;
+    const int64_t kt = split_k_tiles(w0);
+    // blocks of each segment, the padded row map and the tile descriptors
+    std::vector<int32_t> base(nseg);
+    int64_t blocks = 0, ndesc = 0;
+    for (unsigned z = 0; z < nseg; z++) {
+        base[z] = (int32_t)blocks;
+        const int64_t nb = (h_segs[z].cnt + 15) / 16;
+        blocks += nb;
+        ndesc += (nb + 3) / 4;
+    }
+    if (blocks == 0) return;
+    std::vector<int32_t> hm((size_t)(blocks * 16 + ndesc * 4));
+    int32_t *prow = hm.data(), *desc = hm.data() + blocks * 16;
+    int64_t d = 0;
+    for (unsigned z = 0; z < nseg; z++) {
+        const int64_t nb = (h_segs[z].cnt + 15) / 16;
+        for (int64_t i = 0; i < nb * 16; i++)
+            prow[base[z] * 16 + i] = i < h_segs[z].cnt ? (int32_t)(h_segs[z].off + i) : -1;
+        for (int64_t j = 0; j < nb; j += 4) {
+            desc[4 * d] = (int32_t)z;
+            desc[4 * d + 1] = (int32_t)(base[z] + j);
+            desc[4 * d + 2] = (int32_t)(base[z] + nb);
+            desc[4 * d + 3] = (int32_t)(j * 16);
+            d++;
+        }
+    }
+    int32_t *dm = meta->get<int32_t>(hm.size());
+    DITCH_TRY_HIP(hipMemcpyAsync(dm, hm.data(), hm.size() * 4, hipMemcpyHostToDevice, s));
+    void *xs = ws->get<uint8_t>(split_bytes_ldk(blocks * 16, kt, 2));
+    SplitParams sp{(u32x4 *)xs, x, row_index, dm, blocks * 16, ldx, w0.cols, kt, blocks};
+    const int64_t total = blocks * kt * 64;
+    hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
+    DITCH_TRY_HIP(hipGetLastError());
+    TileGemmParams p{};
+    p.w = w0;
+    p.xs = (const u32x4 *)xs;
+    p.kt_total = kt;
+    p.ldk = kt;
+    p.out = out;
+    p.ldo = ldo;
+    p.delta_xa = delta_xa;
+    p.delta_stride = delta_stride;
+    p.gsegs = d_segs;
+    p.gdesc = dm + blocks * 16;
+    p.tiles_m = (int)ndesc;
+    switch (w0.tf) {
+    case TF_BF16: launch_tile_grouped<TF_BF16>(p, s); break;
+    case TF_MX4: launch_tile_grouped<TF_MX4>(p, s); break;
+    case TF_FP8: launch_tile_grouped<TF_FP8>(p, s); break;
+    case TF_INT4: launch_tile_grouped<TF_INT4>(p, s); break;
+    default: throw Error{DITCH_UNSUPPORTED, "grouped tiled GEMM: tile format"};
+    }
+    DITCH_TRY_HIP(hipGetLastError());
 }
 
 bool tile_glu_takes(const TileView &g, const TileView &u, int64_t n) {

@@ -229,9 +229,15 @@ struct GroupSeg {
     const float *delta_b;
     int delta_rank;
 };
-void launch_matmul_grouped(const GroupSeg *d_segs, unsigned nseg, int tf, int64_t rows, int64_t cols,
-                           int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
-                           const float *delta_xa, int delta_stride, hipStream_t s, DevBuf *ws);
+// h_segs: the same table on the host (counts and offsets decide the path);
+// ws and meta: workspaces for activation fragments and the tile table
+void launch_matmul_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, int tf, int64_t rows,
+                           int64_t cols, int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
+                           const float *delta_xa, int delta_stride, hipStream_t s, DevBuf *ws, DevBuf *meta);
+bool tile_grouped_takes(const GroupSeg *h_segs, unsigned nseg, int64_t max_cnt);
+void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, float *out, int64_t ldo,
+                              const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
+                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s);
 
 // attention.hip: prompt attention (model.zig:2935-2986) on the fp32 MFMA for
 // the head shapes it takes; q [n][heads][hd], caches [prompt][T][kvd], out

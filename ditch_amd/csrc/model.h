@@ -110,6 +110,7 @@ struct ditch_hip_model {
     ditch::DevBuf r_logits, r_sel, r_selw, r_ord, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
         segs, segd, e_xa;
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
+    ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
     ditch::ExpertCache *cache = nullptr;

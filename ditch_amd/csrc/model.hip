@@ -801,10 +801,10 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
         DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
         const TileView &vg = sg[0].w, &vd = sd[0].w;
-        launch_matmul_grouped(dsegs, nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0, s,
-                              &m->xsplit);
-        launch_matmul_grouped(dsegs + nseg, nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token, nullptr, 0,
-                              s, &m->xsplit);
+        launch_matmul_grouped(dsegs, sg.data(), nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0,
+                              s, &m->xsplit, &m->gmeta);
+        launch_matmul_grouped(dsegs + nseg, su.data(), nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token,
+                              nullptr, 0, s, &m->xsplit, &m->gmeta);
         {  // act(gate) * up on this chunk's pairs (consecutive experts: one run of pairs)
             const int64_t p0 = sg[0].off, p1 = (int64_t)sg[nseg - 1].off + sg[nseg - 1].cnt;
             launch_gated_act(0, gate + p0 * inter, gate + p0 * inter, up + p0 * inter, p1 - p0, inter, inter, inter, s);
@@ -818,8 +818,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
             hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
             DITCH_TRY_HIP(hipGetLastError());
         }
-        launch_matmul_grouped(dsegs + 2 * nseg, nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa, max_rank,
-                              s, &m->xsplit);
+        launch_matmul_grouped(dsegs + 2 * nseg, sd.data(), nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa,
+                              max_rank, s, &m->xsplit, &m->gmeta);
         if (streamed) {
             cache_release(m, slots, s);
             // a layer in several chunks: the host tables of this chunk go out
