@@ -12,6 +12,8 @@ Beside it, in the same JSON line:
                  forward) timed with HIP events on the library's stream;
   gemv         - configs[1]: the Q8_0 14336x4096 dequant-fused product for
                  M in {1, 4, 16, 64, 256}, achieved HBM GB/s vs 8 TB/s;
+  moe_c4_layer - configs[3]'s layer shape: one INT4 MoE layer (128 experts
+                 top-8) over 32 x 128 tokens, its forward time;
   cpu_baseline - the CPU oracle (oracle/cpu_ref.c, built -march=native on
                  this host) on a bounded sample of the same forward.
 Only rank 0 / one GPU: `--gpus N` with N > 1 exits with a message.
@@ -186,6 +188,54 @@ def roofline_leg(dev, fmt, cfg, reps):
             "avg_launch_ms": round(ms, 4), "algorithmic_flops_per_launch": flops, "mfma_flops_per_algorithmic_flop": 2}
 
 
+C4 = dict(hidden=2048, heads=32, kv_heads=4, head_dim=128, experts=128, top_k=8, moe_inter=768, vocab=8192,
+          prompts=32, tokens=128)
+
+
+def moe_leg(dev, steps=5, warmup=2):
+    """configs[3]'s layer: one Qwen3-30B-A3B-shaped MoE layer (d 2048, 32/4
+    heads of 128, 128 experts top-8 of FFN 768, INT4 group 128 drawn in the
+    packed domain, reduced vocab) over 32 prompts x 128 tokens. Reported
+    beside the headline: the forward's time and the routed-expert products'
+    algorithmic throughput over it (a lower bound for those kernels)."""
+    import torch
+    from ditch_amd import abi, synth
+    from ditch_amd.hip import Model
+    from ditch_amd.spec import ModelSpec
+    c = C4
+    rng = np.random.default_rng(21)
+    h, nh, nkv, hd, E, mi, V = (c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["experts"], c["moe_inter"],
+                                c["vocab"])
+    spec = ModelSpec(hidden=h, inter=4 * h, layers=1, heads=nh, kv_heads=nkv, head_dim=hd, vocab=V, rms_eps=1e-6,
+                     qk_norm=1, tie_embeddings=0, rope_theta=1e6, rope_len=512, n_experts=E, top_k=c["top_k"],
+                     moe_inter=mi, norm_topk_prob=1, scoring=abi.SCORING_SOFTMAX, moe_layers=[1])
+    spec.set("EMBED", synth.bf16_weight(torch.from_numpy(rng.normal(0, 0.02, (V, h)).astype(np.float32))))
+    spec.set("LM_HEAD", synth.int4_random(V, h, rng))
+    spec.set("FINAL_NORM", 1 + rng.normal(0, 0.02, h))
+    spec.set("ATTN_NORM", 1 + rng.normal(0, 0.02, h), 0)
+    spec.set("FFN_NORM", 1 + rng.normal(0, 0.02, h), 0)
+    for name, r, cc in (("Q", nh * hd, h), ("K", nkv * hd, h), ("V", nkv * hd, h), ("O", h, nh * hd)):
+        spec.set(name, synth.int4_random(r, cc, rng), 0)
+    spec.set("Q_NORM", 1 + rng.normal(0, 0.02, hd), 0)
+    spec.set("K_NORM", 1 + rng.normal(0, 0.02, hd), 0)
+    spec.set("ROUTER", synth.bf16_weight(torch.from_numpy(rng.normal(0, 0.02, (E, h)).astype(np.float32))), 0)
+    for e in range(E):
+        spec.set("EXPERT_GATE", synth.int4_random(mi, h, rng), 0, e)
+        spec.set("EXPERT_UP", synth.int4_random(mi, h, rng), 0, e)
+        spec.set("EXPERT_DOWN", synth.int4_random(h, mi, rng), 0, e)
+    model = Model(dev, spec)
+    cfg = dict(layers=1, hidden=h, vocab=V, prompts=c["prompts"], tokens=c["tokens"])
+    ms, _, _, logits, _ = time_forward(dev, model, cfg, steps, warmup)
+    model.free()
+    n = c["prompts"] * c["tokens"]
+    flops = 2.0 * n * c["top_k"] * 3 * h * mi
+    return {"workload": "c4 layer: Qwen3-30B-A3B-shaped MoE layer (d 2048, 128 experts top-8, FFN 768, INT4 g128), "
+                        "32 prompts x 128 tokens, vocab 8192",
+            "ms_per_forward": round(ms, 3), "tokens_per_s": round(n / (ms * 1e-3), 1),
+            "expert_flops": flops, "expert_tflops_over_forward": round(flops / (ms * 1e-3) / 1e12, 2),
+            "outputs_finite": bool(np.isfinite(logits).all())}
+
+
 def gemv_leg(dev, reps):
     """Q8_0 14336 x 4096 times [M, 4096] activations."""
     import torch
@@ -307,7 +357,8 @@ def main():
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (quick runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
-    ap.add_argument("--kernel-only", choices=["gemm", "gemv", "copy"], default=None,
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--kernel-only", choices=["gemm", "gemv", "copy", "moe"], default=None,
                     help="run only the roofline kernel (for rocprofv3 runs)")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
@@ -330,6 +381,9 @@ def main():
         return
     if args.kernel_only == "gemv":
         print(json.dumps({"kernel_only": "gemv", "gemv": gemv_leg(dev, args.reps)}))
+        return
+    if args.kernel_only == "moe":
+        print(json.dumps({"kernel_only": "moe", "moe_c4_layer": moe_leg(dev)}))
         return
     if args.kernel_only == "copy":
         print(json.dumps({"kernel_only": "copy", "copy": copy_leg(dev, args.reps)}))
@@ -354,6 +408,10 @@ def main():
     if gemv:
         for g in gemv:
             log(f"gemv M={g['M']}: {g['avg_launch_us']} us, {g['GB_s']} GB/s ({g['frac_hbm_peak'] * 100:.1f}%)")
+    moe = None if args.no_moe else moe_leg(dev)
+    if moe:
+        log(f"c4 MoE layer: {moe['ms_per_forward']} ms per forward, expert products >= "
+            f"{moe['expert_tflops_over_forward']} TFLOP/s")
     cpu, parity = None, None
     if not args.no_cpu:
         t0 = time.time()
@@ -386,6 +444,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "gemv": gemv,
+        "moe_c4_layer": moe,
     }
     print(json.dumps(out))
     dev.close()
