@@ -103,18 +103,21 @@ template <> struct TileCfg<TF_BF16> { static constexpr int TPS = 2, NU = 2, NS =
 template <> struct TileCfg<TF_FP8> { static constexpr int TPS = 2, NU = 1, NS = 1; };   // unit s; f32 scale
 template <> struct TileCfg<TF_MX4> { static constexpr int TPS = 4, NU = 1, NS = 1; };   // unit s; 4 E8M0 bytes
 template <> struct TileCfg<TF_INT4> { static constexpr int TPS = 4, NU = 1, NS = 2; };  // unit s; two 64-col groups
+template <> struct TileCfg<TF_Q8> { static constexpr int TPS = 2, NU = 1, NS = 1; };    // unit s; two f16 block scales
 
 // Side word of stage s, entry j, for a row whose side row starts at `base`.
 template <int TF>
 __device__ __forceinline__ const uint32_t *side_word(const TileView &w, const uint32_t *side, int64_t base, int64_t s,
                                                      int j) {
     if constexpr (TF == TF_MX4) return side + base + s;
+    else if constexpr (TF == TF_Q8) return side + base + s * 16;  // [group][unit][row % 16]
     else if constexpr (TF == TF_FP8) return side + base + (s * 64) / w.block_cols;
     else return side + base + (s * 128 + 64 * j) / w.group;
 }
 
 // Side row of this lane's weight row (FP8: its row of the scale grid).
 __device__ __forceinline__ int64_t side_row(const TileView &w, int64_t g, int lane) {
+    if (w.tf == TF_Q8) return g * w.units_k * 16 + (lane & 15);
     int64_t r = g * 16 + (lane & 15);
     r = r < w.rows ? r : w.rows - 1;
     if (w.tf == TF_FP8) {
@@ -153,6 +156,16 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
         f[1] = cvt_pk_bf16(__fmul_rn(p1.x, sc), __fmul_rn(p1.y, sc));
         f[2] = cvt_pk_bf16(__fmul_rn(p2.x, sc), __fmul_rn(p2.y, sc));
         f[3] = cvt_pk_bf16(__fmul_rn(p3.x, sc), __fmul_rn(p3.y, sc));
+    } else if constexpr (TF == TF_Q8) {
+        // the int8 codes, exact in bf16; the block scale multiplies the tile's partial sums
+        const uint32_t w0 = c[0][2 * t], w1 = c[0][2 * t + 1];
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j] = (float)(int8_t)((w0 >> (8 * j)) & 0xffu);
+            v[4 + j] = (float)(int8_t)((w1 >> (8 * j)) & 0xffu);
+        }
+        f = u32x4{pack_hi(v[0], v[1]), pack_hi(v[2], v[3]), pack_hi(v[4], v[5]), pack_hi(v[6], v[7])};
     } else if constexpr (TF == TF_INT4) {
         const uint32_t word = sd[t >> 1];
         const uint32_t bits = word & 0xffffu;
@@ -412,12 +425,30 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
                     for (int e = 0; e < XT; e++) a[nx][m][e] = A[((m * TPS + t + 1) * XT + e) * 64];
             }
+            if constexpr (TF == TF_Q8) {
+                // Q8_0: each 32-column k tile is one block; its f16 scale
+                // (side word half t) multiplies the tile's partial sum
+                float sq[WN];
 #pragma unroll
-            for (int m = 0; m < WM; m++)
+                for (int i = 0; i < WN; i++) sq[i] = f16_to_f32_hw((uint16_t)(sd[i][0] >> (16 * t)));
 #pragma unroll
-                for (int e = 0; e < XT; e++)
+                for (int m = 0; m < WM; m++)
 #pragma unroll
-                    for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[cu][m][e], bf[cu][i], acc[m][i]);
+                    for (int i = 0; i < WN; i++) {
+                        floatx4 pt = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int e = 0; e < XT; e++) pt = mfma_bf16(a[cu][m][e], bf[cu][i], pt);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[m][i][r] = __builtin_fmaf(sq[i], pt[r], acc[m][i][r]);
+                    }
+            } else {
+#pragma unroll
+                for (int m = 0; m < WM; m++)
+#pragma unroll
+                    for (int e = 0; e < XT; e++)
+#pragma unroll
+                        for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[cu][m][e], bf[cu][i], acc[m][i]);
+            }
             if (t + 1 < TPS) {
 #pragma unroll
                 for (int i = 0; i < WN; i++) bf[nx][i] = decode_tile_lds<TF>(w, c[i], sd[i], t + 1, second);
@@ -428,7 +459,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         // VALU per product: roughly the decode's instruction count per k tile
         // over the products left after the A reads
         constexpr int NA = WM * XT, NM = WM * XT * WN, NV = NM - NA;
-        constexpr int VPM = TF == TF_BF16 ? 1 : TF == TF_MX4 ? 2 : TF == TF_FP8 ? 3 : 4;
+        constexpr int VPM = TF == TF_BF16 ? 1 : TF == TF_MX4 ? 2 : TF == TF_FP8 ? 3 : TF == TF_Q8 ? 5 : 4;
 #pragma unroll
         for (int t = 0; t < TPS; t++) {
             if (t + 1 < TPS) {
@@ -811,14 +842,14 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
 
 int64_t split_k_tiles(const TileView &w) {
     // a whole number of pipeline stages (4 k tiles; 2 for bf16 and FP8 weights)
-    const int64_t tps = (w.tf == TF_BF16 || w.tf == TF_FP8) ? 2 : 4;
+    const int64_t tps = (w.tf == TF_BF16 || w.tf == TF_FP8 || w.tf == TF_Q8) ? 2 : 4;
     int64_t kt = w.units_k * (unit_k_of(w.tf) / 32);
     return (kt + tps - 1) / tps * tps;
 }
 
 bool tile_gemm_takes(const TileView &w, int64_t n) {
     if (!w.fast || n < 128) return false;
-    return w.tf == TF_BF16 || w.tf == TF_MX4 || w.tf == TF_FP8 || w.tf == TF_INT4;
+    return w.tf == TF_BF16 || w.tf == TF_MX4 || w.tf == TF_FP8 || w.tf == TF_INT4 || w.tf == TF_Q8;
 }
 
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
@@ -857,6 +888,7 @@ static void launch_tile_any(TileGemmParams &p, int xt, hipStream_t s) {
         case TF_MX4: launch_tile_tf<TF_MX4, 2, true>(p, s); break;
         case TF_FP8: launch_tile_tf<TF_FP8, 2, true>(p, s); break;
         case TF_INT4: launch_tile_tf<TF_INT4, 2, true>(p, s); break;
+        case TF_Q8: launch_tile_tf<TF_Q8, 2, true>(p, s); break;
         default: throw Error{DITCH_UNSUPPORTED, "tiled GLU: tile format"};
         }
         DITCH_TRY_HIP(hipGetLastError());
@@ -867,6 +899,7 @@ static void launch_tile_any(TileGemmParams &p, int xt, hipStream_t s) {
         case TF_MX4: x3 ? launch_tile_tf<TF_MX4, 3, false>(p, s) : launch_tile_tf<TF_MX4, 2, false>(p, s); break;
         case TF_FP8: x3 ? launch_tile_tf<TF_FP8, 3, false>(p, s) : launch_tile_tf<TF_FP8, 2, false>(p, s); break;
         case TF_INT4: x3 ? launch_tile_tf<TF_INT4, 3, false>(p, s) : launch_tile_tf<TF_INT4, 2, false>(p, s); break;
+        case TF_Q8: x3 ? launch_tile_tf<TF_Q8, 3, false>(p, s) : launch_tile_tf<TF_Q8, 2, false>(p, s); break;
         default: throw Error{DITCH_UNSUPPORTED, "tiled GEMM: tile format"};
         }
         DITCH_TRY_HIP(hipGetLastError());
@@ -969,6 +1002,7 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
     case TF_MX4: launch_tile_grouped<TF_MX4>(p, s); break;
     case TF_FP8: launch_tile_grouped<TF_FP8>(p, s); break;
     case TF_INT4: launch_tile_grouped<TF_INT4>(p, s); break;
+    case TF_Q8: launch_tile_grouped<TF_Q8>(p, s); break;
     default: throw Error{DITCH_UNSUPPORTED, "grouped tiled GEMM: tile format"};
     }
     DITCH_TRY_HIP(hipGetLastError());
