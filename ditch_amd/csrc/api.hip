@@ -374,8 +374,11 @@ int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, const void *d
         hipStream_t s = stream ? (hipStream_t)stream : h->stream;
         if (kind == 1)
             launch_mx_gemm(w->v, d_out, w->v.rows, d_frags, w->v.units_k, (int64_t)n, ep, s);
-        else
-            launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep, s);
+        else {
+            const size_t pb = tile_part_bytes(w->v, (int64_t)n, 2);
+            launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep, s,
+                             pb ? h->split.get<float>(pb / sizeof(float)) : nullptr);
+        }
     });
 }
 

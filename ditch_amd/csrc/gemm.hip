@@ -144,9 +144,10 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     if (ws && tile_gemm_takes(w, n)) {
         const int xt = ep.exact ? 3 : 2;
         const int64_t ldk = split_k_tiles(w);
-        void *xs = ws->get<uint8_t>(split_bytes_ldk(n, ldk, xt));
+        const size_t xb = (split_bytes_ldk(n, ldk, xt) + 255) & ~(size_t)255, pb = tile_part_bytes(w, n, xt);
+        uint8_t *xs = ws->get<uint8_t>(xb + pb);
         launch_split(xs, x, row_index, n, w.cols, w.cols, ldk, xt, s);
-        launch_tile_gemm(w, out, w.rows, xs, ldk, n, xt, ep, s);
+        launch_tile_gemm(w, out, w.rows, xs, ldk, n, xt, ep, s, pb ? (float *)(xs + xb) : nullptr);
         return;
     }
     GemmParams p{};
@@ -184,7 +185,8 @@ void launch_matmul_act(const TileView &w, float *out, const Act &x, int64_t n, c
         }
     }
     if (x.xs && !ep.exact && tile_gemm_takes(w, n) && x.ldk >= split_k_tiles(w)) {
-        launch_tile_gemm(w, out, w.rows, x.xs, x.ldk, n, 2, ep, s);
+        const size_t pb = ws ? tile_part_bytes(w, n, 2) : 0;
+        launch_tile_gemm(w, out, w.rows, x.xs, x.ldk, n, 2, ep, s, pb ? ws->get<float>(pb / sizeof(float)) : nullptr);
         return;
     }
     DITCH_CHECK(x.f32 != nullptr, DITCH_INVALID_ARGUMENT, "product: no activation form the weight's product takes");

@@ -1,4 +1,4 @@
-// gemm_tile.hip — the large-batch product (prompt forward, n >= 128 tokens).
+// gemm_tile.hip — the large-batch product (prompt forward, n >= 32 tokens).
 //
 // out[n][rows] = x[n][cols] @ W^T (tensor.matmulT, tensor.zig:1023-1045) for
 // weights whose decode the gfx950 conversion instructions do exactly
@@ -210,6 +210,10 @@ struct TileGemmParams {
     // delta come from gsegs
     const GroupSeg *gsegs;
     const int32_t *gdesc;
+    // split-K (plain products): blockIdx.y takes stages [y S / ksplit, (y + 1) S / ksplit)
+    // and stores its raw sums in part[y][n][rows]; ksplit_reduce_kernel adds them
+    int ksplit;
+    float *part;
 };
 
 // Where a tile's outputs go: a plain product's, or a routed segment's
@@ -310,7 +314,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         m16_n = (p.n + 15) / 16;
         tok0 = m16_0 * 16;
     }
-    const int64_t S = p.kt_total / TPS;
+    const int64_t S_all = p.kt_total / TPS;
+    const int ks = GLU || GR ? 0 : (int)blockIdx.y, nks = GLU || GR ? 1 : p.ksplit;
+    const int64_t s_begin = S_all * ks / nks, S = S_all * (ks + 1) / nks;  // this block's stages
+    if (nks > 1) {
+        to = TileOut{p.part + (int64_t)ks * p.n * w.rows, w.rows, p.n, w.rows, nullptr, 0, nullptr, nullptr, 0, 0};
+    }
     const int64_t units = w.units_k;
 
     // Copies: a global_load_lds stalls the issuing wave while the texture
@@ -381,7 +390,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
         for (int i = 0; i < WN; i++) acc[m][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    copy_stage(0, As0, Bs0, Ss0);
+    copy_stage(s_begin, As0, Bs0, Ss0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
@@ -482,7 +491,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         __builtin_amdgcn_s_barrier();              // ... and every other wave's
         __builtin_amdgcn_sched_barrier(0);
     };
-    int64_t s = 0;
+    int64_t s = s_begin;
     for (; s + 1 < S; s += 2) {
         step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
         step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0);
@@ -848,7 +857,7 @@ int64_t split_k_tiles(const TileView &w) {
 }
 
 bool tile_gemm_takes(const TileView &w, int64_t n) {
-    if (!w.fast || n < 128) return false;
+    if (!w.fast || n < 32) return false;
     return w.tf == TF_BF16 || w.tf == TF_MX4 || w.tf == TF_FP8 || w.tf == TF_INT4 || w.tf == TF_Q8;
 }
 
@@ -862,13 +871,65 @@ void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n,
     DITCH_TRY_HIP(hipGetLastError());
 }
 
+// out[t][r] = sum over the split-K parts (in part order) + delta + bias (+ out)
+__global__ void ksplit_reduce_kernel(TileGemmParams p) {
+    const int64_t rows = p.w.rows, total = p.n * rows;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = i / rows, r = i % rows;
+        float v = p.part[i];
+        for (int k = 1; k < p.ksplit; k++) v = __fadd_rn(v, p.part[(int64_t)k * total + i]);
+        const TileOut to{p.out, p.ldo, p.n, rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
+                         p.delta_stride};
+        tile_store(to, t, r, v);
+    }
+}
+
+// Split-K parts for a plain product whose tiles would not fill the GPU's
+// 256 CUs twice (and with at least 4 stages per part).
+static int tile_ksplit(int64_t tiles, int64_t stages) {
+    int ks = 1;
+    while (ks < 8 && tiles * ks < 512 && stages / (2 * ks) >= 4) ks *= 2;
+    return ks;
+}
+
+// the tile a plain product launches: 64 tokens x (WGN x 64) rows
+static constexpr int tile_wgn(int tf, int xt) { return tf == TF_BF16 || xt == 3 ? 4 : 8; }
+
+static int tile_tps(int tf) {
+    switch (tf) {
+    case TF_BF16: return TileCfg<TF_BF16>::TPS;
+    case TF_FP8: return TileCfg<TF_FP8>::TPS;
+    case TF_MX4: return TileCfg<TF_MX4>::TPS;
+    case TF_INT4: return TileCfg<TF_INT4>::TPS;
+    default: return TileCfg<TF_Q8>::TPS;
+    }
+}
+
+static int tile_ksplit_of(const TileView &w, int64_t n, int xt) {
+    const int64_t tiles = (n + 63) / 64 * ((w.rows + 64 * tile_wgn(w.tf, xt) - 1) / (64 * tile_wgn(w.tf, xt)));
+    return tile_ksplit(tiles, split_k_tiles(w) / tile_tps(w.tf));
+}
+
+size_t tile_part_bytes(const TileView &w, int64_t n, int xt) {
+    const int ks = tile_ksplit_of(w, n, xt);
+    return ks > 1 ? (size_t)ks * n * w.rows * sizeof(float) : 0;
+}
+
 template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU>
 static void launch_tile(TileGemmParams &p, hipStream_t s) {
     constexpr int BM = 16 * WM * WGM, BN = 16 * (GLU ? WN / 2 : WN) * WGN;
     p.tiles_m = (int)((p.n + BM - 1) / BM);
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
-    dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+    static_assert(BM == 64 && (GLU || BN == 64 * tile_wgn(TF, XT)), "tile_ksplit_of sizes the same tile");
+    p.ksplit = GLU || !p.part ? 1 : tile_ksplit((int64_t)p.tiles_m * p.tiles_n, p.kt_total / TileCfg<TF>::TPS);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)p.ksplit);
     hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WGM, WGN, WM, WN, GLU>), grid, dim3(WGM * WGN * 64), 0, s, p);
+    if (p.ksplit > 1) {
+        DITCH_TRY_HIP(hipGetLastError());
+        const int64_t total = p.n * p.w.rows;
+        hipLaunchKernelGGL(ksplit_reduce_kernel, dim3((unsigned)std::min<int64_t>((total + 255) / 256, 4096)),
+                           dim3(256), 0, s, p);
+    }
 }
 
 template <int TF, int XT, bool GLU>
@@ -907,8 +968,9 @@ static void launch_tile_any(TileGemmParams &p, int xt, hipStream_t s) {
 }
 
 void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t ldk, int64_t n, int xt,
-                      const MatmulEpilogue &ep, hipStream_t s) {
+                      const MatmulEpilogue &ep, hipStream_t s, float *part) {
     TileGemmParams p{};
+    p.part = ldo == w.rows ? part : nullptr;
     p.w = w;
     p.xs = (const u32x4 *)xs;
     p.kt_total = split_k_tiles(w);
@@ -1009,7 +1071,8 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
 }
 
 bool tile_glu_takes(const TileView &g, const TileView &u, int64_t n) {
-    if (!tile_gemm_takes(g, n) || !tile_gemm_takes(u, n)) return false;
+    // the fused pair has no split-K: it keeps to batches of 128 tokens and more
+    if (n < 128 || !tile_gemm_takes(g, n) || !tile_gemm_takes(u, n)) return false;
     return g.tf == u.tf && g.rows == u.rows && g.cols == u.cols && g.units_k == u.units_k &&
            g.scale_type == u.scale_type && g.block_rows == u.block_rows && g.block_cols == u.block_cols &&
            g.row_shard == u.row_shard && g.group == u.group && g.side_cols == u.side_cols;

@@ -186,8 +186,11 @@ inline int64_t split_ldk(int64_t K) { return (K + 127) / 128 * 4; }
 inline size_t split_bytes_ldk(int64_t n, int64_t ldk, int xt) { return (size_t)((n + 15) / 16) * ldk * xt * 1024; }
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
                   int64_t ldk, int xt, hipStream_t s);
+// part: f32 scratch of tile_part_bytes(w, n, xt) bytes for split-K partial
+// sums (NULL: no split)
+size_t tile_part_bytes(const TileView &w, int64_t n, int xt);
 void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t ldk, int64_t n, int xt,
-                      const MatmulEpilogue &ep, hipStream_t s);
+                      const MatmulEpilogue &ep, hipStream_t s, float *part = nullptr);
 // gate/up in one product: act(x gate^T) * (x up^T) into f32 rows [n][rows]
 // (out, may be NULL) and/or the A fragments of the next product (xs_out)
 // MXFP4 large batches on the scaled MFMA (fp6 activation terms x the fp4

@@ -158,6 +158,32 @@ def test_edit_then_forward(dev, ref):
         cm.free()
 
 
+@pytest.mark.parametrize("lens", [[20, 28], [130, 82]])
+def test_edit_split_k_products(dev, ref, lens):
+    """Rank-2 edits of o_proj and down_proj on a dense FP8 model whose
+    down_proj (K = 1536) splits K over blocks: the delta, residual
+    accumulate and the split-K partial sums meet in the second kernel; 48
+    rows on the f32-row path, 212 on the fused producers."""
+    spec = mg.dense("fp8", hidden=256, inter=1536, seed=9)
+    rng = np.random.default_rng(4)
+    v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+    v = v.T.astype(np.float32)
+    tokens, rows, last = mg.batch(2, lens, spec.config["vocab"], seed=11)
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        for li in range(spec.config["layers"]):
+            for m in (gm, cm):
+                m.edit(li, abi.SLOT["O"], -1, v, 1.0)
+                m.edit(li, abi.SLOT["DOWN"], -1, v, 1.0)
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    check_parity(ref, rg, lg, rc, lc, "edited_split_k")
+
+
 # Shapes that take the MFMA attention kernel (head dims 64/128, and MLA's
 # 192/128): several 64-key chunks, prompts that share 16-row blocks, GQA
 # groups of 4, and one query head per KV head.

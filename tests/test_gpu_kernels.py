@@ -254,7 +254,11 @@ def test_tensor_dequant_refuses_a_short_buffer(dev):
 # -- the large-batch tiled product (n >= 128): split activations + LDS-staged MFMA ----------
 
 TILE_KINDS = ["bf16", "fp8", "mxfp4", "int4", "int4_sym", "mxfp4_t", "int8", "fp8_16x8", "q8_0", "f32"]
-TILE_SHAPES = [(128, 256, 512), (200, 300, 640), (257, 48, 1024), (130, 1000, 384), (300, 17, 128)]
+# (257, 48, 1024), (40, 600, 2048) and (64, 520, 3072) split K over blocks
+# (partial sums added by a second kernel); 40 and 64 tokens fill part of one
+# 64-token tile
+TILE_SHAPES = [(128, 256, 512), (200, 300, 640), (257, 48, 1024), (130, 1000, 384), (300, 17, 128),
+               (40, 600, 2048), (64, 520, 3072)]
 
 
 @pytest.mark.parametrize("kind", TILE_KINDS)
@@ -338,7 +342,7 @@ def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
             assert fb == -(-n // 16) * -(-cols // 128) * 6400
         else:  # [n/16][cols/128 * 4 k tiles][2 terms] x 1 KiB
             assert fb == -(-n // 16) * (-(-cols // 128) * 4) * 2 * 1024
-        assert t.frag_bytes(64) == 0
+        assert t.frag_bytes(16) == 0
         bx, bb = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias)
         o1, o2 = hipmem.Buffer.from_array(prior), hipmem.Buffer.from_array(prior)
         xs = hipmem.Buffer(fb)
@@ -350,9 +354,9 @@ def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
         with pytest.raises(DeviceError, match="too small"):
             t.split_device(xs.ptr, fb - 1, bx.ptr, n)
         with pytest.raises(DeviceError, match="Unsupported"):
-            t.split_device(xs.ptr, fb, bx.ptr, 64)
+            t.split_device(xs.ptr, fb, bx.ptr, 16)
         with pytest.raises(DeviceError, match="Unsupported"):
-            t.matmul_frags_device(o2.ptr, xs.ptr, 64)
+            t.matmul_frags_device(o2.ptr, xs.ptr, 16)
     finally:
         t.free()
     assert np.array_equal(a, b)
