@@ -32,7 +32,11 @@ FLAGS = [
 # accumulator between the two files once per k stage); the GEMV's register
 # ring of in-flight units is unrolled whatever its size (indexed at run time
 # it would live in scratch memory)
-EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+# -disable-machine-sink: the products end each pipeline stage with a wait for
+# the next stage's loads and a barrier; machine sinking moves the stage's
+# register-only MFMAs past them (into the block after the copier branch),
+# which serialises the MFMAs with the memory latency.
+EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-disable-machine-sink"],
          "gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=1000000"],
          "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 

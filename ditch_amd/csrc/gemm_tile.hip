@@ -603,6 +603,10 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 
+// Fourth word of a raw buffer resource (32-bit data format; with stride 0
+// the record count is a byte count and reads past it return zero)
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
+
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 
@@ -624,99 +628,99 @@ __device__ __forceinline__ floatx4 mfma_mx(const MxA &a, int sa, const u32x4 &b,
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 2, 4, E, sa, 0, sb);
 }
 
-// The scaled-MFMA product: the pipeline of tile_gemm_kernel (copies by the
-// younger wave of each SIMD, two stage buffers, one barrier a stage) with a
-// stage of 128 k: A = WM fragment blocks of 6400 B, B = one 1 KiB unit per
-// row group (MXFP4 codes in MFMA order) and its 64 scale bytes. GLU: a wave's
-// first WN/2 row groups are gate rows (w), the others the same rows of the up
-// projection (w2); the epilogue writes act(gate) * up as f32 rows and/or as
-// the MX fragments of the next product.
-template <int WGN, int WM, int WN, bool GLU>
-__global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
-    constexpr int WAVES = WGN, NT = MX_TERMS;
+// The scaled-MFMA product. A workgroup of 8 waves covers 64 tokens (4
+// fragment blocks) x 512 rows (GLU: 256 output columns). Wave (wm, wn) =
+// (wave / 4, wave % 4) takes token blocks 2 wm, 2 wm + 1 and 8 row groups
+// (GLU: 4 gate groups and the same 4 groups of the up projection), so each A
+// operand read from LDS feeds 8 products. A stage is 128 k: the A fragments
+// of the 4 token blocks (4 x 6400 B: four fp6 terms and their E8M0 scales)
+// go to one of two LDS buffers by buffer_load_lds, 1/8 of them from each
+// wave; each wave loads its own row groups' fp4 codes (1 KiB a group) and
+// E8M0 scale bytes straight into registers one stage ahead. Every wave runs
+// the same instruction stream, and the stage's loads are spread between its
+// MFMAs: a wave that issues a load while the texture unit's queue is full
+// stalls, and a burst of loads at the top of the stage would hold back the
+// MFMAs of every wave behind it. One barrier a stage. GLU: the epilogue
+// writes act(gate) * up as f32 rows and/or as the MX fragments of the next
+// product.
+// (The body is a device function: the buffer-resource type exists on the
+// device side only, and the host pass instantiates the kernel for its stub.)
+template <bool GLU>
+__device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
+    constexpr int WAVES = 8, MB = 4, WM = 2, WN = 8, NT = MX_TERMS;
     constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
-    constexpr int AQ = MX_BLOCK / 16;                            // u32x4 per A block
-    __shared__ u32x4 As0[WM * AQ], As1[WM * AQ];                  // [m][block]
-    __shared__ u32x4 Bs0[WAVES * WN * 64], Bs1[WAVES * WN * 64];  // [wave][group][lane]
-    __shared__ uint32_t Ss0[WAVES * 64], Ss1[WAVES * 64];        // [wave][group][lane] bytes
+    constexpr int AQ = MX_BLOCK / 16;     // u32x4 per A block
+    constexpr int PS = OG * 16 + 4;       // GLU patch row stride (floats)
+    __shared__ u32x4 As0[MB * AQ], As1[MB * AQ];  // [block][fragment]
+    __shared__ float patch[GLU ? WAVES * WM * 16 * PS : 1];
     const TileView &w = p.w;
     const TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
                      p.delta_stride};
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
     const int64_t groups = (w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)nt * (OG * WGN) + wave * OG;
-    const int64_t m16_0 = (int64_t)mt * WM, m16_n = (p.n + 15) / 16;
+    const int64_t g0 = (int64_t)nt * (OG * 4) + wn * OG;
+    const int64_t m16_0 = (int64_t)mt * MB, m16_n = (p.n + 15) / 16;
     const int64_t S = w.units_k;  // stages: one 128-column unit each
 
-    // copies of a stage: six KiB pieces and one 256 B piece per A block, one
-    // KiB per row group, 256 B of B scales per wave (four groups)
-    constexpr int NAK = WM * 6, NAS = WM, NB = WAVES * WN, NBS = WAVES;
-    constexpr int CW = WAVES >= 8 ? WAVES / 2 : WAVES;
-    constexpr int CAK = NAK / CW, CAS = (NAS + CW - 1) / CW, CB = NB / CW, CBS = NBS / CW;
-    static_assert(NAK % CW == 0 && NB % CW == 0 && NBS % CW == 0, "copies split evenly");
-    static_assert(WN == 4, "one scale copy covers a wave's four row groups");
-    const bool copier = wave >= WAVES - CW;
-    const int ck = copier ? wave - (WAVES - CW) : 0;
-    auto a_block = [&](int m) {
-        int64_t mb = m16_0 + m;
-        mb = mb < m16_n ? mb : m16_n - 1;
-        return mb * p.ldk * AQ;  // u32x4 offset of block (mb, stage 0)
+    // Operands through buffer resources (base and bounds in SGPRs, one
+    // per-lane offset register, the rest a uniform offset): the A blocks of
+    // the tile, and the codes and scale bytes of the wave's row groups
+    // ([group][stage][lane] 16 B and 1 B, in MFMA order).
+    const int64_t a0 = m16_0 < m16_n ? m16_0 : m16_n - 1;
+    const int64_t a_blocks = (m16_0 + MB < m16_n ? m16_0 + MB : m16_n) - a0;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(p.xs + a0 * p.ldk * AQ), (short)0,
+                                          (int)(a_blocks * p.ldk * MX_BLOCK), BUF_RSRC_WORD3);
+    const int64_t gb = g0 < groups ? g0 : groups - 1;
+    const int b_records = (int)(((gb + OG < groups ? gb + OG : groups) - gb) * S * 1024);
+    auto rsrc_b = [&](const TileView &wi, bool codes) {
+        return codes ? __builtin_amdgcn_make_buffer_rsrc((void *)(wi.mx + gb * S * 1024), (short)0, b_records,
+                                                         BUF_RSRC_WORD3)
+                     : __builtin_amdgcn_make_buffer_rsrc((void *)(wi.mx_scales + gb * S * 64), (short)0,
+                                                         b_records / 16, BUF_RSRC_WORD3);
     };
-    int64_t ak[CAK];
+    const __amdgpu_buffer_rsrc_t rb = rsrc_b(w, true), rs = rsrc_b(w, false);
+    const __amdgpu_buffer_rsrc_t rb2 = GLU ? rsrc_b(p.w2, true) : rb, rs2 = GLU ? rsrc_b(p.w2, false) : rs;
+    int goff[OG];  // stage records from the resource base to row group g0 + i
 #pragma unroll
-    for (int j = 0; j < CAK; j++) {
-        const int q = ck + CW * j;  // [m][piece 0..5]
-        ak[j] = a_block(q / 6) + (q % 6) * 64;
-    }
-    int64_t as_[CAS];
-#pragma unroll
-    for (int j = 0; j < CAS; j++) as_[j] = a_block((ck + CW * j) % WM) + 384;
-    auto group_of = [&](int wq, int i) {
-        const int64_t gi = (int64_t)nt * (OG * WGN) + wq * OG + (i % OG);
-        return gi < groups ? gi : groups - 1;
-    };
-    const u32x4 *bsrc[CB];
-#pragma unroll
-    for (int j = 0; j < CB; j++) {
-        const int q = ck + CW * j, i = q % WN;
-        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
-        bsrc[j] = (const u32x4 *)wi.mx + group_of(q / WN, i) * S * 64;
-    }
-    const uint32_t *bss[CBS];
-#pragma unroll
-    for (int j = 0; j < CBS; j++) {  // lane l: dword l % 16 of group l / 16's 64 bytes
-        const int i = lane >> 4;
-        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
-        bss[j] = (const uint32_t *)(wi.mx_scales + group_of(ck + CW * j, i) * S * 64) + (lane & 15);
-    }
+    for (int i = 0; i < OG; i++) goff[i] = (int)(((g0 + i < groups ? g0 + i : groups - 1) - gb) * S);
 
-    auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
-        if (!copier) return;
-        const u32x4 *xs = p.xs + s * AQ;
+    // A copies of a stage, the same for every wave: three of the 24 KiB
+    // pieces (block q / 6, piece q % 6 for q = wave + 8 j) and the 256 B of
+    // scale words of block wave / 2 (two waves write the same words: an LDS
+    // copy writes a dword per lane, so the block's words take one full wave)
+    static_assert(MB * 6 == 3 * WAVES && MB * 2 == WAVES, "copies split evenly over the waves");
+    auto a_off = [&](int m) {  // bytes from the resource base to block m16_0 + m, stage 0
+        const int64_t mb = m16_0 + m < m16_n ? m16_0 + m : m16_n - 1;
+        return (int)((mb - a0) * p.ldk * MX_BLOCK);
+    };
+    int aoff[3];
 #pragma unroll
-        for (int j = 0; j < CAK; j++) {
-            const int q = ck + CW * j;
-            __builtin_amdgcn_global_load_lds((const void *)(xs + ak[j] + lane),
-                                             (lds_void *)&As[(q / 6) * AQ + (q % 6) * 64], 16, 0, 0);
+    for (int j = 0; j < 3; j++) {
+        const int q = wave + WAVES * j;
+        aoff[j] = a_off(q / 6) + (q % 6) * 1024;
+    }
+    const int soff = a_off(wave / 2) + 6144;
+    auto copy_a = [&](int j, int64_t s, u32x4 *As) {  // j < 3: a KiB piece; j == 3: the scale words
+        const int so = (int)s * MX_BLOCK;
+        if (j < 3) {
+            const int q = wave + WAVES * j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&As[(q / 6) * AQ + (q % 6) * 64], 16, lane * 16,
+                                                     aoff[j] + so, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&As[(wave / 2) * AQ + 384], 4, lane * 4,
+                                                     soff + so, 0, 0);
         }
-#pragma unroll
-        for (int j = 0; j < CAS; j++) {
-            const int q = ck + CW * j;
-            if (q < NAS)
-                __builtin_amdgcn_global_load_lds((const void *)((const uint32_t *)(xs + as_[j]) + lane),
-                                                 (lds_void *)&As[q * AQ + 384], 4, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < CB; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + s * 64 + lane),
-                                             (lds_void *)&Bs[(ck + CW * j) * 64], 16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < CBS; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(bss[j] + s * 16), (lds_void *)&Ss[(ck + CW * j) * 64], 4,
-                                             0, 0);
+    };
+    auto load_b = [&](int i, int64_t s, u32x4 (&b)[WN], int (&sb)[WN]) {
+        const int r = goff[i % OG] + (int)s;
+        b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(i < OG ? rb : rb2, lane * 16,
+                                                                              r * 1024, 0));
+        sb[i] = __builtin_amdgcn_raw_buffer_load_b8(i < OG ? rs : rs2, lane, r * 64, 0);
     };
 
     floatx4 acc[WM][WN];
@@ -725,66 +729,75 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
 #pragma unroll
         for (int i = 0; i < WN; i++) acc[m][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    copy_stage(0, As0, Bs0, Ss0);
+    u32x4 b0[WN], b1[WN];
+    int sb0[WN], sb1[WN];
+#pragma unroll
+    for (int j = 0; j < 4; j++) copy_a(j, 0, As0);
+#pragma unroll
+    for (int i = 0; i < WN; i++) load_b(i, 0, b0, sb0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    auto step = [&](int64_t s, const u32x4 *As, const u32x4 *Bs, const uint32_t *Ss, u32x4 *An, u32x4 *Bn,
-                    uint32_t *Sn) {
-        copy_stage(s + 1 < S ? s + 1 : s, An, Bn, Sn);
-        __builtin_amdgcn_sched_barrier(0);
-        u32x4 b[WN];
-        int sb[WN], sa[WM];
+    auto step = [&](int64_t s, const u32x4 *As, u32x4 *An, const u32x4 (&b)[WN], const int (&sb)[WN],
+                    u32x4 (&bn)[WN], int (&sbn)[WN]) {
+        const int64_t sn = s + 1 < S ? s + 1 : s;
+        const u32x4 *Aw = As + 2 * wm * AQ;  // the wave's two blocks
+        int sa[WM];
 #pragma unroll
-        for (int i = 0; i < WN; i++) {
-            b[i] = Bs[(wave * WN + i) * 64 + lane];
-            sb[i] = ((const uint8_t *)Ss)[wave * 256 + i * 64 + lane];
-        }
-#pragma unroll
-        for (int m = 0; m < WM; m++) sa[m] = (int)((const uint32_t *)(As + m * AQ + 384))[lane];
+        for (int m = 0; m < WM; m++) sa[m] = (int)((const uint32_t *)(Aw + m * AQ + 384))[lane];
         auto read_a = [&](int m, int e) {
             MxA r;
-            r.lo = __builtin_bit_cast(v4i_t, As[m * AQ + e * 64 + lane]);
-            r.hi = ((const v2i_t *)(As + m * AQ + 256))[e * 64 + lane];
+            r.lo = __builtin_bit_cast(v4i_t, Aw[m * AQ + e * 64 + lane]);
+            r.hi = ((const v2i_t *)(Aw + m * AQ + 256))[e * 64 + lane];
             return r;
         };
-        auto mma_term = [&](auto ec, const MxA (&at)[WM]) {
+        // operand (block m, term e) feeds WN products; the next operand is
+        // read while they issue, and one of the next stage's loads goes out
+        // after every second product
+        static_assert(NT == 4 && WM == 2, "the operand sequence below is written out for four terms, two blocks");
+        MxA a[2];
+        a[0] = read_a(0, 0);
+        auto block = [&](auto ec, int m, const MxA &at, int k) {
             constexpr int E = decltype(ec)::value;
 #pragma unroll
-            for (int m = 0; m < WM; m++)
-#pragma unroll
-                for (int i = 0; i < WN; i++) acc[m][i] = mfma_mx<E>(at[m], sa[m], b[i], sb[i], acc[m][i]);
-        };
-        // term e + 1's operands are read while term e's products issue
-        static_assert(NT == 4, "the term sequence below is written out for four terms");
-        MxA a[2][WM];
-#pragma unroll
-        for (int m = 0; m < WM; m++) a[0][m] = read_a(m, 0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int m = 0; m < WM; m++) a[1][m] = read_a(m, 1);
-        mma_term(std::integral_constant<int, 0>{}, a[0]);
-#pragma unroll
-        for (int m = 0; m < WM; m++) a[0][m] = read_a(m, 2);
-        mma_term(std::integral_constant<int, 1>{}, a[1]);
-#pragma unroll
-        for (int m = 0; m < WM; m++) a[1][m] = read_a(m, 3);
-        mma_term(std::integral_constant<int, 2>{}, a[0]);
-        mma_term(std::integral_constant<int, 3>{}, a[1]);
-        constexpr int NA = WM * 2, NM = WM * WN;  // two LDS reads per A operand
-#pragma unroll
-        for (int e = 0; e < NT; e++) {
-            if (e + 1 < NT) {
-#pragma unroll
-                for (int j = 0; j < NA; j++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            for (int i = 0; i < WN; i++) {
+                acc[m][i] = mfma_mx<E>(at, sa[m], b[i], sb[i], acc[m][i]);
+                // loads of the next stage, in the order they are waited for
+                // (none is: the stage ends with a full wait)
+                const int l = k * (WN / 2) + i / 2;  // 0..31 over the stage
+                if (i % 2 == 1) {
+                    if (l < WN) load_b(l, sn, bn, sbn);
+                    else if (l < WN + 4) copy_a(l - WN, sn, An);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, NM - NA, 0);
-            } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+            }
+        };
+        auto term = [&](auto ec) {
+            constexpr int E = decltype(ec)::value;
+#pragma unroll
+            for (int m = 0; m < WM; m++) {
+                const int k = E * WM + m;
+                if (k + 1 < NT * WM) a[(k + 1) & 1] = read_a((m + 1) % WM, m + 1 < WM ? E : E + 1);
+                block(ec, m, a[k & 1], k);
+            }
+        };
+        term(std::integral_constant<int, 0>{});
+        term(std::integral_constant<int, 1>{});
+        term(std::integral_constant<int, 2>{});
+        term(std::integral_constant<int, 3>{});
+        // keep the order written above: per operand, its LDS reads, then
+        // MFMAs with a load after every second one
+#pragma unroll
+        for (int k = 0; k < NT * WM; k++) {
+            if (k == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2 * WM, 0);  // scale words
+            if (k + 1 < NT * WM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < WN; i += 2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                const int l = k * (WN / 2) + i / 2;
+                if (l < WN) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+                else if (l < WN + 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -794,12 +807,13 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
     };
     int64_t s = 0;
     for (; s + 1 < S; s += 2) {
-        step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
-        step(s + 1, As1, Bs1, Ss1, As0, Bs0, Ss0);
+        step(s, As0, As1, b0, sb0, b1, sb1);
+        step(s + 1, As1, As0, b1, sb1, b0, sb0);
     }
-    if (s < S) step(s, As0, Bs0, Ss0, As1, Bs1, Ss1);
+    if (s < S) step(s, As0, As1, b0, sb0, b1, sb1);
 
     const int kq = lane >> 4;
+    const int64_t mw = m16_0 + 2 * wm;  // the wave's first token block
     if constexpr (!GLU) {
 #pragma unroll
         for (int m = 0; m < WM; m++)
@@ -807,16 +821,16 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
             for (int i = 0; i < WN; i++) {
                 const int64_t row = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
-                for (int r = 0; r < 4; r++) tile_store(to, (m16_0 + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
+                for (int r = 0; r < 4; r++) tile_store(to, (mw + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
             }
     } else {
-        // y = act(gate) * up (tensor.gatedActivation) for the wave's 32
-        // columns (one E8M0 block of the next product's k) and 16 WM tokens,
-        // through a per-wave LDS patch [m][16 tokens][32 columns] (the B
-        // stage buffers are idle: the last stage ended with a barrier); then
-        // lane l splits token l % 16 of block m = l / 16 into its slot
-        static_assert(OG == 2 && WM * 16 == 64 && WAVES <= 8, "one 32-column block per wave, a token block per lane group");
-        float *patch = (float *)(wave < 4 ? Bs0 : Bs1) + (wave % 4) * (WM * 16 * 32);
+        // y = act(gate) * up (tensor.gatedActivation) for the wave's 64
+        // columns (two E8M0 blocks of the next product's k) and 32 tokens,
+        // through a per-wave LDS patch [32 tokens][64 columns]; then lane l
+        // splits token l % 16 of block (l / 16) % 2, columns 32 (l / 32)..,
+        // into its slot
+        static_assert(OG * 16 == 64 && WM * 16 == 32, "two 32-column blocks and two token blocks per wave");
+        float *pt = patch + wave * (WM * 16 * PS);
 #pragma unroll
         for (int m = 0; m < WM; m++) {
 #pragma unroll
@@ -824,27 +838,33 @@ __global__ __launch_bounds__(WGN * 64) void mx_gemm_kernel(TileGemmParams p) {
                 const int64_t col = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int64_t tok = (m16_0 + m) * 16 + 4 * kq + r;
+                    const int64_t tok = (mw + m) * 16 + 4 * kq + r;
                     float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
                     if (tok >= p.n || col >= w.rows) y = 0.f;
                     else if (p.out) p.out[tok * p.ldo + col] = y;
-                    patch[(m * 16 + 4 * kq + r) * 32 + i * 16 + (lane & 15)] = y;
+                    pt[(m * 16 + 4 * kq + r) * PS + i * 16 + (lane & 15)] = y;
                 }
             }
         }
-        const int64_t kb = (g0 * 16) / 32;  // the next product's E8M0 block of these columns
-        const int64_t mblk = m16_0 + (lane >> 4);
-        if (p.xs_out && kb / 4 < p.ldk_out) {
+        if (p.xs_out) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            const int half = lane >> 5, mb = (lane >> 4) & 1;
+            const int64_t kb = (g0 * 16) / 32 + half;  // the next product's E8M0 block of these columns
+            const int64_t mblk = mw + mb;
             float r[32];
 #pragma unroll
-            for (int j = 0; j < 32; j++) r[j] = patch[(lane >> 4) * 512 + (lane & 15) * 32 + j];
-            if (mblk < m16_n)
+            for (int j = 0; j < 32; j++) r[j] = pt[(mb * 16 + (lane & 15)) * PS + half * 32 + j];
+            if (mblk < m16_n && kb / 4 < p.ldk_out)
                 mx_write_slot(r, (uint8_t *)p.xs_out + (mblk * p.ldk_out + kb / 4) * MX_BLOCK,
                               (lane & 15) + 16 * (int)(kb % 4));
         }
     }
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(512) void mx_gemm_kernel(TileGemmParams p) {
+    mx_gemm_body<GLU>(p);
 }
 
 // ---------------------------------------------------------------------------
@@ -1115,11 +1135,10 @@ void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t
 
 template <bool GLU>
 static void launch_mx(TileGemmParams &p, hipStream_t s) {
-    constexpr int WGN = 8, WM = 4, WN = 4, OG = GLU ? WN / 2 : WN;
-    p.tiles_m = (int)((p.n + 16 * WM - 1) / (16 * WM));
-    p.tiles_n = (int)((p.w.rows + 16 * OG * WGN - 1) / (16 * OG * WGN));
-    hipLaunchKernelGGL((mx_gemm_kernel<WGN, WM, WN, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(WGN * 64), 0, s,
-                       p);
+    constexpr int BN = GLU ? 256 : 512;  // 64 tokens x BN rows a workgroup
+    p.tiles_m = (int)((p.n + 63) / 64);
+    p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
+    hipLaunchKernelGGL((mx_gemm_kernel<GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
     DITCH_TRY_HIP(hipGetLastError());
 }
 
