@@ -633,11 +633,12 @@ __device__ __forceinline__ floatx4 mfma_mx(const MxA &a, int sa, const u32x4 &b,
 // (wave / 4, wave % 4) takes token blocks 2 wm, 2 wm + 1 and 8 row groups
 // (GLU: 4 gate groups and the same 4 groups of the up projection), so each A
 // operand read from LDS feeds 8 products. A stage is 128 k: the A fragments
-// of the 4 token blocks (4 x 6400 B: four fp6 terms and their E8M0 scales)
-// go to one of two LDS buffers by buffer_load_lds, 1/8 of them from each
-// wave; each wave loads its own row groups' fp4 codes (1 KiB a group) and
-// E8M0 scale bytes straight into registers one stage ahead. Every wave runs
-// the same instruction stream, and the stage's loads are spread between its
+// of the 4 token blocks (4 x 6400 B: four fp6 terms and their E8M0 scales),
+// the 32 row groups' fp4 codes (1 KiB a group) and their E8M0 bytes go to one
+// of two LDS stage buffers by buffer_load_lds, every wave copying 1/8 of
+// them, so each operand crosses the texture path once per workgroup (the two
+// waves that share a row group read it from LDS). Every wave runs the same
+// instruction stream, and the next stage's copies are spread between the
 // MFMAs: a wave that issues a load while the texture unit's queue is full
 // stalls, and a burst of loads at the top of the stage would hold back the
 // MFMAs of every wave behind it. One barrier a stage. GLU: the epilogue
@@ -651,8 +652,15 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
     constexpr int AQ = MX_BLOCK / 16;     // u32x4 per A block
     constexpr int PS = OG * 16 + 4;       // GLU patch row stride (floats)
-    __shared__ u32x4 As0[MB * AQ], As1[MB * AQ];  // [block][fragment]
-    __shared__ float patch[GLU ? WAVES * WM * 16 * PS : 1];
+    // one pipeline stage: A blocks [block][fragment], the workgroup's 32 row
+    // groups' codes [wn][group][lane] and E8M0 bytes [wn][group][64 B]; two
+    // stages as distinct LDS objects
+    struct Stage {
+        u32x4 A[MB * AQ];
+        u32x4 B[4 * WN * 64];
+        uint32_t S[4 * WN * 16];
+    };
+    __shared__ Stage st0, st1;
     const TileView &w = p.w;
     const TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
                      p.delta_stride};
@@ -662,66 +670,67 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     int mt, nt;
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
     const int64_t groups = (w.rows + 15) / 16;
-    const int64_t g0 = (int64_t)nt * (OG * 4) + wn * OG;
+    const int64_t G0 = (int64_t)nt * (OG * 4);  // the workgroup's first row group
+    const int64_t g0 = G0 + wn * OG;
     const int64_t m16_0 = (int64_t)mt * MB, m16_n = (p.n + 15) / 16;
     const int64_t S = w.units_k;  // stages: one 128-column unit each
 
-    // Operands through buffer resources (base and bounds in SGPRs, one
-    // per-lane offset register, the rest a uniform offset): the A blocks of
-    // the tile, and the codes and scale bytes of the wave's row groups
-    // ([group][stage][lane] 16 B and 1 B, in MFMA order).
+    // Copies through buffer resources (base and bounds in SGPRs, one per-lane
+    // offset register, the rest a uniform offset), the same for every wave:
+    // three of the 24 KiB A pieces (block q / 6, piece q % 6 for q = wave +
+    // 8 j) and the 256 B of scale words of block wave / 2 (two waves write
+    // the same words: an LDS copy writes a dword per lane); the codes of row
+    // group `wave` of every wn (4 KiB) and the E8M0 bytes of groups 4 wave ..
+    // 4 wave + 3 (of gate rows for even waves, up rows for odd ones, GLU).
     const int64_t a0 = m16_0 < m16_n ? m16_0 : m16_n - 1;
     const int64_t a_blocks = (m16_0 + MB < m16_n ? m16_0 + MB : m16_n) - a0;
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc((void *)(p.xs + a0 * p.ldk * AQ), (short)0,
                                           (int)(a_blocks * p.ldk * MX_BLOCK), BUF_RSRC_WORD3);
-    const int64_t gb = g0 < groups ? g0 : groups - 1;
-    const int b_records = (int)(((gb + OG < groups ? gb + OG : groups) - gb) * S * 1024);
-    auto rsrc_b = [&](const TileView &wi, bool codes) {
-        return codes ? __builtin_amdgcn_make_buffer_rsrc((void *)(wi.mx + gb * S * 1024), (short)0, b_records,
-                                                         BUF_RSRC_WORD3)
-                     : __builtin_amdgcn_make_buffer_rsrc((void *)(wi.mx_scales + gb * S * 64), (short)0,
-                                                         b_records / 16, BUF_RSRC_WORD3);
+    const int64_t gb = G0 < groups ? G0 : groups - 1;
+    const int b_groups = (int)((gb + 4 * OG < groups ? gb + 4 * OG : groups) - gb);
+    auto grp = [&](int q) {  // piece q = wn * 8 + i -> groups from the resource base
+        const int64_t gi = G0 + (q / WN) * OG + (q % WN) % OG;
+        return (int)((gi < groups ? gi : groups - 1) - gb);
     };
-    const __amdgpu_buffer_rsrc_t rb = rsrc_b(w, true), rs = rsrc_b(w, false);
-    const __amdgpu_buffer_rsrc_t rb2 = GLU ? rsrc_b(p.w2, true) : rb, rs2 = GLU ? rsrc_b(p.w2, false) : rs;
-    int goff[OG];  // stage records from the resource base to row group g0 + i
-#pragma unroll
-    for (int i = 0; i < OG; i++) goff[i] = (int)(((g0 + i < groups ? g0 + i : groups - 1) - gb) * S);
-
-    // A copies of a stage, the same for every wave: three of the 24 KiB
-    // pieces (block q / 6, piece q % 6 for q = wave + 8 j) and the 256 B of
-    // scale words of block wave / 2 (two waves write the same words: an LDS
-    // copy writes a dword per lane, so the block's words take one full wave)
-    static_assert(MB * 6 == 3 * WAVES && MB * 2 == WAVES, "copies split evenly over the waves");
+    const TileView &wb = (GLU && wave >= OG) ? p.w2 : w;      // the codes this wave copies
+    const TileView &ws = (GLU && (wave & 1)) ? p.w2 : w;      // the scale bytes this wave copies
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(wb.mx + gb * S * 1024), (short)0, (int)(b_groups * S * 1024), BUF_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ws.mx_scales + gb * S * 64), (short)0, (int)(b_groups * S * 64), BUF_RSRC_WORD3);
+    static_assert(MB * 6 == 3 * WAVES && MB * 2 == WAVES && WN == WAVES, "copies split evenly over the waves");
     auto a_off = [&](int m) {  // bytes from the resource base to block m16_0 + m, stage 0
         const int64_t mb = m16_0 + m < m16_n ? m16_0 + m : m16_n - 1;
         return (int)((mb - a0) * p.ldk * MX_BLOCK);
     };
-    int aoff[3];
+    int aoff[3], boff[4];
 #pragma unroll
     for (int j = 0; j < 3; j++) {
         const int q = wave + WAVES * j;
         aoff[j] = a_off(q / 6) + (q % 6) * 1024;
     }
+#pragma unroll
+    for (int j = 0; j < 4; j++) boff[j] = grp(j * WN + wave) * (int)S * 1024;
     const int soff = a_off(wave / 2) + 6144;
-    auto copy_a = [&](int j, int64_t s, u32x4 *As) {  // j < 3: a KiB piece; j == 3: the scale words
-        const int so = (int)s * MX_BLOCK;
+    const int sv = grp(4 * wave + (lane >> 4)) * (int)S * 64 + (lane & 15) * 4;  // per-lane scale source
+    // copy j of a stage: 0..2 A pieces, 3 A scale words, 4..7 codes, 8 scale bytes
+    auto copy = [&](int j, int64_t s, Stage &t) {
         if (j < 3) {
             const int q = wave + WAVES * j;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&As[(q / 6) * AQ + (q % 6) * 64], 16, lane * 16,
-                                                     aoff[j] + so, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&t.A[(q / 6) * AQ + (q % 6) * 64], 16, lane * 16,
+                                                     aoff[j] + (int)s * MX_BLOCK, 0, 0);
+        } else if (j == 3) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&t.A[(wave / 2) * AQ + 384], 4, lane * 4,
+                                                     soff + (int)s * MX_BLOCK, 0, 0);
+        } else if (j < 8) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)&t.B[((j - 4) * WN + wave) * 64], 16, lane * 16,
+                                                     boff[j - 4] + (int)s * 1024, 0, 0);
         } else {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&As[(wave / 2) * AQ + 384], 4, lane * 4,
-                                                     soff + so, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)&t.S[wave * 64], 4, sv, (int)s * 64, 0, 0);
         }
     };
-    auto load_b = [&](int i, int64_t s, u32x4 (&b)[WN], int (&sb)[WN]) {
-        const int r = goff[i % OG] + (int)s;
-        b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(i < OG ? rb : rb2, lane * 16,
-                                                                              r * 1024, 0));
-        sb[i] = __builtin_amdgcn_raw_buffer_load_b8(i < OG ? rs : rs2, lane, r * 64, 0);
-    };
+    constexpr int NCOPY = 9;
 
     floatx4 acc[WM][WN];
 #pragma unroll
@@ -729,48 +738,45 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
 #pragma unroll
         for (int i = 0; i < WN; i++) acc[m][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 b0[WN], b1[WN];
-    int sb0[WN], sb1[WN];
 #pragma unroll
-    for (int j = 0; j < 4; j++) copy_a(j, 0, As0);
-#pragma unroll
-    for (int i = 0; i < WN; i++) load_b(i, 0, b0, sb0);
+    for (int j = 0; j < NCOPY; j++) copy(j, 0, st0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    auto step = [&](int64_t s, const u32x4 *As, u32x4 *An, const u32x4 (&b)[WN], const int (&sb)[WN],
-                    u32x4 (&bn)[WN], int (&sbn)[WN]) {
+    auto step = [&](int64_t s, const Stage &t, Stage &tn) {
         const int64_t sn = s + 1 < S ? s + 1 : s;
-        const u32x4 *Aw = As + 2 * wm * AQ;  // the wave's two blocks
-        int sa[WM];
-#pragma unroll
-        for (int m = 0; m < WM; m++) sa[m] = (int)((const uint32_t *)(Aw + m * AQ + 384))[lane];
+        const u32x4 *Aw = t.A + 2 * wm * AQ;  // the wave's two blocks
         auto read_a = [&](int m, int e) {
             MxA r;
             r.lo = __builtin_bit_cast(v4i_t, Aw[m * AQ + e * 64 + lane]);
             r.hi = ((const v2i_t *)(Aw + m * AQ + 256))[e * 64 + lane];
             return r;
         };
-        // operand (block m, term e) feeds WN products; the next operand is
-        // read while they issue, and one of the next stage's loads goes out
-        // after every second product
-        static_assert(NT == 4 && WM == 2, "the operand sequence below is written out for four terms, two blocks");
         MxA a[2];
         a[0] = read_a(0, 0);
+        int sa[WM], sb[WN];
+        u32x4 b[WN];
+#pragma unroll
+        for (int m = 0; m < WM; m++) sa[m] = (int)((const uint32_t *)(Aw + m * AQ + 384))[lane];
+#pragma unroll
+        for (int i = 0; i < WN; i++) {
+            b[i] = t.B[(wn * WN + i) * 64 + lane];
+            sb[i] = ((const uint8_t *)t.S)[(wn * WN + i) * 64 + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // operand (block m, term e) feeds WN products; the next operand is
+        // read while they issue, and one of the next stage's copies goes out
+        // after every second product
+        static_assert(NT == 4 && WM == 2, "the operand sequence below is written out for four terms, two blocks");
         auto block = [&](auto ec, int m, const MxA &at, int k) {
             constexpr int E = decltype(ec)::value;
 #pragma unroll
             for (int i = 0; i < WN; i++) {
                 acc[m][i] = mfma_mx<E>(at, sa[m], b[i], sb[i], acc[m][i]);
-                // loads of the next stage, in the order they are waited for
-                // (none is: the stage ends with a full wait)
                 const int l = k * (WN / 2) + i / 2;  // 0..31 over the stage
-                if (i % 2 == 1) {
-                    if (l < WN) load_b(l, sn, bn, sbn);
-                    else if (l < WN + 4) copy_a(l - WN, sn, An);
-                }
+                if (i % 2 == 1 && l < NCOPY) copy(l, sn, tn);
             }
         };
         auto term = [&](auto ec) {
@@ -786,18 +792,13 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
         term(std::integral_constant<int, 1>{});
         term(std::integral_constant<int, 2>{});
         term(std::integral_constant<int, 3>{});
-        // keep the order written above: per operand, its LDS reads, then
-        // MFMAs with a load after every second one
 #pragma unroll
         for (int k = 0; k < NT * WM; k++) {
-            if (k == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2 * WM, 0);  // scale words
             if (k + 1 < NT * WM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
             for (int i = 0; i < WN; i += 2) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                const int l = k * (WN / 2) + i / 2;
-                if (l < WN) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-                else if (l < WN + 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                if (k * (WN / 2) + i / 2 < NCOPY) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -807,10 +808,10 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     };
     int64_t s = 0;
     for (; s + 1 < S; s += 2) {
-        step(s, As0, As1, b0, sb0, b1, sb1);
-        step(s + 1, As1, As0, b1, sb1, b0, sb0);
+        step(s, st0, st1);
+        step(s + 1, st1, st0);
     }
-    if (s < S) step(s, As0, As1, b0, sb0, b1, sb1);
+    if (s < S) step(s, st0, st1);
 
     const int kq = lane >> 4;
     const int64_t mw = m16_0 + 2 * wm;  // the wave's first token block
@@ -826,11 +827,13 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     } else {
         // y = act(gate) * up (tensor.gatedActivation) for the wave's 64
         // columns (two E8M0 blocks of the next product's k) and 32 tokens,
-        // through a per-wave LDS patch [32 tokens][64 columns]; then lane l
-        // splits token l % 16 of block (l / 16) % 2, columns 32 (l / 32)..,
-        // into its slot
+        // through a per-wave LDS patch [32 tokens][64 columns] in the idle
+        // stage buffers (the last stage ended with a barrier and no copy is
+        // in flight); then lane l splits token l % 16 of block (l / 16) % 2,
+        // columns 32 (l / 32).., into its slot
         static_assert(OG * 16 == 64 && WM * 16 == 32, "two 32-column blocks and two token blocks per wave");
-        float *pt = patch + wave * (WM * 16 * PS);
+        static_assert(WAVES / 2 * WM * 16 * PS * 4 <= (int)sizeof(Stage), "patches fit the stage buffers");
+        float *pt = (float *)(wave < WAVES / 2 ? (void *)&st0 : (void *)&st1) + (wave % (WAVES / 2)) * (WM * 16 * PS);
 #pragma unroll
         for (int m = 0; m < WM; m++) {
 #pragma unroll
