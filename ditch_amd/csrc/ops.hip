@@ -225,9 +225,13 @@ __global__ __launch_bounds__(256) void rmsnorm_split_mx_kernel(uint8_t *xm, int6
     const int st_l = threadIdx.x >> 6, l = lane, row = l & 15, kb = l >> 4;
     const int64_t r = m16 * 16 + row;
     const float inv = inv_s[row];
-    for (int64_t c0 = 0; c0 < ldst * 128; c0 += RS_CHUNK) {
-        // the 16 rows' columns c0 .. c0 + 512 (zero past the matrix)
-        for (int q = threadIdx.x; q < 16 * RS_CHUNK / 4; q += 256) {
+    // the 16 rows' columns c0 .. c0 + 512 (zero past the matrix), 8 float4
+    // a thread; chunk c + 1 is loaded into registers while chunk c is split
+    constexpr int QT = 16 * RS_CHUNK / 4 / 256;
+    auto fetch = [&](int64_t c0, float4 (&buf)[QT]) {
+#pragma unroll
+        for (int j = 0; j < QT; j++) {
+            const int q = threadIdx.x + 256 * j;
             const int qr = q / (RS_CHUNK / 4), qc = (q % (RS_CHUNK / 4)) * 4;
             const int64_t rq = m16 * 16 + qr, k = c0 + qc;
             float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -240,9 +244,19 @@ __global__ __launch_bounds__(256) void rmsnorm_split_mx_kernel(uint8_t *xm, int6
                     a.w = k + 3 < len ? x[rq * len + k + 3] : 0.f;
                 }
             }
-            *(float4 *)&chunk[qr][qc] = a;
+            buf[j] = a;
+        }
+    };
+    float4 pre[QT];
+    fetch(0, pre);
+    for (int64_t c0 = 0; c0 < ldst * 128; c0 += RS_CHUNK) {
+#pragma unroll
+        for (int j = 0; j < QT; j++) {
+            const int q = threadIdx.x + 256 * j;
+            *(float4 *)&chunk[q / (RS_CHUNK / 4)][(q % (RS_CHUNK / 4)) * 4] = pre[j];
         }
         __syncthreads();
+        if (c0 + RS_CHUNK < ldst * 128) fetch(c0 + RS_CHUNK, pre);
         const int64_t st = c0 / 128 + st_l;
         if (st < ldst) {
             const int kl = st_l * 128 + kb * 32;
