@@ -603,6 +603,10 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 
+#ifndef MX_WM
+#define MX_WM 3
+#endif
+
 // Fourth word of a raw buffer resource (32-bit data format; with stride 0
 // the record count is a byte count and reads past it return zero)
 constexpr int BUF_RSRC_WORD3 = 0x00020000;
@@ -646,9 +650,9 @@ __device__ __forceinline__ floatx4 mfma_mx(const MxA &a, int sa, const u32x4 &b,
 // product.
 // (The body is a device function: the buffer-resource type exists on the
 // device side only, and the host pass instantiates the kernel for its stub.)
-template <bool GLU>
+template <int WM, bool GLU>
 __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
-    constexpr int WAVES = 8, MB = 4, WM = 2, WN = 8, NT = MX_TERMS;
+    constexpr int WAVES = 8, MB = 2 * WM, WN = 8, NT = MX_TERMS;
     constexpr int OG = GLU ? WN / 2 : WN;  // output row groups per wave
     constexpr int AQ = MX_BLOCK / 16;     // u32x4 per A block
     constexpr int PS = OG * 16 + 4;       // GLU patch row stride (floats)
@@ -699,38 +703,44 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
         (void *)(wb.mx + gb * S * 1024), (short)0, (int)(b_groups * S * 1024), BUF_RSRC_WORD3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(ws.mx_scales + gb * S * 64), (short)0, (int)(b_groups * S * 64), BUF_RSRC_WORD3);
-    static_assert(MB * 6 == 3 * WAVES && MB * 2 == WAVES && WN == WAVES, "copies split evenly over the waves");
+    static_assert(WN == WAVES, "each wave copies one row group of every wn");
     auto a_off = [&](int m) {  // bytes from the resource base to block m16_0 + m, stage 0
         const int64_t mb = m16_0 + m < m16_n ? m16_0 + m : m16_n - 1;
         return (int)((mb - a0) * p.ldk * MX_BLOCK);
     };
-    int aoff[3], boff[4];
+    // A pieces q = wave + 8 j (the last piece again where 8 does not divide
+    // them: the same bytes to the same place), scale words of block
+    // wave * MB / 8
+    constexpr int NA = MB * 6, CA = (NA + WAVES - 1) / WAVES;
+    int aoff[CA], boff[4];
 #pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const int q = wave + WAVES * j;
+    for (int j = 0; j < CA; j++) {
+        const int q = wave + WAVES * j < NA ? wave + WAVES * j : NA - 1;
         aoff[j] = a_off(q / 6) + (q % 6) * 1024;
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) boff[j] = grp(j * WN + wave) * (int)S * 1024;
-    const int soff = a_off(wave / 2) + 6144;
+    const int sblk = wave * MB / WAVES;
+    const int soff = a_off(sblk) + 6144;
     const int sv = grp(4 * wave + (lane >> 4)) * (int)S * 64 + (lane & 15) * 4;  // per-lane scale source
-    // copy j of a stage: 0..2 A pieces, 3 A scale words, 4..7 codes, 8 scale bytes
+    // copy j of a stage: 0..CA-1 A pieces, CA the A scale words, CA+1..CA+4
+    // codes, CA+5 scale bytes
     auto copy = [&](int j, int64_t s, Stage &t) {
-        if (j < 3) {
-            const int q = wave + WAVES * j;
+        if (j < CA) {
+            const int q = wave + WAVES * j < NA ? wave + WAVES * j : NA - 1;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&t.A[(q / 6) * AQ + (q % 6) * 64], 16, lane * 16,
                                                      aoff[j] + (int)s * MX_BLOCK, 0, 0);
-        } else if (j == 3) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&t.A[(wave / 2) * AQ + 384], 4, lane * 4,
+        } else if (j == CA) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)&t.A[sblk * AQ + 384], 4, lane * 4,
                                                      soff + (int)s * MX_BLOCK, 0, 0);
-        } else if (j < 8) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)&t.B[((j - 4) * WN + wave) * 64], 16, lane * 16,
-                                                     boff[j - 4] + (int)s * 1024, 0, 0);
+        } else if (j < CA + 5) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)&t.B[((j - CA - 1) * WN + wave) * 64], 16,
+                                                     lane * 16, boff[j - CA - 1] + (int)s * 1024, 0, 0);
         } else {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)&t.S[wave * 64], 4, sv, (int)s * 64, 0, 0);
         }
     };
-    constexpr int NCOPY = 9;
+    constexpr int NCOPY = CA + 6;
 
     floatx4 acc[WM][WN];
 #pragma unroll
@@ -747,7 +757,7 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
 
     auto step = [&](int64_t s, const Stage &t, Stage &tn) {
         const int64_t sn = s + 1 < S ? s + 1 : s;
-        const u32x4 *Aw = t.A + 2 * wm * AQ;  // the wave's two blocks
+        const u32x4 *Aw = t.A + WM * wm * AQ;  // the wave's blocks
         auto read_a = [&](int m, int e) {
             MxA r;
             r.lo = __builtin_bit_cast(v4i_t, Aw[m * AQ + e * 64 + lane]);
@@ -769,7 +779,7 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
         // operand (block m, term e) feeds WN products; the next operand is
         // read while they issue, and one of the next stage's copies goes out
         // after every second product
-        static_assert(NT == 4 && WM == 2, "the operand sequence below is written out for four terms, two blocks");
+        static_assert(NT == 4, "the operand sequence below is written out for four terms");
         auto block = [&](auto ec, int m, const MxA &at, int k) {
             constexpr int E = decltype(ec)::value;
 #pragma unroll
@@ -814,7 +824,7 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     if (s < S) step(s, st0, st1);
 
     const int kq = lane >> 4;
-    const int64_t mw = m16_0 + 2 * wm;  // the wave's first token block
+    const int64_t mw = m16_0 + WM * wm;  // the wave's first token block
     if constexpr (!GLU) {
 #pragma unroll
         for (int m = 0; m < WM; m++)
@@ -826,12 +836,13 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
             }
     } else {
         // y = act(gate) * up (tensor.gatedActivation) for the wave's 64
-        // columns (two E8M0 blocks of the next product's k) and 32 tokens,
-        // through a per-wave LDS patch [32 tokens][64 columns] in the idle
-        // stage buffers (the last stage ended with a barrier and no copy is
-        // in flight); then lane l splits token l % 16 of block (l / 16) % 2,
-        // columns 32 (l / 32).., into its slot
-        static_assert(OG * 16 == 64 && WM * 16 == 32, "two 32-column blocks and two token blocks per wave");
+        // columns (two E8M0 blocks of the next product's k) and 16 WM
+        // tokens, through a per-wave LDS patch [16 WM tokens][64 columns] in
+        // the idle stage buffers (the last stage ended with a barrier and no
+        // copy is in flight); then slot l (token l % 16, columns 32 ((l / 16)
+        // % 2).., block l / 32) is split by lane l % 64 into the next
+        // product's fragments
+        static_assert(OG * 16 == 64, "two 32-column blocks per wave");
         static_assert(WAVES / 2 * WM * 16 * PS * 4 <= (int)sizeof(Stage), "patches fit the stage buffers");
         float *pt = (float *)(wave < WAVES / 2 ? (void *)&st0 : (void *)&st1) + (wave % (WAVES / 2)) * (WM * 16 * PS);
 #pragma unroll
@@ -852,22 +863,25 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
         if (p.xs_out) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            const int half = lane >> 5, mb = (lane >> 4) & 1;
-            const int64_t kb = (g0 * 16) / 32 + half;  // the next product's E8M0 block of these columns
-            const int64_t mblk = mw + mb;
-            float r[32];
 #pragma unroll
-            for (int j = 0; j < 32; j++) r[j] = pt[(mb * 16 + (lane & 15)) * PS + half * 32 + j];
-            if (mblk < m16_n && kb / 4 < p.ldk_out)
-                mx_write_slot(r, (uint8_t *)p.xs_out + (mblk * p.ldk_out + kb / 4) * MX_BLOCK,
-                              (lane & 15) + 16 * (int)(kb % 4));
+            for (int sl0 = 0; sl0 < WM * 32; sl0 += 64) {
+                const int sl = sl0 + lane, mb = sl / 32, half = (sl / 16) % 2;
+                const int64_t kb = (g0 * 16) / 32 + half;  // the next product's E8M0 block of these columns
+                const int64_t mblk = mw + mb;
+                float r[32];
+#pragma unroll
+                for (int j = 0; j < 32; j++) r[j] = pt[((mb < WM ? mb : 0) * 16 + (lane & 15)) * PS + half * 32 + j];
+                if (sl < WM * 32 && mblk < m16_n && kb / 4 < p.ldk_out)
+                    mx_write_slot(r, (uint8_t *)p.xs_out + (mblk * p.ldk_out + kb / 4) * MX_BLOCK,
+                                  (lane & 15) + 16 * (int)(kb % 4));
+            }
         }
     }
 }
 
-template <bool GLU>
+template <int WM, bool GLU>
 __global__ __launch_bounds__(512) void mx_gemm_kernel(TileGemmParams p) {
-    mx_gemm_body<GLU>(p);
+    mx_gemm_body<WM, GLU>(p);
 }
 
 // ---------------------------------------------------------------------------
@@ -1138,10 +1152,10 @@ void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t
 
 template <bool GLU>
 static void launch_mx(TileGemmParams &p, hipStream_t s) {
-    constexpr int BN = GLU ? 256 : 512;  // 64 tokens x BN rows a workgroup
-    p.tiles_m = (int)((p.n + 63) / 64);
+    constexpr int WM = MX_WM, BM = 32 * WM, BN = GLU ? 256 : 512;  // BM tokens x BN rows a workgroup
+    p.tiles_m = (int)((p.n + BM - 1) / BM);
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
-    hipLaunchKernelGGL((mx_gemm_kernel<GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
+    hipLaunchKernelGGL((mx_gemm_kernel<WM, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
     DITCH_TRY_HIP(hipGetLastError());
 }
 
