@@ -209,6 +209,7 @@ struct TileGemmParams {
     // first token within the segment; the segment's weight, output rows and
     // delta come from gsegs
     const GroupSeg *gsegs;
+    const GroupSeg *gsegs2;  // GLU and grouped: the up projection of each segment
     const int32_t *gdesc;
     // split-K (plain products): blockIdx.y takes stages [y S / ksplit, (y + 1) S / ksplit)
     // and stores its raw sums in part[y][n][rows]; ksplit_reduce_kernel adds them
@@ -270,7 +271,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 // register inside the loop.
 template <int TF, int XT, int WGM, int WGN, int WM, int WN, bool GLU, bool GR = false>
 __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParams p) {
-    static_assert(!(GLU && GR), "grouped products are plain");
     constexpr int WAVES = WGM * WGN;
     constexpr int TPS = TileCfg<TF>::TPS, NU = TileCfg<TF>::NU, NS = TileCfg<TF>::NS;
     constexpr int NS1 = NS ? NS : 1;
@@ -289,6 +289,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
     const int32_t *gd = GR ? p.gdesc + 4 * mt : nullptr;
     const TileView &w = GR ? p.gsegs[gd[0]].w : p.w;
+    const TileView &w2 = GR && GLU ? p.gsegs2[gd[0]].w : p.w2;
     TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank, p.delta_stride};
     int64_t tok0;  // token (within the output rows) of the tile's first block
     // row groups of this wave: WN of w, or (GLU) the same WN/2 output groups
@@ -350,14 +351,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
     for (int j = 0; j < CB; j++) {
         const int q = ck + CW * j, wq = q / (WN * NU), i = (q / NU) % WN;
-        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        const TileView &wi = (GLU && i >= OG) ? w2 : w;
         bsrc[j] = wi.codes + group_of(wq, i) * units * 1024 + lane * 16;
     }
     const uint32_t *ssrc[CS > 0 ? CS : 1];
 #pragma unroll
     for (int j = 0; j < CS; j++) {
         const int q = ck + CW * j, wq = q / NS1, i = lane >> 4;  // lane l: row l % 16 of row group l / 16
-        const TileView &wi = (GLU && i >= OG) ? p.w2 : w;
+        const TileView &wi = (GLU && i >= OG) ? w2 : w;
         ssrc[j] = wi.side + side_row(wi, group_of(wq, i), lane);
     }
 
@@ -514,6 +515,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         // A fragments of the next product: each 16-token block of the wave's
         // 32-column k tile goes through a per-wave LDS patch [16][32] (the
         // stage buffers are idle: the last stage ended with a barrier)
+        // (grouped: tokens and output rows within the segment, fragment
+        // blocks in the padded order of the row map)
         float *patch = (float *)As0 + wave * 16 * 32;
 #pragma unroll
         for (int m = 0; m < WM; m++) {
@@ -523,10 +526,10 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                 const int64_t col = (g0 + i) * 16 + (lane & 15);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int64_t tok = mblk * 16 + 4 * kq + r;
+                    const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
                     float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
-                    if (tok >= p.n || col >= w.rows) y = 0.f;
-                    else if (p.out) p.out[tok * p.ldo + col] = y;
+                    if (tok >= to.n || col >= w.rows) y = 0.f;
+                    else if (p.out) to.out[tok * to.ldo + col] = y;
                     patch[(4 * kq + r) * 32 + (i & 1) * 16 + (lane & 15)] = y;
                 }
                 if ((i & 1) && p.xs_out && mblk < m16_n && ((g0 + i - 1) * 16) / 32 < p.ldk_out) {
@@ -1029,13 +1032,26 @@ void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs
 // row_index, or consecutive) are split into 16-token blocks of their own, a
 // tile row covers up to 4 blocks of one segment, and the kernel reads the
 // segment's weight, output rows and delta from the device segment table.
-template <int TF>
+template <int TF, bool GLU>
 static void launch_tile_grouped(TileGemmParams &p, hipStream_t s) {
     constexpr bool W4 = TF == TF_BF16;  // the stage buffers of the bf16 format need the 4-wave tile
-    constexpr int WGN = W4 ? 4 : 8, BN = 16 * 4 * WGN;
+    constexpr int WGN = W4 ? 4 : 8, BN = 16 * (GLU ? 2 : 4) * WGN;
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-    hipLaunchKernelGGL((tile_gemm_kernel<TF, 2, 1, WGN, 4, 4, false, true>), grid, dim3(WGN * 64), 0, s, p);
+    hipLaunchKernelGGL((tile_gemm_kernel<TF, 2, 1, WGN, 4, 4, GLU, true>), grid, dim3(WGN * 64), 0, s, p);
+}
+
+template <bool GLU>
+static void launch_tile_grouped_any(TileGemmParams &p, hipStream_t s) {
+    switch (p.w.tf) {
+    case TF_BF16: launch_tile_grouped<TF_BF16, GLU>(p, s); break;
+    case TF_MX4: launch_tile_grouped<TF_MX4, GLU>(p, s); break;
+    case TF_FP8: launch_tile_grouped<TF_FP8, GLU>(p, s); break;
+    case TF_INT4: launch_tile_grouped<TF_INT4, GLU>(p, s); break;
+    case TF_Q8: launch_tile_grouped<TF_Q8, GLU>(p, s); break;
+    default: throw Error{DITCH_UNSUPPORTED, "grouped tiled GEMM: tile format"};
+    }
+    DITCH_TRY_HIP(hipGetLastError());
 }
 
 bool tile_grouped_takes(const GroupSeg *h_segs, unsigned nseg, int64_t max_cnt) {
@@ -1047,9 +1063,16 @@ bool tile_grouped_takes(const GroupSeg *h_segs, unsigned nseg, int64_t max_cnt) 
     return true;
 }
 
-void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, float *out, int64_t ldo,
-                              const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
-                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s) {
+// The row map and tile table of a grouped call (to `meta`), and unless the
+// caller brings them (xs_pre), the split activation fragments (to `ws`).
+struct GroupedPlan {
+    const u32x4 *xs;
+    const int32_t *dm;
+    int64_t blocks, ndesc, kt;
+};
+
+static GroupedPlan grouped_plan(const GroupSeg *h_segs, unsigned nseg, const float *x, int64_t ldx,
+                                const int32_t *row_index, const void *xs_pre, DevBuf *ws, DevBuf *meta, hipStream_t s) {
     const TileView &w0 = h_segs[0].w;
     const int64_t kt = split_k_tiles(w0);
     // blocks of each segment, the padded row map and the tile descriptors
@@ -1061,7 +1084,7 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
         blocks += nb;
         ndesc += (nb + 3) / 4;
     }
-    if (blocks == 0) return;
+    if (blocks == 0) return GroupedPlan{nullptr, nullptr, 0, 0, kt};
     std::vector<int32_t> hm((size_t)(blocks * 16 + ndesc * 4));
     int32_t *prow = hm.data(), *desc = hm.data() + blocks * 16;
     int64_t d = 0;
@@ -1079,32 +1102,67 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
     }
     int32_t *dm = meta->get<int32_t>(hm.size());
     DITCH_TRY_HIP(hipMemcpyAsync(dm, hm.data(), hm.size() * 4, hipMemcpyHostToDevice, s));
+    if (xs_pre) return GroupedPlan{(const u32x4 *)xs_pre, dm, blocks, ndesc, kt};
     void *xs = ws->get<uint8_t>(split_bytes_ldk(blocks * 16, kt, 2));
     SplitParams sp{(u32x4 *)xs, x, row_index, dm, blocks * 16, ldx, w0.cols, kt, blocks};
     const int64_t total = blocks * kt * 64;
     hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
     DITCH_TRY_HIP(hipGetLastError());
+    return GroupedPlan{(const u32x4 *)xs, dm, blocks, ndesc, kt};
+}
+
+int64_t grouped_blocks(const GroupSeg *h_segs, unsigned nseg) {
+    int64_t blocks = 0;
+    for (unsigned z = 0; z < nseg; z++) blocks += (h_segs[z].cnt + 15) / 16;
+    return blocks;
+}
+
+void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, float *out, int64_t ldo,
+                              const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
+                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s, const void *xs_pre) {
+    const GroupedPlan g = grouped_plan(h_segs, nseg, x, ldx, row_index, xs_pre, ws, meta, s);
+    if (g.blocks == 0) return;
     TileGemmParams p{};
-    p.w = w0;
-    p.xs = (const u32x4 *)xs;
-    p.kt_total = kt;
-    p.ldk = kt;
+    p.w = h_segs[0].w;
+    p.xs = g.xs;
+    p.kt_total = g.kt;
+    p.ldk = g.kt;
     p.out = out;
     p.ldo = ldo;
     p.delta_xa = delta_xa;
     p.delta_stride = delta_stride;
     p.gsegs = d_segs;
-    p.gdesc = dm + blocks * 16;
-    p.tiles_m = (int)ndesc;
-    switch (w0.tf) {
-    case TF_BF16: launch_tile_grouped<TF_BF16>(p, s); break;
-    case TF_MX4: launch_tile_grouped<TF_MX4>(p, s); break;
-    case TF_FP8: launch_tile_grouped<TF_FP8>(p, s); break;
-    case TF_INT4: launch_tile_grouped<TF_INT4>(p, s); break;
-    case TF_Q8: launch_tile_grouped<TF_Q8>(p, s); break;
-    default: throw Error{DITCH_UNSUPPORTED, "grouped tiled GEMM: tile format"};
-    }
-    DITCH_TRY_HIP(hipGetLastError());
+    p.gdesc = g.dm + g.blocks * 16;
+    p.tiles_m = (int)g.ndesc;
+    launch_tile_grouped_any<false>(p, s);
+}
+
+void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const GroupSeg *h_gate,
+                             const GroupSeg *h_up, unsigned nseg, uint32_t act, float *out, void *xs_out,
+                             int64_t ldk_out, const float *x, int64_t ldx, const int32_t *row_index, DevBuf *ws,
+                             DevBuf *meta, hipStream_t s) {
+    DITCH_CHECK(tile_glu_takes(h_gate[0].w, h_up[0].w, 128), DITCH_INVALID_ARGUMENT,
+                "grouped GLU: gate and up must share format and shape");
+    DITCH_CHECK(!xs_out || ldk_out * 32 >= h_gate[0].w.rows, DITCH_INVALID_ARGUMENT,
+                "grouped GLU: output fragments too short");
+    const GroupedPlan g = grouped_plan(h_gate, nseg, x, ldx, row_index, nullptr, ws, meta, s);
+    if (g.blocks == 0) return;
+    TileGemmParams p{};
+    p.w = h_gate[0].w;
+    p.w2 = h_up[0].w;
+    p.act = act;
+    p.xs = g.xs;
+    p.kt_total = g.kt;
+    p.ldk = g.kt;
+    p.xs_out = (u32x4 *)xs_out;
+    p.ldk_out = ldk_out;
+    p.out = out;
+    p.ldo = h_gate[0].w.rows;
+    p.gsegs = d_gate;
+    p.gsegs2 = d_up;
+    p.gdesc = g.dm + g.blocks * 16;
+    p.tiles_m = (int)g.ndesc;
+    launch_tile_grouped_any<true>(p, s);
 }
 
 bool tile_glu_takes(const TileView &g, const TileView &u, int64_t n) {

@@ -238,9 +238,20 @@ void launch_matmul_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsig
                            int64_t cols, int64_t max_cnt, float *out, const float *x, const int32_t *row_index,
                            const float *delta_xa, int delta_stride, hipStream_t s, DevBuf *ws, DevBuf *meta);
 bool tile_grouped_takes(const GroupSeg *h_segs, unsigned nseg, int64_t max_cnt);
+// xs_pre: the activation fragments already split in the grouped row order
+// (grouped_blocks(h_segs) 16-token blocks of split_k_tiles(w) k tiles);
+// NULL: split x here
 void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, unsigned nseg, float *out, int64_t ldo,
                               const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
-                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s);
+                              int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s, const void *xs_pre = nullptr);
+int64_t grouped_blocks(const GroupSeg *h_segs, unsigned nseg);
+// Routed gate/up in one tiled product: act(x gate_z^T) * (x up_z^T) per
+// segment z, as f32 rows of out (may be NULL) and as the down product's
+// activation fragments xs_out (ldk_out k tiles, grouped row order)
+void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const GroupSeg *h_gate,
+                             const GroupSeg *h_up, unsigned nseg, uint32_t act, float *out, void *xs_out,
+                             int64_t ldk_out, const float *x, int64_t ldx, const int32_t *row_index, DevBuf *ws,
+                             DevBuf *meta, hipStream_t s);
 
 // attention.hip: prompt attention (model.zig:2935-2986) on the fp32 MFMA for
 // the head shapes it takes; q [n][heads][hd], caches [prompt][T][kvd], out

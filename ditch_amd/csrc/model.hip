@@ -801,11 +801,23 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         DITCH_TRY_HIP(hipMemcpyAsync(dsegs + nseg, su.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
         DITCH_TRY_HIP(hipMemcpyAsync(dsegs + 2 * nseg, sd.data(), nseg * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
         const TileView &vg = sg[0].w, &vd = sd[0].w;
-        launch_matmul_grouped(dsegs, sg.data(), nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0,
-                              s, &m->xsplit, &m->gmeta);
-        launch_matmul_grouped(dsegs + nseg, su.data(), nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token,
-                              nullptr, 0, s, &m->xsplit, &m->gmeta);
-        {  // act(gate) * up on this chunk's pairs (consecutive experts: one run of pairs)
+        // gate, up and SwiGLU in one tiled product whose epilogue writes the
+        // down product's fragments (f32 rows too when a down delta needs them)
+        const bool fused = tile_grouped_takes(sg.data(), nseg, max_cnt) && tile_grouped_takes(sd.data(), nseg, max_cnt) &&
+                           tile_glu_takes(vg, su[0].w, 128);
+        const void *dfr = nullptr;
+        if (fused) {
+            const int64_t ldk_d = split_k_tiles(vd);
+            void *fr = m->acts.get<uint8_t>(split_bytes_ldk(grouped_blocks(sg.data(), nseg) * 16, ldk_d, 2));
+            launch_tile_glu_grouped(dsegs, dsegs + nseg, sg.data(), su.data(), nseg, 0, max_rank > 0 ? gate : nullptr,
+                                    fr, ldk_d, h, hidden, pair_token, &m->xsplit, &m->gmeta, s);
+            dfr = fr;
+        } else {
+            launch_matmul_grouped(dsegs, sg.data(), nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0,
+                                  s, &m->xsplit, &m->gmeta);
+            launch_matmul_grouped(dsegs + nseg, su.data(), nseg, su[0].w.tf, inter, hidden, max_cnt, up, h, pair_token,
+                                  nullptr, 0, s, &m->xsplit, &m->gmeta);
+            // act(gate) * up on this chunk's pairs (consecutive experts: one run of pairs)
             const int64_t p0 = sg[0].off, p1 = (int64_t)sg[nseg - 1].off + sg[nseg - 1].cnt;
             launch_gated_act(0, gate + p0 * inter, gate + p0 * inter, up + p0 * inter, p1 - p0, inter, inter, inter, s);
         }
@@ -818,8 +830,12 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
             hipLaunchKernelGGL(grouped_delta_xa_kernel, grid, dim3(256), 0, s, dxa, gate, nullptr, dsd, inter, max_rank);
             DITCH_TRY_HIP(hipGetLastError());
         }
-        launch_matmul_grouped(dsegs + 2 * nseg, sd.data(), nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr, dxa,
-                              max_rank, s, &m->xsplit, &m->gmeta);
+        if (dfr)
+            launch_tile_gemm_grouped(dsegs + 2 * nseg, sd.data(), nseg, eo, hidden, nullptr, inter, nullptr, dxa, max_rank,
+                                     &m->xsplit, &m->gmeta, s, dfr);
+        else
+            launch_matmul_grouped(dsegs + 2 * nseg, sd.data(), nseg, vd.tf, hidden, inter, max_cnt, eo, gate, nullptr,
+                                  dxa, max_rank, s, &m->xsplit, &m->gmeta);
         if (streamed) {
             cache_release(m, slots, s);
             // a layer in several chunks: the host tables of this chunk go out
