@@ -351,41 +351,47 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 }
 
 // Per-expert token counts.
-__global__ void expert_count_kernel(const int32_t *sel, int64_t nk, int32_t *counts) {
+// Selections per expert: a histogram in LDS per block, then one global
+// atomic per expert and block (the selections of a layer hit ~E addresses).
+__global__ __launch_bounds__(256) void expert_count_kernel(const int32_t *sel, int64_t nk, int32_t *counts, int64_t E) {
+    __shared__ int32_t hist[ROUTE_MAXE];
+    for (int64_t e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nk; i += (int64_t)gridDim.x * blockDim.x)
-        atomicAdd(&counts[sel[i]], 1);
+        atomicAdd(&hist[sel[i]], 1);
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < E; e += blockDim.x)
+        if (hist[e]) atomicAdd(&counts[e], hist[e]);
 }
 
 // Expert e's pair list in (token, slot) order (moe.zig:1174-1188): one block
-// per expert walks the selections in order and compacts its matches.
-__global__ void expert_list_kernel(const int32_t *sel, int64_t n, int64_t k, const int32_t *offsets, int32_t *pair_token,
-                                   int32_t *pair_of) {
-    __shared__ int32_t base;
-    int e = blockIdx.x;
-    if (threadIdx.x == 0) base = offsets[e];
+// per expert; each wave takes a contiguous run of the selections, counts its
+// matches, and after one block-wide prefix writes them in order.
+constexpr int LIST_WAVES = 16;
+__global__ __launch_bounds__(LIST_WAVES * 64) void expert_list_kernel(const int32_t *sel, int64_t n, int64_t k,
+                                                                     const int32_t *offsets, int32_t *pair_token,
+                                                                     int32_t *pair_of) {
+    __shared__ int32_t wave_cnt[LIST_WAVES];
+    const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t nk = n * k;
+    const int64_t seg = (nk + LIST_WAVES * 64 - 1) / (LIST_WAVES * 64) * 64;
+    const int64_t lo = wave * seg, hi = lo + seg < nk ? lo + seg : nk;
+    int32_t cnt = 0;
+    for (int64_t c = lo; c < hi; c += 64) cnt += __popcll(__ballot(c + lane < hi && sel[c + lane] == e));
+    if (lane == 0) wave_cnt[wave] = cnt;
     __syncthreads();
-    int64_t nk = n * k;
-    for (int64_t c0 = 0; c0 < nk; c0 += blockDim.x) {
-        int64_t i = c0 + threadIdx.x;
-        bool hit = i < nk && sel[i] == e;
-        // block-wide exclusive scan of hits
-        __shared__ int32_t wave_cnt[4];
-        unsigned long long ballot = __ballot(hit);
-        int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        int before = __popcll(ballot & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_cnt[wave] = __popcll(ballot);
-        __syncthreads();
-        int prefix = 0;
-        for (int w = 0; w < wave; w++) prefix += wave_cnt[w];
-        int total = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    int32_t base = offsets[e];
+    for (int w = 0; w < wave; w++) base += wave_cnt[w];
+    for (int64_t c = lo; c < hi; c += 64) {
+        const int64_t i = c + lane;
+        const bool hit = i < hi && sel[i] == e;
+        const unsigned long long ballot = __ballot(hit);
         if (hit) {
-            int p = base + prefix + before;
+            const int32_t p = base + __popcll(ballot & ((1ull << lane) - 1ull));
             pair_token[p] = (int32_t)(i / k);
             pair_of[i] = p;
         }
-        __syncthreads();
-        if (threadIdx.x == 0) base += total;
-        __syncthreads();
+        base += __popcll(ballot);
     }
 }
 
@@ -395,16 +401,59 @@ __global__ void expert_list_kernel(const int32_t *sel, int64_t n, int64_t k, con
 __global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared, const int32_t *ord,
                                    const float *selw, const int32_t *pair_of, int64_t n, int64_t k, int64_t hidden) {
     const int64_t h4 = (hidden + 3) / 4, total = n * h4;
+    const bool vec = (hidden % 4) == 0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t t = i / h4, c0 = (i % h4) * 4;
-        float m[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int64_t j = 0; j < k; j++) {
-            const int64_t sidx = t * k + ord[t * k + j];
-            const float w = selw[sidx];
-            const float *er = eo + (int64_t)pair_of[sidx] * hidden;
+        // the token's k (<= 16) rows and weights first, then every row load
+        // in flight together, added in the order ord gives (fixed-size
+        // register arrays, entries j >= k unused)
+        const float *er[16];
+        float wt[16];
+        float4 ev[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (c0 + u < hidden) m[u] = __fadd_rn(m[u], __fmul_rn(w, er[c0 + u]));
+        for (int j = 0; j < 16; j++) {
+            wt[j] = 0.f;
+            er[j] = eo;
+            if (j < k) {
+                const int64_t sidx = t * k + ord[t * k + j];
+                wt[j] = selw[sidx];
+                er[j] = eo + (int64_t)pair_of[sidx] * hidden + c0;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            ev[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < k) {
+                if (vec) ev[j] = *(const float4 *)er[j];
+                else {
+                    ev[j].x = er[j][0];
+                    ev[j].y = c0 + 1 < hidden ? er[j][1] : 0.f;
+                    ev[j].z = c0 + 2 < hidden ? er[j][2] : 0.f;
+                    ev[j].w = c0 + 3 < hidden ? er[j][3] : 0.f;
+                }
+            }
+        }
+        float m[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (j >= k) continue;
+            m[0] = __fadd_rn(m[0], __fmul_rn(wt[j], ev[j].x));
+            m[1] = __fadd_rn(m[1], __fmul_rn(wt[j], ev[j].y));
+            m[2] = __fadd_rn(m[2], __fmul_rn(wt[j], ev[j].z));
+            m[3] = __fadd_rn(m[3], __fmul_rn(wt[j], ev[j].w));
+        }
+        if (vec) {
+            float4 *xo = (float4 *)(x + t * hidden + c0);
+            float4 o = *xo;
+            if (eo_shared) {
+                const float4 sh = *(const float4 *)(eo_shared + t * hidden + c0);
+                m[0] = __fadd_rn(m[0], sh.x);
+                m[1] = __fadd_rn(m[1], sh.y);
+                m[2] = __fadd_rn(m[2], sh.z);
+                m[3] = __fadd_rn(m[3], sh.w);
+            }
+            *xo = make_float4(__fadd_rn(o.x, m[0]), __fadd_rn(o.y, m[1]), __fadd_rn(o.z, m[2]), __fadd_rn(o.w, m[3]));
+            continue;
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -737,7 +786,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     DITCH_TRY_HIP(hipGetLastError());
     int32_t *counts = m->r_counts.get<int32_t>(E);
     DITCH_TRY_HIP(hipMemsetAsync(counts, 0, E * 4, s));
-    hipLaunchKernelGGL(expert_count_kernel, dim3(grid_for(n * k)), dim3(256), 0, s, sel, n * k, counts);
+    hipLaunchKernelGGL(expert_count_kernel, dim3((unsigned)std::min<int64_t>((n * k + 2047) / 2048, 64)), dim3(256), 0,
+                       s, sel, n * k, counts, E);
     DITCH_TRY_HIP(hipGetLastError());
     std::vector<int32_t> hc(E), ho(E);
     DITCH_TRY_HIP(hipMemcpyAsync(hc.data(), counts, E * 4, hipMemcpyDeviceToHost, s));
@@ -753,7 +803,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     DITCH_TRY_HIP(hipMemcpyAsync(offsets, ho.data(), E * 4, hipMemcpyHostToDevice, s));
     int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
     int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
-    hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(256), 0, s, sel, n, k, offsets, pair_token, pair_of);
+    hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(LIST_WAVES * 64), 0, s, sel, n, k, offsets, pair_token,
+                       pair_of);
     DITCH_TRY_HIP(hipGetLastError());
     // segments (experts with tokens), in index order; with expert streaming
     // in chunks of experts resident together in the cache
