@@ -606,10 +606,6 @@ __global__ __launch_bounds__(256) void split_mx_kernel(MxSplitParams p) {
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 
-#ifndef MX_WM
-#define MX_WM 3
-#endif
-
 // Fourth word of a raw buffer resource (32-bit data format; with stride 0
 // the record count is a byte count and reads past it return zero)
 constexpr int BUF_RSRC_WORD3 = 0x00020000;
@@ -1210,10 +1206,17 @@ void launch_split_mx(void *xm, const float *x, const int32_t *row_index, int64_t
 
 template <bool GLU>
 static void launch_mx(TileGemmParams &p, hipStream_t s) {
-    constexpr int WM = MX_WM, BM = 32 * WM, BN = GLU ? 256 : 512;  // BM tokens x BN rows a workgroup
-    p.tiles_m = (int)((p.n + BM - 1) / BM);
+    // 96 x BN tiles, or 64 x BN ones when the larger tiles would leave CUs
+    // idle (the k and v projections: 172 tiles against 256 CUs)
+    constexpr int BN = GLU ? 256 : 512;
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
-    hipLaunchKernelGGL((mx_gemm_kernel<WM, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
+    if ((p.n + 95) / 96 * p.tiles_n >= 256) {
+        p.tiles_m = (int)((p.n + 95) / 96);
+        hipLaunchKernelGGL((mx_gemm_kernel<3, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
+    } else {
+        p.tiles_m = (int)((p.n + 63) / 64);
+        hipLaunchKernelGGL((mx_gemm_kernel<2, GLU>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, s, p);
+    }
     DITCH_TRY_HIP(hipGetLastError());
 }
 
