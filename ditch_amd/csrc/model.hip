@@ -111,11 +111,66 @@ __device__ void head_norm_rope(float *x, float *dst2, const float *nw, const Rop
     }
 }
 
+// head_norm_rope for head_dim 128 rotated whole in neox order (element d and
+// d + 64 form a pair, both held by lane d): HB heads of the wave at a time,
+// every load of the group issued before the first use; the same operations
+// in the same order as head_norm_rope.
+template <int HB>
+__device__ void heads_rope_128(const RopeArgs &a, int64_t i, int64_t pos, float *kd) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int64_t H = a.heads + a.kv_heads;
+    const int64_t p = pos < a.rope_len - 1 ? pos : a.rope_len - 1;
+    const float c = a.cos_t[p * 64 + lane], sn = a.sin_t[p * 64 + lane];
+    for (int64_t h0 = (int64_t)wave * HB; h0 < H; h0 += (int64_t)nw * HB) {
+        float x0[HB], x1[HB];
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            const int64_t h = h0 + j;
+            x0[j] = x1[j] = 0.f;
+            if (h < H) {
+                const float *x = h < a.heads ? a.q + (i * a.heads + h) * 128 : a.k + (i * a.kv_heads + (h - a.heads)) * 128;
+                x0[j] = x[lane];
+                x1[j] = x[lane + 64];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            const int64_t h = h0 + j;
+            if (h >= H) continue;
+            const bool qh = h < a.heads;
+            const float *nwt = qh ? a.q_norm : a.k_norm;
+            float v0 = x0[j], v1 = x1[j];
+            if (nwt) {
+                float ss = __builtin_fmaf(v1, v1, __builtin_fmaf(v0, v0, 0.f));
+                ss = wave_sum64(ss);
+                const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, 128.f), a.eps)));
+                v0 = __fmul_rn(__fmul_rn(v0, inv), nwt[lane]);
+                v1 = __fmul_rn(__fmul_rn(v1, inv), nwt[lane + 64]);
+            }
+            const float ya = __fsub_rn(__fmul_rn(v0, c), __fmul_rn(v1, sn));
+            const float yb = __fadd_rn(__fmul_rn(v1, c), __fmul_rn(v0, sn));
+            float *x = qh ? a.q + (i * a.heads + h) * 128 : a.k + (i * a.kv_heads + (h - a.heads)) * 128;
+            x[lane] = ya;
+            x[lane + 64] = yb;
+            if (!qh) {
+                float *d2 = kd + (h - a.heads) * 128;
+                d2[lane] = ya;
+                d2[lane + 64] = yb;
+            }
+        }
+    }
+}
+
 __global__ void qk_rope_cache_kernel(RopeArgs a) {
     int64_t i = blockIdx.x;
     int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int64_t pos = a.rows[i].pos, b = a.rows[i].b;
     float *kd = a.kc + (b * a.T + pos) * a.kvd, *vd = a.vc + (b * a.T + pos) * a.kvd;
+    if (a.hd == 128 && a.rope_off == 0 && a.rot == 128 && a.half == 64 && a.style == DITCH_ROPE_NEOX) {
+        heads_rope_128<4>(a, i, pos, kd);
+        for (int64_t d = threadIdx.x; d < a.kvd; d += blockDim.x) vd[d] = a.v[i * a.kvd + d];
+        return;
+    }
     for (int64_t h = wave; h < a.heads + a.kv_heads; h += nw) {
         if (h < a.heads) {
             head_norm_rope(a.q + (i * a.heads + h) * a.hd, nullptr, a.q_norm, a, pos);
