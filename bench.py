@@ -363,8 +363,8 @@ def main():
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the boxes of this pool have one "
-              f"MI355X; how the path shards is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the prompt forward would shard "
+              f"data-parallel over prompts, one model copy per GPU; nothing of that is built)", file=sys.stderr)
         sys.exit(2)
 
     from ditch_amd.hip import Device, Model
