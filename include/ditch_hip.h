@@ -210,12 +210,13 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x,
  * large-batch product over a given tensor reads, for callers that multiply
  * the same activations by several tensors or keep them resident (the
  * resident forward's own producers write them). The layout depends on the
- * tensor's format: two bf16 terms per value in MFMA operand order for BF16,
- * FP8 and INT4 tensors, four fp6 (e2m3) terms with E8M0 block scales for
- * MXFP4 tensors (the operands of the scaled MFMA). No reference
- * counterpart: matmulT (compute.zig:100) takes f32 rows.
+ * tensor's format and n: four fp6 (e2m3) terms with E8M0 block scales for
+ * MXFP4 tensors on n >= 128 rows (the operands of the scaled MFMA), else
+ * two bf16 terms per value in MFMA operand order (BF16, FP8, INT4, Q8_0 and
+ * MXFP4 tensors on n >= 32). No reference counterpart: matmulT
+ * (compute.zig:100) takes f32 rows.
  * ditch_hip_frag_bytes: bytes for n rows of activations against w, or 0
- * when the large-batch product does not take w (n < 128, or a format it does
+ * when the large-batch product does not take w (n < 32, or a format it does
  * not decode exactly); the f32 entry point then applies.                  */
 uint64_t ditch_hip_frag_bytes(const ditch_hip_tensor *w, uint64_t n);
 /* Writes the fragments of d_x [n][cols of w] (f32) for products over w into
