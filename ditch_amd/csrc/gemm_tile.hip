@@ -797,6 +797,9 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
                 block(ec, m, a[k & 1], k);
             }
         };
+        // a wave issuing its products outranks one still at the top of the
+        // stage (s_setprio: issue arbitration only)
+        __builtin_amdgcn_s_setprio(1);
         term(std::integral_constant<int, 0>{});
         term(std::integral_constant<int, 1>{});
         term(std::integral_constant<int, 2>{});
@@ -811,6 +814,7 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
