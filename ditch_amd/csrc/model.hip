@@ -820,6 +820,8 @@ static void mm_act(ditch_hip_model *m, const Mat &mt, float *out, const Act &x, 
 // A product whose input may come as bf16-term fragments alone (no f32 rows):
 // the bf16 tiled kernel takes it (MXFP4 included: its producers write bf16
 // terms; given f32 rows an MXFP4 product takes the scaled-MFMA path).
+constexpr bool attn_split_fragments = false;
+
 static bool frag_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && tile_gemm_takes(mt.t->v, n); }
 // A product that reads MX fragments alone (MXFP4 on the scaled MFMA).
 static bool mx_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && mx_gemm_takes(mt.t->v, n); }
@@ -1080,7 +1082,11 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0};
         const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
         Act aact{att, nullptr, 0};
-        if (frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n) && !mx_only(L.o, n)) {
+        // (the kernel's own bf16-fragment epilogue needs 34 KB more LDS a
+        // workgroup, which halves its occupancy: the o product splitting the
+        // f32 rows costs less)
+        if (attn_split_fragments && frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n) &&
+            !mx_only(L.o, n)) {
             aa.ldk = split_ldk(nh * vd);
             aa.xs = m->atts.get<uint8_t>(split_bytes_ldk(n, aa.ldk, 2));
             aact = Act{att, aa.xs, aa.ldk};
