@@ -211,6 +211,7 @@ struct TileGemmParams {
     const GroupSeg *gsegs;
     const GroupSeg *gsegs2;  // GLU and grouped: the up projection of each segment
     const int32_t *gdesc;
+    const int32_t *gcount;   // grouped, planned on the device: tile rows in use (the grid covers a bound)
     // split-K (plain products): blockIdx.y takes stages [y S / ksplit, (y + 1) S / ksplit)
     // and stores its raw sums in part[y][n][rows]; ksplit_reduce_kernel adds them
     int ksplit;
@@ -286,7 +287,19 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wave_m = wave / WGN, wave_n = wave % WGN;
     int mt, nt;
-    map_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, mt, nt);
+    {
+        // grouped and planned on the device: the grid covers a bound, the
+        // tiles in use (the first *gcount tile rows) are spread over the
+        // first blocks as a grid of their own size would be, and the rest
+        // of the workgroups exit at once
+        int tm = p.tiles_m, G = (int)gridDim.x;
+        if (GR && p.gcount) {
+            tm = *p.gcount;
+            G = tm * p.tiles_n;
+            if ((int)blockIdx.x >= G) return;
+        }
+        map_tile(blockIdx.x, G, tm, p.tiles_n, mt, nt);
+    }
     const int32_t *gd = GR ? p.gdesc + 4 * mt : nullptr;
     const TileView &w = GR ? p.gsegs[gd[0]].w : p.w;
     const TileView &w2 = GR && GLU ? p.gsegs2[gd[0]].w : p.w2;
@@ -1163,6 +1176,55 @@ void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const
     p.gdesc = g.dm + g.blocks * 16;
     p.tiles_m = (int)g.ndesc;
     launch_tile_grouped_any<true>(p, s);
+}
+
+// Grouped products whose row map and tile table a device kernel wrote
+// (GroupedDevPlan): the grid covers plan.max_desc tile rows and the rows past
+// *plan.count exit at once; no host copy of the counts.
+void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
+                                 const TileView &up0, uint32_t act, void *xs_out, int64_t ldk_out, const float *x,
+                                 int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan, DevBuf *ws,
+                                 hipStream_t s) {
+    DITCH_CHECK(tile_glu_takes(gate0, up0, 128), DITCH_INVALID_ARGUMENT, "grouped GLU: gate and up must share format and shape");
+    DITCH_CHECK(!xs_out || ldk_out * 32 >= gate0.rows, DITCH_INVALID_ARGUMENT, "grouped GLU: output fragments too short");
+    const int64_t kt = split_k_tiles(gate0);
+    void *xs = ws->get<uint8_t>(split_bytes_ldk(plan.max_blocks * 16, kt, 2));
+    SplitParams sp{(u32x4 *)xs, x, row_index, plan.prow, plan.max_blocks * 16, ldx, gate0.cols, kt, plan.max_blocks};
+    const int64_t total = plan.max_blocks * kt * 64;
+    hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
+    DITCH_TRY_HIP(hipGetLastError());
+    TileGemmParams p{};
+    p.w = gate0;
+    p.w2 = up0;
+    p.act = act;
+    p.xs = (const u32x4 *)xs;
+    p.kt_total = kt;
+    p.ldk = kt;
+    p.xs_out = (u32x4 *)xs_out;
+    p.ldk_out = ldk_out;
+    p.ldo = gate0.rows;
+    p.gsegs = d_gate;
+    p.gsegs2 = d_up;
+    p.gdesc = plan.desc;
+    p.gcount = plan.count;
+    p.tiles_m = (int)plan.max_desc;
+    launch_tile_grouped_any<true>(p, s);
+}
+
+void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,
+                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s) {
+    TileGemmParams p{};
+    p.w = w0;
+    p.xs = (const u32x4 *)xs;
+    p.kt_total = split_k_tiles(w0);
+    p.ldk = p.kt_total;
+    p.out = out;
+    p.ldo = ldo;
+    p.gsegs = d_segs;
+    p.gdesc = plan.desc;
+    p.gcount = plan.count;
+    p.tiles_m = (int)plan.max_desc;
+    launch_tile_grouped_any<false>(p, s);
 }
 
 bool tile_glu_takes(const TileView &g, const TileView &u, int64_t n) {

@@ -245,6 +245,20 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
                               const float *x, int64_t ldx, const int32_t *row_index, const float *delta_xa,
                               int delta_stride, DevBuf *ws, DevBuf *meta, hipStream_t s, const void *xs_pre = nullptr);
 int64_t grouped_blocks(const GroupSeg *h_segs, unsigned nseg);
+// A grouped call planned on the device: prow [max_blocks * 16] (fragment row
+// -> gathered row, -1 for zero rows), desc [max_desc][4] (segment, first
+// block, segment's block end, first token within the segment), *count tile
+// rows in use; the segment table's off/cnt written on the device too.
+struct GroupedDevPlan {
+    const int32_t *prow, *desc, *count;
+    int64_t max_blocks, max_desc;
+};
+void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
+                                 const TileView &up0, uint32_t act, void *xs_out, int64_t ldk_out, const float *x,
+                                 int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan, DevBuf *ws,
+                                 hipStream_t s);
+void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,
+                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s);
 // Routed gate/up in one tiled product: act(x gate_z^T) * (x up_z^T) per
 // segment z, as f32 rows of out (may be NULL) and as the down product's
 // activation fragments xs_out (ldk_out k tiles, grouped row order)

@@ -450,6 +450,56 @@ __global__ __launch_bounds__(LIST_WAVES * 64) void expert_list_kernel(const int3
     }
 }
 
+// Device planning of a routed layer's grouped products, every expert a
+// segment in index order (no count read-back): the offsets of each expert's
+// pairs, off/cnt of the nt segment tables, the padded row map (16-row blocks
+// per expert, -1 for padding and for the rows past the last block up to
+// max_blocks) and the tile table (one entry per 4 blocks of an expert).
+__global__ __launch_bounds__(1024) void moe_plan_kernel(const int32_t *counts, int64_t E, GroupSeg *segs, int nt,
+                                                        int32_t *offsets, int32_t *prow, int32_t *desc, int32_t *count,
+                                                        int64_t max_blocks) {
+    __shared__ int32_t cnt_s[ROUTE_MAXE], off_s[ROUTE_MAXE], base_s[ROUTE_MAXE], dbase_s[ROUTE_MAXE];
+    __shared__ int32_t tot_blocks;
+    for (int64_t e = threadIdx.x; e < E; e += blockDim.x) cnt_s[e] = counts[e];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t o = 0, b = 0, d = 0;
+        for (int64_t e = 0; e < E; e++) {
+            const int32_t nb = (cnt_s[e] + 15) / 16;
+            off_s[e] = o;
+            base_s[e] = b;
+            dbase_s[e] = d;
+            o += cnt_s[e];
+            b += nb;
+            d += (nb + 3) / 4;
+        }
+        tot_blocks = b;
+        *count = d;
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < E; e += blockDim.x) {
+        offsets[e] = off_s[e];
+        for (int t = 0; t < nt; t++) {
+            segs[t * E + e].off = off_s[e];
+            segs[t * E + e].cnt = cnt_s[e];
+        }
+        const int32_t nb = (cnt_s[e] + 15) / 16;
+        for (int32_t j = 0; j < nb; j += 4) {
+            int32_t *dd = desc + 4 * (int64_t)(dbase_s[e] + j / 4);
+            dd[0] = (int32_t)e;
+            dd[1] = base_s[e] + j;
+            dd[2] = base_s[e] + nb;
+            dd[3] = j * 16;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int64_t e = wave; e < E; e += nw) {
+        const int32_t c = cnt_s[e], nb = (c + 15) / 16;
+        for (int32_t i = lane; i < nb * 16; i += 64) prow[(int64_t)base_s[e] * 16 + i] = i < c ? off_s[e] + i : -1;
+    }
+    for (int64_t r = (int64_t)tot_blocks * 16 + threadIdx.x; r < max_blocks * 16; r += blockDim.x) prow[r] = -1;
+}
+
 // out[t] = x[t] + (sum over the token's experts in ascending index of
 // w * eo + shared) (moe.zig:1197-1227 then the residual add); ord holds each
 // token's selections in that order. Four columns per thread.
@@ -826,6 +876,26 @@ static bool frag_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0
 // A product that reads MX fragments alone (MXFP4 on the scaled MFMA).
 static bool mx_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 && mx_gemm_takes(mt.t->v, n); }
 
+// Whether a routed layer's grouped products can be planned on the device:
+// every expert resident (no cache), gate/up/down of one tiled format and
+// shape (the fused GLU then the down product), no down delta, and enough
+// pairs per expert on average for the 16-token blocks.
+static bool moe_device_plan(ditch_hip_model *m, const Layer &L, int64_t n) {
+    const ditch_model_config &c = m->c;
+    const int64_t E = (int64_t)c.n_experts, k = (int64_t)c.top_k;
+    if (E <= 0 || E > ROUTE_MAXE || n * k < 16 * E) return false;
+    for (int64_t e = 0; e < E; e++) {
+        if (!L.eg[e].ok() || !L.eu[e].ok() || !L.ed[e].ok() || L.eg[e].streamed() || L.ed[e].rank != 0) return false;
+        const TileView &g = L.eg[e].t->v, &u = L.eu[e].t->v, &d = L.ed[e].t->v, &g0 = L.eg[0].t->v,
+                       &d0 = L.ed[0].t->v;
+        if (!tile_gemm_takes(g, 128) || !tile_gemm_takes(d, 128) || !tile_glu_takes(g, u, 128) || g.tf != g0.tf ||
+            g.units_k != g0.units_k || d.tf != d0.tf || d.units_k != d0.units_k || g.rows != g0.rows ||
+            d.rows != d0.rows)
+            return false;
+    }
+    return true;
+}
+
 // Routed experts (moe.zig:998-1228) with the residual add: x += moe(h).
 static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, int64_t n, hipStream_t s) {
     const ditch_model_config &c = m->c;
@@ -846,6 +916,40 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     hipLaunchKernelGGL(expert_count_kernel, dim3((unsigned)std::min<int64_t>((n * k + 2047) / 2048, 64)), dim3(256), 0,
                        s, sel, n * k, counts, E);
     DITCH_TRY_HIP(hipGetLastError());
+    int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
+    float *eo = nullptr;
+    if (moe_device_plan(m, L, n)) {
+        // every expert resident and on the tiled product, no down delta:
+        // the grouped products are planned on the device
+        const int64_t P = n * k, max_blocks = (P + 15) / 16 + E, max_desc = (max_blocks + 3) / 4 + E;
+        int32_t *offsets = m->r_offsets.get<int32_t>(E);
+        int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
+        eo = m->e_out.get<float>(P * hidden);
+        std::vector<GroupSeg> tab((size_t)(3 * E));
+        for (int64_t e = 0; e < E; e++) {
+            tab[e] = GroupSeg{L.eg[e].t->v, 0, 0, nullptr, 0};
+            tab[E + e] = GroupSeg{L.eu[e].t->v, 0, 0, nullptr, 0};
+            tab[2 * E + e] = GroupSeg{L.ed[e].t->v, 0, 0, nullptr, 0};
+        }
+        GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * E);
+        DITCH_TRY_HIP(hipMemcpyAsync(dsegs, tab.data(), tab.size() * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+        int32_t *meta = m->gmeta.get<int32_t>(max_blocks * 16 + max_desc * 4 + 1);
+        const GroupedDevPlan plan{meta, meta + max_blocks * 16, meta + max_blocks * 16 + max_desc * 4, max_blocks,
+                                  max_desc};
+        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, counts, E, dsegs, 3, offsets,
+                           const_cast<int32_t *>(plan.prow), const_cast<int32_t *>(plan.desc),
+                           const_cast<int32_t *>(plan.count), max_blocks);
+        DITCH_TRY_HIP(hipGetLastError());
+        hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(LIST_WAVES * 64), 0, s, sel, n, k, offsets,
+                           pair_token, pair_of);
+        DITCH_TRY_HIP(hipGetLastError());
+        const TileView &vd = L.ed[0].t->v;
+        const int64_t ldk_d = split_k_tiles(vd);
+        void *fr = m->acts.get<uint8_t>(split_bytes_ldk(max_blocks * 16, ldk_d, 2));
+        launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, fr, ldk_d, h, hidden, pair_token,
+                                    plan, &m->xsplit, s);
+        launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s);
+    } else {
     std::vector<int32_t> hc(E), ho(E);
     DITCH_TRY_HIP(hipMemcpyAsync(hc.data(), counts, E * 4, hipMemcpyDeviceToHost, s));
     DITCH_TRY_HIP(hipStreamSynchronize(s));
@@ -859,7 +963,6 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     int32_t *offsets = m->r_offsets.get<int32_t>(E);
     DITCH_TRY_HIP(hipMemcpyAsync(offsets, ho.data(), E * 4, hipMemcpyHostToDevice, s));
     int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
-    int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
     hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(LIST_WAVES * 64), 0, s, sel, n, k, offsets, pair_token,
                        pair_of);
     DITCH_TRY_HIP(hipGetLastError());
@@ -874,7 +977,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     const bool streamed = !used.empty() && L.eg[used[0]].streamed();
     const int64_t li = &L - m->layers.data();
     float *gate = m->e_gate.get<float>(P * inter), *up = m->e_up.get<float>(P * inter);
-    float *eo = m->e_out.get<float>(P * hidden);
+    eo = m->e_out.get<float>(P * hidden);
     size_t from = 0;
     while (from < used.size()) {
         std::vector<int> slots;
@@ -956,6 +1059,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     if (streamed) {
         cache_note_layer(m, li, used);
         cache_prefetch_next(m, li);
+    }
     }
     float *esh = nullptr;
     if (L.sh_gate.ok()) {
