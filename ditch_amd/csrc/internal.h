@@ -250,7 +250,7 @@ int64_t grouped_blocks(const GroupSeg *h_segs, unsigned nseg);
 // block, segment's block end, first token within the segment), *count tile
 // rows in use; the segment table's off/cnt written on the device too.
 struct GroupedDevPlan {
-    const int32_t *prow, *desc, *count;
+    int32_t *prow, *desc, *count;
     int64_t max_blocks, max_desc;
 };
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,

@@ -936,9 +936,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         int32_t *meta = m->gmeta.get<int32_t>(max_blocks * 16 + max_desc * 4 + 1);
         const GroupedDevPlan plan{meta, meta + max_blocks * 16, meta + max_blocks * 16 + max_desc * 4, max_blocks,
                                   max_desc};
-        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, counts, E, dsegs, 3, offsets,
-                           const_cast<int32_t *>(plan.prow), const_cast<int32_t *>(plan.desc),
-                           const_cast<int32_t *>(plan.count), max_blocks);
+        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, counts, E, dsegs, 3, offsets, plan.prow,
+                           plan.desc, plan.count, max_blocks);
         DITCH_TRY_HIP(hipGetLastError());
         hipLaunchKernelGGL(expert_list_kernel, dim3((unsigned)E), dim3(LIST_WAVES * 64), 0, s, sel, n, k, offsets,
                            pair_token, pair_of);
