@@ -119,6 +119,11 @@ class Row(C.Structure):
     _fields_ = [("b", C.c_uint32), ("pos", C.c_uint32)]
 
 
+class PathStats(C.Structure):
+    """`ditch_model_path_stats`."""
+    _fields_ = [("moe_device_planned", C.c_uint64), ("moe_host_planned", C.c_uint64)]
+
+
 class ExpertCacheStats(C.Structure):
     """`ditch_expert_cache_stats` (expert_cache.Stats)."""
     _fields_ = [(n, C.c_uint64) for n in ("capacity", "slots", "resident", "hits", "misses", "prefetched",
@@ -155,10 +160,12 @@ PROTOTYPES = {
     "ditch_hip_tensor_free": (None, [P, P]),
     "ditch_hip_tensor_bytes": (U64, [P]),
     "ditch_hip_tensor_dequant": (I32, [P, P, U64, P, U64, U64]),
-    "ditch_hip_matmulT_device": (I32, [P, P, P, U64, P, P, I32, P]),
+    "ditch_hip_matmulT_device": (I32, [P, P, U64, P, U64, U64, P, P, I32, P]),
     "ditch_hip_frag_bytes": (U64, [P, U64]),
     "ditch_hip_split_device": (I32, [P, P, U64, P, U64, P, P]),
-    "ditch_hip_matmulT_frags_device": (I32, [P, P, P, U64, P, P, I32, P]),
+    "ditch_hip_glu_frag_bytes": (U64, [P, P, U64]),
+    "ditch_hip_glu_device": (I32, [P, P, U64, P, U64, U64, P, P, U32, P]),
+    "ditch_hip_matmulT_frags_device": (I32, [P, P, U64, P, U64, U64, P, P, I32, P]),
     "ditch_hip_model_create": (P, [P, P]),
     "ditch_hip_model_free": (None, [P]),
     "ditch_hip_model_set": (I32, [P, I32, I32, I32, P]),
@@ -168,11 +175,14 @@ PROTOTYPES = {
     "ditch_hip_model_reset_deltas": (I32, [P]),
     "ditch_hip_model_bytes": (U64, [P]),
     "ditch_hip_forward": (I32, [P, P, P, U64, P, U64, P, P, U64, P]),
-    "ditch_hip_forward_device": (I32, [P, P, P, U64, P, U64, P, P, U64, P]),
+    "ditch_hip_forward_device": (I32, [P, P, P, U64, U32, U32, P, U64, P, U64, P, U64, P, U64]),
+    "ditch_hip_model_path_stats": (I32, [P, P]),
     "ditch_hip_edit_delta": (I32, [P, P, P, P, P, U64, FLT]),
     "ditch_hip_model_edit": (I32, [P, I32, I32, I32, P, U64, FLT]),
     "ditch_hip_logSoftmaxRows": (I32, [P, P, P, U64, U64]),
     "ditch_hip_klRows": (I32, [P, P, P, P, U64, U64]),
+    "ditch_hip_logSoftmaxRows_device": (I32, [P, P, P, U64, U64, P]),
+    "ditch_hip_klRows_device": (I32, [P, P, P, P, U64, U64, P]),
 }
 
 

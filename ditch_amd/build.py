@@ -46,8 +46,22 @@ def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src, build_dir):
+def _stale(src, obj):
+    """The object is older than its source or any header of csrc/ or include/."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)]
+    deps += [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    inc = os.path.join(os.path.dirname(HERE), "include")
+    deps += [os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile(src, build_dir, incremental=False):
     obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -55,12 +69,14 @@ def _compile(src, build_dir):
     return obj
 
 
-def build(verbose=True):
+def build(verbose=True, incremental=False):
+    """Compiles every source (incremental=True: only those whose object is
+    older than the source or a header) and links the library."""
     build_dir = os.path.join(CSRC, "_build")
     os.makedirs(build_dir, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, build_dir), srcs))
+        objs = list(ex.map(lambda s: _compile(s, build_dir, incremental), srcs))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -74,7 +90,7 @@ def build(verbose=True):
 
 if __name__ == "__main__":
     try:
-        build()
+        build(incremental="--incremental" in sys.argv)
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

@@ -19,9 +19,9 @@ void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64
 void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight);
 void model_reset_deltas(ditch_hip_model *m);
 uint64_t model_bytes(const ditch_hip_model *m);
-void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vector<ditch_row> &rows,
-                   const ditch_row *d_rows, int64_t n, const uint64_t *d_capture, int64_t n_capture, float *d_res,
-                   const uint64_t *d_logit_rows, int64_t n_logit, float *d_logits);
+void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
+                   int64_t T, const uint64_t *d_capture, int64_t n_capture, float *d_res, const uint64_t *d_logit_rows,
+                   int64_t n_logit, float *d_logits);
 
 // Device buffer owned for the duration of one call.
 struct Tmp {
@@ -314,10 +314,13 @@ int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, uint64_t out_bytes, 
     });
 }
 
-int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x, uint64_t n, const ditch_hip_tensor *w,
-                                 const float *d_bias, int32_t accumulate, void *stream) {
+int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, uint64_t out_bytes, const float *d_x, uint64_t x_bytes,
+                                 uint64_t n, const ditch_hip_tensor *w, const float *d_bias, int32_t accumulate,
+                                 void *stream) {
     return guarded(h, [&] {
         DITCH_CHECK(w && d_out && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        DITCH_CHECK(out_bytes >= n * (uint64_t)w->v.rows * 4 && x_bytes >= n * (uint64_t)w->v.cols * 4,
+                    DITCH_INVALID_ARGUMENT, "matmulT_device: output or input buffer shorter than n rows");
         MatmulEpilogue ep;
         ep.bias = d_bias;
         ep.accumulate = accumulate;
@@ -359,15 +362,17 @@ int32_t ditch_hip_split_device(ditch_hip *h, void *d_frags, uint64_t frag_bytes,
     });
 }
 
-int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, const void *d_frags, uint64_t n,
-                                       const ditch_hip_tensor *w, const float *d_bias, int32_t accumulate,
-                                       void *stream) {
+int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, uint64_t out_bytes, const void *d_frags,
+                                       uint64_t frag_bytes, uint64_t n, const ditch_hip_tensor *w,
+                                       const float *d_bias, int32_t accumulate, void *stream) {
     return guarded(h, [&] {
         DITCH_CHECK(w && d_out && d_frags, DITCH_INVALID_ARGUMENT, "NULL argument");
         if (n == 0) return;
         const int kind = frag_kind(w->v, (int64_t)n);
         DITCH_CHECK(kind != 0, DITCH_UNSUPPORTED,
                     "matmulT_frags: the large-batch product does not take this weight or batch");
+        DITCH_CHECK(out_bytes >= n * (uint64_t)w->v.rows * 4 && frag_bytes >= ditch_hip_frag_bytes(w, n),
+                    DITCH_INVALID_ARGUMENT, "matmulT_frags: output or fragment buffer shorter than n rows");
         MatmulEpilogue ep;
         ep.bias = d_bias;
         ep.accumulate = accumulate;
@@ -379,6 +384,44 @@ int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out, const void *d
             launch_tile_gemm(w->v, d_out, w->v.rows, d_frags, split_ldk(w->v.cols), (int64_t)n, 2, ep, s,
                              pb ? h->split.get<float>(pb / sizeof(float)) : nullptr);
         }
+    });
+}
+
+// the fused gate/up pair: 1 = scaled MFMA (MX fragments in and out), 2 =
+// bf16-term tiled product, 0 = not taken
+static int glu_kind(const TileView &g, const TileView &u, int64_t n) {
+    if (mx_glu_takes(g, u, n) && g.rows % 128 == 0) return 1;
+    if (!mx_gemm_takes(g, n) && tile_glu_takes(g, u, n)) return 2;
+    return 0;
+}
+
+uint64_t ditch_hip_glu_frag_bytes(const ditch_hip_tensor *gate, const ditch_hip_tensor *up, uint64_t n) {
+    if (!gate || !up || n == 0) return 0;
+    switch (glu_kind(gate->v, up->v, (int64_t)n)) {
+    case 1: return mx_frag_bytes((int64_t)n, gate->v.rows / 128);
+    case 2: return split_bytes_ldk((int64_t)n, split_ldk(gate->v.rows), 2);
+    default: return 0;
+    }
+}
+
+int32_t ditch_hip_glu_device(ditch_hip *h, void *d_out_frags, uint64_t out_bytes, const void *d_frags,
+                             uint64_t frag_bytes, uint64_t n, const ditch_hip_tensor *gate, const ditch_hip_tensor *up,
+                             uint32_t act, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_out_frags && d_frags && gate && up, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0) return;
+        DITCH_CHECK(act <= 5, DITCH_INVALID_ARGUMENT, "unknown activation");
+        const int kind = glu_kind(gate->v, up->v, (int64_t)n);
+        DITCH_CHECK(kind != 0, DITCH_UNSUPPORTED, "glu: the fused product does not take this pair or batch");
+        DITCH_CHECK(frag_bytes >= ditch_hip_frag_bytes(gate, n) && out_bytes >= ditch_hip_glu_frag_bytes(gate, up, n),
+                    DITCH_INVALID_ARGUMENT, "glu: fragment buffers shorter than n rows");
+        hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+        const TileView &g = gate->v, &u = up->v;
+        if (kind == 1)
+            launch_mx_glu(g, u, act, nullptr, d_out_frags, g.rows / 128, d_frags, g.units_k, (int64_t)n, s);
+        else
+            launch_tile_glu(g, u, act, nullptr, d_out_frags, split_ldk(g.rows), d_frags, split_ldk(g.cols),
+                            (int64_t)n, s);
     });
 }
 
@@ -469,7 +512,11 @@ int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens, const ditc
         for (uint64_t i = 0; i < n_capture; i++) DITCH_CHECK(capture_rows[i] < n, DITCH_INVALID_ARGUMENT, "capture row");
         for (uint64_t i = 0; i < n_logit; i++) DITCH_CHECK(logit_rows[i] < n, DITCH_INVALID_ARGUMENT, "logit row");
         hipStream_t s = m->h->stream;
-        std::vector<ditch_row> hrows(rows, rows + n);
+        int64_t B = 0, T = 0;
+        for (uint64_t i = 0; i < n; i++) {
+            B = std::max<int64_t>(B, (int64_t)rows[i].b + 1);
+            T = std::max<int64_t>(T, (int64_t)rows[i].pos + 1);
+        }
         size_t res_bytes = (c.layers + 1) * n_capture * c.hidden * 4, log_bytes = n_logit * c.vocab * 4;
         Tmp dt(n * 4), dr(n * sizeof(ditch_row)), dc(n_capture * 8 + 8), dl(n_logit * 8 + 8), dres(res_bytes + 4),
             dlog(log_bytes + 4);
@@ -477,7 +524,7 @@ int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens, const ditc
         h2d(dr.p, rows, n * sizeof(ditch_row), s);
         h2d(dc.p, capture_rows, n_capture * 8, s);
         h2d(dl.p, logit_rows, n_logit * 8, s);
-        model_forward(m, dt.as<uint32_t>(), hrows, dr.as<ditch_row>(), (int64_t)n, dc.as<uint64_t>(),
+        model_forward(m, dt.as<uint32_t>(), dr.as<ditch_row>(), (int64_t)n, B, T, dc.as<uint64_t>(),
                       (int64_t)n_capture, n_capture ? dres.as<float>() : nullptr, dl.as<uint64_t>(), (int64_t)n_logit,
                       n_logit ? dlog.as<float>() : nullptr);
         d2h(residuals, dres.p, n_capture ? res_bytes : 0, s);
@@ -487,20 +534,32 @@ int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens, const ditc
 }
 
 int32_t ditch_hip_forward_device(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, uint64_t n,
-                                 const uint64_t *d_capture_rows, uint64_t n_capture, float *d_residuals,
-                                 const uint64_t *d_logit_rows, uint64_t n_logit, float *d_logits) {
+                                 uint32_t n_prompts, uint32_t max_len, const uint64_t *d_capture_rows,
+                                 uint64_t n_capture, float *d_residuals, uint64_t residuals_bytes,
+                                 const uint64_t *d_logit_rows, uint64_t n_logit, float *d_logits,
+                                 uint64_t logits_bytes) {
     if (!m) return DITCH_INVALID_ARGUMENT;
     return guarded(m->h, [&] {
         DITCH_CHECK(d_tokens && d_rows, DITCH_INVALID_ARGUMENT, "NULL tokens/rows");
         if (n == 0) return;
-        hipStream_t s = m->h->stream;
-        // the row descriptors size the KV cache: read them back once
-        std::vector<ditch_row> hrows(n);
-        d2h(hrows.data(), d_rows, n * sizeof(ditch_row), s);
-        DITCH_TRY_HIP(hipStreamSynchronize(s));
-        model_forward(m, d_tokens, hrows, d_rows, (int64_t)n, d_capture_rows, (int64_t)n_capture, d_residuals,
-                      d_logit_rows, (int64_t)n_logit, d_logits);
+        const ditch_model_config &c = m->c;
+        DITCH_CHECK(n_prompts > 0 && max_len > 0, DITCH_INVALID_ARGUMENT, "forward_device: empty KV cache shape");
+        DITCH_CHECK(n_capture == 0 || (d_capture_rows && d_residuals &&
+                                       residuals_bytes >= (c.layers + 1) * n_capture * c.hidden * 4),
+                    DITCH_INVALID_ARGUMENT, "forward_device: capture rows or residual buffer missing or too short");
+        DITCH_CHECK(n_logit == 0 || (d_logit_rows && d_logits && logits_bytes >= n_logit * c.vocab * 4),
+                    DITCH_INVALID_ARGUMENT, "forward_device: logit rows or logit buffer missing or too short");
+        model_forward(m, d_tokens, d_rows, (int64_t)n, (int64_t)n_prompts, (int64_t)max_len, d_capture_rows,
+                      (int64_t)n_capture, n_capture ? d_residuals : nullptr, d_logit_rows, (int64_t)n_logit,
+                      n_logit ? d_logits : nullptr);
     });
+}
+
+int32_t ditch_hip_model_path_stats(const ditch_hip_model *m, ditch_model_path_stats *out) {
+    if (!m || !out) return DITCH_INVALID_ARGUMENT;
+    out->moe_device_planned = m->moe_device_planned;
+    out->moe_host_planned = m->moe_host_planned;
+    return DITCH_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -538,7 +597,7 @@ int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x, uint6
         hipStream_t s = h->stream;
         Tmp dx(n * len * 4), dout(n * len * 4);
         h2d(dx.p, x, n * len * 4, s);
-        launch_log_softmax_rows(dout.as<float>(), dx.as<float>(), n, len, s);
+        launch_log_softmax_rows(dout.as<float>(), dx.as<float>(), n, len, s, &h->rowred);
         d2h(out, dout.p, n * len * 4, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
     });
@@ -553,9 +612,29 @@ int32_t ditch_hip_klRows(ditch_hip *h, double *kl, const float *base_logprobs, c
         Tmp db(n * vocab * 4), dt(n * vocab * 4), dk(n * 8);
         h2d(db.p, base_logprobs, n * vocab * 4, s);
         h2d(dt.p, trial_logits, n * vocab * 4, s);
-        launch_kl_rows(dk.as<double>(), db.as<float>(), dt.as<float>(), n, vocab, s);
+        launch_kl_rows(dk.as<double>(), db.as<float>(), dt.as<float>(), n, vocab, s, &h->rowred);
         d2h(kl, dk.p, n * 8, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int32_t ditch_hip_logSoftmaxRows_device(ditch_hip *h, float *d_out, const float *d_x, uint64_t n, uint64_t len,
+                                        void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_out && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0 || len == 0) return;
+        launch_log_softmax_rows(d_out, d_x, (int64_t)n, (int64_t)len, stream ? (hipStream_t)stream : h->stream,
+                                &h->rowred);
+    });
+}
+
+int32_t ditch_hip_klRows_device(ditch_hip *h, double *d_kl, const float *d_base_logprobs,
+                                const float *d_trial_logits, uint64_t n, uint64_t vocab, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_kl && d_base_logprobs && d_trial_logits, DITCH_INVALID_ARGUMENT, "NULL argument");
+        if (n == 0) return;
+        launch_kl_rows(d_kl, d_base_logprobs, d_trial_logits, (int64_t)n, (int64_t)vocab,
+                       stream ? (hipStream_t)stream : h->stream, &h->rowred);
     });
 }
 

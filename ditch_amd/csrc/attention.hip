@@ -89,8 +89,10 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     const int64_t h = hkv * a.groups + (head_ok ? hq : 0);
     if (threadIdx.x < 16) {
         int64_t r = r0 + threadIdx.x;
-        rb[threadIdx.x] = r < a.n ? (int32_t)a.rows[r].b : -1;
-        rp[threadIdx.x] = r < a.n ? (int32_t)a.rows[r].pos : -1;
+        // rows outside the KV cache are skipped like the padding rows
+        const bool in = r < a.n && (int64_t)a.rows[r].b < a.nb && (int64_t)a.rows[r].pos < a.T;
+        rb[threadIdx.x] = in ? (int32_t)a.rows[r].b : -1;
+        rp[threadIdx.x] = in ? (int32_t)a.rows[r].pos : -1;
     }
     if constexpr (SPLIT) {
         for (int i = lane; i < 16 * OS; i += 64) Ot[wave][i] = 0.f;

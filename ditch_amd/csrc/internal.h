@@ -148,6 +148,8 @@ struct ditch_hip {
     int cu_count = 0;
     // activation fragments of the tiled GEMM for the context's own products
     ditch::DevBuf split;
+    // per-chunk partials of the row-split log-softmax / KL
+    ditch::DevBuf rowred;
 };
 
 namespace ditch {
@@ -280,6 +282,7 @@ struct AttnArgs {
     // vd + dim; heads * vd a multiple of 128)
     void *xs;
     int64_t ldk;
+    int64_t nb;  // prompt slots of the KV cache: rows with b >= nb or pos >= T are skipped
 };
 bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups);
 void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
@@ -298,8 +301,10 @@ void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t 
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
                       int64_t len, float eps, int one_plus, hipStream_t s);
 void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
-void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s);
-void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s);
+// `tmp` holds the per-chunk partials (3 * n * chunks doubles)
+void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s, DevBuf *tmp);
+void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s,
+                    DevBuf *tmp);
 void launch_gated_act(uint32_t act, float *out, const float *gate, const float *up, int64_t n, int64_t len,
                       int64_t in_stride, int64_t out_stride, hipStream_t s);
 void launch_rope_rows(float *x, int64_t n, int64_t dim, const float *cos_t, const float *sin_t, int64_t half,

@@ -113,6 +113,9 @@ struct ditch_hip_model {
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
+    // routed layers run with the grouped products planned on the device /
+    // on the host (after reading the expert counts back), since creation
+    uint64_t moe_device_planned = 0, moe_host_planned = 0;
     ditch::ExpertCache *cache = nullptr;
     ~ditch_hip_model();
 };

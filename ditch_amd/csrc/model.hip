@@ -42,8 +42,8 @@ __global__ void capture_kernel(float *res, const float *x, const uint64_t *rows,
     int64_t total = n_capture * hidden;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         int64_t ci = i / hidden, c = i % hidden;
-        int64_t r = (int64_t)rows[ci];
-        r = r < n ? r : n - 1;
+        const uint64_t ru = rows[ci];
+        const int64_t r = ru < (uint64_t)n ? (int64_t)ru : n - 1;
         res[i] = x[r * hidden + c];
     }
 }
@@ -64,7 +64,7 @@ struct RopeArgs {
     const ditch_row *rows;
     const float *cos_t, *sin_t;
     const float *q_norm, *k_norm;
-    int64_t n, heads, kv_heads, hd, rope_off, rot, half, rope_len, T, kvd;
+    int64_t n, heads, kv_heads, hd, rope_off, rot, half, rope_len, T, kvd, nb;
     float eps;
     int style;
 };
@@ -165,6 +165,7 @@ __global__ void qk_rope_cache_kernel(RopeArgs a) {
     int64_t i = blockIdx.x;
     int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int64_t pos = a.rows[i].pos, b = a.rows[i].b;
+    if (b >= a.nb || pos >= a.T) return;  // outside the KV cache: the row is skipped
     float *kd = a.kc + (b * a.T + pos) * a.kvd, *vd = a.vc + (b * a.T + pos) * a.kvd;
     if (a.hd == 128 && a.rope_off == 0 && a.rot == 128 && a.half == 64 && a.style == DITCH_ROPE_NEOX) {
         heads_rope_128<4>(a, i, pos, kd);
@@ -196,6 +197,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     if (task >= a.n * a.heads) return;
     int64_t r = task / a.heads, h = task % a.heads;
     int64_t pos = a.rows[r].pos, b = a.rows[r].b;
+    if (b >= a.nb || pos >= a.T) return;  // outside the KV cache: the row is skipped
     int64_t kvh = h / a.groups;
     const float *q = a.q + (r * a.heads + h) * a.hd;
     for (int64_t d = lane; d < a.hd; d += 64) qs[wave][d] = q[d];
@@ -735,6 +737,48 @@ ditch_hip_model *model_create(ditch_hip *h, const ditch_model_config *cfg) {
     return m;
 }
 
+// The shape every matrix slot must have under the model's configuration
+// (the reference's Layer fields, model.zig:312-390, and MoE experts,
+// moe.zig:95-123); a mismatch is refused before anything reaches the device,
+// so no kernel is ever launched on a matrix its grid was not sized for.
+// Dense gate/up widths may differ per layer (DeepSeek's first dense layers):
+// only their hidden side is fixed here, the forward checks the three agree.
+static void check_mat_shape(const ditch_hip_model *m, int slot, const ditch_weight *w) {
+    const ditch_model_config &c = m->c;
+    const uint64_t H = c.hidden, r = w->rows, k = w->cols;
+    const uint64_t qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim, od = c.heads * c.v_head_dim;
+    auto want = [&](bool ok, const char *what) {
+        DITCH_CHECK(ok, DITCH_INVALID_ARGUMENT,
+                    std::string("model_set: ") + what + " has the wrong shape (" + std::to_string(r) + " x " +
+                        std::to_string(k) + ")");
+    };
+    switch (slot) {
+    case DITCH_SLOT_EMBED: want(k == H && r > 0, "embedding"); break;
+    case DITCH_SLOT_LM_HEAD: want(k == H && r == c.vocab, "lm_head"); break;
+    case DITCH_SLOT_Q: want(r == qd && k == H, "q_proj"); break;
+    case DITCH_SLOT_K:
+    case DITCH_SLOT_V: want(r == kvd && k == H, "k/v_proj"); break;
+    case DITCH_SLOT_O: want(r == H && k == (c.mla ? od : qd), "o_proj"); break;
+    case DITCH_SLOT_GATE:
+    case DITCH_SLOT_UP: want(k == H && r > 0, "gate/up_proj"); break;
+    case DITCH_SLOT_DOWN: want(r == H && k > 0, "down_proj"); break;
+    case DITCH_SLOT_ROUTER: want(r == c.n_experts && k == H, "router"); break;
+    case DITCH_SLOT_EXPERT_GATE:
+    case DITCH_SLOT_EXPERT_UP: want(r == c.moe_inter && k == H, "expert gate/up"); break;
+    case DITCH_SLOT_EXPERT_DOWN: want(r == H && k == c.moe_inter, "expert down"); break;
+    case DITCH_SLOT_SHARED_GATE:
+    case DITCH_SLOT_SHARED_UP: want(k == H && (c.shared_inter == 0 || r == c.shared_inter), "shared gate/up"); break;
+    case DITCH_SLOT_SHARED_DOWN: want(r == H && (c.shared_inter == 0 || k == c.shared_inter), "shared down"); break;
+    case DITCH_SLOT_MLA_Q_A: want(r == c.q_lora_rank && k == H, "q_a_proj"); break;
+    case DITCH_SLOT_MLA_Q_B: want(r == qd && k == (c.q_lora_rank ? c.q_lora_rank : H), "q_b_proj"); break;
+    case DITCH_SLOT_MLA_KV_A: want(r == c.kv_lora_rank + c.qk_rope_dim && k == H, "kv_a_proj"); break;
+    case DITCH_SLOT_MLA_KV_B:
+        want(r == c.heads * (c.qk_nope_dim + c.v_head_dim) && k == c.kv_lora_rank, "kv_b_proj");
+        break;
+    default: break;
+    }
+}
+
 void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_weight *w) {
     hipStream_t s = m->h->stream;
     if (vector_slot(slot)) {
@@ -745,6 +789,7 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
         return;
     }
     Mat *mt = mat_slot(m, layer, slot, expert);
+    check_mat_shape(m, slot, w);
     ditch_hip_tensor *t = upload_weight(m->h, w, s);
     mt->release();
     mt->t = t;
@@ -755,8 +800,19 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
     }
 }
 
+// Slots whose product the forward runs without a delta epilogue: the
+// embedding is a row lookup, and a routed expert carries a delta on its down
+// projection only (moe.zig:99-100). A delta there would have no effect, so it
+// is refused rather than dropped.
+static void check_delta_slot(int slot) {
+    DITCH_CHECK(slot != DITCH_SLOT_EMBED && slot != DITCH_SLOT_EXPERT_GATE && slot != DITCH_SLOT_EXPERT_UP,
+                DITCH_UNSUPPORTED, "a delta on the embedding or a routed expert's gate/up projection is not applied "
+                                   "by the forward");
+}
+
 void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64_t rank, const float *a,
                      const float *b) {
+    if (rank > 0) check_delta_slot(slot);
     Mat *mt = mat_slot(m, layer, slot, expert);
     DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "delta on an empty slot");
     DITCH_CHECK(rank <= 64, DITCH_UNSUPPORTED, "delta rank above 64");
@@ -775,6 +831,7 @@ void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64
 // The same edit as abliterate.computeOutputDelta (none mode): a = V^T W on
 // the device over the resident codes, b = -weight V.
 void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight) {
+    check_delta_slot(slot);
     Mat *mt = mat_slot(m, layer, slot, expert);
     DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "edit of an empty slot");
     hipStream_t s = m->h->stream;
@@ -921,6 +978,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     if (moe_device_plan(m, L, n)) {
         // every expert resident and on the tiled product, no down delta:
         // the grouped products are planned on the device
+        m->moe_device_planned++;
         const int64_t P = n * k, max_blocks = (P + 15) / 16 + E, max_desc = (max_blocks + 3) / 4 + E;
         int32_t *offsets = m->r_offsets.get<int32_t>(E);
         int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
@@ -949,6 +1007,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
                                     plan, &m->xsplit, s);
         launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s);
     } else {
+    m->moe_host_planned++;
     std::vector<int32_t> hc(E), ho(E);
     DITCH_TRY_HIP(hipMemcpyAsync(hc.data(), counts, E * 4, hipMemcpyDeviceToHost, s));
     DITCH_TRY_HIP(hipStreamSynchronize(s));
@@ -1063,6 +1122,8 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     float *esh = nullptr;
     if (L.sh_gate.ok()) {
         int64_t si = L.sh_gate.t->v.rows;
+        DITCH_CHECK(L.sh_up.ok() && L.sh_down.ok() && L.sh_up.t->v.rows == si && L.sh_down.t->v.cols == si,
+                    DITCH_INVALID_ARGUMENT, "forward: shared expert gate/up/down widths disagree");
         float *sgb = m->g.get<float>(n * si), *sub = m->u.get<float>(n * si);
         mm(m, L.sh_gate, sgb, h, n, nullptr, 0, s);
         mm(m, L.sh_up, sub, h, n, nullptr, 0, s);
@@ -1075,19 +1136,18 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     DITCH_TRY_HIP(hipGetLastError());
 }
 
-void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vector<ditch_row> &rows,
-                   const ditch_row *d_rows, int64_t n, const uint64_t *d_capture, int64_t n_capture, float *d_res,
-                   const uint64_t *d_logit_rows, int64_t n_logit, float *d_logits) {
+// `B` prompt slots of `T` positions size the KV cache (KvCache.initFor,
+// engine.zig:388-390); rows outside it are skipped by the kernels that read
+// the row descriptors.
+void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
+                   int64_t T, const uint64_t *d_capture, int64_t n_capture, float *d_res, const uint64_t *d_logit_rows,
+                   int64_t n_logit, float *d_logits) {
     const ditch_model_config &c = m->c;
     hipStream_t s = m->h->stream;
     if (n <= 0) return;
     DITCH_CHECK(m->embed.ok(), DITCH_INVALID_ARGUMENT, "forward: no embedding");
     int64_t hidden = (int64_t)c.hidden;
-    int64_t B = 0, T = 0;
-    for (auto &r : rows) {
-        B = std::max<int64_t>(B, (int64_t)r.b + 1);
-        T = std::max<int64_t>(T, (int64_t)r.pos + 1);
-    }
+    DITCH_CHECK(B > 0 && T > 0 && B <= (int64_t)INT32_MAX, DITCH_INVALID_ARGUMENT, "forward: KV cache shape");
     DITCH_CHECK(T <= ATT_MAXK, DITCH_UNSUPPORTED, "forward: positions beyond 1024 per prompt");
     int64_t nh = (int64_t)c.heads, nkv = c.mla ? nh : (int64_t)c.kv_heads, hd = (int64_t)c.head_dim;
     int64_t vd = c.mla ? (int64_t)c.v_head_dim : hd;
@@ -1177,12 +1237,13 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         ra.half = (int64_t)(c.rotary_dim / 2);
         ra.rope_len = (int64_t)c.rope_len;
         ra.T = T;
+        ra.nb = B;
         ra.kvd = kvd;
         ra.eps = c.rms_eps;
         ra.style = c.rope_style;
         hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
         DITCH_TRY_HIP(hipGetLastError());
-        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0};
+        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0, B};
         const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
         Act aact{att, nullptr, 0};
         // (the kernel's own bf16-fragment epilogue needs 34 KB more LDS a
@@ -1199,6 +1260,10 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         DITCH_TRY_HIP(hipGetLastError());
         mm_act(m, L.o, x, aact, n, nullptr, 1, s);  // x += o(att)
         const bool moe_layer = c.n_experts && m->moe_layers[li];
+        if (!moe_layer)
+            DITCH_CHECK(L.gate.ok() && L.up.ok() && L.down.ok() && L.up.t->v.rows == L.gate.t->v.rows &&
+                            L.down.t->v.cols == L.gate.t->v.rows,
+                        DITCH_INVALID_ARGUMENT, "forward: gate/up/down missing or their widths disagree");
         // MXFP4 gate/up in one scaled-MFMA product whose epilogue applies the
         // activation and writes the down projection's MX fragments
         const bool mx_glu = frags && !moe_layer && L.gate.ok() && L.up.ok() && L.gate.rank == 0 && L.up.rank == 0 &&
@@ -1232,7 +1297,7 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const std::vect
         if (moe_layer) {
             moe_forward(m, L, x, h, n, s);
         } else {
-            int64_t inter = L.gate.t ? L.gate.t->v.rows : 0;
+            int64_t inter = L.gate.t->v.rows;
             float *g = m->g.get<float>(n * inter), *u = m->u.get<float>(n * inter);
             mm(m, L.gate, g, h, n, nullptr, 0, s);
             mm(m, L.up, u, h, n, nullptr, 0, s);

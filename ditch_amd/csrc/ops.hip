@@ -68,7 +68,7 @@ __global__ void rmsnorm_kernel(float *out, const float *x, const float *w, int64
     __shared__ float sh[8];
     int64_t r = blockIdx.x;
     int64_t src = row_index ? row_index[r] : r;
-    src = src < n_src ? src : n_src - 1;
+    src = (uint64_t)src < (uint64_t)n_src ? src : n_src - 1;  // the row lists are unsigned
     const float *xr = x + src * in_stride;
     float ss = 0.f;
     for (int64_t i = threadIdx.x; i < len; i += blockDim.x) ss = __builtin_fmaf(xr[i], xr[i], ss);
@@ -344,43 +344,94 @@ __global__ void softmax_kernel(float *x, int64_t len) {
 }
 
 // log-softmax (tensor.zig:1203-1210): f32 max, f64 sum of exp, f32 x - lse.
-__global__ void log_softmax_kernel(float *out, const float *x, int64_t len) {
-    __shared__ float shf[8];
-    __shared__ double shd[8];
-    const float *xr = x + (int64_t)blockIdx.x * len;
+// log-softmax and KL over long rows (tensor.zig:1203-1210, scorers.zig:
+// 387-394), each row split into `S` chunks so that a few rows of a 128 k
+// vocabulary still spread over every CU. The arithmetic is the reference's:
+// the f32 row maximum m (exact in any order), then s = sum exp(f64(x - m))
+// in f64 with x - m taken in f32, lse = m + f32(log s), out = x - lse.
+//   pass 1  per chunk: its maximum                         -> part_m[row][S]
+//   pass 2  per chunk: m = max of the row's part_m, the chunk's f64 sum
+//                                                          -> part_s[row][S]
+//   pass 3  per chunk: s = the row's part_s added in chunk order, lse, and
+//           the chunk's outputs (log-probs, or the KL terms -> part_k)
+//   pass 4  (KL only) per row: part_k added in chunk order.
+struct RowSplit {
+    int64_t len, chunk;
+    int S;
+};
+
+__global__ __launch_bounds__(256) void rowsplit_max_kernel(float *part_m, const float *x, RowSplit rs) {
+    __shared__ float sh[8];
+    const int64_t row = blockIdx.y, c = blockIdx.x;
+    const float *xr = x + row * rs.len;
+    const int64_t i0 = c * rs.chunk, i1 = i0 + rs.chunk < rs.len ? i0 + rs.chunk : rs.len;
     float m = -INFINITY;
-    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) m = fmaxf(m, xr[i]);
-    m = block_max(m, shf);
-    double s = 0.0;
-    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) s += exp((double)__fsub_rn(xr[i], m));
-    s = block_sum_d(s, shd);
-    float lse = __fadd_rn(m, (float)log(s));
-    float *o = out + (int64_t)blockIdx.x * len;
-    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) o[i] = __fsub_rn(xr[i], lse);
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) m = fmaxf(m, xr[i]);
+    m = block_max(m, sh);
+    if (threadIdx.x == 0) part_m[row * rs.S + c] = m;
 }
 
-// KL(base || trial) per row (scorers.zig:387-394): the trial row's
-// log-softmax, then sum exp(lb) (lb - lt) in f64.
-__global__ void kl_kernel(double *kl, const float *base, const float *trial, int64_t vocab) {
-    __shared__ float shf[8];
-    __shared__ double shd[8];
-    const float *tr = trial + (int64_t)blockIdx.x * vocab;
-    const float *br = base + (int64_t)blockIdx.x * vocab;
+__device__ __forceinline__ float rowsplit_row_max(const float *part_m, int64_t row, int S) {
     float m = -INFINITY;
-    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) m = fmaxf(m, tr[i]);
-    m = block_max(m, shf);
-    double s = 0.0;
-    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) s += exp((double)__fsub_rn(tr[i], m));
-    s = block_sum_d(s, shd);
-    float lse = __fadd_rn(m, (float)log(s));
+    for (int c = 0; c < S; c++) m = fmaxf(m, part_m[row * S + c]);
+    return m;
+}
+
+__global__ __launch_bounds__(256) void rowsplit_sum_kernel(double *part_s, const float *part_m, const float *x,
+                                                           RowSplit rs) {
+    __shared__ double sh[8];
+    const int64_t row = blockIdx.y, c = blockIdx.x;
+    const float m = rowsplit_row_max(part_m, row, rs.S);
+    const float *xr = x + row * rs.len;
+    const int64_t i0 = c * rs.chunk, i1 = i0 + rs.chunk < rs.len ? i0 + rs.chunk : rs.len;
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) {
-        double lb = (double)br[i];
-        double lt = (double)__fsub_rn(tr[i], lse);
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) acc += exp((double)__fsub_rn(xr[i], m));
+    acc = block_sum_d(acc, sh);
+    if (threadIdx.x == 0) part_s[row * rs.S + c] = acc;
+}
+
+__device__ __forceinline__ float rowsplit_lse(const double *part_s, const float *part_m, int64_t row, int S) {
+    const float m = rowsplit_row_max(part_m, row, S);
+    double s = 0.0;
+    for (int c = 0; c < S; c++) s += part_s[row * S + c];
+    return __fadd_rn(m, (float)log(s));
+}
+
+__global__ __launch_bounds__(256) void rowsplit_logsoftmax_kernel(float *out, const double *part_s,
+                                                                  const float *part_m, const float *x, RowSplit rs) {
+    const int64_t row = blockIdx.y, c = blockIdx.x;
+    const float lse = rowsplit_lse(part_s, part_m, row, rs.S);
+    const float *xr = x + row * rs.len;
+    float *o = out + row * rs.len;
+    const int64_t i0 = c * rs.chunk, i1 = i0 + rs.chunk < rs.len ? i0 + rs.chunk : rs.len;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) o[i] = __fsub_rn(xr[i], lse);
+}
+
+// KL terms of one chunk: sum exp(lb) (lb - lt) in f64 with lt = t - lse
+// (scorers.zig:390-394)
+__global__ __launch_bounds__(256) void rowsplit_kl_kernel(double *part_k, const double *part_s, const float *part_m,
+                                                          const float *base, const float *trial, RowSplit rs) {
+    __shared__ double sh[8];
+    const int64_t row = blockIdx.y, c = blockIdx.x;
+    const float lse = rowsplit_lse(part_s, part_m, row, rs.S);
+    const float *tr = trial + row * rs.len, *br = base + row * rs.len;
+    const int64_t i0 = c * rs.chunk, i1 = i0 + rs.chunk < rs.len ? i0 + rs.chunk : rs.len;
+    double acc = 0.0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        const double lb = (double)br[i];
+        const double lt = (double)__fsub_rn(tr[i], lse);
         acc += exp(lb) * (lb - lt);
     }
-    acc = block_sum_d(acc, shd);
-    if (threadIdx.x == 0) kl[blockIdx.x] = acc;
+    acc = block_sum_d(acc, sh);
+    if (threadIdx.x == 0) part_k[row * rs.S + c] = acc;
+}
+
+__global__ void rowsplit_kl_total_kernel(double *kl, const double *part_k, int64_t n, int S) {
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= n) return;
+    double s = 0.0;
+    for (int c = 0; c < S; c++) s += part_k[row * S + c];
+    kl[row] = s;
 }
 
 // out[i][j] = act(gate[i][j]) * up[i][j] (tensor.zig:1296-1337)
@@ -534,14 +585,59 @@ void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s) {
     hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)n), dim3(256), 0, s, x, len);
     DITCH_TRY_HIP(hipGetLastError());
 }
-void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s) {
-    if (n <= 0) return;
-    hipLaunchKernelGGL(log_softmax_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, len);
+// Chunks per row: enough workgroups to cover the CUs about twice, chunks
+// of at least 2048 elements.
+static RowSplit row_split(int64_t n, int64_t len) {
+    int64_t S = (512 + n - 1) / n;
+    const int64_t most = (len + 2047) / 2048;
+    S = S < most ? S : most;
+    S = S < 1 ? 1 : S;
+    RowSplit rs;
+    rs.len = len;
+    rs.chunk = (len + S - 1) / S;
+    rs.S = (int)((len + rs.chunk - 1) / rs.chunk);
+    return rs;
+}
+
+// part_m [n][S] f32, part_s [n][S] f64 (and part_k [n][S] f64 for KL) in `tmp`
+static void row_split_passes(const RowSplit &rs, const float *x, int64_t n, float *&pm, double *&ps, double **pk,
+                             hipStream_t s, DevBuf *tmp) {
+    const size_t cells = (size_t)n * rs.S;
+    double *d = tmp->get<double>(3 * cells);
+    ps = d;
+    if (pk) *pk = d + cells;
+    pm = (float *)(d + 2 * cells);
+    dim3 grid((unsigned)rs.S, (unsigned)n);
+    hipLaunchKernelGGL(rowsplit_max_kernel, grid, dim3(256), 0, s, pm, x, rs);
+    DITCH_TRY_HIP(hipGetLastError());
+    hipLaunchKernelGGL(rowsplit_sum_kernel, grid, dim3(256), 0, s, ps, pm, x, rs);
     DITCH_TRY_HIP(hipGetLastError());
 }
-void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s) {
+
+void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s, DevBuf *tmp) {
+    if (n <= 0 || len <= 0) return;
+    DITCH_CHECK(n <= 65535, DITCH_UNSUPPORTED, "log-softmax: more than 65535 rows in one call");
+    const RowSplit rs = row_split(n, len);
+    float *pm;
+    double *ps;
+    row_split_passes(rs, x, n, pm, ps, nullptr, s, tmp);
+    hipLaunchKernelGGL(rowsplit_logsoftmax_kernel, dim3((unsigned)rs.S, (unsigned)n), dim3(256), 0, s, out, ps, pm, x,
+                       rs);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s,
+                    DevBuf *tmp) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(kl_kernel, dim3((unsigned)n), dim3(256), 0, s, kl, base, trial, vocab);
+    DITCH_CHECK(n <= 65535, DITCH_UNSUPPORTED, "KL: more than 65535 rows in one call");
+    DITCH_CHECK(vocab > 0, DITCH_INVALID_ARGUMENT, "KL: empty rows");
+    const RowSplit rs = row_split(n, vocab);
+    float *pm;
+    double *ps, *pk;
+    row_split_passes(rs, trial, n, pm, ps, &pk, s, tmp);
+    hipLaunchKernelGGL(rowsplit_kl_kernel, dim3((unsigned)rs.S, (unsigned)n), dim3(256), 0, s, pk, ps, pm, base, trial,
+                       rs);
+    DITCH_TRY_HIP(hipGetLastError());
+    hipLaunchKernelGGL(rowsplit_kl_total_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kl, pk, n, rs.S);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_gated_act(uint32_t act, float *out, const float *gate, const float *up, int64_t n, int64_t len,

@@ -172,6 +172,12 @@ class Device:
         self.check(self.lib.ditch_hip_klRows(self.h, _p(out), _p(b), _p(t), b.shape[0], b.shape[1]))
         return out
 
+    def logSoftmaxRows_device(self, d_out, d_x, n, length, stream=None):
+        self.check(self.lib.ditch_hip_logSoftmaxRows_device(self.h, d_out, d_x, n, length, stream))
+
+    def klRows_device(self, d_kl, d_base, d_trial, n, vocab, stream=None):
+        self.check(self.lib.ditch_hip_klRows_device(self.h, d_kl, d_base, d_trial, n, vocab, stream))
+
 
 class Tensor:
     """A weight resident in HBM (ditch_hip_upload)."""
@@ -189,8 +195,12 @@ class Tensor:
             self.dev.lib.ditch_hip_tensor_free(self.dev.h, self.handle)
             self.handle = None
 
-    def matmul_device(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None):
-        self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, d_x, n, self.handle, d_bias,
+    def matmul_device(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None, out_bytes=None,
+                      x_bytes=None):
+        """out_bytes / x_bytes: the device buffers' lengths (default: exactly n rows)."""
+        ob = n * self.rows * 4 if out_bytes is None else out_bytes
+        xb = n * self.cols * 4 if x_bytes is None else x_bytes
+        self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, ob, d_x, xb, n, self.handle, d_bias,
                                                              int(accumulate), stream))
 
     def frag_bytes(self, n):
@@ -203,10 +213,23 @@ class Tensor:
         self.dev.check(self.dev.lib.ditch_hip_split_device(self.dev.h, d_frags, frag_bytes, d_x, n, self.handle,
                                                            stream))
 
-    def matmul_frags_device(self, d_out, d_frags, n, d_bias=None, accumulate=False, stream=None):
+    def matmul_frags_device(self, d_out, d_frags, n, d_bias=None, accumulate=False, stream=None, out_bytes=None,
+                            frag_bytes=None):
         """The large-batch product on activation fragments (ditch_hip_split_device)."""
-        self.dev.check(self.dev.lib.ditch_hip_matmulT_frags_device(self.dev.h, d_out, d_frags, n, self.handle, d_bias,
-                                                                   int(accumulate), stream))
+        ob = n * self.rows * 4 if out_bytes is None else out_bytes
+        fb = self.frag_bytes(n) if frag_bytes is None else frag_bytes
+        self.dev.check(self.dev.lib.ditch_hip_matmulT_frags_device(self.dev.h, d_out, ob, d_frags, fb, n, self.handle,
+                                                                   d_bias, int(accumulate), stream))
+
+    def glu_frag_bytes(self, up, n):
+        """Bytes of the fused gate/up product's output fragments (0: not taken)."""
+        return self.dev.lib.ditch_hip_glu_frag_bytes(self.handle, up.handle, n)
+
+    def glu_device(self, up, d_out_frags, out_bytes, d_frags, frag_bytes, n, act=0, stream=None):
+        """act(x self^T) * (x up^T) on fragments split for this tensor, written
+        as the down projection's input fragments (ditch_hip_glu_device)."""
+        self.dev.check(self.dev.lib.ditch_hip_glu_device(self.dev.h, d_out_frags, out_bytes, d_frags, frag_bytes, n,
+                                                         self.handle, up.handle, act, stream))
 
     def dequant_device(self, d_out, out_bytes, row0, nrows):
         self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, out_bytes, self.handle, row0, nrows))
@@ -270,6 +293,18 @@ class Model:
             _p(logits) if lr.size else None))
         return res, logits
 
-    def forward_device(self, d_tokens, d_rows, n, d_capture, n_capture, d_res, d_logit_rows, n_logit, d_logits):
-        self.dev.check(self.dev.lib.ditch_hip_forward_device(self.h, d_tokens, d_rows, n, d_capture, n_capture,
-                                                             d_res, d_logit_rows, n_logit, d_logits))
+    def forward_device(self, d_tokens, d_rows, n, n_prompts, max_len, d_capture, n_capture, d_res, d_logit_rows,
+                       n_logit, d_logits, res_bytes=None, logit_bytes=None):
+        """Device buffers throughout; the KV cache holds n_prompts x max_len
+        positions. res_bytes / logit_bytes default to exactly the outputs' sizes."""
+        c = self.spec.config
+        rb = (c["layers"] + 1) * n_capture * c["hidden"] * 4 if res_bytes is None else res_bytes
+        lb = n_logit * c["vocab"] * 4 if logit_bytes is None else logit_bytes
+        self.dev.check(self.dev.lib.ditch_hip_forward_device(self.h, d_tokens, d_rows, n, n_prompts, max_len,
+                                                             d_capture, n_capture, d_res, rb, d_logit_rows, n_logit,
+                                                             d_logits, lb))
+
+    def path_stats(self):
+        st = abi.PathStats()
+        self.dev.check(self.dev.lib.ditch_hip_model_path_stats(self.h, ctypes.byref(st)))
+        return {name: getattr(st, name) for name, _ in st._fields_}

@@ -200,8 +200,12 @@ int32_t ditch_hip_tensor_dequant(ditch_hip *h, void *d_out, uint64_t out_bytes,
                                  uint64_t nrows);
 /* d_out[n][rows] (=|+=) d_x[n][cols] @ W^T (+ d_bias[rows]) on device
  * memory, enqueued on `stream` (NULL = the context stream), not waited for.
- * `accumulate` != 0 adds into d_out (the residual add of model.zig:4944).  */
-int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, const float *d_x,
+ * `accumulate` != 0 adds into d_out (the residual add of model.zig:4944).
+ * `out_bytes` / `x_bytes` are the buffers' lengths (the `out` and `x`
+ * slices of compute.zig:100); shorter than n * rows * 4 / n * cols * 4 is
+ * refused before anything is launched.                                     */
+int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, uint64_t out_bytes,
+                                 const float *d_x, uint64_t x_bytes,
                                  uint64_t n, const ditch_hip_tensor *w,
                                  const float *d_bias, int32_t accumulate,
                                  void *stream);
@@ -226,12 +230,31 @@ int32_t ditch_hip_split_device(ditch_hip *h, void *d_frags, uint64_t frag_bytes,
                                const ditch_hip_tensor *w, void *stream);
 /* ditch_hip_matmulT_device on fragments that ditch_hip_split_device wrote
  * for w (or for a tensor of the same format and cols). Unsupported where
- * ditch_hip_frag_bytes is 0.                                               */
+ * ditch_hip_frag_bytes is 0; buffers shorter than n * rows * 4 (out) or
+ * ditch_hip_frag_bytes(w, n) (frags) are refused.                          */
 int32_t ditch_hip_matmulT_frags_device(ditch_hip *h, float *d_out,
-                                       const void *d_frags, uint64_t n,
+                                       uint64_t out_bytes, const void *d_frags,
+                                       uint64_t frag_bytes, uint64_t n,
                                        const ditch_hip_tensor *w,
                                        const float *d_bias, int32_t accumulate,
                                        void *stream);
+
+/* The MLP block's fused first product (model.zig:4430-4486: gate and up
+ * projections, then act(gate) * up, tensor.zig:1309-1337) on activation
+ * fragments written by ditch_hip_split_device for `gate`; the result is
+ * written as the fragments a product over a gate.rows-column tensor of the
+ * same format reads (the down projection's input), never as f32 rows.
+ * `act` follows tensor.Activation (0 = silu). No reference counterpart as
+ * one call: the reference runs two matmulT and gatedActivation.
+ * ditch_hip_glu_frag_bytes: the output's bytes, 0 when the fused product
+ * does not take the pair (formats or shapes differ, n < 128).             */
+uint64_t ditch_hip_glu_frag_bytes(const ditch_hip_tensor *gate,
+                                  const ditch_hip_tensor *up, uint64_t n);
+int32_t ditch_hip_glu_device(ditch_hip *h, void *d_out_frags, uint64_t out_bytes,
+                             const void *d_frags, uint64_t frag_bytes,
+                             uint64_t n, const ditch_hip_tensor *gate,
+                             const ditch_hip_tensor *up, uint32_t act,
+                             void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Resident forward pass (model.zig:4619-4853 with ForwardOptions,
@@ -394,13 +417,36 @@ int32_t ditch_hip_forward(ditch_hip_model *m, const uint32_t *tokens,
                           float *residuals, const uint64_t *logit_rows,
                           uint64_t n_logit, float *logits);
 /* The same with every buffer in device memory, enqueued on the context
- * stream and not waited for (for callers that keep activations resident). */
+ * stream (for callers that keep activations resident). The caller sizes the
+ * KV cache as the engine does (KvCache.initFor(model, batch, max_len),
+ * engine.zig:388-390): `n_prompts` prompt slots of `max_len` positions.
+ * Nothing is read back: a dense model's call returns once its kernels are
+ * enqueued. A routed layer whose grouped products are planned on the host
+ * (streamed experts, a delta on a routed down projection, too few tokens
+ * per expert) reads its expert counts back and waits for them.
+ * The row descriptors stay on the device, so they are checked there: a row
+ * with b >= n_prompts or pos >= max_len, a token id outside the embedding
+ * or a capture/logit row >= n is clamped or skipped (no access leaves its
+ * buffer) and its outputs are unspecified. `residuals_bytes` / `logits_bytes`
+ * are the output buffers' lengths, checked against
+ * (layers+1) * n_capture * hidden * 4 and n_logit * vocab * 4.            */
 int32_t ditch_hip_forward_device(ditch_hip_model *m, const uint32_t *d_tokens,
                                  const ditch_row *d_rows, uint64_t n,
+                                 uint32_t n_prompts, uint32_t max_len,
                                  const uint64_t *d_capture_rows,
                                  uint64_t n_capture, float *d_residuals,
+                                 uint64_t residuals_bytes,
                                  const uint64_t *d_logit_rows, uint64_t n_logit,
-                                 float *d_logits);
+                                 float *d_logits, uint64_t logits_bytes);
+
+/* Which plan the routed layers took since the model was created: grouped
+ * products planned on the device (no host round trip) or on the host after
+ * reading the expert counts back. No reference counterpart (diagnostics).  */
+typedef struct ditch_model_path_stats {
+    uint64_t moe_device_planned;
+    uint64_t moe_host_planned;
+} ditch_model_path_stats;
+int32_t ditch_hip_model_path_stats(const ditch_hip_model *m, ditch_model_path_stats *out);
 
 /* ------------------------------------------------------------------------ */
 /* Rank-k edit, `none` mode (abliterate.zig:264-280): a = V^T W ([k][cols]),
@@ -422,6 +468,16 @@ int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x,
  * the baseline log-softmax rows, trial_logits raw logits.                 */
 int32_t ditch_hip_klRows(ditch_hip *h, double *kl, const float *base_logprobs,
                          const float *trial_logits, uint64_t n, uint64_t vocab);
+/* The same two on device memory, enqueued on `stream` (NULL = the context
+ * stream) and not waited for: the scorer's inputs stay in HBM after
+ * ditch_hip_forward_device. d_out may equal d_x (in place).               */
+int32_t ditch_hip_logSoftmaxRows_device(ditch_hip *h, float *d_out,
+                                        const float *d_x, uint64_t n,
+                                        uint64_t len, void *stream);
+int32_t ditch_hip_klRows_device(ditch_hip *h, double *d_kl,
+                                const float *d_base_logprobs,
+                                const float *d_trial_logits, uint64_t n,
+                                uint64_t vocab, void *stream);
 
 #ifdef __cplusplus
 }

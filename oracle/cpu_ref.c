@@ -1457,3 +1457,268 @@ int ref_forward(ref_model *m, const uint32_t *tokens, const ditch_row *rows, siz
     free(x); free(h); free(o); free(kc); free(vc);
     return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Direction pipeline (test oracle): the per-batch residual reduction of
+ * Engine.forEachResidual, the difference-of-means directions, Moments and the
+ * Nystrom sketch of multi-direction bases.                                 */
+
+static int cmp_f32(const void *a, const void *b) {
+    float x = *(const float *)a, y = *(const float *)b;
+    return (x > y) - (x < y);
+}
+
+/* quantile, engine.zig:492-499 (torch.quantile's linear interpolation, f32) */
+static float quantile_sorted(const float *s, size_t n, float q) {
+    if (n == 0) return 0;
+    float pos = q * (float)(n - 1);
+    size_t lo = (size_t)floorf(pos);
+    size_t hi = lo + 1 < n - 1 ? lo + 1 : n - 1;
+    float frac = pos - floorf(pos);
+    return s[lo] + frac * (s[hi] - s[lo]);
+}
+
+/* engine.zig:414-431 for one batch: per prompt b and entry l the mean of the
+ * prompt's `take[b]` captured rows (from capture index first[b]) by axpy with
+ * inv = 1/take, winsorised at quantile q of |v| (q outside [0,1): none),
+ * written to vout[b][l] and added to the f64 sums (Acc.add, engine.zig:
+ * 320-326) and, when sq is given, Moments.add (directions.zig:196-205).     */
+int ref_residual_reduce(const float *res, size_t entries, size_t n_capture, size_t hidden, const uint32_t *first,
+                        const uint32_t *take, size_t prompts, float q, float *vout, double *sum, double *sq) {
+    float *sorted = (q >= 0 && q < 1) ? (float *)malloc(hidden * sizeof(float)) : NULL;
+    for (size_t b = 0; b < prompts; b++) {
+        size_t t_n = take[b];
+        float inv = 1.0f / (float)(t_n > 1 ? t_n : 1);
+        for (size_t l = 0; l < entries; l++) {
+            float *v = vout + (b * entries + l) * hidden;
+            memset(v, 0, hidden * sizeof(float));
+            for (size_t t = 0; t < t_n; t++)
+                axpy(v, inv, res + (l * n_capture + first[b] + t) * hidden, hidden);
+            if (sorted) {
+                for (size_t i = 0; i < hidden; i++) sorted[i] = fabsf(v[i]);
+                qsort(sorted, hidden, sizeof(float), cmp_f32);
+                float thr = quantile_sorted(sorted, hidden, q);
+                for (size_t i = 0; i < hidden; i++) v[i] = fmaxf(-thr, fminf(v[i], thr));
+            }
+            if (sum)
+                for (size_t i = 0; i < hidden; i++) sum[l * hidden + i] += v[i];
+            if (sq)
+                for (size_t i = 0; i < hidden; i++) sq[l * hidden + i] += (double)v[i] * (double)v[i];
+        }
+    }
+    free(sorted);
+    return 0;
+}
+
+/* tensor.normalize (tensor.zig:580-584) */
+static void normalize_f32(float *x, size_t n) {
+    float nrm = sqrtf(ref_dot(x, x, n));
+    if (nrm > 1e-12f) {
+        float s = 1.0f / nrm;
+        for (size_t i = 0; i < n; i++) x[i] *= s;
+    }
+}
+
+/* abliterate.computeDirections (abliterate.zig:88-109) */
+void ref_directions(float *dirs, const float *good, const float *bad, size_t entries, size_t hidden,
+                    int orthogonalize) {
+    float *gd = (float *)malloc(hidden * sizeof(float));
+    for (size_t e = 0; e < entries; e++) {
+        float *d = dirs + e * hidden;
+        const float *g = good + e * hidden, *b = bad + e * hidden;
+        for (size_t i = 0; i < hidden; i++) d[i] = b[i] - g[i];
+        normalize_f32(d, hidden);
+        if (orthogonalize) {
+            memcpy(gd, g, hidden * sizeof(float));
+            normalize_f32(gd, hidden);
+            float p = ref_dot(d, gd, hidden);
+            axpy(d, -p, gd, hidden);
+            normalize_f32(d, hidden);
+        }
+    }
+    free(gd);
+}
+
+/* abliterate.orthonormalize (abliterate.zig:409-423): modified Gram-Schmidt,
+ * two passes, rows normalised (or zeroed below 1e-20). */
+void ref_orthonormalize(float *vecs, size_t q, size_t n) {
+    for (size_t i = 0; i < q; i++) {
+        float *vi = vecs + i * n;
+        for (int pass = 0; pass < 2; pass++)
+            for (size_t j = 0; j < i; j++) {
+                const float *vj = vecs + j * n;
+                float p = ref_dot(vi, vj, n);
+                axpy(vi, -p, vj, n);
+            }
+        float nrm = sqrtf(ref_dot(vi, vi, n));
+        if (nrm > 1e-20f) {
+            float s = 1.0f / nrm;
+            for (size_t k = 0; k < n; k++) vi[k] *= s;
+        } else {
+            memset(vi, 0, n * sizeof(float));
+        }
+    }
+}
+
+/* directions.Sketch.add (directions.zig:80-104) for prompts x entries
+ * residuals v[b][e][hidden] in prompt order: z = r - center, p = Omega^T z,
+ * Y[e] += z p^T ([m][hidden]), W[e] += p p^T ([m][m]), all f64.           */
+void ref_sketch_add(double *y, double *w, const float *omega, size_t m, const float *center, const float *v,
+                    size_t prompts, size_t entries, size_t hidden) {
+    double *z = (double *)malloc(hidden * sizeof(double));
+    double *p = (double *)malloc(m * sizeof(double));
+    for (size_t b = 0; b < prompts; b++)
+        for (size_t e = 0; e < entries; e++) {
+            const float *r = v + (b * entries + e) * hidden;
+            const float *c = center + e * hidden;
+            for (size_t i = 0; i < hidden; i++) z[i] = (double)r[i] - (double)c[i];
+            for (size_t j = 0; j < m; j++) {
+                double acc = 0;
+                for (size_t i = 0; i < hidden; i++) acc += z[i] * (double)omega[j * hidden + i];
+                p[j] = acc;
+            }
+            double *ye = y + e * m * hidden, *we = w + e * m * m;
+            for (size_t j = 0; j < m; j++)
+                for (size_t i = 0; i < hidden; i++) ye[j * hidden + i] += z[i] * p[j];
+            for (size_t j = 0; j < m; j++)
+                for (size_t l = 0; l < m; l++) we[j * m + l] += p[j] * p[l];
+        }
+    free(z);
+    free(p);
+}
+
+static double sign_f64(double x) { return x > 0 ? 1.0 : x < 0 ? -1.0 : 0.0; }
+
+/* directions.symmetricEigen (directions.zig:463-500): cyclic Jacobi in f64,
+ * m overwritten by its diagonalisation, eigenvectors in the columns of vecs. */
+void ref_symmetric_eigen(double *m, double *vecs, size_t n) {
+    memset(vecs, 0, n * n * sizeof(double));
+    for (size_t i = 0; i < n; i++) vecs[i * n + i] = 1;
+    for (int sweep = 0; sweep < 60; sweep++) {
+        double off = 0, diag = 0;
+        for (size_t i = 0; i < n; i++)
+            for (size_t j = 0; j < n; j++) {
+                if (i != j) off += m[i * n + j] * m[i * n + j];
+                else diag += m[i * n + j] * m[i * n + j];
+            }
+        if (off <= 1e-24 * (diag > 1e-300 ? diag : 1e-300)) break;
+        for (size_t p = 0; p < n; p++)
+            for (size_t q = p + 1; q < n; q++) {
+                double apq = m[p * n + q];
+                if (fabs(apq) < 1e-300) continue;
+                double theta = (m[q * n + q] - m[p * n + p]) / (2.0 * apq);
+                double t = theta == 0 ? 1.0 : sign_f64(theta) / (fabs(theta) + sqrt(theta * theta + 1.0));
+                double cs = 1.0 / sqrt(t * t + 1.0), sn = t * cs;
+                for (size_t k = 0; k < n; k++) {
+                    double akp = m[k * n + p], akq = m[k * n + q];
+                    m[k * n + p] = cs * akp - sn * akq;
+                    m[k * n + q] = sn * akp + cs * akq;
+                }
+                for (size_t k = 0; k < n; k++) {
+                    double apk = m[p * n + k], aqk = m[q * n + k];
+                    m[p * n + k] = cs * apk - sn * aqk;
+                    m[q * n + k] = sn * apk + cs * aqk;
+                }
+                for (size_t k = 0; k < n; k++) {
+                    double vkp = vecs[k * n + p], vkq = vecs[k * n + q];
+                    vecs[k * n + p] = cs * vkp - sn * vkq;
+                    vecs[k * n + q] = sn * vkp + cs * vkq;
+                }
+            }
+    }
+}
+
+static void remove_f64(double *col, const float *unit, size_t n) {
+    double p = 0;
+    for (size_t i = 0; i < n; i++) p += col[i] * unit[i];
+    for (size_t i = 0; i < n; i++) col[i] -= p * unit[i];
+}
+
+/* Sketch.factor (directions.zig:108-134) then directions.computeBasisFrom
+ * (directions.zig:371-455): dirs [entries][k][hidden] from the first
+ * directions, the good means and the sketch (y [entries][m][hidden], w
+ * [entries][m][m]).                                                        */
+int ref_basis(float *dirs, const float *first, const float *good_means, size_t entries, size_t hidden, size_t k,
+              int orthogonalize, const double *y, const double *w, size_t m) {
+    memset(dirs, 0, entries * k * hidden * sizeof(float));
+    if (k == 1) {
+        memcpy(dirs, first, entries * hidden * sizeof(float));
+        return 0;
+    }
+    double *wm = (double *)malloc(m * m * sizeof(double)), *vecs = (double *)malloc(m * m * sizeof(double));
+    double *bf = (double *)malloc(m * hidden * sizeof(double));
+    double *gram = (double *)malloc(m * m * sizeof(double)), *gv = (double *)malloc(m * m * sizeof(double));
+    float *gd = (float *)malloc(hidden * sizeof(float));
+    size_t *order = (size_t *)malloc(m * sizeof(size_t));
+    for (size_t e = 0; e < entries; e++) {
+        float *basis = dirs + e * k * hidden;
+        memcpy(basis, first + e * hidden, hidden * sizeof(float));
+        memcpy(gd, good_means + e * hidden, hidden * sizeof(float));
+        normalize_f32(gd, hidden);
+        /* factor */
+        memcpy(wm, w + e * m * m, m * m * sizeof(double));
+        ref_symmetric_eigen(wm, vecs, m);
+        double max_ev = 0;
+        for (size_t j = 0; j < m; j++) max_ev = wm[j * m + j] > max_ev ? wm[j * m + j] : max_ev;
+        const double *ye = y + e * m * hidden;
+        size_t r = 0;
+        for (size_t j = 0; j < m; j++) {
+            double ev = wm[j * m + j];
+            if (ev <= max_ev * 1e-9 || ev <= 0) continue;
+            double s = 1.0 / sqrt(ev);
+            double *col = bf + r * hidden;
+            memset(col, 0, hidden * sizeof(double));
+            for (size_t l = 0; l < m; l++) {
+                double coef = vecs[l * m + j] * s;
+                if (coef == 0) continue;
+                for (size_t i = 0; i < hidden; i++) col[i] += coef * ye[l * hidden + i];
+            }
+            r++;
+        }
+        for (size_t c = 0; c < r; c++) {
+            remove_f64(bf + c * hidden, basis, hidden);
+            if (orthogonalize) remove_f64(bf + c * hidden, gd, hidden);
+        }
+        for (size_t i = 0; i < r; i++)
+            for (size_t j = 0; j < r; j++) {
+                double acc = 0;
+                for (size_t t = 0; t < hidden; t++) acc += bf[i * hidden + t] * bf[j * hidden + t];
+                gram[i * r + j] = acc;
+            }
+        ref_symmetric_eigen(gram, gv, r);
+        /* order by descending eigenvalue, ties in index order (a stable sort) */
+        for (size_t i = 0; i < r; i++) order[i] = i;
+        for (size_t i = 1; i < r; i++) {
+            size_t o = order[i], j = i;
+            while (j > 0 && gram[order[j - 1] * r + order[j - 1]] < gram[o * r + o]) {
+                order[j] = order[j - 1];
+                j--;
+            }
+            order[j] = o;
+        }
+        for (size_t d = 1; d < k; d++) {
+            float *dir = basis + d * hidden;
+            memset(dir, 0, hidden * sizeof(float));
+            if (d - 1 >= r) continue;
+            size_t src = order[d - 1];
+            double lambda = gram[src * r + src];
+            if (lambda <= 0) continue;
+            for (size_t c = 0; c < r; c++) {
+                float coef = (float)(gv[c * r + src] / sqrt(lambda));
+                const double *col = bf + c * hidden;
+                for (size_t i = 0; i < hidden; i++) dir[i] = dir[i] + coef * (float)col[i];
+            }
+        }
+        ref_orthonormalize(basis, k, hidden);
+        if (e > 0) {
+            const float *prev = dirs + (e - 1) * k * hidden;
+            for (size_t d = 1; d < k; d++) {
+                float *dir = basis + d * hidden;
+                if (ref_dot(dir, prev + d * hidden, hidden) < 0)
+                    for (size_t i = 0; i < hidden; i++) dir[i] *= -1.0f;
+            }
+        }
+    }
+    free(wm); free(vecs); free(bf); free(gram); free(gv); free(gd); free(order);
+    return 0;
+}

@@ -92,6 +92,20 @@ double ref_kl_row(const float *base_logprobs, const float *trial_logits,
 int ref_edit_delta(float *a, float *b, const ditch_weight *w, const float *v,
                    size_t k, float weight, int threads);
 
+/* direction pipeline: engine.zig:414-431 (window mean, winsorising, f64
+ * sums), directions.zig:196-205 (Moments), abliterate.zig:88-109, 409-423,
+ * directions.zig:80-134, 371-500 (Sketch, computeBasisFrom)               */
+int ref_residual_reduce(const float *res, size_t entries, size_t n_capture, size_t hidden, const uint32_t *first,
+                        const uint32_t *take, size_t prompts, float q, float *vout, double *sum, double *sq);
+void ref_directions(float *dirs, const float *good, const float *bad, size_t entries, size_t hidden,
+                    int orthogonalize);
+void ref_orthonormalize(float *vecs, size_t q, size_t n);
+void ref_sketch_add(double *y, double *w, const float *omega, size_t m, const float *center, const float *v,
+                    size_t prompts, size_t entries, size_t hidden);
+void ref_symmetric_eigen(double *m, double *vecs, size_t n);
+int ref_basis(float *dirs, const float *first, const float *good_means, size_t entries, size_t hidden, size_t k,
+              int orthogonalize, const double *y, const double *w, size_t m);
+
 /* model (model.zig:4619-4959, moe.zig:998-1228, model.zig:3292-3342) */
 typedef struct ref_model ref_model;
 ref_model *ref_model_create(const ditch_model_config *cfg);
