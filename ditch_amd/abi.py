@@ -161,6 +161,8 @@ PROTOTYPES = {
     "ditch_hip_tensor_bytes": (U64, [P]),
     "ditch_hip_tensor_dequant": (I32, [P, P, U64, P, U64, U64]),
     "ditch_hip_matmulT_device": (I32, [P, P, U64, P, U64, U64, P, P, I32, P]),
+    "ditch_hip_matmulT_device_noalloc": (I32, [P, P, U64, P, U64, U64, P, P, I32, P]),
+    "ditch_hip_static_scratch_bytes": (U64, []),
     "ditch_hip_frag_bytes": (U64, [P, U64]),
     "ditch_hip_split_device": (I32, [P, P, U64, P, U64, P, P]),
     "ditch_hip_glu_frag_bytes": (U64, [P, P, U64]),

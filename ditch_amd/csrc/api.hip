@@ -63,6 +63,14 @@ static int32_t guarded(ditch_hip *h, F &&f) {
 
 using namespace ditch;
 
+// The allocation-free product's scratch: activation fragments, GEMV term
+// staging and split-K partial sums of ditch_hip_matmulT_device_noalloc.
+// Each GPU the library runs on holds its own copy for the life of the
+// process. Host code never uses this name as an address: the context keeps
+// the device's copy from hipGetSymbolAddress (h->static_scratch).
+static constexpr size_t STATIC_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
 extern "C" {
 
 ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
@@ -89,6 +97,14 @@ ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");
+    }
+    // this device's copy of the static scratch array (device `device` is
+    // current); on failure only the allocation-free entry point is refused
+    const hipError_t se = hipGetSymbolAddress(&h->static_scratch, HIP_SYMBOL(scratch));
+    if (se != hipSuccess) {
+        h->static_scratch = nullptr;
+        h->scratch_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se);
+        (void)hipGetLastError();
     }
     return h;
 }
@@ -327,6 +343,24 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, uint64_t out_bytes,
         launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream, nullptr, &h->split);
     });
 }
+
+int32_t ditch_hip_matmulT_device_noalloc(ditch_hip *h, float *d_out, uint64_t out_bytes, const float *d_x,
+                                         uint64_t x_bytes, uint64_t n, const ditch_hip_tensor *w, const float *d_bias,
+                                         int32_t accumulate, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(w && d_out && d_x, DITCH_INVALID_ARGUMENT, "NULL argument");
+        DITCH_CHECK(out_bytes >= n * (uint64_t)w->v.rows * 4 && x_bytes >= n * (uint64_t)w->v.cols * 4,
+                    DITCH_INVALID_ARGUMENT, "matmulT_device_noalloc: output or input buffer shorter than n rows");
+        DITCH_CHECK(h->static_scratch, DITCH_DEVICE_FAILED, "static scratch not resolved: " + h->scratch_error);
+        MatmulEpilogue ep;
+        ep.bias = d_bias;
+        ep.accumulate = accumulate;
+        DevBuf ws(h->static_scratch, STATIC_SCRATCH_BYTES);  // never allocates: too large a need is refused
+        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream, nullptr, &ws);
+    });
+}
+
+uint64_t ditch_hip_static_scratch_bytes(void) { return STATIC_SCRATCH_BYTES; }
 
 // fragment layout of the large-batch product over w: 2 = bf16 terms, 1 = MX
 // fp6 terms, 0 = none

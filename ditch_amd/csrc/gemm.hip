@@ -144,7 +144,11 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     if (ws && tile_gemm_takes(w, n)) {
         const int xt = ep.exact ? 3 : 2;
         const int64_t ldk = split_k_tiles(w);
-        const size_t xb = (split_bytes_ldk(n, ldk, xt) + 255) & ~(size_t)255, pb = tile_part_bytes(w, n, xt);
+        const size_t xb = (split_bytes_ldk(n, ldk, xt) + 255) & ~(size_t)255;
+        size_t pb = tile_part_bytes(w, n, xt);
+        // a borrowed scratch too small for the split-K partial sums: the
+        // product runs unsplit (the same sums, added in one pass)
+        if (ws->borrowed && xb + pb > ws->bytes) pb = 0;
         uint8_t *xs = ws->get<uint8_t>(xb + pb);
         launch_split(xs, x, row_index, n, w.cols, w.cols, ldk, xt, s);
         launch_tile_gemm(w, out, w.rows, xs, ldk, n, xt, ep, s, pb ? (float *)(xs + xb) : nullptr);

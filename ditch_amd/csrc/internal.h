@@ -103,14 +103,28 @@ void *dev_alloc(size_t bytes);
 void dev_free(void *p);
 
 // A device buffer that grows on demand (contents are not kept on growth).
+// A borrowed buffer wraps memory owned elsewhere (the library's static
+// scratch array): it never allocates, grows or frees, and a request beyond
+// its size is refused before anything is launched on it.
 struct DevBuf {
     void *p = nullptr;
     size_t bytes = 0;
-    ~DevBuf() { dev_free(p); }
+    bool borrowed = false;
+    DevBuf() = default;
+    DevBuf(void *mem, size_t cap) : p(mem), bytes(cap), borrowed(true) {}
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    ~DevBuf() {
+        if (!borrowed) dev_free(p);
+    }
     template <typename T>
     T *get(size_t count) {
         size_t need = count * sizeof(T);
         if (need > bytes) {
+            if (borrowed)
+                throw Error{DITCH_INVALID_ARGUMENT, "scratch: the call needs " + std::to_string(need) +
+                                                        " bytes of scratch, the static scratch holds " +
+                                                        std::to_string(bytes)};
             dev_free(p);
             p = nullptr;
             bytes = 0;
@@ -150,6 +164,10 @@ struct ditch_hip {
     ditch::DevBuf split;
     // per-chunk partials of the row-split log-softmax / KL
     ditch::DevBuf rowred;
+    // this device's copy of the static scratch array (api.hip), resolved
+    // with hipGetSymbolAddress when the context opens
+    void *static_scratch = nullptr;
+    std::string scratch_error;
 };
 
 namespace ditch {

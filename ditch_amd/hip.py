@@ -203,6 +203,15 @@ class Tensor:
         self.dev.check(self.dev.lib.ditch_hip_matmulT_device(self.dev.h, d_out, ob, d_x, xb, n, self.handle, d_bias,
                                                              int(accumulate), stream))
 
+    def matmul_device_noalloc(self, d_out, d_x, n, d_bias=None, accumulate=False, stream=None, out_bytes=None,
+                              x_bytes=None):
+        """matmul_device with its scratch in the library's static array
+        (ditch_hip_matmulT_device_noalloc): allocates no device memory."""
+        ob = n * self.rows * 4 if out_bytes is None else out_bytes
+        xb = n * self.cols * 4 if x_bytes is None else x_bytes
+        self.dev.check(self.dev.lib.ditch_hip_matmulT_device_noalloc(self.dev.h, d_out, ob, d_x, xb, n, self.handle,
+                                                                     d_bias, int(accumulate), stream))
+
     def frag_bytes(self, n):
         """Bytes of the activation fragments of n rows for products over this
         tensor (0: the large-batch product does not take it)."""

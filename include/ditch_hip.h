@@ -210,6 +210,24 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, uint64_t out_bytes,
                                  const float *d_bias, int32_t accumulate,
                                  void *stream);
 
+/* ditch_hip_matmulT_device for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The same kernels, with their
+ * scratch (activation fragments, GEMV staging, split-K partial sums) in a
+ * static device array of ditch_hip_static_scratch_bytes() (64 MiB) that
+ * each GPU holds for the life of the process: the call allocates nothing.
+ * A call needing more scratch than that is refused (InvalidArgument) before
+ * anything is launched; when only the split-K partial sums do not fit, the
+ * product runs unsplit. Every call on one GPU shares that GPU's array, so
+ * calls that overlap on one GPU (different streams) race: serialise them. */
+int32_t ditch_hip_matmulT_device_noalloc(ditch_hip *h, float *d_out,
+                                         uint64_t out_bytes, const float *d_x,
+                                         uint64_t x_bytes, uint64_t n,
+                                         const ditch_hip_tensor *w,
+                                         const float *d_bias,
+                                         int32_t accumulate, void *stream);
+uint64_t ditch_hip_static_scratch_bytes(void);
+
 /* Activation fragments: the activations already in the layout the
  * large-batch product over a given tensor reads, for callers that multiply
  * the same activations by several tensors or keep them resident (the

@@ -1,0 +1,83 @@
+"""ditch_hip_matmulT_device_noalloc (scratch in the library's static device
+array, no allocation) against ditch_hip_matmulT_device on the same inputs:
+two calls in a row, the second smaller, over the product's paths (GEMV with
+and without term staging, the generic GEMM, the tiled product with split-K,
+the scaled-MFMA product, and a product whose split-K partial sums do not fit
+the scratch, which then runs unsplit). The bar is the product tolerance of
+the VTable products (abs 1e-4, rel 1e-3 of the output scale); where the two
+calls pick the same kernels the outputs are identical."""
+import numpy as np
+import pytest
+import torch
+
+from ditch_amd import hipmem, synth
+from ditch_amd.hip import DeviceError
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    # name: (format, rows, cols, n first call, n second call, identical)
+    "gemv_bf16": ("bf16", 1000, 2048, 12, 3, True),
+    "gemm_fp8": ("fp8", 520, 1024, 24, 17, True),
+    "tiled_splitk_fp8": ("fp8", 4096, 4096, 64, 48, True),
+    "mx_mxfp4": ("mxfp4", 2048, 4096, 256, 160, True),
+    "tiled_int4": ("int4", 1536, 2048, 200, 33, True),
+    "unsplit_q8_0": ("q8_0", 14336, 4096, 256, 128, False),
+}
+
+
+def _weight(fmt, rows, cols, seed):
+    gen = torch.Generator().manual_seed(seed)
+    if fmt == "q8_0":
+        return synth.q8_0_random(rows, cols, gen)
+    return synth.QUANTIZERS[fmt](torch.randn(rows, cols, generator=gen) * 0.02)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_noalloc_matches_matmul_device(dev, name):
+    fmt, rows, cols, n1, n2, identical = CASES[name]
+    t = dev.upload(_weight(fmt, rows, cols, len(name)))
+    try:
+        rng = np.random.default_rng(len(name) + 1)
+        bias = hipmem.Buffer.from_array(rng.standard_normal(rows).astype(np.float32))
+        for n in (n1, n2):
+            x = rng.standard_normal((n, cols)).astype(np.float32)
+            bx = hipmem.Buffer.from_array(x)
+            o1, o2 = hipmem.Buffer(n * rows * 4), hipmem.Buffer(n * rows * 4)
+            init = rng.standard_normal((n, rows)).astype(np.float32)
+            o1.upload(init)
+            o2.upload(init)
+            t.matmul_device(o1.ptr, bx.ptr, n, d_bias=bias.ptr, accumulate=True)
+            t.matmul_device_noalloc(o2.ptr, bx.ptr, n, d_bias=bias.ptr, accumulate=True)
+            dev.sync()
+            a = o1.download(np.float32, (n, rows))
+            b = o2.download(np.float32, (n, rows))
+            if identical:
+                np.testing.assert_array_equal(b, a)
+            else:
+                # the same sums in another order: f32 rounding only
+                assert np.abs(b - a).max() <= 1e-4 * max(1.0, float(np.abs(a).max())), name
+    finally:
+        t.free()
+
+
+def test_noalloc_refuses_more_than_the_scratch(dev):
+    """A batch whose activation fragments alone exceed the static scratch is
+    refused before any launch; the next call still works."""
+    cap = dev.lib.ditch_hip_static_scratch_bytes()
+    assert cap == 64 << 20
+    rows, cols = 256, 4096
+    t = dev.upload(_weight("bf16", rows, cols, 3))
+    try:
+        n = 8192  # two bf16 terms of 8192 x 4096: 128 MiB of fragments
+        bx, bo = hipmem.Buffer(n * cols * 4), hipmem.Buffer(n * rows * 4)
+        with pytest.raises(DeviceError, match="static scratch holds"):
+            t.matmul_device_noalloc(bo.ptr, bx.ptr, n)
+        x = np.random.default_rng(4).standard_normal((40, cols)).astype(np.float32)
+        bx2, o1, o2 = hipmem.Buffer.from_array(x), hipmem.Buffer(40 * rows * 4), hipmem.Buffer(40 * rows * 4)
+        t.matmul_device(o1.ptr, bx2.ptr, 40)
+        t.matmul_device_noalloc(o2.ptr, bx2.ptr, 40)
+        dev.sync()
+        np.testing.assert_array_equal(o2.download(np.float32, (40, rows)), o1.download(np.float32, (40, rows)))
+    finally:
+        t.free()
