@@ -184,6 +184,11 @@ PROTOTYPES = {
     "ditch_hip_logSoftmaxRows": (I32, [P, P, P, U64, U64]),
     "ditch_hip_klRows": (I32, [P, P, P, P, U64, U64]),
     "ditch_hip_logSoftmaxRows_device": (I32, [P, P, P, U64, U64, P]),
+    "ditch_hip_residual_reduce_device": (I32, [P, P, U64, U64, U64, P, P, U64, FLT, P, P, P, P]),
+    "ditch_hip_residual_mean_device": (I32, [P, P, P, U64, U64, P]),
+    "ditch_hip_directions_device": (I32, [P, P, P, P, U64, U64, I32, P]),
+    "ditch_hip_sketch_add_device": (I32, [P, P, P, P, U64, P, P, U64, U64, U64, P]),
+    "ditch_hip_basis_device": (I32, [P, P, P, P, U64, U64, U64, I32, P, P, U64, P]),
     "ditch_hip_klRows_device": (I32, [P, P, P, P, U64, U64, P]),
 }
 

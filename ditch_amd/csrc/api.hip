@@ -672,4 +672,62 @@ int32_t ditch_hip_klRows_device(ditch_hip *h, double *d_kl, const float *d_base_
     });
 }
 
+// ---------------------------------------------------------------------------
+// Direction pipeline
+
+static hipStream_t pick(ditch_hip *h, void *stream) { return stream ? (hipStream_t)stream : h->stream; }
+
+int32_t ditch_hip_residual_reduce_device(ditch_hip *h, const float *d_residuals, uint64_t entries, uint64_t n_capture,
+                                         uint64_t hidden, const uint32_t *d_first, const uint32_t *d_take,
+                                         uint64_t prompts, float winsor_q, float *d_vout, double *d_sum, double *d_sq,
+                                         void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_residuals && d_first && d_take && d_vout, DITCH_INVALID_ARGUMENT, "NULL argument");
+        launch_residual_reduce(d_residuals, (int64_t)entries, (int64_t)n_capture, (int64_t)hidden, d_first, d_take,
+                               (int64_t)prompts, winsor_q, d_vout, d_sum, d_sq, pick(h, stream));
+    });
+}
+
+int32_t ditch_hip_residual_mean_device(ditch_hip *h, float *d_mean, const double *d_sum, uint64_t count, uint64_t n,
+                                       void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_mean && d_sum, DITCH_INVALID_ARGUMENT, "NULL argument");
+        launch_residual_mean(d_mean, d_sum, count, (int64_t)n, pick(h, stream));
+    });
+}
+
+int32_t ditch_hip_directions_device(ditch_hip *h, float *d_dirs, const float *d_good_means, const float *d_bad_means,
+                                    uint64_t entries, uint64_t hidden, int32_t orthogonalize, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_dirs && d_good_means && d_bad_means, DITCH_INVALID_ARGUMENT, "NULL argument");
+        DITCH_CHECK(entries <= 65535, DITCH_UNSUPPORTED, "directions: more than 65535 entries");
+        launch_directions(d_dirs, d_good_means, d_bad_means, (int64_t)entries, (int64_t)hidden, orthogonalize,
+                          pick(h, stream), &h->dirtmp);
+    });
+}
+
+int32_t ditch_hip_sketch_add_device(ditch_hip *h, double *d_y, double *d_w, const float *d_omega, uint64_t m,
+                                    const float *d_center, const float *d_v, uint64_t prompts, uint64_t entries,
+                                    uint64_t hidden, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_y && d_w && d_omega && d_center && d_v, DITCH_INVALID_ARGUMENT, "NULL argument");
+        DITCH_CHECK(prompts <= 65535 && entries <= 65535, DITCH_UNSUPPORTED, "sketch: grid");
+        launch_sketch_add(d_y, d_w, d_omega, (int64_t)m, d_center, d_v, (int64_t)prompts, (int64_t)entries,
+                          (int64_t)hidden, pick(h, stream), &h->dirtmp);
+    });
+}
+
+int32_t ditch_hip_basis_device(ditch_hip *h, float *d_dirs, const float *d_first, const float *d_good_means,
+                               uint64_t entries, uint64_t hidden, uint64_t k, int32_t orthogonalize, const double *d_y,
+                               const double *d_w, uint64_t m, void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_dirs && d_first && d_good_means && (k <= 1 || (d_y && d_w)), DITCH_INVALID_ARGUMENT,
+                    "NULL argument");
+        DITCH_CHECK(k >= 1 && k <= 8, DITCH_UNSUPPORTED, "basis: 1 to 8 directions");
+        DITCH_CHECK(entries <= 65535, DITCH_UNSUPPORTED, "basis: more than 65535 entries");
+        launch_basis(d_dirs, d_first, d_good_means, (int64_t)entries, (int64_t)hidden, (int64_t)k, orthogonalize, d_y,
+                     d_w, (int64_t)m, pick(h, stream), &h->dirtmp);
+    });
+}
+
 }  // extern "C"

@@ -164,6 +164,8 @@ struct ditch_hip {
     ditch::DevBuf split;
     // per-chunk partials of the row-split log-softmax / KL
     ditch::DevBuf rowred;
+    // scratch of the direction pipeline (projections, basis columns)
+    ditch::DevBuf dirtmp;
     // this device's copy of the static scratch array (api.hip), resolved
     // with hipGetSymbolAddress when the context opens
     void *static_scratch = nullptr;
@@ -319,6 +321,18 @@ void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t 
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
                       int64_t len, float eps, int one_plus, hipStream_t s);
 void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
+// directions.hip
+void launch_residual_reduce(const float *res, int64_t entries, int64_t n_capture, int64_t hidden,
+                            const uint32_t *first, const uint32_t *take, int64_t prompts, float q, float *vout,
+                            double *sum, double *sq, hipStream_t s);
+void launch_residual_mean(float *mean, const double *sum, uint64_t count, int64_t n, hipStream_t s);
+void launch_directions(float *dirs, const float *good, const float *bad, int64_t entries, int64_t hidden,
+                       int orthogonalize, hipStream_t s, DevBuf *tmp);
+void launch_sketch_add(double *y, double *w, const float *omega, int64_t m, const float *center, const float *v,
+                       int64_t prompts, int64_t entries, int64_t hidden, hipStream_t s, DevBuf *tmp);
+void launch_basis(float *dirs, const float *first, const float *good, int64_t entries, int64_t hidden, int64_t k,
+                  int orthogonalize, const double *y, const double *w, int64_t m, hipStream_t s, DevBuf *tmp);
+
 // `tmp` holds the per-chunk partials (3 * n * chunks doubles)
 void launch_log_softmax_rows(float *out, const float *x, int64_t n, int64_t len, hipStream_t s, DevBuf *tmp);
 void launch_kl_rows(double *kl, const float *base, const float *trial, int64_t n, int64_t vocab, hipStream_t s,

@@ -497,6 +497,53 @@ int32_t ditch_hip_klRows_device(ditch_hip *h, double *d_kl,
                                 const float *d_trial_logits, uint64_t n,
                                 uint64_t vocab, void *stream);
 
+/* ------------------------------------------------------------------------ */
+/* The step after residual capture, on device memory (enqueued on `stream`,
+ * NULL = the context stream, not waited for).                              */
+
+/* Engine.forEachResidual's per-batch reduction (engine.zig:414-431): for
+ * prompt b and layer entry l, v = mean of the prompt's take[b] captured rows
+ * starting at capture index first[b] (the residuals of forward_device,
+ * [entries][n_capture][hidden]), clamped to +-quantile(|v|, winsor_q) when
+ * 0 <= winsor_q < 1 (torch.quantile interpolation, engine.zig:492-499);
+ * written to d_vout [prompts][entries][hidden] and added, prompt after
+ * prompt, to the f64 sums d_sum [entries][hidden] (getResidualMeanObserved,
+ * engine.zig:314-337) and, when d_sq is not NULL, to the squares d_sq
+ * (directions.Moments, directions.zig:196-205). Winsorising needs
+ * hidden <= 16384.                                                          */
+int32_t ditch_hip_residual_reduce_device(ditch_hip *h, const float *d_residuals,
+                                         uint64_t entries, uint64_t n_capture,
+                                         uint64_t hidden, const uint32_t *d_first,
+                                         const uint32_t *d_take, uint64_t prompts,
+                                         float winsor_q, float *d_vout,
+                                         double *d_sum, double *d_sq, void *stream);
+/* mean[i] = f32(sum[i] / max(count, 1))          (engine.zig:333-335)       */
+int32_t ditch_hip_residual_mean_device(ditch_hip *h, float *d_mean, const double *d_sum,
+                                       uint64_t count, uint64_t n, void *stream);
+/* abliterate.computeDirections (abliterate.zig:88-109): unit bad - good per
+ * entry, optionally orthogonal to the good mean.                           */
+int32_t ditch_hip_directions_device(ditch_hip *h, float *d_dirs, const float *d_good_means,
+                                    const float *d_bad_means, uint64_t entries,
+                                    uint64_t hidden, int32_t orthogonalize, void *stream);
+/* directions.Sketch.add (directions.zig:80-104) for a batch of per-prompt
+ * residuals d_v [prompts][entries][hidden] (ditch_hip_residual_reduce's
+ * d_vout): z = v - center, p = Omega^T z, Y += z p^T, W += p p^T in f64.
+ * d_y [entries][m][hidden], d_w [entries][m][m], d_omega [m][hidden] (the
+ * caller's Gaussian test matrix), m <= 32.                                 */
+int32_t ditch_hip_sketch_add_device(ditch_hip *h, double *d_y, double *d_w,
+                                    const float *d_omega, uint64_t m,
+                                    const float *d_center, const float *d_v,
+                                    uint64_t prompts, uint64_t entries,
+                                    uint64_t hidden, void *stream);
+/* directions.computeBasisFrom with Sketch.factor (directions.zig:108-134,
+ * 371-455): the [entries][k][hidden] orthonormal bases from the first
+ * directions, the good means and the sketch; k <= 8 (m <= 32).             */
+int32_t ditch_hip_basis_device(ditch_hip *h, float *d_dirs, const float *d_first,
+                               const float *d_good_means, uint64_t entries,
+                               uint64_t hidden, uint64_t k, int32_t orthogonalize,
+                               const double *d_y, const double *d_w, uint64_t m,
+                               void *stream);
+
 #ifdef __cplusplus
 }
 #endif

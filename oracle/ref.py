@@ -50,6 +50,12 @@ PROTOS = {
     "ref_model_limit_layers": (None, [P, SZ, SZ]),
     "ref_set_threads": (None, [P, ctypes.c_int]),
     "ref_last_error": (ctypes.c_char_p, []),
+    "ref_residual_reduce": (ctypes.c_int, [P, SZ, SZ, SZ, P, P, SZ, FLT, P, P, P]),
+    "ref_directions": (None, [P, P, P, SZ, SZ, ctypes.c_int]),
+    "ref_orthonormalize": (None, [P, SZ, SZ]),
+    "ref_sketch_add": (None, [P, P, P, SZ, P, P, SZ, SZ, SZ]),
+    "ref_symmetric_eigen": (None, [P, P, SZ]),
+    "ref_basis": (ctypes.c_int, [P, P, P, SZ, SZ, SZ, ctypes.c_int, P, P, SZ]),
 }
 
 _lib = None
@@ -82,6 +88,10 @@ def load(path=LIB):
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
 
 
 class OracleError(RuntimeError):
@@ -203,6 +213,54 @@ class Ref:
         sin_t = np.zeros_like(cos_t)
         self.lib.ref_fill_rope(ctypes.byref(cfg), _p(cos_t), _p(sin_t))
         return cos_t, sin_t
+
+
+    # -- direction pipeline (engine.zig:414-431, abliterate.zig:88-109,
+    #    directions.zig:80-134, 371-500) --------------------------------
+
+    def residual_reduce(self, res, first, take, q, sum_=None, sq=None):
+        """res [entries][n_capture][hidden]; returns vout [prompts][entries][hidden]
+        and adds into sum_/sq ([entries][hidden] f64) when given."""
+        res = np.ascontiguousarray(res, dtype=np.float32)
+        E, NC, H = res.shape
+        first = np.ascontiguousarray(first, dtype=np.uint32)
+        take = np.ascontiguousarray(take, dtype=np.uint32)
+        vout = np.empty((first.size, E, H), dtype=np.float32)
+        self._check(self.lib.ref_residual_reduce(_p(res), E, NC, H, _p(first), _p(take), first.size, q, _p(vout),
+                                                 _p(sum_) if sum_ is not None else None,
+                                                 _p(sq) if sq is not None else None))
+        return vout
+
+    def directions(self, good, bad, orthogonalize):
+        good, bad = _f32(good), _f32(bad)
+        out = np.empty_like(good)
+        self.lib.ref_directions(_p(out), _p(good), _p(bad), good.shape[0], good.shape[1], int(orthogonalize))
+        return out
+
+    def orthonormalize(self, vecs):
+        v = np.array(vecs, dtype=np.float32, order="C")
+        self.lib.ref_orthonormalize(_p(v), v.shape[0], v.shape[1])
+        return v
+
+    def sketch_add(self, y, w, omega, center, v):
+        omega, center, v = _f32(omega), _f32(center), _f32(v)
+        P_, E, H = v.shape
+        self.lib.ref_sketch_add(_p(y), _p(w), _p(omega), omega.shape[0], _p(center), _p(v), P_, E, H)
+
+    def symmetric_eigen(self, m):
+        a = np.array(m, dtype=np.float64, order="C")
+        vecs = np.empty_like(a)
+        self.lib.ref_symmetric_eigen(_p(a), _p(vecs), a.shape[0])
+        return a, vecs
+
+    def basis(self, first, good, k, orthogonalize, y, w):
+        first, good = _f32(first), _f32(good)
+        E, H = first.shape
+        out = np.empty((E, k, H), dtype=np.float32)
+        m = w.shape[1]
+        self._check(self.lib.ref_basis(_p(out), _p(first), _p(good), E, H, k, int(orthogonalize),
+                                       _p(np.ascontiguousarray(y)), _p(np.ascontiguousarray(w)), m))
+        return out
 
 
 class RefModel:
