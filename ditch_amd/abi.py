@@ -119,6 +119,15 @@ class Row(C.Structure):
     _fields_ = [("b", C.c_uint32), ("pos", C.c_uint32)]
 
 
+class EditOptions(C.Structure):
+    """`ditch_edit_options` (abliterate.Options)."""
+    _fields_ = [("row_normalization", C.c_int32), ("lora_rank", C.c_uint32), ("seed", C.c_uint64),
+                ("ablate_inputs", C.c_int32)]
+
+
+ROWNORM = {"none": 0, "pre": 1, "full": 2}
+
+
 class PathStats(C.Structure):
     """`ditch_model_path_stats`."""
     _fields_ = [("moe_device_planned", C.c_uint64), ("moe_host_planned", C.c_uint64)]
@@ -183,6 +192,10 @@ PROTOTYPES = {
     "ditch_hip_model_edit": (I32, [P, I32, I32, I32, P, U64, FLT]),
     "ditch_hip_logSoftmaxRows": (I32, [P, P, P, U64, U64]),
     "ditch_hip_klRows": (I32, [P, P, P, P, U64, U64]),
+    "ditch_hip_edit_rank": (U64, [U64, U64, U64, P]),
+    "ditch_hip_edit_delta_ex": (I32, [P, P, U64, P, U64, P, P, U64, FLT, P]),
+    "ditch_hip_model_edit_ex": (I32, [P, I32, I32, I32, P, U64, FLT, P]),
+    "ditch_hip_edit_gaussian": (None, [P, U64, U64]),
     "ditch_hip_logSoftmaxRows_device": (I32, [P, P, P, U64, U64, P]),
     "ditch_hip_residual_reduce_device": (I32, [P, P, U64, U64, U64, P, P, U64, FLT, P, P, P, P]),
     "ditch_hip_residual_mean_device": (I32, [P, P, P, U64, U64, P]),

@@ -18,6 +18,8 @@ void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64
                      const float *b);
 void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight);
 void model_reset_deltas(ditch_hip_model *m);
+void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight,
+                   int mode, int64_t lora_rank, uint64_t seed, int ablate);
 uint64_t model_bytes(const ditch_hip_model *m);
 void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
                    int64_t T, const uint64_t *d_capture, int64_t n_capture, float *d_res, const uint64_t *d_logit_rows,
@@ -622,6 +624,62 @@ int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot, in
         DITCH_CHECK(v && k > 0, DITCH_INVALID_ARGUMENT, "edit arguments");
         model_edit(m, layer, slot, expert, v, k, weight);
     });
+}
+
+static void edit_opts_check(const ditch_edit_options *o) {
+    DITCH_CHECK(o, DITCH_INVALID_ARGUMENT, "NULL edit options");
+    DITCH_CHECK(o->row_normalization >= DITCH_ROWNORM_NONE && o->row_normalization <= DITCH_ROWNORM_FULL,
+                DITCH_INVALID_ARGUMENT, "edit: unknown row normalisation");
+}
+
+uint64_t ditch_hip_edit_rank(uint64_t rows, uint64_t cols, uint64_t k, const ditch_edit_options *opts) {
+    if (!opts) return 0;
+    return (uint64_t)edit_rank((int64_t)rows, (int64_t)cols, (int64_t)k, opts->row_normalization,
+                               (int64_t)opts->lora_rank, opts->ablate_inputs != 0);
+}
+
+int32_t ditch_hip_edit_delta_ex(ditch_hip *h, float *a, uint64_t a_len, float *b, uint64_t b_len,
+                                const ditch_weight *w, const float *v, uint64_t k, float weight,
+                                const ditch_edit_options *opts) {
+    return guarded(h, [&] {
+        DITCH_CHECK(a && b && w && v && k > 0, DITCH_INVALID_ARGUMENT, "edit_delta_ex arguments");
+        edit_opts_check(opts);
+        const uint64_t rank = ditch_hip_edit_rank(w->rows, w->cols, k, opts);
+        DITCH_CHECK(a_len >= rank * w->cols && b_len >= w->rows * rank, DITCH_INVALID_ARGUMENT,
+                    "edit_delta_ex: a or b shorter than the delta");
+        hipStream_t s = h->stream;
+        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        float *da = nullptr, *db = nullptr;
+        int64_t r = 0;
+        edit_delta_device(t->v, v, (int64_t)k, weight, opts->row_normalization, (int64_t)opts->lora_rank, opts->seed,
+                          opts->ablate_inputs != 0, s, &da, &db, &r);
+        try {
+            d2h(a, da, r * w->cols * 4, s);
+            d2h(b, db, w->rows * r * 4, s);
+            DITCH_TRY_HIP(hipStreamSynchronize(s));
+        } catch (...) {
+            dev_free(da);
+            dev_free(db);
+            throw;
+        }
+        dev_free(da);
+        dev_free(db);
+    });
+}
+
+int32_t ditch_hip_model_edit_ex(ditch_hip_model *m, int32_t layer, int32_t slot, int32_t expert, const float *v,
+                                uint64_t k, float weight, const ditch_edit_options *opts) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(v && k > 0, DITCH_INVALID_ARGUMENT, "edit arguments");
+        edit_opts_check(opts);
+        model_edit_ex(m, layer, slot, expert, v, k, weight, opts->row_normalization, (int64_t)opts->lora_rank,
+                      opts->seed, opts->ablate_inputs != 0);
+    });
+}
+
+void ditch_hip_edit_gaussian(float *out, uint64_t n, uint64_t seed) {
+    if (out) edit_gaussian(out, (size_t)n, seed);
 }
 
 int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x, uint64_t n, uint64_t len) {

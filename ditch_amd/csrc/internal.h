@@ -321,6 +321,12 @@ void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t 
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
                       int64_t len, float eps, int one_plus, hipStream_t s);
 void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
+// edit.hip
+void edit_gaussian(float *out, size_t n, uint64_t seed);
+int64_t edit_rank(int64_t rows, int64_t cols, int64_t k, int mode, int64_t lora_rank, int ablate);
+void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weight, int mode, int64_t lora_rank,
+                       uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out, int64_t *rank_out);
+
 // directions.hip
 void launch_residual_reduce(const float *res, int64_t entries, int64_t n_capture, int64_t hidden,
                             const uint32_t *first, const uint32_t *take, int64_t prompts, float q, float *vout,

@@ -858,6 +858,30 @@ void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float
     mt->rank = (int)k;
 }
 
+// abliterate.computeDelta in any mode on a registered matrix, installed as
+// its delta (a streamed expert's blob is staged on the device for the passes)
+void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight,
+                   int mode, int64_t lora_rank, uint64_t seed, int ablate) {
+    check_delta_slot(slot);
+    Mat *mt = mat_slot(m, layer, slot, expert);
+    DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "edit of an empty slot");
+    hipStream_t s = m->h->stream;
+    DevBuf staged;
+    TileView w = mt->t->v;
+    if (mt->streamed()) {
+        uint8_t *d = staged.get<uint8_t>(mt->hm.bytes);
+        DITCH_TRY_HIP(hipMemcpyAsync(d, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, s));
+        w = view_at(*mt, d);
+    }
+    float *da = nullptr, *db = nullptr;
+    int64_t rank = 0;
+    edit_delta_device(w, v, (int64_t)k, weight, mode, lora_rank, seed, ablate, s, &da, &db, &rank);
+    mt->clear_delta();
+    mt->da = da;
+    mt->db = db;
+    mt->rank = (int)rank;
+}
+
 void model_reset_deltas(ditch_hip_model *m) {
     for (auto &L : m->layers) {
         for (Mat *mt : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.router, &L.sh_gate, &L.sh_up, &L.sh_down,

@@ -501,7 +501,7 @@ __global__ void row_norms_kernel(float *out, TileView w) {
 // W^T y, first pass: block (column chunk, row chunk) -> partial sums
 // [row_chunk][q][cols]; the second pass adds the chunks in order.
 constexpr int MVT_ROWS = 256;
-constexpr int MVT_MAXQ = 8;
+constexpr int MVT_MAXQ = 16;
 
 __global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q) {
     int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -677,7 +677,7 @@ size_t matvecT_partials_floats(const TileView &w, int64_t q) {
     return (size_t)chunks * q * w.cols;
 }
 void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials) {
-    DITCH_CHECK(q >= 1 && q <= MVT_MAXQ, DITCH_UNSUPPORTED, "matvecTMulti: q must be 1..8");
+    DITCH_CHECK(q >= 1 && q <= MVT_MAXQ, DITCH_UNSUPPORTED, "matvecTMulti: q must be 1..16");
     int64_t chunks = (w.rows + MVT_ROWS - 1) / MVT_ROWS;
     dim3 grid((unsigned)((w.cols + 255) / 256), (unsigned)chunks);
     hipLaunchKernelGGL(matvecT_partial_kernel, grid, dim3(256), 0, s, partials, w, y, q);

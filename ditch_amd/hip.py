@@ -160,6 +160,18 @@ class Device:
         self.check(self.lib.ditch_hip_edit_delta(self.h, _p(a), _p(b), w.ref(), _p(v), k, weight))
         return a, b
 
+    def edit_delta_ex(self, w: HostWeight, v, weight, mode="full", lora_rank=3, seed=0, ablate=False):
+        """abliterate.computeDelta in any mode: (a [rank][cols], b [rows][rank])."""
+        v = _f32(v)
+        k = v.shape[0]
+        o = abi.EditOptions(abi.ROWNORM[mode], lora_rank, seed, int(ablate))
+        rank = self.lib.ditch_hip_edit_rank(w.rows, w.cols, k, ctypes.byref(o))
+        a = np.empty((rank, w.cols), dtype=np.float32)
+        b = np.empty((w.rows, rank), dtype=np.float32)
+        self.check(self.lib.ditch_hip_edit_delta_ex(self.h, _p(a), a.size, _p(b), b.size, w.ref(), _p(v), k, weight,
+                                                    ctypes.byref(o)))
+        return a, b
+
     def logSoftmaxRows(self, x):
         x = _f32(x)
         out = np.empty_like(x)
@@ -283,6 +295,12 @@ class Model:
     def edit(self, layer, slot, expert, v, weight):
         v = _f32(v)
         self.dev.check(self.dev.lib.ditch_hip_model_edit(self.h, layer, slot, expert, _p(v), v.shape[0], weight))
+
+    def edit_ex(self, layer, slot, expert, v, weight, mode="full", lora_rank=3, seed=0, ablate=False):
+        v = _f32(v)
+        o = abi.EditOptions(abi.ROWNORM[mode], lora_rank, seed, int(ablate))
+        self.dev.check(self.dev.lib.ditch_hip_model_edit_ex(self.h, layer, slot, expert, _p(v), v.shape[0], weight,
+                                                            ctypes.byref(o)))
 
     def reset_deltas(self):
         self.dev.check(self.dev.lib.ditch_hip_model_reset_deltas(self.h))

@@ -478,6 +478,41 @@ int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot,
                              int32_t expert, const float *v, uint64_t k,
                              float weight);
 
+/* The edit in every row-normalisation mode (abliterate.computeDelta,
+ * abliterate.zig:223-350; Options abliterate.zig:63-84): `none` as above,
+ * `pre` (directions over the row-normalised matrix, B scaled by the row
+ * norms), `full` (the default: the renormalised edit's delta approximated by
+ * a rank-max(lora_rank, k) randomised SVD with 2r+4 columns and 6 power
+ * iterations, abliterate.zig:282-349, 473-538), and the input-side
+ * ablation that widens the delta by k (abliterate.zig:234-261). All passes
+ * over W run on the device over the resident (quantised) weight.
+ * The SVD's Gaussian test matrix is ditch_hip_edit_gaussian(q * cols, seed)
+ * (splitmix64 of seed and index, Box-Muller): the reference draws its own
+ * from Zig's Xoshiro256, so the two deltas agree to the SVD's accuracy,
+ * not bit for bit.                                                          */
+enum { DITCH_ROWNORM_NONE = 0, DITCH_ROWNORM_PRE = 1, DITCH_ROWNORM_FULL = 2 };
+typedef struct ditch_edit_options {
+    int32_t row_normalization; /* DITCH_ROWNORM_*                              */
+    uint32_t lora_rank;        /* `full`: rank r (the reference's default: 3)   */
+    uint64_t seed;             /* `full`: the test matrix's seed                */
+    int32_t ablate_inputs;     /* nonzero: the input-side ablation as well      */
+} ditch_edit_options;
+/* Rank of the delta for a rows x cols matrix and k directions (<= 64).     */
+uint64_t ditch_hip_edit_rank(uint64_t rows, uint64_t cols, uint64_t k,
+                             const ditch_edit_options *opts);
+/* Host buffers: a [rank][cols], b [rows][rank] with rank = ditch_hip_edit_rank
+ * (a_len / b_len: their lengths in floats, checked).                       */
+int32_t ditch_hip_edit_delta_ex(ditch_hip *h, float *a, uint64_t a_len, float *b,
+                                uint64_t b_len, const ditch_weight *w,
+                                const float *v, uint64_t k, float weight,
+                                const ditch_edit_options *opts);
+/* The same on a registered model matrix, installing the delta
+ * (model.setDelta, abliterate.zig:193-197).                                */
+int32_t ditch_hip_model_edit_ex(ditch_hip_model *m, int32_t layer, int32_t slot,
+                                int32_t expert, const float *v, uint64_t k,
+                                float weight, const ditch_edit_options *opts);
+void ditch_hip_edit_gaussian(float *out, uint64_t n, uint64_t seed);
+
 /* ------------------------------------------------------------------------ */
 /* log-softmax of n rows (tensor.zig:1203-1210: f32 max, f64 sum, f32 x-lse). */
 int32_t ditch_hip_logSoftmaxRows(ditch_hip *h, float *out, const float *x,

@@ -1722,3 +1722,224 @@ int ref_basis(float *dirs, const float *first, const float *good_means, size_t e
     free(wm); free(vecs); free(bf); free(gram); free(gv); free(gd); free(order);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The edit in every row-normalisation mode (test oracle):
+ * abliterate.computeDelta / computeOutputDelta / ablateInputs /
+ * DeltaOperator / randomizedSvd / jacobiEigen (abliterate.zig:223-538).    */
+
+static uint64_t splitmix64_ref(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+/* The full mode's test matrix: standard normals from splitmix64 of the seed
+ * and index, Box-Muller in f64 (the reference draws them from Zig's
+ * Xoshiro256, abliterate.zig:476-481; any Gaussian start converges). */
+void ref_edit_gaussian(float *out, size_t n, uint64_t seed) {
+    for (size_t t = 0; t < n; t++) {
+        uint64_t r1 = splitmix64_ref(seed ^ (2 * (uint64_t)t) * 0xD1B54A32D192ED03ull);
+        uint64_t r2 = splitmix64_ref(seed ^ (2 * (uint64_t)t + 1) * 0xD1B54A32D192ED03ull);
+        double u1 = ((double)(r1 >> 11) + 1.0) * 0x1.0p-53;
+        double u2 = (double)(r2 >> 11) * 0x1.0p-53;
+        out[t] = (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+    }
+}
+
+/* jacobiEigen (abliterate.zig:427-469): f32 cyclic Jacobi, f64 off-norm */
+void ref_jacobi_f32(float *m, float *vecs, size_t n) {
+    memset(vecs, 0, n * n * sizeof(float));
+    for (size_t i = 0; i < n; i++) vecs[i * n + i] = 1;
+    for (int sweep = 0; sweep < 50; sweep++) {
+        double off = 0;
+        for (size_t i = 0; i < n; i++)
+            for (size_t j = 0; j < n; j++)
+                if (i != j) off += (double)m[i * n + j] * m[i * n + j];
+        if (off < 1e-18) break;
+        for (size_t p = 0; p < n; p++)
+            for (size_t q = p + 1; q < n; q++) {
+                float apq = m[p * n + q];
+                if (fabsf(apq) < 1e-20f) continue;
+                float app = m[p * n + p], aqq = m[q * n + q];
+                float theta = (aqq - app) / (2.0f * apq);
+                float sg = theta > 0 ? 1.0f : theta < 0 ? -1.0f : 0.0f;
+                float t = sg / (fabsf(theta) + sqrtf(theta * theta + 1.0f));
+                float tf = theta == 0 ? 1.0f : t;
+                float cs = 1.0f / sqrtf(tf * tf + 1.0f), sn = tf * cs;
+                for (size_t k = 0; k < n; k++) {
+                    float akp = m[k * n + p], akq = m[k * n + q];
+                    m[k * n + p] = cs * akp - sn * akq;
+                    m[k * n + q] = sn * akp + cs * akq;
+                }
+                for (size_t k = 0; k < n; k++) {
+                    float apk = m[p * n + k], aqk = m[q * n + k];
+                    m[p * n + k] = cs * apk - sn * aqk;
+                    m[q * n + k] = sn * apk + cs * aqk;
+                }
+                for (size_t k = 0; k < n; k++) {
+                    float vkp = vecs[k * n + p], vkq = vecs[k * n + q];
+                    vecs[k * n + p] = cs * vkp - sn * vkq;
+                    vecs[k * n + q] = sn * vkp + cs * vkq;
+                }
+            }
+    }
+}
+
+typedef struct {
+    const ditch_weight *w;
+    const float *a, *c, *d;
+    size_t k;
+    int threads;
+} dop;
+
+/* DeltaOperator.applyMulti: out[q][rows] = (D X)^T (abliterate.zig:363-376) */
+static int dop_apply(const dop *o, float *out, const float *x, size_t q) {
+    size_t rows = o->w->rows, cols = o->w->cols;
+    if (ref_matmulT(out, x, q, o->w, 0, NULL, NULL, o->threads)) return -1;
+    for (size_t j = 0; j < q; j++) {
+        float *oj = out + j * rows;
+        for (size_t i = 0; i < rows; i++) oj[i] *= o->c[i];
+        for (size_t l = 0; l < o->k; l++) {
+            float ax = ref_dot(o->a + l * cols, x + j * cols, cols);
+            axpy(oj, ax, o->d + l * rows, rows);
+        }
+    }
+    return 0;
+}
+
+/* DeltaOperator.applyTMulti: out[q][cols] = (D^T Y)^T (abliterate.zig:379-393) */
+static int dop_applyT(const dop *o, float *out, const float *y, size_t q) {
+    size_t rows = o->w->rows, cols = o->w->cols;
+    float *cy = (float *)calloc(q * rows, sizeof(float));
+    for (size_t j = 0; j < q; j++)
+        for (size_t i = 0; i < rows; i++) cy[j * rows + i] = o->c[i] * y[j * rows + i];
+    int rc = ref_matvecTMulti(out, o->w, cy, q, o->threads);
+    free(cy);
+    if (rc) return -1;
+    for (size_t j = 0; j < q; j++)
+        for (size_t l = 0; l < o->k; l++) {
+            float dy = ref_dot(o->d + l * rows, y + j * rows, rows);
+            axpy(out + j * cols, dy, o->a + l * cols, cols);
+        }
+    return 0;
+}
+
+/* computeOutputDelta (abliterate.zig:264-350) then ablateInputs (234-261):
+ * a [rank][cols], b [rows][rank]; *rank_out set. mode 0 none, 1 pre, 2 full. */
+int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_weight *w, const float *v, size_t k,
+                      float weight, int mode, size_t lora_rank, uint64_t seed, int ablate, int threads) {
+    size_t rows = w->rows, cols = w->cols, r_out = k;
+    float *pa = (float *)malloc(64 * cols * sizeof(float)), *pb = (float *)malloc(rows * 64 * sizeof(float));
+    int rc = 0;
+    if (mode == 0) {
+        rc = ref_matvecTMulti(pa, w, v, k, threads);
+        for (size_t i = 0; i < rows; i++)
+            for (size_t j = 0; j < k; j++) pb[i * k + j] = -weight * v[j * rows + i];
+    } else {
+        float *norms = (float *)malloc(rows * sizeof(float)), *vn = (float *)malloc(k * rows * sizeof(float));
+        rc |= ref_rowNorms(norms, w, threads);
+        for (size_t j = 0; j < k; j++)
+            for (size_t i = 0; i < rows; i++) vn[j * rows + i] = norms[i] > 0 ? v[j * rows + i] / norms[i] : 0;
+        float *a = (float *)malloc(k * cols * sizeof(float));
+        rc |= ref_matvecTMulti(a, w, vn, k, threads);
+        if (mode == 1) {
+            memcpy(pa, a, k * cols * sizeof(float));
+            for (size_t i = 0; i < rows; i++)
+                for (size_t j = 0; j < k; j++) pb[i * k + j] = -weight * v[j * rows + i] * norms[i];
+        } else {
+            float *wa = (float *)malloc(k * rows * sizeof(float)), *gram = (float *)malloc(k * k * sizeof(float));
+            float *c = (float *)malloc(rows * sizeof(float)), *d = (float *)malloc(k * rows * sizeof(float));
+            rc |= ref_matmulT(wa, a, k, w, 0, NULL, NULL, threads);
+            for (size_t j = 0; j < k; j++)
+                for (size_t l = 0; l < k; l++) gram[j * k + l] = ref_dot(a + j * cols, a + l * cols, cols);
+            for (size_t i = 0; i < rows; i++) {
+                float s2 = 1.0f;
+                for (size_t j = 0; j < k; j++) {
+                    float bij = -weight * v[j * rows + i];
+                    float wnda = norms[i] > 0 ? wa[j * rows + i] / norms[i] : 0;
+                    s2 += 2.0f * bij * wnda;
+                    for (size_t l = 0; l < k; l++) s2 += bij * (-weight * v[l * rows + i]) * gram[j * k + l];
+                }
+                float s = sqrtf(s2 > 1e-12f ? s2 : 1e-12f);
+                c[i] = 1.0f / s - 1.0f;
+                for (size_t j = 0; j < k; j++) d[j * rows + i] = norms[i] * (-weight * v[j * rows + i]) / s;
+            }
+            size_t r = lora_rank > k ? lora_rank : k;
+            size_t q = 2 * r + 4;
+            if (q > rows) q = rows;
+            if (q > cols) q = cols;
+            dop o = {w, a, c, d, k, threads};
+            float *omega = (float *)malloc(q * cols * sizeof(float)), *qy = (float *)malloc(q * rows * sizeof(float));
+            float *qx = (float *)malloc(q * cols * sizeof(float));
+            ref_edit_gaussian(omega, q * cols, seed);
+            rc |= dop_apply(&o, qy, omega, q);
+            ref_orthonormalize(qy, q, rows);
+            for (int it = 0; it < 6; it++) {
+                rc |= dop_applyT(&o, qx, qy, q);
+                ref_orthonormalize(qx, q, cols);
+                rc |= dop_apply(&o, qy, qx, q);
+                ref_orthonormalize(qy, q, rows);
+            }
+            rc |= dop_applyT(&o, qx, qy, q); /* bt */
+            float *bbt = (float *)malloc(q * q * sizeof(float)), *ev = (float *)malloc(q * q * sizeof(float));
+            for (size_t i = 0; i < q; i++)
+                for (size_t j = 0; j < q; j++) bbt[i * q + j] = ref_dot(qx + i * cols, qx + j * cols, cols);
+            ref_jacobi_f32(bbt, ev, q);
+            size_t order[64];
+            for (size_t i = 0; i < q; i++) order[i] = i;
+            for (size_t i = 1; i < q; i++) {
+                size_t ov = order[i], j = i;
+                while (j > 0 && bbt[order[j - 1] * q + order[j - 1]] < bbt[ov * q + ov]) {
+                    order[j] = order[j - 1];
+                    j--;
+                }
+                order[j] = ov;
+            }
+            r_out = r < q ? r : q;
+            float *uk = (float *)malloc(rows * sizeof(float)), *vk = (float *)malloc(cols * sizeof(float));
+            for (size_t t = 0; t < r_out; t++) {
+                size_t src = order[t];
+                float lambda = bbt[src * q + src] > 0 ? bbt[src * q + src] : 0;
+                float sv = sqrtf(lambda);
+                memset(uk, 0, rows * sizeof(float));
+                memset(vk, 0, cols * sizeof(float));
+                for (size_t i = 0; i < q; i++) axpy(uk, ev[i * q + src], qy + i * rows, rows);
+                for (size_t i = 0; i < q; i++) axpy(vk, ev[i * q + src], qx + i * cols, cols);
+                if (sv > 1e-12f) {
+                    float inv = 1.0f / sv;
+                    for (size_t j = 0; j < cols; j++) vk[j] *= inv;
+                } else {
+                    memset(vk, 0, cols * sizeof(float));
+                }
+                float sq = sqrtf(sv > 0 ? sv : 0);
+                for (size_t j = 0; j < cols; j++) pa[t * cols + j] = sq * vk[j];
+                for (size_t i = 0; i < rows; i++) pb[i * r_out + t] = uk[i] * sq;
+            }
+            free(uk); free(vk); free(bbt); free(ev); free(omega); free(qy); free(qx);
+            free(wa); free(gram); free(c); free(d);
+        }
+        free(norms); free(vn); free(a);
+    }
+    size_t rank = r_out + (ablate ? k : 0);
+    if (!ablate) {
+        memcpy(a_out, pa, r_out * cols * sizeof(float));
+        memcpy(b_out, pb, rows * r_out * sizeof(float));
+    } else {
+        float *u = (float *)malloc(k * cols * sizeof(float)), *wu = (float *)malloc(k * rows * sizeof(float));
+        rc |= ref_matvecTMulti(u, w, v, k, threads);
+        ref_orthonormalize(u, k, cols);
+        rc |= ref_matmulT(wu, u, k, w, r_out, pa, pb, threads);
+        memcpy(a_out, pa, r_out * cols * sizeof(float));
+        memcpy(a_out + r_out * cols, u, k * cols * sizeof(float));
+        for (size_t i = 0; i < rows; i++) {
+            memcpy(b_out + i * rank, pb + i * r_out, r_out * sizeof(float));
+            for (size_t j = 0; j < k; j++) b_out[i * rank + r_out + j] = -weight * wu[j * rows + i];
+        }
+        free(u); free(wu);
+    }
+    free(pa); free(pb);
+    *rank_out = rank;
+    return rc ? -1 : 0;
+}

@@ -106,6 +106,14 @@ void ref_symmetric_eigen(double *m, double *vecs, size_t n);
 int ref_basis(float *dirs, const float *first, const float *good_means, size_t entries, size_t hidden, size_t k,
               int orthogonalize, const double *y, const double *w, size_t m);
 
+/* the edit in every mode (abliterate.zig:223-538): mode 0 none, 1 pre,
+ * 2 full (rank-r randomised SVD seeded by ref_edit_gaussian), optional
+ * input-side ablation; a [rank][cols], b [rows][rank] (rank <= 64)         */
+void ref_edit_gaussian(float *out, size_t n, uint64_t seed);
+void ref_jacobi_f32(float *m, float *vecs, size_t n);
+int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_weight *w, const float *v, size_t k,
+                      float weight, int mode, size_t lora_rank, uint64_t seed, int ablate, int threads);
+
 /* model (model.zig:4619-4959, moe.zig:998-1228, model.zig:3292-3342) */
 typedef struct ref_model ref_model;
 ref_model *ref_model_create(const ditch_model_config *cfg);

@@ -56,6 +56,9 @@ PROTOS = {
     "ref_sketch_add": (None, [P, P, P, SZ, P, P, SZ, SZ, SZ]),
     "ref_symmetric_eigen": (None, [P, P, SZ]),
     "ref_basis": (ctypes.c_int, [P, P, P, SZ, SZ, SZ, ctypes.c_int, P, P, SZ]),
+    "ref_edit_gaussian": (None, [P, SZ, U64]),
+    "ref_jacobi_f32": (None, [P, P, SZ]),
+    "ref_edit_delta_ex": (ctypes.c_int, [P, P, P, P, P, SZ, FLT, ctypes.c_int, SZ, U64, ctypes.c_int, ctypes.c_int]),
 }
 
 _lib = None
@@ -261,6 +264,31 @@ class Ref:
         self._check(self.lib.ref_basis(_p(out), _p(first), _p(good), E, H, k, int(orthogonalize),
                                        _p(np.ascontiguousarray(y)), _p(np.ascontiguousarray(w)), m))
         return out
+
+
+    def edit_gaussian(self, n, seed):
+        out = np.empty(n, dtype=np.float32)
+        self.lib.ref_edit_gaussian(_p(out), n, seed)
+        return out
+
+    def jacobi_f32(self, m):
+        a = np.array(m, dtype=np.float32, order="C")
+        vecs = np.empty_like(a)
+        self.lib.ref_jacobi_f32(_p(a), _p(vecs), a.shape[0])
+        return a, vecs
+
+    def edit_delta_ex(self, w, v, weight, mode=0, lora_rank=3, seed=0, ablate=False):
+        """abliterate.computeDelta: (a [rank][cols], b [rows][rank]); mode 0 none,
+        1 pre, 2 full."""
+        v = _f32(v)
+        k = v.shape[0]
+        a = np.empty((64, w.cols), dtype=np.float32)
+        b = np.empty((w.rows * 64,), dtype=np.float32)
+        rank = ctypes.c_size_t()
+        self._check(self.lib.ref_edit_delta_ex(_p(a), _p(b), ctypes.byref(rank), w.ref(), _p(v), k, weight, mode,
+                                               lora_rank, seed, int(ablate), self.threads))
+        r = rank.value
+        return a[:r].copy(), b[:w.rows * r].reshape(w.rows, r).copy()
 
 
 class RefModel:
