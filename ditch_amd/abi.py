@@ -128,6 +128,11 @@ class EditOptions(C.Structure):
 ROWNORM = {"none": 0, "pre": 1, "full": 2}
 
 
+class Sampler(C.Structure):
+    """`ditch_sampler` (model.Sampler)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("seed", C.c_uint64)]
+
+
 class PathStats(C.Structure):
     """`ditch_model_path_stats`."""
     _fields_ = [("moe_device_planned", C.c_uint64), ("moe_host_planned", C.c_uint64)]
@@ -188,6 +193,11 @@ PROTOTYPES = {
     "ditch_hip_forward": (I32, [P, P, P, U64, P, U64, P, P, U64, P]),
     "ditch_hip_forward_device": (I32, [P, P, P, U64, U32, U32, P, U64, P, U64, P, U64, P, U64]),
     "ditch_hip_model_path_stats": (I32, [P, P]),
+    "ditch_hip_kv_cache_create": (P, [P, U32, U32]),
+    "ditch_hip_kv_cache_free": (None, [P]),
+    "ditch_hip_forward_cached": (I32, [P, P, P, P, U64, P, U64, P, U64]),
+    "ditch_hip_pick_tokens_device": (I32, [P, P, P, U64, U64, P, U64, P, P]),
+    "ditch_hip_generate": (I32, [P, P, P, P, U64, U64, P, U64, P, P, P, P]),
     "ditch_hip_edit_delta": (I32, [P, P, P, P, P, U64, FLT]),
     "ditch_hip_model_edit": (I32, [P, I32, I32, I32, P, U64, FLT]),
     "ditch_hip_logSoftmaxRows": (I32, [P, P, P, U64, U64]),

@@ -20,10 +20,14 @@ void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float
 void model_reset_deltas(ditch_hip_model *m);
 void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight,
                    int mode, int64_t lora_rank, uint64_t seed, int ablate);
+ditch_hip_kv_cache *kv_cache_create(ditch_hip_model *m, int64_t B, int64_t T);
+void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens, const uint64_t *lens, int64_t B,
+              int64_t max_new, const uint32_t *eos, int64_t n_eos, const ditch_sampler *smp, uint32_t *out_tokens,
+              uint64_t *out_lens, float *first_logits);
 uint64_t model_bytes(const ditch_hip_model *m);
 void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
                    int64_t T, const uint64_t *d_capture, int64_t n_capture, float *d_res, const uint64_t *d_logit_rows,
-                   int64_t n_logit, float *d_logits);
+                   int64_t n_logit, float *d_logits, ditch_hip_kv_cache *pc = nullptr);
 
 // Device buffer owned for the duration of one call.
 struct Tmp {
@@ -588,6 +592,57 @@ int32_t ditch_hip_forward_device(ditch_hip_model *m, const uint32_t *d_tokens, c
         model_forward(m, d_tokens, d_rows, (int64_t)n, (int64_t)n_prompts, (int64_t)max_len, d_capture_rows,
                       (int64_t)n_capture, n_capture ? d_residuals : nullptr, d_logit_rows, (int64_t)n_logit,
                       n_logit ? d_logits : nullptr);
+    });
+}
+
+ditch_hip_kv_cache *ditch_hip_kv_cache_create(ditch_hip_model *m, uint32_t n_prompts, uint32_t max_len) {
+    if (!m) return nullptr;
+    ditch_hip_kv_cache *c = nullptr;
+    int32_t rc = guarded(m->h, [&] { c = kv_cache_create(m, (int64_t)n_prompts, (int64_t)max_len); });
+    return rc == DITCH_OK ? c : nullptr;
+}
+
+void ditch_hip_kv_cache_free(ditch_hip_kv_cache *c) {
+    if (!c) return;
+    (void)hipStreamSynchronize(c->m->h->stream);
+    delete c;
+}
+
+int32_t ditch_hip_forward_cached(ditch_hip_model *m, ditch_hip_kv_cache *c, const uint32_t *d_tokens,
+                                 const ditch_row *d_rows, uint64_t n, const uint64_t *d_logit_rows, uint64_t n_logit,
+                                 float *d_logits, uint64_t logits_bytes) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(c && c->m == m, DITCH_INVALID_ARGUMENT, "forward_cached: the KV cache belongs to another model");
+        DITCH_CHECK(d_tokens && d_rows, DITCH_INVALID_ARGUMENT, "NULL tokens/rows");
+        if (n == 0) return;
+        DITCH_CHECK(n_logit == 0 || (d_logit_rows && d_logits && logits_bytes >= n_logit * m->c.vocab * 4),
+                    DITCH_INVALID_ARGUMENT, "forward_cached: logit rows or logit buffer missing or too short");
+        model_forward(m, d_tokens, d_rows, (int64_t)n, c->B, c->T, nullptr, 0, nullptr, d_logit_rows,
+                      (int64_t)n_logit, n_logit ? d_logits : nullptr, c);
+    });
+}
+
+int32_t ditch_hip_pick_tokens_device(ditch_hip *h, uint32_t *d_out, const float *d_logits, uint64_t n, uint64_t vocab,
+                                     const ditch_sampler *sampler, uint64_t step, const uint32_t *d_row_ids,
+                                     void *stream) {
+    return guarded(h, [&] {
+        DITCH_CHECK(d_out && d_logits, DITCH_INVALID_ARGUMENT, "NULL argument");
+        launch_pick(d_out, d_logits, (int64_t)n, (int64_t)vocab, sampler, step, d_row_ids,
+                    stream ? (hipStream_t)stream : h->stream);
+    });
+}
+
+int32_t ditch_hip_generate(ditch_hip_model *m, ditch_hip_kv_cache *c, const uint32_t *tokens,
+                           const uint64_t *prompt_lens, uint64_t n_prompts, uint64_t max_new_tokens,
+                           const uint32_t *eos_ids, uint64_t n_eos, const ditch_sampler *sampler, uint32_t *out_tokens,
+                           uint64_t *out_lens, float *first_logits) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(tokens && prompt_lens && out_tokens && out_lens && (n_eos == 0 || eos_ids), DITCH_INVALID_ARGUMENT,
+                    "NULL argument");
+        generate(m, c, tokens, prompt_lens, (int64_t)n_prompts, (int64_t)max_new_tokens, eos_ids, (int64_t)n_eos,
+                 sampler, out_tokens, out_lens, first_logits);
     });
 }
 

@@ -321,6 +321,10 @@ void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t 
 void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, const float *bias, int64_t n,
                       int64_t len, float eps, int one_plus, hipStream_t s);
 void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
+// generate.hip
+void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, const ditch_sampler *smp,
+                 uint64_t step, const uint32_t *row_ids, hipStream_t s);
+
 // edit.hip
 void edit_gaussian(float *out, size_t n, uint64_t seed);
 int64_t edit_rank(int64_t rows, int64_t cols, int64_t k, int mode, int64_t lora_rank, int ablate);

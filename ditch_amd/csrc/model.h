@@ -97,6 +97,16 @@ struct Layer {
 
 }  // namespace ditch
 
+// KvCache.initFor(model, batch, max_len) (model.zig:2586-2724): every layer's
+// keys and values for `B` prompt slots of `T` positions, f32, [layer][b][pos]
+// [kv_dim], kept across forward calls (prefill, then decode steps).
+struct ditch_hip_kv_cache {
+    ditch_hip_model *m = nullptr;
+    int64_t B = 0, T = 0, kvd = 0, layers = 0;
+    float *k = nullptr, *v = nullptr;
+    ~ditch_hip_kv_cache();
+};
+
 struct ditch_hip_model {
     ditch_hip *h = nullptr;
     ditch_model_config c{};

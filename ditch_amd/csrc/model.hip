@@ -1163,9 +1163,12 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
 // `B` prompt slots of `T` positions size the KV cache (KvCache.initFor,
 // engine.zig:388-390); rows outside it are skipped by the kernels that read
 // the row descriptors.
+// With `pc`, the keys and values of every layer live in that persistent
+// cache (its B x T), so later calls attend to the positions earlier calls
+// wrote (decode steps after a prefill).
 void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
                    int64_t T, const uint64_t *d_capture, int64_t n_capture, float *d_res, const uint64_t *d_logit_rows,
-                   int64_t n_logit, float *d_logits) {
+                   int64_t n_logit, float *d_logits, ditch_hip_kv_cache *pc) {
     const ditch_model_config &c = m->c;
     hipStream_t s = m->h->stream;
     if (n <= 0) return;
@@ -1181,7 +1184,11 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
     float *h = m->hbuf.get<float>(n * hidden);
     float *q = m->q.get<float>(n * qd), *kk = m->k.get<float>(n * kvd), *vv = m->v.get<float>(n * kvd);
     float *att = m->att.get<float>(n * nh * vd);
-    float *kc = m->kc.get<float>(B * T * kvd), *vc = m->vc.get<float>(B * T * kvd);
+    if (pc) {
+        DITCH_CHECK(pc->m == m && pc->B == B && pc->T == T && pc->kvd == kvd, DITCH_INVALID_ARGUMENT,
+                    "forward: the KV cache belongs to another model or shape");
+    }
+    float *kc = pc ? pc->k : m->kc.get<float>(B * T * kvd), *vc = pc ? pc->v : m->vc.get<float>(B * T * kvd);
 
     hipLaunchKernelGGL(embed_kernel, dim3(grid_for(n * hidden)), dim3(256), 0, s, x, m->embed.t->v, d_tokens, n);
     DITCH_TRY_HIP(hipGetLastError());
@@ -1240,6 +1247,10 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             mm_act(m, L.q, q, hact, n, L.q_bias.p, 0, s);
             mm_act(m, L.k, kk, hact, n, L.k_bias.p, 0, s);
             mm_act(m, L.v, vv, hact, n, L.v_bias.p, 0, s);
+        }
+        if (pc) {  // this layer's slice of the persistent cache
+            kc = pc->k + li * B * T * kvd;
+            vc = pc->v + li * B * T * kvd;
         }
         RopeArgs ra{};
         ra.q = q;
@@ -1395,6 +1406,37 @@ static void host_fill_rope(const ditch_model_config &c, std::vector<float> &cos_
             cos_t[pos * half + i] = (float)(cos(angle) * attention_factor);
             sin_t[pos * half + i] = (float)(sin(angle) * attention_factor);
         }
+}
+
+}  // namespace ditch
+
+ditch_hip_kv_cache::~ditch_hip_kv_cache() {
+    ditch::dev_free(k);
+    ditch::dev_free(v);
+}
+
+namespace ditch {
+
+ditch_hip_kv_cache *kv_cache_create(ditch_hip_model *m, int64_t B, int64_t T) {
+    const ditch_model_config &c = m->c;
+    DITCH_CHECK(B > 0 && T > 0 && T <= ATT_MAXK && B <= (int64_t)INT32_MAX, DITCH_INVALID_ARGUMENT,
+                "kv cache: 1..1024 positions and at least one prompt");
+    const int64_t nkv = c.mla ? (int64_t)c.heads : (int64_t)c.kv_heads;
+    auto *kc = new ditch_hip_kv_cache();
+    kc->m = m;
+    kc->B = B;
+    kc->T = T;
+    kc->kvd = nkv * (int64_t)c.head_dim;
+    kc->layers = (int64_t)c.layers;
+    const size_t bytes = (size_t)(kc->layers * B * T * kc->kvd) * 4;
+    try {
+        kc->k = (float *)dev_alloc(bytes);
+        kc->v = (float *)dev_alloc(bytes);
+    } catch (...) {
+        delete kc;
+        throw;
+    }
+    return kc;
 }
 
 }  // namespace ditch

@@ -331,6 +331,36 @@ class Model:
                                                              d_capture, n_capture, d_res, rb, d_logit_rows, n_logit,
                                                              d_logits, lb))
 
+    def kv_cache(self, n_prompts, max_len):
+        """A persistent KV cache (ditch_hip_kv_cache_create); free it with
+        kv_cache_free before the model."""
+        c = self.dev.lib.ditch_hip_kv_cache_create(self.h, n_prompts, max_len)
+        if not c:
+            raise DeviceError(abi.DEVICE_FAILED, self.dev.lib.ditch_hip_last_error(self.dev.h).decode())
+        return c
+
+    def kv_cache_free(self, c):
+        self.dev.lib.ditch_hip_kv_cache_free(c)
+
+    def generate(self, cache, prompts, max_new_tokens, eos=(), sampler=None, first_logits=False):
+        """generateKeep: prompts = list of token-id lists; returns (list of
+        generated token lists, first-token logits [prompts][vocab] or None)."""
+        lens = np.array([len(p) for p in prompts], dtype=np.uint64)
+        toks = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts]))
+        B = len(prompts)
+        out = np.zeros((B, max_new_tokens), dtype=np.uint32)
+        out_lens = np.zeros(B, dtype=np.uint64)
+        eos_a = np.ascontiguousarray(eos, dtype=np.uint32)
+        fl = np.empty((B, self.spec.config["vocab"]), dtype=np.float32) if first_logits else None
+        smp = None
+        if sampler is not None:
+            smp = abi.Sampler(sampler.get("temperature", 1.0), sampler.get("top_k", 50), sampler.get("top_p", 0.95),
+                              sampler.get("seed", 0))
+        self.dev.check(self.dev.lib.ditch_hip_generate(
+            self.h, cache, _p(toks), _p(lens), B, max_new_tokens, _p(eos_a) if eos_a.size else None, eos_a.size,
+            ctypes.byref(smp) if smp is not None else None, _p(out), _p(out_lens), _p(fl) if fl is not None else None))
+        return [list(out[b, :int(out_lens[b])]) for b in range(B)], fl
+
     def path_stats(self):
         st = abi.PathStats()
         self.dev.check(self.dev.lib.ditch_hip_model_path_stats(self.h, ctypes.byref(st)))

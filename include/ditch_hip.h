@@ -467,6 +467,56 @@ typedef struct ditch_model_path_stats {
 int32_t ditch_hip_model_path_stats(const ditch_hip_model *m, ditch_model_path_stats *out);
 
 /* ------------------------------------------------------------------------ */
+/* Generation (model.generate / generateKeep, model.zig:5358-5444; the
+ * keyword scorer's decode loop, engine.zig:254-268).                       */
+
+/* KvCache.initFor(model, batch, max_len) (model.zig:2586-2724): every
+ * layer's keys and values for n_prompts x max_len positions in HBM, kept
+ * across calls (max_len <= 1024).                                          */
+typedef struct ditch_hip_kv_cache ditch_hip_kv_cache;
+ditch_hip_kv_cache *ditch_hip_kv_cache_create(ditch_hip_model *m, uint32_t n_prompts,
+                                              uint32_t max_len);
+void ditch_hip_kv_cache_free(ditch_hip_kv_cache *c);
+/* model.forward through the persistent cache: rows {b, pos} write their
+ * keys and values at (b, pos) of every layer and attend to positions
+ * 0..pos of their prompt, including those earlier calls wrote (a prefill,
+ * then one row per prompt a step). Device buffers, the context stream; rows
+ * outside the cache are skipped as in ditch_hip_forward_device.            */
+int32_t ditch_hip_forward_cached(ditch_hip_model *m, ditch_hip_kv_cache *c,
+                                 const uint32_t *d_tokens, const ditch_row *d_rows,
+                                 uint64_t n, const uint64_t *d_logit_rows,
+                                 uint64_t n_logit, float *d_logits,
+                                 uint64_t logits_bytes);
+/* model.Sampler (model.zig:5208-5264): temperature <= 0 is greedy; top_k is
+ * clamped to 1..256. The draw is a uniform from splitmix64 of (seed, step,
+ * prompt) (the reference draws from Zig's Xoshiro256 stream), so sampled
+ * tokens follow the same distribution, not the same sequence.             */
+typedef struct ditch_sampler {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    uint64_t seed;
+} ditch_sampler;
+/* The next token of each of n logit rows on the device: the first maximum
+ * (argmax, model.zig:5194-5204) when `sampler` is NULL or greedy, else the
+ * Sampler's pick. d_row_ids (may be NULL) names the prompt of each row.    */
+int32_t ditch_hip_pick_tokens_device(ditch_hip *h, uint32_t *d_out, const float *d_logits,
+                                     uint64_t n, uint64_t vocab,
+                                     const ditch_sampler *sampler, uint64_t step,
+                                     const uint32_t *d_row_ids, void *stream);
+/* generateKeep: prefill of n_prompts prompts (tokens flattened, prompt_lens
+ * each), then up to max_new_tokens tokens per prompt, a prompt stopping at
+ * an EOS id or a full cache. Host buffers: out_tokens [n_prompts]
+ * [max_new_tokens], out_lens [n_prompts], first_logits (NULL or
+ * [n_prompts][vocab], the prefill's next-token logits).                    */
+int32_t ditch_hip_generate(ditch_hip_model *m, ditch_hip_kv_cache *c,
+                           const uint32_t *tokens, const uint64_t *prompt_lens,
+                           uint64_t n_prompts, uint64_t max_new_tokens,
+                           const uint32_t *eos_ids, uint64_t n_eos,
+                           const ditch_sampler *sampler, uint32_t *out_tokens,
+                           uint64_t *out_lens, float *first_logits);
+
+/* ------------------------------------------------------------------------ */
 /* Rank-k edit, `none` mode (abliterate.zig:264-280): a = V^T W ([k][cols]),
  * b = -weight * V ([rows][k]) for directions v [k][rows]. Host buffers.    */
 int32_t ditch_hip_edit_delta(ditch_hip *h, float *a, float *b,
