@@ -193,6 +193,8 @@ PROTOTYPES = {
     "ditch_hip_forward": (I32, [P, P, P, U64, P, U64, P, P, U64, P]),
     "ditch_hip_forward_device": (I32, [P, P, P, U64, U32, U32, P, U64, P, U64, P, U64, P, U64]),
     "ditch_hip_model_path_stats": (I32, [P, P]),
+    "ditch_hip_model_load": (P, [P, C.c_char_p, U64]),
+    "ditch_hip_model_get_config": (I32, [P, P]),
     "ditch_hip_kv_cache_create": (P, [P, U32, U32]),
     "ditch_hip_kv_cache_free": (None, [P]),
     "ditch_hip_forward_cached": (I32, [P, P, P, P, U64, P, U64, P, U64]),

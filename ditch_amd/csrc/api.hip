@@ -21,6 +21,7 @@ void model_reset_deltas(ditch_hip_model *m);
 void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight,
                    int mode, int64_t lora_rank, uint64_t seed, int ablate);
 ditch_hip_kv_cache *kv_cache_create(ditch_hip_model *m, int64_t B, int64_t T);
+ditch_hip_model *model_load(ditch_hip *h, const char *path, uint64_t expert_cache);
 void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens, const uint64_t *lens, int64_t B,
               int64_t max_new, const uint32_t *eos, int64_t n_eos, const ditch_sampler *smp, uint32_t *out_tokens,
               uint64_t *out_lens, float *first_logits);
@@ -475,6 +476,19 @@ ditch_hip_model *ditch_hip_model_create(ditch_hip *h, const ditch_model_config *
         m = model_create(h, cfg);
     });
     return rc == DITCH_OK ? m : nullptr;
+}
+
+ditch_hip_model *ditch_hip_model_load(ditch_hip *h, const char *path, uint64_t expert_cache_bytes) {
+    ditch_hip_model *m = nullptr;
+    int32_t rc = guarded(h, [&] { m = model_load(h, path, expert_cache_bytes); });
+    return rc == DITCH_OK ? m : nullptr;
+}
+
+int32_t ditch_hip_model_get_config(const ditch_hip_model *m, ditch_model_config *out) {
+    if (!m || !out) return DITCH_INVALID_ARGUMENT;
+    *out = m->c;
+    out->rope_factors = nullptr;
+    return DITCH_OK;
 }
 
 void ditch_hip_model_free(ditch_hip_model *m) {

@@ -6,6 +6,7 @@ HIP library; a failing status raises `DeviceError` (there is no CPU path
 here, the reference's own tensor.zig is the CPU path of a Zig caller).
 """
 import ctypes
+import os
 
 import numpy as np
 
@@ -256,6 +257,13 @@ class Tensor:
         self.dev.check(self.dev.lib.ditch_hip_tensor_dequant(self.dev.h, d_out, out_bytes, self.handle, row0, nrows))
 
 
+class _LoadedSpec:
+    """The configuration of a model read from disk (what Model needs of a spec)."""
+
+    def __init__(self, config):
+        self.config = config
+
+
 class Model:
     """A resident model (ditch_hip_model) built from a ModelSpec."""
 
@@ -272,6 +280,22 @@ class Model:
             dev.check(dev.lib.ditch_hip_model_set_expert_cache(self.h, int(expert_cache_bytes)))
         for (layer, slot, expert), w in spec.tensors.items():
             dev.check(dev.lib.ditch_hip_model_set(self.h, layer, slot, expert, w.ref()))
+
+    @classmethod
+    def load(cls, dev: Device, path, expert_cache_bytes=0):
+        """A model read from a checkpoint on disk (ditch_hip_model_load): a
+        Hugging Face directory or a GGUF file."""
+        h = dev.lib.ditch_hip_model_load(dev.h, os.fsencode(path), int(expert_cache_bytes))
+        if not h:
+            raise DeviceError(abi.DEVICE_FAILED, dev.lib.ditch_hip_last_error(dev.h).decode())
+        m = cls.__new__(cls)
+        m.dev, m.h = dev, h
+        cfg = abi.ModelConfig()
+        dev.check(dev.lib.ditch_hip_model_get_config(h, ctypes.byref(cfg)))
+        m.cfg = cfg
+        m.spec = _LoadedSpec({name: getattr(cfg, name) for name, _ in cfg._fields_ if name not in ("moe_layers",
+                                                                                                   "rope_factors")})
+        return m
 
     def expert_cache_stats(self):
         st = abi.ExpertCacheStats()

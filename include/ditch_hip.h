@@ -425,6 +425,23 @@ int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m);
 /* HBM bytes held by the model's weights.                                   */
 uint64_t ditch_hip_model_bytes(const ditch_hip_model *m);
 
+/* Loads a checkpoint from disk into a resident model (Model.load,
+ * model.zig, with safetensors.zig / gguf_model.zig underneath): `path` is a
+ * Hugging Face directory (config.json and *.safetensors shards: plain
+ * f32/f16/bf16, FP8 with block scales, compressed-tensors pack-quantized
+ * INT and mxfp4-pack-quantized, all kept packed) or a GGUF v3 file (block
+ * types kept packed; llama's q/k rows restored to the Hugging Face order).
+ * Families: llama, qwen2, qwen3, qwen3_moe, deepseek_v3. The files are
+ * memory-mapped and each weight goes through pinned host memory to HBM.
+ * expert_cache_bytes > 0 streams the routed experts as
+ * ditch_hip_model_set_expert_cache does. NULL on failure, with the message
+ * in ditch_hip_last_error(h).                                              */
+ditch_hip_model *ditch_hip_model_load(ditch_hip *h, const char *path,
+                                      uint64_t expert_cache_bytes);
+/* The model's configuration (moe_layers points into the model; valid while
+ * it lives; rope_factors is NULL).                                         */
+int32_t ditch_hip_model_get_config(const ditch_hip_model *m, ditch_model_config *out);
+
 /* model.forward with ForwardOptions{capture_rows, residuals, logit_rows}:
  * host buffers. residuals: [(layers+1)][n_capture][hidden] (entry 0 = the
  * embedding, entry l+1 = after layer l, model.zig:4856-4862); logits:
