@@ -292,7 +292,9 @@ __device__ __forceinline__ void decode_tile(const TileView &w, const Raw &raw, c
 }
 
 // acc += (sum of the activation terms) . B, with the format's structure
-template <int TF, int XT>
+// (NR < 4: only the first NR of the lane's four tokens are used, so the
+// block-scale multiply-adds of the others are skipped)
+template <int TF, int XT, int NR = 4>
 __device__ __forceinline__ void mac(floatx4 &acc, const u32x4 (&x)[XT], const u32x4 &bh, const u32x4 &bl,
                                     float tile_scale) {
     if constexpr (Fmt<TF>::acc_scale) {
@@ -300,7 +302,7 @@ __device__ __forceinline__ void mac(floatx4 &acc, const u32x4 (&x)[XT], const u3
 #pragma unroll
         for (int e = 0; e < XT; e++) t = mfma_bf16(x[e], bh, t);
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(tile_scale, t[r], acc[r]);
+        for (int r = 0; r < NR; r++) acc[r] = __builtin_fmaf(tile_scale, t[r], acc[r]);
     } else if constexpr (Fmt<TF>::fp32) {
         // 8 rank-4 steps over k = 8 * (lane / 16) + s: A and B hold the same
         // k in the same register, so the 32 products of the tile are summed

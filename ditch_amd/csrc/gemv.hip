@@ -124,8 +124,11 @@ __global__ __launch_bounds__(256) void gv_split_kernel(GvSplitParams q) {
 // ---------------------------------------------------------------------------
 
 // LX: the activations are f32 rows split in the kernel (n <= GV_XN), else
-// fragments from gv_split_kernel.
-template <int TF, int NT, int XT, int D, int W, bool LX>
+// fragments from gv_split_kernel. PPC > 0 (LX): the column-pair passes are
+// known at compile time and every unit lies inside K with 8-byte aligned
+// rows, so the activation loads carry no per-pass or per-unit conditions.
+// NR < 4: n = NR tokens (the lanes' other accumulator rows are not stored).
+template <int TF, int NT, int XT, int D, int W, bool LX, int PPC = 0, int NR = 4>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
     if (!select_segment(p, 0)) return;
     constexpr int TL = Fmt<TF>::tiles;
@@ -155,8 +158,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
     // LX: the lane's column pairs: pass m takes pair lane + 64 m of the unit's
     // n x UK / 2 (token-major); passes past n tokens are skipped, lanes past
     // them repeat token n - 1
-    const int pp = LX ? (int)((p.n * UK / 2 + 63) / 64) : 0;
+    const int pp = PPC ? PPC : LX ? (int)((p.n * UK / 2 + 63) / 64) : 0;
     const float *xrow[PP];
+    uint32_t xo[PP];  // PPC: byte offset of the lane's pair in unit 0 (activations under 4 GiB)
     uint32_t lofs[PP];  // LDS byte offset of the pair's first term word in the wave's slot
     int kl[PP];         // column of the pair in the unit
 #pragma unroll
@@ -166,6 +170,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
         const int k = 2 * (P % (UK / 2));
         kl[m] = k;
         xrow[m] = LX ? p.x + (p.row_index ? (int64_t)p.row_index[pt] : pt) * p.ldx : nullptr;
+        xo[m] = LX ? (uint32_t)(((p.row_index ? (int64_t)p.row_index[pt] : pt) * p.ldx + k) * 4) : 0u;
         if constexpr (FP32) lofs[m] = (uint32_t)(((((k / 32) * XT + (k % 8) / 4) * 4 + (k % 32) / 8) * GV_XN + pt) * 16 + (k % 4) * 4);
         else lofs[m] = (uint32_t)(((((k / 32) * XT) * 4 + (k % 32) / 8) * GV_XN + pt) * 16 + ((k % 8) / 2) * 4);
     }
@@ -194,7 +199,10 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
         // unit u - 1 is multiplied) waits on them and not on u's codes
         if constexpr (LX) {
             const int64_t kb = u * UK;
-            if (x_pairs && kb + UK <= K) {
+            if (PPC > 0) {
+#pragma unroll
+                for (int m = 0; m < PPC; m++) xp[j][m] = gload<float2>((const char *)(p.x + kb) + xo[m]);
+            } else if (x_pairs && kb + UK <= K) {
 #pragma unroll
                 for (int m = 0; m < PP; m++)
                     if (m < pp) xp[j][m] = gload<float2>(xrow[m] + kb + kl[m]);
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
         if constexpr (LX) {
 #pragma unroll
             for (int m = 0; m < PP; m++)
-                if (m < pp) {
+                if (PPC > 0 ? m < PPC : m < pp) {
                     if constexpr (FP32) {
                         *(uint2 *)(slot + lofs[m]) = make_uint2(f2u(xp[j][m].x), f2u(xp[j][m].y));
                     } else {
@@ -282,7 +290,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
                 u32x4 bh, bl = u32x4{0, 0, 0, 0};
                 float ts = 1.f;
                 gv_decode<TF>(p.w, raw[j][i], sd[j][i], t, bh, bl, ts);
-                mac<TF, XT>(acc[i], xa[t], bh, bl, ts);
+                mac<TF, XT, NR>(acc[i], xa[t], bh, bl, ts);
             }
         }
     };
@@ -358,8 +366,20 @@ static void gemv_launch(const GemmParams &p, int64_t rows, unsigned nseg, bool l
     constexpr int NT = GEMV_NT, D = GEMV_D / Fmt<TF>::tiles > 1 ? GEMV_D / Fmt<TF>::tiles : 1, W = GEMV_W;
     const int64_t groups = (rows + 15) / 16;
     const dim3 grid((unsigned)((groups + NT - 1) / NT), 1, nseg);
-    if (lx) hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, true>), grid, dim3(64 * W), 0, s, p);
-    else hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, false>), grid, dim3(64 * W), 0, s, p);
+    if (lx) {
+        // every unit inside K, rows 8-byte aligned: the passes as a constant
+        constexpr int UK = TF == TF_Q8 || TF == TF_FP8 ? 64 : (TF == TF_MX4 || TF == TF_INT4) ? 128 : 32;
+        const int pp = (int)((p.n * UK / 2 + 63) / 64);
+        const bool full = p.w.cols % UK == 0 && (p.ldx & 1) == 0 && ((uintptr_t)p.x & 7) == 0 && nseg == 1 &&
+                          !p.row_index && (uint64_t)p.n * p.ldx * 4 < (1ull << 32);
+        if (XT == 2 && full && pp == 1 && p.n == 1)
+            hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, true, 1, 1>), grid, dim3(64 * W), 0, s, p);
+        else if (XT == 2 && full && pp == 1)
+            hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, true, 1>), grid, dim3(64 * W), 0, s, p);
+        else if (XT == 2 && full && pp == 2)
+            hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, true, 2>), grid, dim3(64 * W), 0, s, p);
+        else hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, true>), grid, dim3(64 * W), 0, s, p);
+    } else hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, false>), grid, dim3(64 * W), 0, s, p);
 }
 
 template <int TF>
