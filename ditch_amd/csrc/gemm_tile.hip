@@ -106,6 +106,16 @@ template <> struct TileCfg<TF_INT4> { static constexpr int TPS = 4, NU = 1, NS =
 template <> struct TileCfg<TF_Q8> { static constexpr int TPS = 2, NU = 1, NS = 1; };    // unit s; two f16 block scales
 
 // Side word of stage s, entry j, for a row whose side row starts at `base`.
+// Calls f(std::integral_constant<int, j>) for j = 0 .. N-1 (instruction
+// immediates must be constant expressions).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 template <int TF>
 __device__ __forceinline__ const uint32_t *side_word(const TileView &w, const uint32_t *side, int64_t base, int64_t s,
                                                      int j) {
@@ -345,56 +355,70 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     constexpr int CA = FR / CW, CB = WAVES * WN * NU / CW, CS = NS ? WAVES * NS / CW : 0;
     static_assert(FR % CW == 0 && (WAVES * WN * NU) % CW == 0 && (WAVES * NS) % CW == 0, "copies split evenly");
     static_assert(WN == 4, "one side-word copy covers a wave's four row groups");
+    // Copier ck takes a contiguous run of each stage array (A fragments
+    // ck CA .., code pieces ck CB .., side words ck CS ..) and writes it in
+    // 4 KiB windows: an LDS copy writes at M0 plus its instruction offset
+    // (which moves the global address too, so the source pointer is lowered
+    // by it), and an M0 write stalls the wave until the previous copy has
+    // landed; one M0 value per window instead of one per copy.
     const bool copier = wave >= WAVES - CW;
     const int ck = copier ? wave - (WAVES - CW) : 0;
-    const u32x4 *asrc[CA];
-#pragma unroll
-    for (int j = 0; j < CA; j++) {
-        const int f = ck + CW * j;
+    // sources: a uniform base per copy (scalar registers) plus the lane's 16
+    // bytes of the 1 KiB piece (one shared 32-bit register); per-lane 64-bit
+    // pointers would not fit beside the products' registers, and a spilled
+    // pointer's reload waits for every copy in flight
+    // (computed per copy from a few uniform values in scalar registers:
+    // arrays of precomputed bases exhaust them and end up spilled)
+    const uint32_t lofs = (uint32_t)lane * 16;
+    auto asrc = [&](int j) {  // copy j's A fragment, stage 0
+        const int f = ck * CA + j;
         const int m = f / (TPS * XT), t = (f / XT) % TPS, e = f % XT;
         int64_t mb = m16_0 + m;
         mb = mb < m16_n ? mb : m16_n - 1;
-        asrc[j] = p.xs + ((mb * p.ldk + t) * XT + e) * 64 + lane;
-    }
+        return (const char *)(p.xs + ((mb * p.ldk + t) * XT + e) * 64);
+    };
     auto group_of = [&](int wq, int i) {
         const int64_t gi = (int64_t)nt * (OG * WGN) + (wq % WGN) * OG + (i % OG);
         return gi < groups ? gi : groups - 1;
     };
-    const uint8_t *bsrc[CB];
-#pragma unroll
-    for (int j = 0; j < CB; j++) {
-        const int q = ck + CW * j, wq = q / (WN * NU), i = (q / NU) % WN;
+    auto bsrc = [&](int j) {  // copy j's code pieces, unit 0
+        const int q = ck * CB + j, wq = q / (WN * NU), i = (q / NU) % WN;
         const TileView &wi = (GLU && i >= OG) ? w2 : w;
-        bsrc[j] = wi.codes + group_of(wq, i) * units * 1024 + lane * 16;
-    }
+        return wi.codes + group_of(wq, i) * units * 1024;
+    };
     const uint32_t *ssrc[CS > 0 ? CS : 1];
 #pragma unroll
     for (int j = 0; j < CS; j++) {
-        const int q = ck + CW * j, wq = q / NS1, i = lane >> 4;  // lane l: row l % 16 of row group l / 16
+        const int q = ck * CS + j, wq = q / NS1, i = lane >> 4;  // lane l: row l % 16 of row group l / 16
         const TileView &wi = (GLU && i >= OG) ? w2 : w;
         ssrc[j] = wi.side + side_row(wi, group_of(wq, i), lane);
     }
 
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
         if (!copier) return;
-#pragma unroll
-        for (int j = 0; j < CA; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + TPS * s * XT * 64),
-                                             (lds_void *)&As[(ck + CW * j) * 64], 16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < CB; j++) {
-            const int q = ck + CW * j, u = q % NU;
+        // copy j of a run of 1 KiB pieces: window j / 4, offset (j % 4) KiB
+        static_for<CA>([&](auto jc) {
+            constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
+            __builtin_amdgcn_global_load_lds((const void *)(asrc(j) + (TPS * s * XT * 64 * 16 - off) + lofs),
+                                             (lds_void *)&As[(ck * CA + j / 4 * 4) * 64], 16, off, 0);
+        });
+        static_for<CB>([&](auto jc) {
+            constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
+            const int q = ck * CB + j, u = q % NU;
             int64_t un = s * NU + u;
             un = un < units ? un : units - 1;  // a bf16 stage's missing second unit: decoded as zero
-            __builtin_amdgcn_global_load_lds((const void *)(bsrc[j] + un * 1024), (lds_void *)&Bs[q * 64], 16, 0, 0);
-        }
+            __builtin_amdgcn_global_load_lds((const void *)(bsrc(j) + (un * 1024 - off) + lofs),
+                                             (lds_void *)&Bs[(ck * CB + j / 4 * 4) * 64], 16, off, 0);
+        });
         if constexpr (NS > 0) {
-#pragma unroll
-            for (int j = 0; j < CS; j++) {
-                const int q = ck + CW * j;
-                __builtin_amdgcn_global_load_lds((const void *)side_word<TF>(w, ssrc[j], 0, s, q % NS1),
-                                                 (lds_void *)&Ss[q * 64], 4, 0, 0);
-            }
+            // 256 B each: sixteen to a window
+            static_for<CS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value, off = (j % 16) * 256;
+                const int q = ck * CS + j;
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)((const char *)side_word<TF>(w, ssrc[j], 0, s, q % NS1) - off),
+                    (lds_void *)&Ss[(ck * CS + j / 16 * 16) * 64], 4, off, 0);
+            });
         }
     };
 
