@@ -138,6 +138,11 @@ class PathStats(C.Structure):
     _fields_ = [("moe_device_planned", C.c_uint64), ("moe_host_planned", C.c_uint64)]
 
 
+class ResidencyStats(C.Structure):
+    """`ditch_residency_stats` (compute.Residency's counters)."""
+    _fields_ = [(n, C.c_uint64) for n in ("budget", "used", "entries", "hits", "misses", "evictions", "enabled")]
+
+
 class ExpertCacheStats(C.Structure):
     """`ditch_expert_cache_stats` (expert_cache.Stats)."""
     _fields_ = [(n, C.c_uint64) for n in ("capacity", "slots", "resident", "hits", "misses", "prefetched",
@@ -157,6 +162,8 @@ PROTOTYPES = {
     "ditch_hip_name": (C.c_char_p, [P]),
     "ditch_hip_last_error": (C.c_char_p, [P]),
     "ditch_hip_forget_weights": (None, [P]),
+    "ditch_hip_set_residency": (I32, [P, U64, I32]),
+    "ditch_hip_residency_stats": (I32, [P, P]),
     "ditch_hip_stream": (P, [P]),
     "ditch_hip_sync": (I32, [P]),
     "ditch_hip_matmulT": (I32, [P, P, P, U64, P]),

@@ -119,13 +119,35 @@ ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
 void ditch_hip_close(ditch_hip *h) {
     if (!h) return;
     (void)hipStreamSynchronize(h->stream);
+    residency_clear(h);
     (void)hipStreamDestroy(h->stream);
     delete h;
 }
 
 const char *ditch_hip_name(ditch_hip *h) { return h ? h->name.c_str() : ""; }
 const char *ditch_hip_last_error(ditch_hip *h) { return h ? h->last_error.c_str() : "null context"; }
-void ditch_hip_forget_weights(ditch_hip *h) { (void)h; }
+void ditch_hip_forget_weights(ditch_hip *h) {
+    if (!h) return;
+    std::lock_guard<std::mutex> lk(h->mu);
+    (void)hipStreamSynchronize(h->stream);
+    residency_clear(h);
+}
+
+int32_t ditch_hip_set_residency(ditch_hip *h, uint64_t budget_bytes, int32_t weights_stable) {
+    return guarded(h, [&] {
+        DITCH_TRY_HIP(hipStreamSynchronize(h->stream));
+        residency_configure(h, budget_bytes, weights_stable != 0);
+    });
+}
+
+int32_t ditch_hip_residency_stats(ditch_hip *h, ditch_residency_stats *out) {
+    return guarded(h, [&] {
+        DITCH_CHECK(out, DITCH_INVALID_ARGUMENT, "NULL stats");
+        const auto &r = h->res;
+        *out = ditch_residency_stats{r.budget, r.used, (uint64_t)r.entries.size(), r.hits, r.misses, r.evictions,
+                                     (uint64_t)(r.budget > 0 && r.stable)};
+    });
+}
 void *ditch_hip_stream(ditch_hip *h) { return h ? (void *)h->stream : nullptr; }
 int32_t ditch_hip_sync(ditch_hip *h) {
     return guarded(h, [&] { DITCH_TRY_HIP(hipStreamSynchronize(h->stream)); });
@@ -139,7 +161,8 @@ int32_t ditch_hip_matmulT(ditch_hip *h, float *out, const float *x, uint64_t n, 
         DITCH_CHECK(w && out && x, DITCH_INVALID_ARGUMENT, "NULL argument");
         if (n == 0 || w->rows == 0) return;
         hipStream_t s = h->stream;
-        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        WeightRef t;
+        acquire_weight(h, w, s, t);
         Tmp dx(n * w->cols * 4), dout(n * w->rows * 4);
         h2d(dx.p, x, n * w->cols * 4, s);
         MatmulEpilogue ep;
@@ -155,7 +178,8 @@ int32_t ditch_hip_matvecTMulti(ditch_hip *h, float *out, const ditch_weight *w, 
         DITCH_CHECK(w && out && y, DITCH_INVALID_ARGUMENT, "NULL argument");
         if (q == 0) return;
         hipStream_t s = h->stream;
-        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        WeightRef t;
+        acquire_weight(h, w, s, t);
         Tmp dy(q * w->rows * 4), dout(q * w->cols * 4), part(matvecT_partials_floats(t->v, q) * 4);
         h2d(dy.p, y, q * w->rows * 4, s);
         launch_matvecT(dout.as<float>(), t->v, dy.as<float>(), (int64_t)q, s, part.as<float>());
@@ -168,7 +192,8 @@ int32_t ditch_hip_rowNorms(ditch_hip *h, float *out, const ditch_weight *w) {
     return guarded(h, [&] {
         DITCH_CHECK(w && out, DITCH_INVALID_ARGUMENT, "NULL argument");
         hipStream_t s = h->stream;
-        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        WeightRef t;
+        acquire_weight(h, w, s, t);
         Tmp dout(w->rows * 4);
         launch_row_norms(dout.as<float>(), t->v, s);
         d2h(out, dout.p, w->rows * 4, s);
@@ -675,7 +700,8 @@ int32_t ditch_hip_edit_delta(ditch_hip *h, float *a, float *b, const ditch_weigh
     return guarded(h, [&] {
         DITCH_CHECK(a && b && w && v && k > 0, DITCH_INVALID_ARGUMENT, "edit_delta arguments");
         hipStream_t s = h->stream;
-        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        WeightRef t;
+        acquire_weight(h, w, s, t);
         Tmp dv(k * w->rows * 4), da(k * w->cols * 4), part(matvecT_partials_floats(t->v, k) * 4);
         h2d(dv.p, v, k * w->rows * 4, s);
         launch_matvecT(da.as<float>(), t->v, dv.as<float>(), (int64_t)k, s, part.as<float>());
@@ -717,7 +743,8 @@ int32_t ditch_hip_edit_delta_ex(ditch_hip *h, float *a, uint64_t a_len, float *b
         DITCH_CHECK(a_len >= rank * w->cols && b_len >= w->rows * rank, DITCH_INVALID_ARGUMENT,
                     "edit_delta_ex: a or b shorter than the delta");
         hipStream_t s = h->stream;
-        std::unique_ptr<ditch_hip_tensor, void (*)(ditch_hip_tensor *)> t(upload_weight(h, w, s), free_tensor);
+        WeightRef t;
+        acquire_weight(h, w, s, t);
         float *da = nullptr, *db = nullptr;
         int64_t r = 0;
         edit_delta_device(t->v, v, (int64_t)k, weight, opts->row_normalization, (int64_t)opts->lora_rank, opts->seed,

@@ -170,6 +170,23 @@ struct ditch_hip {
     // with hipGetSymbolAddress when the context opens
     void *static_scratch = nullptr;
     std::string scratch_error;
+    // registered copies of the weights the per-call entry points receive
+    // (tiles.hip, residency_*)
+    struct ResidencyEntry {
+        const void *data;
+        size_t len;
+        uint64_t desc;  // hash of the rest of the descriptor
+        uint64_t sig;   // hash of sampled bytes of the weight's buffers
+        uint64_t bytes; // device bytes of the registered copy
+        ditch_hip_tensor *t;
+        uint64_t used_at;
+    };
+    struct Residency {
+        uint64_t budget = 0;
+        bool stable = false;
+        uint64_t used = 0, clock = 0, hits = 0, misses = 0, evictions = 0;
+        std::vector<ResidencyEntry> entries;
+    } res;
 };
 
 namespace ditch {
@@ -177,6 +194,22 @@ namespace ditch {
 // tiles.hip
 ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s);
 void free_tensor(ditch_hip_tensor *t);
+// A per-call weight: the residency cache's copy (owned = false) or a fresh
+// upload the caller frees (owned = true).
+struct WeightRef {
+    ditch_hip_tensor *t = nullptr;
+    bool owned = false;
+    WeightRef() = default;
+    WeightRef(const WeightRef &) = delete;
+    WeightRef &operator=(const WeightRef &) = delete;
+    ditch_hip_tensor *operator->() const { return t; }
+    ~WeightRef() {
+        if (owned) free_tensor(t);
+    }
+};
+void acquire_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s, WeightRef &ref);
+void residency_configure(ditch_hip *h, uint64_t budget, bool stable);
+void residency_clear(ditch_hip *h);
 void launch_dequant(const TileView &v, void *out, int64_t row0, int64_t nrows, hipStream_t s);
 bool is_bf16_virtual(int32_t dtype);
 

@@ -857,4 +857,125 @@ ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t
     return t;
 }
 
+// ---------------------------------------------------------------------------
+// Residency of the per-call weights (compute.Residency, compute.zig:567-693):
+// a byte-budgeted least-recently-used set of registered copies keyed by the
+// host address and length of the weight's codes and the rest of its
+// descriptor, each with a signature of sampled bytes so that new contents
+// at a cached address are a miss, never a stale copy. Caching by address is
+// sound only while the host buffers stay valid and unique (memory-mapped
+// weights), so it is on only with `stable`; forget_weights clears it.
+
+static uint64_t mix64(uint64_t h) {
+    h ^= h >> 33;
+    h *= 0xff51afd7ed558ccdull;
+    h ^= h >> 33;
+    h *= 0xc4ceb9fe1a85ec53ull;
+    return h ^ (h >> 33);
+}
+
+// up to four 64-byte samples (start, two interior points, end), or the whole
+// buffer when it is at most 256 bytes
+static uint64_t sample_hash(uint64_t h, const void *p, size_t len) {
+    if (!p || !len) return mix64(h ^ 0x9e3779b97f4a7c15ull);
+    const uint8_t *b = (const uint8_t *)p;
+    auto feed = [&](size_t at, size_t n) {
+        for (size_t k = 0; k < n; k++) h = (h ^ b[at + k]) * 0x100000001b3ull;
+    };
+    h = mix64(h ^ len);
+    if (len <= 256) feed(0, len);
+    else
+        for (size_t at : {(size_t)0, len / 3, 2 * (len / 3), len - 64}) feed(at, 64);
+    return mix64(h);
+}
+
+static uint64_t weight_signature(const ditch_weight *w, const RawSizes &z) {
+    uint64_t h = sample_hash(0x5151, w->data, z.data);
+    h = sample_hash(h, w->scale, z.scale);
+    h = sample_hash(h, w->zero, z.zero);
+    return sample_hash(h, w->g_idx, z.gidx);
+}
+
+static uint64_t weight_desc(const ditch_weight *w) {
+    const uint64_t f[] = {(uint64_t)w->dtype, (uint64_t)w->scale_dtype, w->rows, w->cols,
+                          (uint64_t)(uintptr_t)w->scale, w->scale_rows, w->scale_cols, w->block_rows,
+                          w->block_cols, w->row_shard, (uint64_t)w->fp8_e5m2, (uint64_t)w->bits, w->group,
+                          (uint64_t)(uintptr_t)w->zero, (uint64_t)(uintptr_t)w->g_idx};
+    uint64_t h = 0x1234;
+    for (uint64_t v : f) h = mix64(h ^ v);
+    return h;
+}
+
+static void residency_drop(ditch_hip *h, size_t i) {
+    auto &r = h->res;
+    free_tensor(r.entries[i].t);
+    r.used -= r.entries[i].bytes < r.used ? r.entries[i].bytes : r.used;
+    r.entries[i] = r.entries.back();
+    r.entries.pop_back();
+    r.evictions++;
+}
+
+// evicts least recently used entries until `bytes` more fit; false when they
+// cannot (larger than the budget)
+static bool residency_make_room(ditch_hip *h, uint64_t bytes) {
+    auto &r = h->res;
+    if (bytes > r.budget) return false;
+    while (r.used + bytes > r.budget && !r.entries.empty()) {
+        size_t oldest = 0;
+        for (size_t k = 1; k < r.entries.size(); k++)
+            if (r.entries[k].used_at < r.entries[oldest].used_at) oldest = k;
+        residency_drop(h, oldest);
+    }
+    return r.used + bytes <= r.budget;
+}
+
+void residency_clear(ditch_hip *h) {
+    auto &r = h->res;
+    for (auto &e : r.entries) free_tensor(e.t);
+    r.entries.clear();
+    r.used = 0;
+}
+
+void residency_configure(ditch_hip *h, uint64_t budget, bool stable) {
+    auto &r = h->res;
+    r.budget = budget;
+    r.stable = stable;
+    if (!stable || budget == 0) residency_clear(h);
+    else residency_make_room(h, 0);
+}
+
+void acquire_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s, WeightRef &ref) {
+    auto &r = h->res;
+    DITCH_CHECK(w && w->rows > 0 && w->cols > 0, DITCH_INVALID_ARGUMENT, "empty weight");
+    if (r.budget == 0 || !r.stable) {
+        ref.t = upload_weight(h, w, s);
+        ref.owned = true;
+        return;
+    }
+    const RawSizes z = raw_sizes(w);
+    const uint64_t desc = weight_desc(w), sig = weight_signature(w, z);
+    for (size_t k = 0; k < r.entries.size(); k++) {
+        auto &e = r.entries[k];
+        if (e.data == w->data && e.len == z.data && e.desc == desc) {
+            if (e.sig != sig) {  // new contents at a cached address
+                residency_drop(h, k);
+                break;
+            }
+            e.used_at = ++r.clock;
+            r.hits++;
+            ref.t = e.t;
+            ref.owned = false;
+            return;
+        }
+    }
+    r.misses++;
+    ref.t = upload_weight(h, w, s);
+    ref.owned = true;
+    if (residency_make_room(h, ref.t->bytes)) {
+        r.entries.push_back(ditch_hip::ResidencyEntry{w->data, z.data, desc, sig, ref.t->bytes, ref.t, ++r.clock});
+        r.used += ref.t->bytes;
+        ref.owned = false;
+    }
+}
+
 }  // namespace ditch

@@ -62,6 +62,18 @@ class Device:
     def sync(self):
         self.check(self.lib.ditch_hip_sync(self.h))
 
+    def set_residency(self, budget_bytes, weights_stable=True):
+        """compute.Residency for the per-call entry points (0: upload, compute, drop)."""
+        self.check(self.lib.ditch_hip_set_residency(self.h, int(budget_bytes), 1 if weights_stable else 0))
+
+    def residency_stats(self):
+        st = abi.ResidencyStats()
+        self.check(self.lib.ditch_hip_residency_stats(self.h, ctypes.byref(st)))
+        return {k: getattr(st, k) for k, _ in abi.ResidencyStats._fields_}
+
+    def forget_weights(self):
+        self.lib.ditch_hip_forget_weights(self.h)
+
     # VTable -----------------------------------------------------------------
 
     def matmulT(self, x, w: HostWeight):

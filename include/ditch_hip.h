@@ -119,6 +119,28 @@ const char *ditch_hip_last_error(ditch_hip *h);
 /* VTable.forgetWeights (compute.zig:96-97, 325-327): drops every weight the
  * per-call entry points keep resident. Registered tensors are unaffected. */
 void ditch_hip_forget_weights(ditch_hip *h);
+/* compute.Residency (compute.zig:567-693, the `--gpu-memory N` budget): the
+ * per-call entry points that take a ditch_weight (matmulT, matvecTMulti,
+ * rowNorms, edit_delta, edit_delta_ex) keep the registered (re-tiled) copy
+ * of each weight in a least-recently-used set of at most `budget_bytes`
+ * device bytes, keyed by the host address and length of its codes and the
+ * rest of its descriptor, with a signature of sampled bytes of its buffers:
+ * new contents at a cached address are a miss. Keying by address is sound
+ * only while host weights stay valid and unique (memory-mapped files,
+ * compute.weights_stable); with weights_stable = 0 or a zero budget every
+ * call uploads, computes and drops (the default). A smaller budget evicts
+ * at once; forget_weights clears.                                          */
+int32_t ditch_hip_set_residency(ditch_hip *h, uint64_t budget_bytes, int32_t weights_stable);
+typedef struct ditch_residency_stats {
+    uint64_t budget;
+    uint64_t used;
+    uint64_t entries;
+    uint64_t hits;
+    uint64_t misses;
+    uint64_t evictions;
+    uint64_t enabled;
+} ditch_residency_stats;
+int32_t ditch_hip_residency_stats(ditch_hip *h, ditch_residency_stats *out);
 /* The HIP stream every call of this context runs on (hipStream_t).         */
 void *ditch_hip_stream(ditch_hip *h);
 /* Waits for the context's stream.                                          */
