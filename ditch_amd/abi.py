@@ -146,7 +146,12 @@ class ResidencyStats(C.Structure):
 class ExpertCacheStats(C.Structure):
     """`ditch_expert_cache_stats` (expert_cache.Stats)."""
     _fields_ = [(n, C.c_uint64) for n in ("capacity", "slots", "resident", "hits", "misses", "prefetched",
-                                          "bytes_read", "evictions", "slot_bytes")]
+                                          "bytes_read", "evictions", "slot_bytes", "warmed")]
+
+
+class HotExpert(C.Structure):
+    """`ditch_hot_expert` (ExpertCache.Hot)."""
+    _fields_ = [("layer", C.c_uint32), ("expert", C.c_uint32), ("uses", C.c_uint64)]
 
 
 P = C.c_void_p
@@ -163,6 +168,8 @@ PROTOTYPES = {
     "ditch_hip_last_error": (C.c_char_p, [P]),
     "ditch_hip_forget_weights": (None, [P]),
     "ditch_hip_set_residency": (I32, [P, U64, I32]),
+    "ditch_hip_model_hot_experts": (I32, [P, P, U64, P]),
+    "ditch_hip_model_warm_experts": (I32, [P, P, U64, P]),
     "ditch_hip_residency_stats": (I32, [P, P]),
     "ditch_hip_stream": (P, [P]),
     "ditch_hip_sync": (I32, [P]),

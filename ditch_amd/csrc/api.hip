@@ -564,8 +564,34 @@ int32_t ditch_hip_model_expert_cache_stats(const ditch_hip_model *m, ditch_exper
         out->bytes_read = c->bytes_read;
         out->evictions = c->evictions;
         out->slot_bytes = c->slot_bytes;
+        out->warmed = c->warmed;
     }
     return DITCH_OK;
+}
+
+int32_t ditch_hip_model_hot_experts(ditch_hip_model *m, ditch_hot_expert *out, uint64_t capacity,
+                                    uint64_t *count) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(count && (out || capacity == 0), DITCH_INVALID_ARGUMENT, "hot_experts arguments");
+        const std::vector<HotExpert> hot = cache_hot_experts(m);
+        *count = hot.size();
+        for (uint64_t k = 0; k < capacity && k < hot.size(); k++)
+            out[k] = ditch_hot_expert{hot[k].layer, hot[k].expert, hot[k].uses};
+    });
+}
+
+int32_t ditch_hip_model_warm_experts(ditch_hip_model *m, const ditch_hot_expert *hot, uint64_t n,
+                                     uint64_t *warmed) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(hot || n == 0, DITCH_INVALID_ARGUMENT, "warm_experts arguments");
+        DITCH_CHECK(m->expert_budget > 0, DITCH_INVALID_ARGUMENT, "warm_experts: the model streams no experts");
+        std::vector<HotExpert> h((size_t)n);
+        for (uint64_t k = 0; k < n; k++) h[k] = HotExpert{hot[k].layer, hot[k].expert, hot[k].uses};
+        const uint64_t w = cache_warm(m, h.data(), n);
+        if (warmed) *warmed = w;
+    });
 }
 
 int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m) {

@@ -174,6 +174,7 @@ static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64
     sl.layer = layer;
     sl.expert = e;
     sl.used_pending = false;
+    sl.prefetched = false;
     sl.stamp = ++c.clock;
 }
 
@@ -195,8 +196,12 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
     for (size_t k = from; k < experts.size(); k++) {
         const int64_t e = experts[k];
         int i = find_slot(c, layer, e);
+        c.uses[(uint64_t)layer << 32 | (uint64_t)e]++;
         if (i >= 0) {
-            c.hits++;
+            // an expert filled ahead of use was still a read (expert_cache.zig:403-410)
+            if (c.slots[i].prefetched) c.misses++;
+            else c.hits++;
+            c.slots[i].prefetched = false;
         } else {
             i = victim(c, layer, nl);
             if (i < 0) break;  // every slot pinned by this chunk
@@ -249,8 +254,55 @@ void cache_prefetch_next(ditch_hip_model *m, int64_t layer) {
         // never displace an expert the forward needs before `next`
         if (sl.layer >= 0 && ((sl.layer - layer - 1) % nl + nl) % nl <= dist_next) return;
         fill(c, m, i, next, e);
+        c.slots[i].prefetched = true;
         c.prefetches++;
     }
+}
+
+// ExpertCache.hotExperts (expert_cache.zig:501-523): every (layer, expert)
+// acquired so far with its count, most used first, ties by layer then expert.
+std::vector<HotExpert> cache_hot_experts(ditch_hip_model *m) {
+    std::vector<HotExpert> out;
+    if (!m->cache) return out;
+    for (const auto &kv : m->cache->uses)
+        out.push_back(HotExpert{(uint32_t)(kv.first >> 32), (uint32_t)(kv.first & 0xffffffffu), kv.second});
+    std::sort(out.begin(), out.end(), [](const HotExpert &a, const HotExpert &b) {
+        if (a.uses != b.uses) return a.uses > b.uses;
+        if (a.layer != b.layer) return a.layer < b.layer;
+        return a.expert < b.expert;
+    });
+    return out;
+}
+
+// ExpertCache.warm (expert_cache.zig:567-607): copies in the hottest experts
+// of `hot` (most used first) that exist in the model as streamed routed
+// experts and fit the free slots, before a run starts. Stops at the first
+// entry with no uses or when no slot is free; resident ones are skipped.
+// Returns the number copied in.
+uint64_t cache_warm(ditch_hip_model *m, const HotExpert *hot, uint64_t n) {
+    ExpertCache &c = cache_of(m);
+    uint64_t warmed = 0;
+    for (uint64_t k = 0; k < n; k++) {
+        const HotExpert &h = hot[k];
+        if (h.uses == 0) break;
+        if (h.layer >= m->layers.size()) continue;
+        const Layer &L = m->layers[h.layer];
+        if (!m->moe_layers[h.layer] || h.expert >= L.eg.size()) continue;
+        if (!(L.eg[h.expert].streamed() && L.eu[h.expert].streamed() && L.ed[h.expert].streamed())) continue;
+        if (find_slot(c, h.layer, h.expert) >= 0) continue;
+        int free = -1;
+        for (size_t i = 0; i < c.slots.size(); i++)
+            if (c.slots[i].layer < 0) {
+                free = (int)i;
+                break;
+            }
+        if (free < 0) break;
+        fill(c, m, free, h.layer, h.expert);
+        c.slots[free].prefetched = true;
+        warmed++;
+    }
+    c.warmed += warmed;
+    return warmed;
 }
 
 void cache_note_layer(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts) {

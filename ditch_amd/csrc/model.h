@@ -1,6 +1,7 @@
 // model.h — host-side state of a resident model (not part of the ABI).
 #pragma once
 #include <cstdint>
+#include <unordered_map>
 #include <vector>
 
 #include "internal.h"
@@ -69,6 +70,7 @@ struct ExpertCache {
         int pins = 0;
         uint64_t stamp = 0;
         bool used_pending = false;  // `used` recorded since the last load
+        bool prefetched = false;    // filled ahead of use (prefetch, warm): its first use counts as a miss
         hipEvent_t used = nullptr;   // the compute stream's last use
         hipEvent_t loaded = nullptr; // the copy stream's last fill
     };
@@ -78,6 +80,8 @@ struct ExpertCache {
     hipStream_t copy = nullptr;
     uint64_t hits = 0, misses = 0, prefetches = 0, bytes_read = 0, evictions = 0;
     std::vector<std::vector<int32_t>> last_used;  // per layer: experts routed by the last forward
+    std::unordered_map<uint64_t, uint64_t> uses;   // (layer << 32 | expert) -> acquisitions
+    uint64_t warmed = 0;
     ~ExpertCache();
 };
 
@@ -87,6 +91,12 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
 void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_t s);
 void cache_note_layer(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts);
 void cache_prefetch_next(ditch_hip_model *m, int64_t layer);
+struct HotExpert {
+    uint32_t layer, expert;
+    uint64_t uses;
+};
+std::vector<HotExpert> cache_hot_experts(ditch_hip_model *m);
+uint64_t cache_warm(ditch_hip_model *m, const HotExpert *hot, uint64_t n);
 void expert_views(ExpertCache &c, int slot, const Layer &L, int64_t e, TileView &g, TileView &u, TileView &d);
 
 struct Layer {

@@ -314,6 +314,21 @@ class Model:
         self.dev.check(self.dev.lib.ditch_hip_model_expert_cache_stats(self.h, ctypes.byref(st)))
         return {name: getattr(st, name) for name, _ in st._fields_}
 
+    def hot_experts(self):
+        """[(layer, expert, uses)], most used first (ExpertCache.hotExperts)."""
+        n = ctypes.c_uint64(0)
+        self.dev.check(self.dev.lib.ditch_hip_model_hot_experts(self.h, None, 0, ctypes.byref(n)))
+        arr = (abi.HotExpert * max(n.value, 1))()
+        self.dev.check(self.dev.lib.ditch_hip_model_hot_experts(self.h, arr, n.value, ctypes.byref(n)))
+        return [(h.layer, h.expert, h.uses) for h in arr[:n.value]]
+
+    def warm_experts(self, hot):
+        """ExpertCache.warm: copies the hottest experts of `hot` in; returns how many."""
+        arr = (abi.HotExpert * max(len(hot), 1))(*[abi.HotExpert(l, e, u) for l, e, u in hot])
+        w = ctypes.c_uint64(0)
+        self.dev.check(self.dev.lib.ditch_hip_model_warm_experts(self.h, arr, len(hot), ctypes.byref(w)))
+        return w.value
+
     def free(self):
         if self.h:
             self.dev.lib.ditch_hip_model_free(self.h)

@@ -439,9 +439,29 @@ typedef struct ditch_expert_cache_stats {
     uint64_t bytes_read;  /* host -> device bytes                             */
     uint64_t evictions;
     uint64_t slot_bytes;  /* bytes of one expert's slot                       */
+    uint64_t warmed;      /* experts copied in by ditch_hip_model_warm_experts */
 } ditch_expert_cache_stats;
-/* Zeros before the first forward of a streaming model.                    */
+/* Zeros before the first forward of a streaming model. An expert copied in
+ * ahead of its use (prefetched or warmed) counts as a miss at its first use
+ * (expert_cache.zig:403-410).                                              */
 int32_t ditch_hip_model_expert_cache_stats(const ditch_hip_model *m, ditch_expert_cache_stats *out);
+/* ExpertCache.hotExperts / warm (expert_cache.zig:501-607): the routed
+ * experts acquired so far with their use counts, most used first (ties by
+ * layer, then expert), for the caller to keep (ditch writes it as a hotlist
+ * file) and give back to the next run's model: warm copies the hottest
+ * streamed experts that fit the free slots in before the first forward,
+ * stopping at the first entry with no uses; entries naming no streamed
+ * routed expert of the model are skipped. hot_experts writes min(capacity,
+ * count) entries and sets *count to the number there are.                  */
+typedef struct ditch_hot_expert {
+    uint32_t layer;
+    uint32_t expert;
+    uint64_t uses;
+} ditch_hot_expert;
+int32_t ditch_hip_model_hot_experts(ditch_hip_model *m, ditch_hot_expert *out, uint64_t capacity,
+                                    uint64_t *count);
+int32_t ditch_hip_model_warm_experts(ditch_hip_model *m, const ditch_hot_expert *hot, uint64_t n,
+                                     uint64_t *warmed);
 
 int32_t ditch_hip_model_reset_deltas(ditch_hip_model *m);
 /* HBM bytes held by the model's weights.                                   */
