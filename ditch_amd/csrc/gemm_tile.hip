@@ -454,8 +454,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         const bool second = TF != TF_BF16 || 2 * s + 1 < units;
         const u32x4 *A = As + wave_m * WM * TPS * XT * 64 + lane;
         // k tile t + 1's A fragments are read and its weight tiles decoded
-        // while k tile t's products issue (two register sets)
-        u32x4 a[2][WM][XT], bf[2][WN];
+        // while k tile t's products issue (two register sets). Q8_0 keeps one
+        // A set, read again once k tile t's products have issued: its block-
+        // scaled partial sums need the registers, and a kernel that spills
+        // reloads its copy addresses behind a wait for every copy in flight.
+        constexpr int AS = TF == TF_Q8 ? 1 : 2;
+        u32x4 a[AS][WM][XT], bf[2][WN];
 #pragma unroll
         for (int m = 0; m < WM; m++)
 #pragma unroll
@@ -466,11 +470,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
         for (int t = 0; t < TPS; t++) {
             const int cu = t & 1, nx = cu ^ 1;
-            if (t + 1 < TPS) {
+            const int ca = AS == 2 ? cu : 0;
+            if (AS == 2 && t + 1 < TPS) {
 #pragma unroll
                 for (int m = 0; m < WM; m++)
 #pragma unroll
-                    for (int e = 0; e < XT; e++) a[nx][m][e] = A[((m * TPS + t + 1) * XT + e) * 64];
+                    for (int e = 0; e < XT; e++) a[AS == 2 ? nx : 0][m][e] = A[((m * TPS + t + 1) * XT + e) * 64];
             }
             if constexpr (TF == TF_Q8) {
                 // Q8_0: each 32-column k tile is one block; its f16 scale
@@ -484,7 +489,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                     for (int i = 0; i < WN; i++) {
                         floatx4 pt = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                        for (int e = 0; e < XT; e++) pt = mfma_bf16(a[cu][m][e], bf[cu][i], pt);
+                        for (int e = 0; e < XT; e++) pt = mfma_bf16(a[ca][m][e], bf[cu][i], pt);
 #pragma unroll
                         for (int r = 0; r < 4; r++) acc[m][i][r] = __builtin_fmaf(sq[i], pt[r], acc[m][i][r]);
                     }
@@ -494,7 +499,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
                     for (int e = 0; e < XT; e++)
 #pragma unroll
-                        for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[cu][m][e], bf[cu][i], acc[m][i]);
+                        for (int i = 0; i < WN; i++) acc[m][i] = mfma_bf16(a[ca][m][e], bf[cu][i], acc[m][i]);
+            }
+            if (AS == 1 && t + 1 < TPS) {
+#pragma unroll
+                for (int m = 0; m < WM; m++)
+#pragma unroll
+                    for (int e = 0; e < XT; e++) a[0][m][e] = A[((m * TPS + t + 1) * XT + e) * 64];
             }
             if (t + 1 < TPS) {
 #pragma unroll
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         constexpr int VPM = TF == TF_BF16 ? 1 : TF == TF_MX4 ? 2 : TF == TF_FP8 ? 3 : TF == TF_Q8 ? 5 : 4;
 #pragma unroll
         for (int t = 0; t < TPS; t++) {
-            if (t + 1 < TPS) {
+            if (t + 1 < TPS && AS == 2) {
 #pragma unroll
                 for (int j = 0; j < NA; j++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -520,6 +531,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
                 }
+            } else if (t + 1 < TPS) {  // one A set: the next tile's reads after the products
+#pragma unroll
+                for (int j = 0; j < NM; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, NA, 0);
             } else {
                 __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
             }
