@@ -146,7 +146,7 @@ class ResidencyStats(C.Structure):
 class ExpertCacheStats(C.Structure):
     """`ditch_expert_cache_stats` (expert_cache.Stats)."""
     _fields_ = [(n, C.c_uint64) for n in ("capacity", "slots", "resident", "hits", "misses", "prefetched",
-                                          "bytes_read", "evictions", "slot_bytes", "warmed")]
+                                          "bytes_read", "evictions", "slot_bytes", "warmed", "bytes_staged")]
 
 
 class HotExpert(C.Structure):

@@ -565,6 +565,7 @@ int32_t ditch_hip_model_expert_cache_stats(const ditch_hip_model *m, ditch_exper
         out->evictions = c->evictions;
         out->slot_bytes = c->slot_bytes;
         out->warmed = c->warmed;
+        out->bytes_staged = c->bytes_staged;
     }
     return DITCH_OK;
 }

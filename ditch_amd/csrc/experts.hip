@@ -12,6 +12,7 @@
 // layer used in the previous forward are copied ahead while this layer
 // computes (prompts of a search share their routing from trial to trial).
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "model.h"
@@ -19,14 +20,18 @@
 namespace ditch {
 
 void host_mat_free(HostMat &hm) {
-    if (hm.host) (void)hipHostFree(hm.host);
+    if (hm.host) {
+        if (hm.pinned) (void)hipHostFree(hm.host);
+        else free(hm.host);
+    }
     hm.host = nullptr;
     hm.bytes = 0;
+    hm.pinned = false;
 }
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-void stream_out(Mat &mt) {
+void stream_out(Mat &mt, uint64_t &pinned_bytes, bool &pinned_exhausted) {
     ditch_hip_tensor *t = mt.t;
     DITCH_CHECK(t, DITCH_INVALID_ARGUMENT, "stream_out of an empty slot");
     void *parts[6] = {t->codes, t->scale, t->zero, t->side, t->mx, t->mx_scales};
@@ -36,7 +41,25 @@ void stream_out(Mat &mt) {
         if (parts[i]) total += align256(t->part_bytes[i]);
     }
     HostMat hm;
-    DITCH_TRY_HIP(hipHostMalloc((void **)&hm.host, total ? total : 256, hipHostMallocDefault));
+    const size_t alloc = total ? total : 256;
+    uint64_t limit = EXPERT_PINNED_LIMIT;
+    if (const char *ev = getenv("DITCH_HIP_EXPERT_PINNED_LIMIT")) limit = strtoull(ev, nullptr, 10);
+    if (!pinned_exhausted && pinned_bytes + alloc <= limit) {
+        if (hipHostMalloc((void **)&hm.host, alloc, hipHostMallocDefault) == hipSuccess) {
+            hm.pinned = true;
+            pinned_bytes += alloc;
+        } else {
+            (void)hipGetLastError();
+            hm.host = nullptr;
+            pinned_exhausted = true;
+        }
+    }
+    if (!hm.host) {
+        void *p = nullptr;
+        DITCH_CHECK(posix_memalign(&p, 4096, (alloc + 4095) / 4096 * 4096) == 0, DITCH_OUT_OF_MEMORY,
+                    "expert streaming: host out of memory");
+        hm.host = (uint8_t *)p;
+    }
     hm.bytes = total;
     for (int i = 0; i < 6; i++)
         if (parts[i] && t->part_bytes[i]) DITCH_TRY_HIP(hipMemcpy(hm.host + off[i], parts[i], t->part_bytes[i], hipMemcpyDeviceToHost));
@@ -85,6 +108,10 @@ ExpertCache::~ExpertCache() {
     for (Slot &sl : slots) {
         if (sl.used) (void)hipEventDestroy(sl.used);
         if (sl.loaded) (void)hipEventDestroy(sl.loaded);
+    }
+    for (int b = 0; b < NSTAGE; b++) {
+        if (stage[b]) (void)hipHostFree(stage[b]);
+        if (stage_done[b]) (void)hipEventDestroy(stage_done[b]);
     }
     dev_free(arena);
     if (copy) (void)hipStreamDestroy(copy);
@@ -156,6 +183,29 @@ static int victim(const ExpertCache &c, int64_t cur, int64_t nlayers) {
     return best;
 }
 
+// A pageable blob to the device through the pinned staging ring (the role of
+// stream.zig's pinned buffers): each piece is copied on the host into the
+// next staging buffer once the copy stream has finished with it, then sent
+// on the copy stream.
+static void stage_copy(ExpertCache &c, uint8_t *dst, const uint8_t *src, size_t bytes) {
+    for (size_t off = 0; off < bytes;) {
+        const int b = c.stage_next;
+        c.stage_next = (b + 1) % ExpertCache::NSTAGE;
+        if (!c.stage[b]) {
+            DITCH_TRY_HIP(hipHostMalloc((void **)&c.stage[b], ExpertCache::STAGE_BYTES, hipHostMallocDefault));
+            DITCH_TRY_HIP(hipEventCreateWithFlags(&c.stage_done[b], hipEventDisableTiming));
+        }
+        if (c.stage_pending[b]) DITCH_TRY_HIP(hipEventSynchronize(c.stage_done[b]));
+        const size_t n = std::min(ExpertCache::STAGE_BYTES, bytes - off);
+        memcpy(c.stage[b], src + off, n);
+        DITCH_TRY_HIP(hipMemcpyAsync(dst + off, c.stage[b], n, hipMemcpyHostToDevice, c.copy));
+        DITCH_TRY_HIP(hipEventRecord(c.stage_done[b], c.copy));
+        c.stage_pending[b] = true;
+        c.bytes_staged += n;
+        off += n;
+    }
+}
+
 // Fills slot `i` with expert (layer, e): the copy stream waits for the
 // compute stream's last use of the slot, then copies the three blobs.
 static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64_t e) {
@@ -166,7 +216,8 @@ static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64
     uint8_t *base = c.arena + (uint64_t)i * c.slot_bytes;
     uint64_t off = 0;
     for (const Mat *mt : {&L.eg[e], &L.eu[e], &L.ed[e]}) {
-        DITCH_TRY_HIP(hipMemcpyAsync(base + off, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, c.copy));
+        if (mt->hm.pinned) DITCH_TRY_HIP(hipMemcpyAsync(base + off, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, c.copy));
+        else stage_copy(c, base + off, mt->hm.host, mt->hm.bytes);
         c.bytes_read += mt->hm.bytes;
         off += align256(mt->hm.bytes);
     }

@@ -17,6 +17,7 @@ namespace ditch {
 struct HostMat {
     uint8_t *host = nullptr;
     size_t bytes = 0;
+    bool pinned = false;  // else pageable: copied to the device through the cache's pinned staging ring
     int64_t field_off[6] = {-1, -1, -1, -1, -1, -1};
 };
 void host_mat_free(HostMat &hm);
@@ -53,7 +54,12 @@ struct Vec {
 };
 
 // Moves an uploaded matrix to pinned host memory (frees its device parts).
-void stream_out(Mat &mt);
+// Moves a registered routed expert matrix to host memory: pinned while the
+// model's pinned bytes stay under EXPERT_PINNED_LIMIT and the allocation
+// succeeds, pageable after that (systems cap pinned memory; these GPU hosts
+// pin about 65 GiB).
+constexpr uint64_t EXPERT_PINNED_LIMIT = (uint64_t)48 << 30;
+void stream_out(Mat &mt, uint64_t &pinned_bytes, bool &pinned_exhausted);
 // The matrix's TileView with its device pointers inside a copy of its host
 // blob at `base`.
 TileView view_at(const Mat &mt, const uint8_t *base);
@@ -82,6 +88,15 @@ struct ExpertCache {
     std::vector<std::vector<int32_t>> last_used;  // per layer: experts routed by the last forward
     std::unordered_map<uint64_t, uint64_t> uses;   // (layer << 32 | expert) -> acquisitions
     uint64_t warmed = 0;
+    // pinned staging ring for pageable blobs: a buffer is refilled once the
+    // copy stream has passed its last copy
+    static constexpr int NSTAGE = 4;
+    static constexpr size_t STAGE_BYTES = (size_t)16 << 20;
+    uint8_t *stage[NSTAGE] = {};
+    hipEvent_t stage_done[NSTAGE] = {};
+    bool stage_pending[NSTAGE] = {};
+    int stage_next = 0;
+    uint64_t bytes_staged = 0;
     ~ExpertCache();
 };
 
@@ -133,6 +148,8 @@ struct ditch_hip_model {
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
+    uint64_t expert_pinned = 0;    // host bytes of routed experts held pinned
+    bool expert_pinned_exhausted = false;
     // routed layers run with the grouped products planned on the device /
     // on the host (after reading the expert counts back), since creation
     uint64_t moe_device_planned = 0, moe_host_planned = 0;

@@ -796,7 +796,7 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
     if (m->expert_budget > 0 &&
         (slot == DITCH_SLOT_EXPERT_GATE || slot == DITCH_SLOT_EXPERT_UP || slot == DITCH_SLOT_EXPERT_DOWN)) {
         DITCH_CHECK(!m->cache, DITCH_INVALID_ARGUMENT, "expert registered after the expert cache was built");
-        stream_out(*mt);
+        stream_out(*mt, m->expert_pinned, m->expert_pinned_exhausted);
     }
 }
 

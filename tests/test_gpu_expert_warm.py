@@ -64,3 +64,33 @@ def test_hot_experts_and_warm_start(dev):
         assert fresh.expert_cache_stats()["resident"] == 0
     finally:
         fresh.free()
+
+
+def test_pageable_experts_through_the_staging_ring(dev, monkeypatch):
+    """Experts registered past the pinned limit stay in pageable memory and
+    reach the cache through the pinned staging ring: the same forward, bit
+    for bit, as with every expert pinned, in a cache of a quarter of them."""
+    spec = mg.moe("int4", layers=3, dense_first=1, experts=16, top_k=4, seed=21)
+    b = mg.batch(3, [40, 17, 64], spec.config["vocab"], seed=9)
+    probe = Model(dev, spec, expert_cache_bytes=1 << 40)
+    try:
+        _fw(probe, b)
+        slot = probe.expert_cache_stats()["slot_bytes"]
+    finally:
+        probe.free()
+    budget = 8 * slot
+    pinned = Model(dev, spec, expert_cache_bytes=budget)
+    monkeypatch.setenv("DITCH_HIP_EXPERT_PINNED_LIMIT", str(3 * slot))  # a few pinned, the rest pageable
+    paged = Model(dev, spec, expert_cache_bytes=budget)
+    try:
+        for _ in range(2):
+            rp, lp = _fw(pinned, b)
+            rq, lq = _fw(paged, b)
+            np.testing.assert_array_equal(lq, lp)
+            np.testing.assert_array_equal(rq, rp)
+        sp, sq = pinned.expert_cache_stats(), paged.expert_cache_stats()
+        assert sp["bytes_staged"] == 0 and sq["bytes_staged"] > 0
+        assert sq["bytes_staged"] < sq["bytes_read"] == sp["bytes_read"]
+    finally:
+        pinned.free()
+        paged.free()
