@@ -12,6 +12,7 @@
 // first one if both are NaN), an invalid product (0 * inf) is the negative
 // default NaN 0xffc00000.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -168,6 +169,36 @@ __device__ __forceinline__ float act_apply(uint32_t act, float x) {
     case 4: { float r = fmaxf(x, 0.0f); return __fmul_rn(r, r); }
     case 5: return __fdiv_rn(x, __fadd_rn(1.0f, exp_cephes(__fmul_rn(-1.702f, x))));
     default: return x;
+    }
+}
+
+// The activation inside a fused gate/up epilogue whose output is split into
+// fp6 or bf16 terms right away (so within 15^-4 of its block maximum, or
+// 2^-18 of itself): SiLU as x * rcp(1 + 2^(-x log2 e)) on the hardware
+// exp2 and reciprocal (about an ulp from x / (1 + expVec(-x))), the other
+// activations exactly as act_apply. A is a compile-time activation code.
+template <int A>
+__device__ __forceinline__ float act_fused(float x) {
+    if constexpr (A == 0) {
+        const float e = __builtin_amdgcn_exp2f(__fmul_rn(x, -1.4426950408889634f));
+        return __fmul_rn(x, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e)));
+    } else {
+        return act_apply(A, x);
+    }
+}
+
+// f(std::integral_constant<int, act>) with the run-time activation code made
+// a compile-time one (one switch outside the loops that apply it).
+template <typename F>
+__device__ __forceinline__ void with_act(uint32_t act, F &&f) {
+    switch (act) {
+    case 0: f(std::integral_constant<int, 0>{}); break;
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 5: f(std::integral_constant<int, 5>{}); break;
+    default: f(std::integral_constant<int, 6>{}); break;
     }
 }
 

@@ -573,6 +573,16 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         // (grouped: tokens and output rows within the segment, fragment
         // blocks in the padded order of the row map)
         float *patch = (float *)As0 + wave * 16 * 32;
+        // the gates' activation first, the activation's switch outside the loops
+        with_act(p.act, [&](auto ac) {
+            constexpr int A = decltype(ac)::value;
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int i = 0; i < OG; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[m][i][r] = act_fused<A>(acc[m][i][r]);
+        });
 #pragma unroll
         for (int m = 0; m < WM; m++) {
             const int64_t mblk = m16_0 + wave_m * WM + m;
@@ -582,7 +592,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
-                    float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
+                    float y = __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
                     if (tok >= to.n || col >= w.rows) y = 0.f;
                     else if (p.out) to.out[tok * to.ldo + col] = y;
                     patch[(4 * kq + r) * 32 + (i & 1) * 16 + (lane & 15)] = y;
@@ -903,6 +913,16 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
         static_assert(OG * 16 == 64, "two 32-column blocks per wave");
         static_assert(WAVES / 2 * WM * 16 * PS * 4 <= (int)sizeof(Stage), "patches fit the stage buffers");
         float *pt = (float *)(wave < WAVES / 2 ? (void *)&st0 : (void *)&st1) + (wave % (WAVES / 2)) * (WM * 16 * PS);
+        // the gates' activation first, the activation's switch outside the loops
+        with_act(p.act, [&](auto ac) {
+            constexpr int A = decltype(ac)::value;
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int i = 0; i < OG; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[m][i][r] = act_fused<A>(acc[m][i][r]);
+        });
 #pragma unroll
         for (int m = 0; m < WM; m++) {
 #pragma unroll
@@ -911,7 +931,7 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int64_t tok = (mw + m) * 16 + 4 * kq + r;
-                    float y = __fmul_rn(act_apply(p.act, acc[m][i][r]), acc[m][i + OG][r]);
+                    float y = __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
                     if (tok >= p.n || col >= w.rows) y = 0.f;
                     else if (p.out) p.out[tok * p.ldo + col] = y;
                     pt[(m * 16 + 4 * kq + r) * PS + i * 16 + (lane & 15)] = y;
