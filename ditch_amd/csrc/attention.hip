@@ -80,6 +80,7 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     constexpr int OS = VD + 4;
     __shared__ float Ot[SPLIT ? NW : 1][SPLIT ? 16 * OS : 1];
 
+    if (a.dense && *a.dense) return;  // the whole-prompt kernel took these rows
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int64_t r0 = (int64_t)blockIdx.x * 16;
@@ -394,6 +395,201 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Whole-prompt attention for dense batches (row r = prompt r / T at position
+// r % T) of at most PK positions: one workgroup per (prompt, KV head) stages
+// the prompt's keys and values in LDS once, as bf16 terms (the per-block
+// kernel stages a block's chunks again for every 16 rows), then each wave
+// takes (query head, 16-row block) units with no further barrier, the
+// scores of a unit's keys kept in registers between the max and the exp.
+// The arithmetic is the per-block kernel's, operation for operation (the
+// same three-product score and P.V MFMAs in the same chunk order, the row
+// max, the Cephes exp and the sum in the lane's key order), and the values
+// past a block's last row are read as zero as that kernel stages them, so
+// both give the same bits.
+constexpr int PK = 128;  // positions a prompt may have
+
+// flag = 1 when every row r < n is (r / T, r % T) and inside the KV cache
+__global__ __launch_bounds__(1024) void attn_dense_check_kernel(const ditch_row *rows, int64_t n, int64_t T,
+                                                                int64_t nb, int *flag) {
+    int bad = 0;
+    for (int64_t r = threadIdx.x; r < n; r += 1024) {
+        const ditch_row w = rows[r];
+        bad |= (int64_t)w.b != r / T || (int64_t)w.pos != r % T;
+    }
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0) *flag = !bad && (n + T - 1) / T <= nb;
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void attn_prompt_kernel(AttnArgs a) {
+    if (*a.dense == 0) return;  // the per-block kernel takes these rows
+    constexpr int NW = 8, VD = HD, QS = HD / 32, VB = VD / 16, KB = AK / 16, NCH = PK / AK;
+    constexpr int KRS = HD + 8, VRS = PK + 8;  // row strides (bf16), as in the per-block kernel
+    __shared__ __attribute__((aligned(16))) uint16_t Kh[PK * KRS], Kl[PK * KRS];
+    __shared__ __attribute__((aligned(16))) uint16_t Vh[VD * VRS], Vl[VD * VRS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int64_t b = blockIdx.x, hkv = blockIdx.y;
+    const int64_t L = a.n - b * a.T < a.T ? a.n - b * a.T : a.T;  // the prompt's positions 0 .. L - 1
+    if (L <= 0) return;
+
+    // keys (item = key, 8 dims) and values (item = key pair, 4 dims, stored
+    // [dim][key]) of positions 0 .. PK, zero past L; every load first
+    {
+        constexpr int KI = PK * (HD / 8) / (NW * 64), VI = (PK / 2) * (VD / 4) / (NW * 64);
+        static_assert(KI * NW * 64 == PK * (HD / 8) && VI * NW * 64 == (PK / 2) * (VD / 4), "items per thread");
+        const float *kb = a.kc + (b * a.T) * a.kvd + hkv * a.hd, *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
+        float4 kr[KI][2], vr[VI][2];
+#pragma unroll
+        for (int t = 0; t < KI; t++) {
+            const int i = threadIdx.x + t * NW * 64, key = i / (HD / 8), d = (i % (HD / 8)) * 8;
+            kr[t][0] = kr[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (key < L) {
+                kr[t][0] = *(const float4 *)(kb + key * a.kvd + d);
+                kr[t][1] = *(const float4 *)(kb + key * a.kvd + d + 4);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < VI; t++) {
+            const int i = threadIdx.x + t * NW * 64, kp = i / (VD / 4), d = (i % (VD / 4)) * 4, p = 2 * kp;
+            vr[t][0] = vr[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p < L) vr[t][0] = *(const float4 *)(vb + p * a.kvd + d);
+            if (p + 1 < L) vr[t][1] = *(const float4 *)(vb + (p + 1) * a.kvd + d);
+        }
+#pragma unroll
+        for (int t = 0; t < KI; t++) {
+            const int i = threadIdx.x + t * NW * 64, key = i / (HD / 8), d = (i % (HD / 8)) * 8;
+            const float v[8] = {kr[t][0].x, kr[t][0].y, kr[t][0].z, kr[t][0].w,
+                                kr[t][1].x, kr[t][1].y, kr[t][1].z, kr[t][1].w};
+            u32x4 hi, lo;
+            split8_words(v, hi, lo);
+            *(u32x4 *)&Kh[key * KRS + d] = hi;
+            *(u32x4 *)&Kl[key * KRS + d] = lo;
+        }
+#pragma unroll
+        for (int t = 0; t < VI; t++) {
+            const int i = threadIdx.x + t * NW * 64, kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const float x0[4] = {vr[t][0].x, vr[t][0].y, vr[t][0].z, vr[t][0].w};
+            const float x1[4] = {vr[t][1].x, vr[t][1].y, vr[t][1].z, vr[t][1].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint2 w2 = split_pair(x0[j], x1[j]);
+                *(uint32_t *)&Vh[(d + j) * VRS + 2 * kp] = w2.x;
+                *(uint32_t *)&Vl[(d + j) * VRS + 2 * kp] = w2.y;
+            }
+        }
+    }
+    __syncthreads();
+
+    // units (row block rb, query head j), rb-major: wave w takes w, w + NW, ..
+    const int64_t nrb = (L + 15) / 16, units = nrb * a.groups;
+    for (int64_t u = wave; u < units; u += NW) {
+        const int64_t rb = u / a.groups, h = hkv * a.groups + u % a.groups;
+        const int p0 = (int)(rb * 16);
+        const int kmax = (int)(p0 + 15 < L - 1 ? p0 + 15 : L - 1);  // the block's last position
+        const int nch = (kmax + AK) / AK;
+        const int row_pos = p0 + c16 <= kmax ? p0 + c16 : -1;  // this lane's score row
+        int pos[4];                                            // its four output rows
+#pragma unroll
+        for (int r = 0; r < 4; r++) pos[r] = p0 + 4 * g + r <= kmax ? p0 + 4 * g + r : -1;
+        const int64_t r0 = b * a.T + p0;
+
+        u32x4 qh[QS], ql[QS];
+        {
+            const bool ok = row_pos >= 0;
+            const float *q = a.q + ((ok ? r0 + c16 : r0) * a.heads + h) * a.hd + 8 * g;
+#pragma unroll
+            for (int st = 0; st < QS; st++) {
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (ok) {
+                    v0 = *(const float4 *)(q + 32 * st);
+                    v1 = *(const float4 *)(q + 32 * st + 4);
+                }
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                split8_words(v, qh[st], ql[st]);
+            }
+        }
+
+        // scores of chunks 0 .. nch (transposed D layout), scaled and masked
+        floatx4 sc[NCH][KB];
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            if (c < nch) {
+#pragma unroll
+                for (int kb = 0; kb < KB; kb++) {
+                    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int st = 0; st < QS; st++) {
+                        const int key = c * AK + kb * 16 + c16;
+                        const u32x4 kh = *(const u32x4 *)&Kh[key * KRS + 32 * st + 8 * g];
+                        const u32x4 kl = *(const u32x4 *)&Kl[key * KRS + 32 * st + 8 * g];
+                        acc = mfma3(kh, kl, qh[st], ql[st], acc);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int key = c * AK + kb * 16 + 4 * g + r;
+                        sc[c][kb][r] = key <= row_pos ? __fmul_rn(acc[r], a.scale) : -INFINITY;
+                        m = fmaxf(m, sc[c][kb][r]);
+                    }
+                }
+            }
+        }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+
+        float sum = 0.f;
+        floatx4 o[VB];
+#pragma unroll
+        for (int db = 0; db < VB; db++) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            if (c < nch) {
+                float e[8];
+#pragma unroll
+                for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float s = sc[c][kb][r];
+                        const float v = row_pos >= 0 && s != -INFINITY ? exp_cephes(__fsub_rn(s, m)) : 0.f;
+                        sum = __fadd_rn(sum, v);
+                        e[kb * 4 + r] = v;
+                    }
+                u32x4 ph, pl;
+                split8_words(e, ph, pl);
+                // keys 16 .. 31 of the chunk past the block's last row: zero
+                // values, as the per-block kernel stages them
+                const bool upper = c * AK + 16 <= kmax;
+#pragma unroll
+                for (int db = 0; db < VB; db++) {
+                    const uint16_t *vh = &Vh[(db * 16 + c16) * VRS + c * AK + 4 * g];
+                    const uint16_t *vl = &Vl[(db * 16 + c16) * VRS + c * AK + 4 * g];
+                    const uint2 h0 = *(const uint2 *)vh, l0 = *(const uint2 *)vl;
+                    uint2 h1 = *(const uint2 *)(vh + 16), l1 = *(const uint2 *)(vl + 16);
+                    if (!upper) h1 = l1 = make_uint2(0u, 0u);
+                    o[db] = mfma3(ph, pl, u32x4{h0.x, h0.y, h1.x, h1.y}, u32x4{l0.x, l0.y, l1.x, l1.y}, o[db]);
+                }
+            }
+        }
+        sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
+        sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
+        float inv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float t = __shfl(sum, 4 * g + r, 64);
+            inv[r] = t > 0.f ? __fdiv_rn(1.0f, t) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if (pos[r] < 0) continue;
+            float *orow = a.out + ((r0 + 4 * g + r) * a.heads + h) * a.vd;
+#pragma unroll
+            for (int db = 0; db < VB; db++) orow[db * 16 + c16] = __fmul_rn(o[db][r], inv[r]);
+        }
+    }
+}
+
 bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups) {
     return groups >= 1 && ((hd == 64 && vd == 64) || (hd == 128 && vd == 128) || (hd == 192 && vd == 128));
 }
@@ -418,7 +614,28 @@ static void launch_attn(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
     else launch_attn_nw<HD, VD, 1>(a, kv_heads, s);
 }
 
+// Whether the whole-prompt kernel can take a forward's attention (head dims
+// 64 or 128, at most PK positions a prompt, f32 output), and the check of
+// its rows into `flag` (once a forward: every layer has the same rows).
+bool attention_prompt_takes(int64_t hd, int64_t vd, int64_t T) {
+    return hd == vd && (hd == 64 || hd == 128) && T <= PK;
+}
+void launch_attention_dense_check(const ditch_row *rows, int64_t n, int64_t T, int64_t nb, int *flag, hipStream_t s) {
+    hipLaunchKernelGGL(attn_dense_check_kernel, dim3(1), dim3(1024), 0, s, rows, n, T, nb, flag);
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
+// With a.dense (set by launch_attention_dense_check for these rows), both
+// kernels are launched and the one the flag does not select exits at once.
 void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
+    if (a.dense) {
+        DITCH_CHECK(!a.xs && attention_prompt_takes(a.hd, a.vd, a.T), DITCH_INVALID_ARGUMENT,
+                    "attention: the whole-prompt kernel does not take this shape");
+        const dim3 grid((unsigned)((a.n + a.T - 1) / a.T), (unsigned)kv_heads);
+        if (a.hd == 64) hipLaunchKernelGGL(attn_prompt_kernel<64>, grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL(attn_prompt_kernel<128>, grid, dim3(512), 0, s, a);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
     if (a.hd == 64) launch_attn<64, 64>(a, kv_heads, s);
     else if (a.hd == 128) launch_attn<128, 128>(a, kv_heads, s);
     else launch_attn<192, 128>(a, kv_heads, s);

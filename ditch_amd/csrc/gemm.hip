@@ -82,14 +82,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             }
         }
     }
+    int64_t tb[MT], rw[NT];
 #pragma unroll
-    for (int m = 0; m < MT; m++)
+    for (int m = 0; m < MT; m++) tb[m] = m0 + 16 * m + 4 * kq;
 #pragma unroll
-        for (int i = 0; i < NT; i++) {
-            int64_t row = (g0 + i) * 16 + lane % 16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) store_out(p, m0 + 16 * m + 4 * kq + r, row, acc[m][i][r]);
-        }
+    for (int i = 0; i < NT; i++) rw[i] = (g0 + i) * 16 + lane % 16;
+    store_block(p, tb, rw, acc);
 }
 
 // ---------------------------------------------------------------------------

@@ -336,19 +336,73 @@ __device__ __forceinline__ void load_x8(const GemmParams &p, int64_t tok, int64_
     }
 }
 
-// Epilogue for one output element.
-__device__ __forceinline__ void store_out(const GemmParams &p, int64_t tok, int64_t row, float v) {
-    if (tok >= p.n || row >= p.w.rows) return;
-    if (p.delta_rank > 0) {
-        float d = 0.f;
-        for (int j = 0; j < p.delta_rank; j++)
-            d = __fadd_rn(d, __fmul_rn(p.delta_b[row * p.delta_rank + j], p.delta_xa[tok * p.delta_stride + j]));
-        v = __fadd_rn(v, d);
+// Epilogue of a lane's tile (tokens tb[m] + r, rows rw[i]): out = acc + delta
+// (the rank-k sum from 0 in j order) + bias (+ the old output), one 16-token
+// block at a time. The block's operands (delta factors, bias, old outputs)
+// are all read before its first store, so their loads are in flight
+// together (element by element, each read of an output would wait for the
+// possibly aliasing store before it).
+template <int NM, int NI>
+__device__ __forceinline__ void store_block(const GemmParams &p, const int64_t (&tb)[NM], const int64_t (&rw)[NI],
+                                            const floatx4 (&acc)[NM][NI]) {
+    bool rin[NI];
+    float bias[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        rin[i] = rw[i] < p.w.rows;
+        bias[i] = p.bias && rin[i] ? p.bias[rw[i]] : 0.f;
     }
-    if (p.bias) v = __fadd_rn(v, p.bias[row]);
-    float *o = p.out + tok * p.w.rows + row;
-    if (p.accumulate) v = __fadd_rn(*o, v);
-    *o = v;
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        bool tin[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) tin[r] = tb[m] + r < p.n;
+        floatx4 v[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) v[i] = acc[m][i];
+        if (p.delta_rank > 0) {
+            floatx4 d[NI];
+#pragma unroll
+            for (int i = 0; i < NI; i++) d[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < p.delta_rank; j++) {
+                float bj[NI], xj[4];
+#pragma unroll
+                for (int i = 0; i < NI; i++) bj[i] = rin[i] ? p.delta_b[rw[i] * p.delta_rank + j] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) xj[r] = tin[r] ? p.delta_xa[(tb[m] + r) * p.delta_stride + j] : 0.f;
+#pragma unroll
+                for (int i = 0; i < NI; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[i], xj[r]));
+            }
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(v[i][r], d[i][r]);
+        }
+        if (p.bias) {
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(v[i][r], bias[i]);
+        }
+        if (p.accumulate) {
+            floatx4 old[NI];
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) old[i][r] = rin[i] && tin[r] ? p.out[(tb[m] + r) * p.w.rows + rw[i]] : 0.f;
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(old[i][r], v[i][r]);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (rin[i] && tin[r]) p.out[(tb[m] + r) * p.w.rows + rw[i]] = v[i][r];
+    }
 }
 
 // Rebases the parameters on segment blockIdx.z of a grouped product: the

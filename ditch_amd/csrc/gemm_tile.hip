@@ -269,6 +269,76 @@ __device__ __forceinline__ void tile_store(const TileOut &p, int64_t tok, int64_
     *o = v;
 }
 
+// tile_store over a lane's tile (tokens tb[m] + r, rows rw[i]) with the
+// same arithmetic in the same order, one 16-token block at a time: the
+// block's operands (delta factors, bias, old outputs) are all read before
+// its first store, so their loads are in flight together. Element by
+// element, each read of an output waits for the store before it (the
+// addresses may alias), and the residual add then pays one memory latency
+// per element.
+template <int NM, int NI>
+__device__ __forceinline__ void tile_store_block(const TileOut &p, const int64_t (&tb)[NM], const int64_t (&rw)[NI],
+                                                 floatx4 (&acc)[NM][NI]) {
+    bool rin[NI];
+    float bias[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        rin[i] = rw[i] < p.rows;
+        bias[i] = p.bias && rin[i] ? p.bias[rw[i]] : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        bool tin[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) tin[r] = tb[m] + r < p.n;
+        floatx4 v[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) v[i] = acc[m][i];
+        if (p.delta_rank > 0) {
+            floatx4 d[NI];
+#pragma unroll
+            for (int i = 0; i < NI; i++) d[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < p.delta_rank; j++) {
+                float bj[NI], xj[4];
+#pragma unroll
+                for (int i = 0; i < NI; i++) bj[i] = rin[i] ? p.delta_b[rw[i] * p.delta_rank + j] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) xj[r] = tin[r] ? p.delta_xa[(tb[m] + r) * p.delta_stride + j] : 0.f;
+#pragma unroll
+                for (int i = 0; i < NI; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[i], xj[r]));
+            }
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(v[i][r], d[i][r]);
+        }
+        if (p.bias) {
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(v[i][r], bias[i]);
+        }
+        if (p.accumulate) {
+            floatx4 old[NI];
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) old[i][r] = rin[i] && tin[r] ? p.out[(tb[m] + r) * p.ldo + rw[i]] : 0.f;
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][r] = __fadd_rn(old[i][r], v[i][r]);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (rin[i] && tin[r]) p.out[(tb[m] + r) * p.ldo + rw[i]] = v[i][r];
+    }
+}
+
 // s_waitcnt operand: wait until at most n vector memory loads are in flight
 // (expcnt and lgkmcnt left at their no-wait maxima).
 __host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -556,15 +626,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
 
     const int kq = lane >> 4;
     if constexpr (!GLU) {
+        int64_t tb[WM], rw[WN];
 #pragma unroll
-        for (int m = 0; m < WM; m++)
+        for (int m = 0; m < WM; m++) tb[m] = tok0 + (wave_m * WM + m) * 16 + 4 * kq;
 #pragma unroll
-            for (int i = 0; i < WN; i++) {
-                int64_t row = (g0 + i) * 16 + (lane & 15);
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    tile_store(to, tok0 + (wave_m * WM + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
-            }
+        for (int i = 0; i < WN; i++) rw[i] = (g0 + i) * 16 + (lane & 15);
+        tile_store_block(to, tb, rw, acc);
     } else {
         // act(gate) * up (tensor.gatedActivation), as f32 rows and/or as the
         // A fragments of the next product: each 16-token block of the wave's
@@ -894,14 +961,12 @@ __device__ __forceinline__ void mx_gemm_body(const TileGemmParams &p) {
     const int kq = lane >> 4;
     const int64_t mw = m16_0 + WM * wm;  // the wave's first token block
     if constexpr (!GLU) {
+        int64_t tb[WM], rw[WN];
 #pragma unroll
-        for (int m = 0; m < WM; m++)
+        for (int m = 0; m < WM; m++) tb[m] = (mw + m) * 16 + 4 * kq;
 #pragma unroll
-            for (int i = 0; i < WN; i++) {
-                const int64_t row = (g0 + i) * 16 + (lane & 15);
-#pragma unroll
-                for (int r = 0; r < 4; r++) tile_store(to, (mw + m) * 16 + 4 * kq + r, row, acc[m][i][r]);
-            }
+        for (int i = 0; i < WN; i++) rw[i] = (g0 + i) * 16 + (lane & 15);
+        tile_store_block(to, tb, rw, acc);
     } else {
         // y = act(gate) * up (tensor.gatedActivation) for the wave's 64
         // columns (two E8M0 blocks of the next product's k) and 16 WM

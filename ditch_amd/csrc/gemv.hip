@@ -343,18 +343,20 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemmParams p) {
     }
     __syncthreads();
     if (wave == 0) {
+        floatx4 a[1][NT];
+        int64_t rw[NT];
+        const int64_t tb[1] = {4 * kq};
 #pragma unroll
         for (int i = 0; i < NT; i++) {
-            floatx4 a = acc[i];
+            a[0][i] = acc[i];
 #pragma unroll
             for (int w = 0; w < W - 1; w++) {
                 floatx4 b = red[w][i][lane];
-                a[0] += b[0]; a[1] += b[1]; a[2] += b[2]; a[3] += b[3];
+                a[0][i][0] += b[0]; a[0][i][1] += b[1]; a[0][i][2] += b[2]; a[0][i][3] += b[3];
             }
-            int64_t row = (g0 + i) * 16 + lane % 16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) store_out(p, 4 * kq + r, row, a[r]);
+            rw[i] = (g0 + i) * 16 + lane % 16;
         }
+        store_block(p, tb, rw, a);
     }
 }
 

@@ -336,8 +336,14 @@ struct AttnArgs {
     void *xs;
     int64_t ldk;
     int64_t nb;  // prompt slots of the KV cache: rows with b >= nb or pos >= T are skipped
+    // optional: the flag launch_attention_dense_check wrote for these rows
+    // (1: dense, row r = prompt r / T at position r % T); the whole-prompt
+    // kernel then takes them and the per-block kernel's workgroups exit
+    const int *dense;
 };
 bool attention_mfma_takes(int64_t hd, int64_t vd, int64_t groups);
+bool attention_prompt_takes(int64_t hd, int64_t vd, int64_t T);
+void launch_attention_dense_check(const ditch_row *rows, int64_t n, int64_t T, int64_t nb, int *flag, hipStream_t s);
 void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s);
 
 // ops.hip

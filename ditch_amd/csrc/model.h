@@ -147,6 +147,7 @@ struct ditch_hip_model {
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
+    ditch::DevBuf attn_dense;      // the attention's dense-rows flag
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
     uint64_t expert_pinned = 0;    // host bytes of routed experts held pinned
     bool expert_pinned_exhausted = false;

@@ -1189,6 +1189,8 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
                     "forward: the KV cache belongs to another model or shape");
     }
     float *kc = pc ? pc->k : m->kc.get<float>(B * T * kvd), *vc = pc ? pc->v : m->vc.get<float>(B * T * kvd);
+    int *dense_flag = m->attn_dense.get<int>(1);  // checked at the first layer that can use it
+    bool dense_checked = false;
 
     hipLaunchKernelGGL(embed_kernel, dim3(grid_for(n * hidden)), dim3(256), 0, s, x, m->embed.t->v, d_tokens, n);
     DITCH_TRY_HIP(hipGetLastError());
@@ -1278,7 +1280,7 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
         ra.style = c.rope_style;
         hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
         DITCH_TRY_HIP(hipGetLastError());
-        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0, B};
+        AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0, B, nullptr};
         const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
         Act aact{att, nullptr, 0};
         // (the kernel's own bf16-fragment epilogue needs 34 KB more LDS a
@@ -1289,6 +1291,11 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             aa.ldk = split_ldk(nh * vd);
             aa.xs = m->atts.get<uint8_t>(split_bytes_ldk(n, aa.ldk, 2));
             aact = Act{att, aa.xs, aa.ldk};
+        }
+        if (mfma_attn && !aa.xs && attention_prompt_takes(hd, vd, T)) {
+            if (!dense_checked) launch_attention_dense_check(d_rows, n, T, B, dense_flag, s);
+            dense_checked = true;
+            aa.dense = dense_flag;
         }
         if (mfma_attn) launch_attention_mfma(aa, nkv, s);
         else hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);

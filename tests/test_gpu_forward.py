@@ -215,6 +215,48 @@ def test_long_prompt_attention_matches_oracle(dev, ref, name):
     check_parity(ref, rg, lg, rc, lc, name)
 
 
+# Equal-length prompts flattened in order are dense rows (row r = prompt r / T
+# at position r % T): the whole-prompt attention kernel's case when T <= 128.
+DENSE_CASES = {
+    "gqa4_hd128_T128": (lambda: mg.dense("bf16", hidden=512, inter=512, heads=8, kv_heads=2, head_dim=128, seed=3),
+                        3, 128),
+    "gqa7_hd64_T64": (lambda: mg.dense("f32", hidden=896, inter=512, heads=14, kv_heads=2, head_dim=64,
+                                       embed_fmt="f32", seed=6), 4, 64),
+    "gqa8_hd128_T100": (lambda: mg.dense("mxfp4", hidden=512, inter=512, heads=16, kv_heads=2, head_dim=128, seed=7),
+                        2, 100),
+    "gqa1_hd64_T33": (lambda: mg.dense("fp8", hidden=256, inter=512, heads=4, kv_heads=4, head_dim=64, seed=8), 3, 33),
+}
+
+
+@pytest.mark.parametrize("name", list(DENSE_CASES))
+def test_dense_prompt_attention_matches_per_block_kernel_and_oracle(dev, ref, name):
+    """The dense batch (whole-prompt attention kernel) gives the same bits at
+    every row as the same rows shuffled (not dense: the per-block kernel),
+    and matches the oracle; T = 100 and 33 leave partial 16-row blocks and
+    32-key chunks."""
+    make, B, T = DENSE_CASES[name]
+    spec = make()
+    tokens, rows, last = mg.batch(B, [T], spec.config["vocab"], seed=T)
+    n = len(tokens)
+    assert rows == [(r // T, r % T) for r in range(n)]
+    perm = np.random.default_rng(T).permutation(n)
+    inv = np.argsort(perm)
+    rows_p = [rows[i] for i in perm]
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    try:
+        rg, lg = gm.forward(tokens, rows, capture_rows=list(range(n)), logit_rows=last)
+        rp, lp = gm.forward(tokens[perm], rows_p, capture_rows=[int(inv[r]) for r in range(n)],
+                            logit_rows=[int(inv[r]) for r in last])
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    np.testing.assert_array_equal(rg, rp)
+    np.testing.assert_array_equal(lg, lp)
+    check_parity(ref, rg[:, last], lg, rc, lc, name)
+
+
 # ---------------------------------------------------------------------------
 # Routed-expert streaming (expert_cache.zig:108-607)
 
