@@ -46,15 +46,27 @@ def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def _includes(path, seen):
+    """The source and every local header it includes, directly or not."""
+    path = os.path.normpath(path)
+    if path in seen or not os.path.exists(path):
+        return seen
+    seen.add(path)
+    with open(path) as f:
+        for line in f:
+            line = line.strip()
+            if line.startswith("#include \""):
+                name = line.split('"')[1]
+                _includes(os.path.join(os.path.dirname(path), name), seen)
+    return seen
+
+
 def _stale(src, obj):
-    """The object is older than its source or any header of csrc/ or include/."""
+    """The object is older than its source or a local header it includes."""
     if not os.path.exists(obj):
         return True
     t = os.path.getmtime(obj)
-    deps = [os.path.join(CSRC, src)]
-    deps += [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
-    inc = os.path.join(os.path.dirname(HERE), "include")
-    deps += [os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h")]
+    deps = _includes(os.path.join(CSRC, src), set())
     return any(os.path.getmtime(d) > t for d in deps)
 
 

@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "gemm_common.h"
+#include "gemm_wide.h"
 
 namespace ditch {
 
@@ -1091,6 +1092,7 @@ static int tile_ksplit_of(const TileView &w, int64_t n, int xt) {
 }
 
 size_t tile_part_bytes(const TileView &w, int64_t n, int xt) {
+    if (wide_gemm_takes(w, n, xt, split_k_tiles(w))) return 0;  // no partial sums
     const int ks = tile_ksplit_of(w, n, xt);
     return ks > 1 ? (size_t)ks * n * w.rows * sizeof(float) : 0;
 }
@@ -1149,6 +1151,10 @@ static void launch_tile_any(TileGemmParams &p, int xt, hipStream_t s) {
 
 void launch_tile_gemm(const TileView &w, float *out, int64_t ldo, const void *xs, int64_t ldk, int64_t n, int xt,
                       const MatmulEpilogue &ep, hipStream_t s, float *part) {
+    if (wide_gemm_takes(w, n, xt, ldk)) {
+        launch_wide_gemm(w, out, ldo, xs, ldk, n, ep, s);
+        return;
+    }
     TileGemmParams p{};
     p.part = ldo == w.rows ? part : nullptr;
     p.w = w;

@@ -320,6 +320,34 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("n,rows,cols", [(32, 72, 512), (33, 1000, 2880), (64, 520, 3072), (65, 136, 576),
+                                         (128, 64, 4096), (129, 520, 1024), (200, 300, 640), (256, 1040, 2048)])
+def test_q8_0_mid_batch_product_bias_accumulate(dev, ref, n, rows, cols):
+    """The mid-batch Q8_0 product (32..256 tokens: one workgroup per 64 weight
+    rows and every token, K split over its waves and added in LDS): ragged
+    tokens, rows and k slices, with the bias and accumulate epilogue, against
+    the oracle within the two-term split bound."""
+    from ditch_amd import hipmem
+    rng = np.random.default_rng(n * 17 + rows + cols)
+    w = wg.make("q8_0", rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    prior = rng.standard_normal((n, rows)).astype(np.float32)
+    t = dev.upload(w)
+    try:
+        bx, bb, bo = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias), hipmem.Buffer.from_array(prior)
+        t.matmul_device(bo.ptr, bx.ptr, n, d_bias=bb.ptr, accumulate=True)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    want = (prior.astype(np.float64) + ref.matmulT(x, w).astype(np.float64) + bias)
+    split = split_bound("q8_0", x, dequant_f32(ref, w))
+    bad = np.abs(got - want) > TOL_MATMUL["atol"] + TOL_MATMUL["rtol"] * np.abs(want) + split
+    assert not bad.any(), f"{bad.sum()} outside the split bound"
+    assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
+
+
 @pytest.mark.parametrize("kind,n,rows,cols", [("bf16", 200, 136, 576), ("fp8", 130, 520, 576),
                                                ("mxfp4", 256, 520, 640), ("int4", 321, 72, 1024)])
 def test_matmul_frags_device_matches_matmul_device(dev, kind, n, rows, cols):
