@@ -320,13 +320,15 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("n,rows,cols", [(32, 72, 512), (33, 1000, 2880), (64, 520, 3072), (65, 136, 576),
+@pytest.mark.parametrize("n,rows,cols", [(1, 72, 512), (2, 1000, 2880), (3, 33, 4096), (4, 520, 8192), (4, 17, 256),
+                                         (32, 72, 512), (33, 1000, 2880), (64, 520, 3072), (65, 136, 576),
                                          (128, 64, 4096), (129, 520, 1024), (200, 300, 640), (256, 1040, 2048)])
-def test_q8_0_mid_batch_product_bias_accumulate(dev, ref, n, rows, cols):
-    """The mid-batch Q8_0 product (32..256 tokens: one workgroup per 64 weight
-    rows and every token, K split over its waves and added in LDS): ragged
-    tokens, rows and k slices, with the bias and accumulate epilogue, against
-    the oracle within the two-term split bound."""
+def test_q8_0_few_and_mid_batch_product_bias_accumulate(dev, ref, n, rows, cols):
+    """The few-token Q8_0 product (1..4 tokens, the GEMV) and the mid-batch
+    one (32..256 tokens: one workgroup per 64 weight rows and every token, K
+    split over its waves and added in LDS):
+    ragged tokens, rows, columns and k slices, with the bias and accumulate
+    epilogue, against the oracle within the two-term split bound."""
     from ditch_amd import hipmem
     rng = np.random.default_rng(n * 17 + rows + cols)
     w = wg.make("q8_0", rows, cols, rng)
