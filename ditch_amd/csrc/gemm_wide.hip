@@ -9,23 +9,25 @@
 // every token, so each weight is read from HBM exactly once and nothing but
 // the outputs is written:
 //
-//   - 8 waves = KS k slices x TH token parts of 64 tokens (KS * TH = 8;
-//     TH = ceil(n / 64)); a wave multiplies its 64 tokens by the 64 rows
-//     over its slice of the 64-column units (16 accumulator tiles,
-//     v_mfma_f32_16x16x32_bf16);
-//   - the weight codes go straight from HBM to registers (one 16-byte load
-//     per lane and row group: the tile layout is the MFMA's B operand, two
-//     32-column k tiles per load), are widened to bf16 (exact for int8) once
-//     per wave, and every 32-column partial sum is scaled by its f16 block
-//     scale with one multiply-add per output (acc += s * sum), as in the
-//     tiled product;
+//   - every multiplying wave owns a 64-token x 64-row tile (16 accumulator
+//     tiles of v_mfma_f32_16x16x32_bf16) over a slice of the 64-column units;
+//     the workgroup's slices are added in slice order in LDS at the end, then
+//     delta, bias and accumulate are applied as everywhere else;
+//   - the weight codes are the MFMA's B operand as laid out in HBM (one
+//     16-byte load per lane and row group covers two 32-column k tiles),
+//     widened to bf16 (exact for int8), and every 32-column partial sum is
+//     scaled by its f16 block scale with one multiply-add per output
+//     (acc += s * sum), as in the tiled product;
 //   - the A fragments (two bf16 terms per activation, split_kernel layout)
-//     come from L2: all workgroups read the same few MiB;
-//   - loads run one unit (64 columns) ahead: the next unit's codes and side
-//     words when a unit starts, each A fragment of the next unit as soon as
-//     its current one has been multiplied;
-//   - the KS partial tiles meet in LDS (128 KiB) and are added in slice
-//     order, then delta, bias and accumulate are applied as everywhere else.
+//     come from L2: all workgroups read the same few MiB.
+//
+// Two kernels:
+//   - wide_q8_direct_kernel (n <= 64): 8 waves, each its own eighth of the
+//     units; a wave loads its codes and A fragments itself, one unit ahead;
+//   - wide_q8_kernel<KS> (64 < n <= 256): 4 multiplying waves (KS k slices x
+//     4 / KS token parts) fed by 4 producer waves, which load the codes
+//     several units ahead and write bf16 B fragments and scale words into a
+//     two-stage LDS ring.
 #include "gemm_wide.h"
 
 namespace ditch {
