@@ -39,7 +39,8 @@ FLAGS = [
 # which serialises the MFMAs with the memory latency.
 EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-disable-machine-sink"],
          "gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=1000000"],
-         "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+         "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

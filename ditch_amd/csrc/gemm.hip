@@ -2,6 +2,7 @@
 // kernel (gemm_tile.hip) does not take, and the launchers of every product
 // (the GEMV regime lives in gemv.hip).
 #include "gemm_common.h"
+#include "gemm_f32.h"
 
 namespace ditch {
 
@@ -168,6 +169,10 @@ void launch_matmul(const TileView &w, float *out, const float *x, int64_t n, con
     p.segs = nullptr;
     if (n <= 16) {
         launch_gemv(p, w.tf, w.rows, w.cols, ep.exact != 0, 1, ws, s);
+        return;
+    }
+    if (f32_gemm_takes(w, n)) {  // exact products whatever ep.exact asks
+        launch_f32_gemm(p, s);
         return;
     }
     dispatch_tf(w.tf, p, w.rows, n, 1, ep.exact != 0, s);

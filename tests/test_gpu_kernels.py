@@ -124,13 +124,38 @@ def test_gemv_long_rows_matches_oracle(dev, ref, kind, n, rows, cols):
     close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
 
 
-def test_matmulT_odd_k(dev, ref):
-    """K not a multiple of 8 takes the guarded activation loads."""
+@pytest.mark.parametrize("kind", ["bf16", "f32", "f16"])
+def test_matmulT_odd_k(dev, ref, kind):
+    """K not a multiple of 8 (or of 4) takes the guarded activation loads."""
     rng = np.random.default_rng(11)
-    for n, rows, cols in [(1, 5, 12), (20, 7, 20), (70, 33, 44)]:
-        w = wg.float_random("bf16", rows, cols, rng)
+    for n, rows, cols in [(1, 5, 12), (20, 7, 20), (70, 33, 44), (33, 40, 301)]:
+        w = wg.float_random(kind, rows, cols, rng)
         x = rng.standard_normal((n, cols)).astype(np.float32)
         close(dev.matmulT(x, w), ref.matmulT(x, w), **TOL_MATMUL)
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16"])
+@pytest.mark.parametrize("n,rows,cols", [(17, 896, 896), (1024, 128, 896), (300, 520, 4864), (64, 33, 96)])
+def test_float_weight_product_bias_accumulate(dev, ref, kind, n, rows, cols):
+    """f32 / f16 weights above the GEMV regime (exact products on the fp32
+    MFMA, k slices added in LDS when the tiles are few), with the bias and
+    accumulate epilogue, at the C1 projection shapes and ragged ones."""
+    from ditch_amd import hipmem
+    rng = np.random.default_rng(n + rows + cols)
+    w = wg.float_random(kind, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    prior = rng.standard_normal((n, rows)).astype(np.float32)
+    t = dev.upload(w)
+    try:
+        bx, bb, bo = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(bias), hipmem.Buffer.from_array(prior)
+        t.matmul_device(bo.ptr, bx.ptr, n, d_bias=bb.ptr, accumulate=True)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    want = prior.astype(np.float64) + ref.matmulT(x, w).astype(np.float64) + bias
+    close(got, want, **TOL_MATMUL)
 
 
 # -- VTable element-wise ops ------------------------------------------------------
