@@ -301,6 +301,182 @@ __global__ __launch_bounds__(256) void rmsnorm_split_mx_kernel(uint8_t *xm, int6
     }
 }
 
+// The same as rmsnorm_split_kernel with each row read once: wave w of 16
+// holds row 16 m16 + w in registers (lane l: columns 1024 j + 16 l .. +16,
+// j < NPH), sums its squares with a butterfly over the wave, normalises, and
+// writes each phase's two-term words (32 k tiles) into LDS in fragment
+// order; the workgroup then copies the phase's 64 KiB to the fragments in
+// whole 16-byte words.
+template <int NPH>
+__global__ __launch_bounds__(1024) void rmsnorm_split_rows_kernel(u32x4 *xs, int64_t ldk, float *out, const float *x,
+                                                                  const float *w, int64_t wlen, int64_t len,
+                                                                  float eps, int gemma, int64_t n) {
+    __shared__ u32x4 phase_buf[32 * 2 * 64];  // [k tile][term][lane], 64 KiB
+    const int64_t m16 = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r = m16 * 16 + wave;
+    const bool row_in = r < n;
+    const bool vec = (len % 4) == 0 && ((uintptr_t)x & 15) == 0;
+    float xv[NPH][16];
+#pragma unroll
+    for (int j = 0; j < NPH; j++) {
+        const int64_t k0 = 1024 * j + 16 * lane;
+        if (row_in && vec && k0 + 16 <= len) {
+#pragma unroll
+            for (int q = 0; q < 16; q += 4) {
+                const float4 a = *(const float4 *)(x + r * len + k0 + q);
+                xv[j][q] = a.x; xv[j][q + 1] = a.y; xv[j][q + 2] = a.z; xv[j][q + 3] = a.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; q++) xv[j][q] = row_in && k0 + q < len ? x[r * len + k0 + q] : 0.f;
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPH; j++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) ss = __builtin_fmaf(xv[j][q], xv[j][q], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+    const float inv = row_in ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps))) : 0.f;
+#pragma unroll
+    for (int j = 0; j < NPH; j++) {
+        const int64_t kt0 = 32 * j;
+        if (kt0 >= ldk) break;
+        const int64_t k0 = 1024 * j + 16 * lane;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 16; q += 4) {
+            float4 b = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (wlen > 0 && (wlen % 4) == 0 && k0 + q + 4 <= wlen) b = *(const float4 *)(w + k0 + q);
+            else if (wlen > 0) {
+                b.x = k0 + q < wlen ? w[k0 + q] : 1.f;
+                b.y = k0 + q + 1 < wlen ? w[k0 + q + 1] : 1.f;
+                b.z = k0 + q + 2 < wlen ? w[k0 + q + 2] : 1.f;
+                b.w = k0 + q + 3 < wlen ? w[k0 + q + 3] : 1.f;
+            }
+            const float wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float y = 0.f;
+                if (row_in && k0 + q + u < len) {
+                    y = __fmul_rn(xv[j][q + u], inv);
+                    if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wb[u]) : wb[u]);
+                }
+                v[q + u] = y;
+            }
+        }
+        if (out && row_in) {
+            if (vec && k0 + 16 <= len) {
+#pragma unroll
+                for (int q = 0; q < 16; q += 4) *(float4 *)(out + r * len + k0 + q) = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    if (k0 + q < len) out[r * len + k0 + q] = v[q];
+            }
+        }
+        // k tile kt0 + lane / 2, its 8-column chunks 2 (lane % 2) and 2 (lane % 2) + 1
+        const int ktl = lane >> 1;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            float v8[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) v8[q] = v[8 * c + q];
+            u32x4 words[2];
+            a_words<false, 2>(v8, words);
+            const int slot = wave + 16 * (2 * (lane & 1) + c);
+            phase_buf[(ktl * 2 + 0) * 64 + slot] = words[0];
+            phase_buf[(ktl * 2 + 1) * 64 + slot] = words[1];
+        }
+        __syncthreads();
+        const int64_t nkt = ldk - kt0 < 32 ? ldk - kt0 : 32;
+        u32x4 *dst = xs + (m16 * ldk + kt0) * 2 * 64;
+        for (int64_t i = threadIdx.x; i < nkt * 128; i += 1024) dst[i] = phase_buf[i];
+        __syncthreads();
+    }
+}
+
+// RMSNorm of 16 rows written as MX fragments, each row read once: wave w of
+// 16 holds row 16 m16 + w in registers (lane l: 32-column blocks l + 64 j,
+// j < NB), sums its squares with a butterfly over the wave, normalises, and
+// splits its blocks into fp6 terms into LDS in fragment order, 16 stages
+// (64 blocks) a phase; the workgroup then writes each phase's 16 x 6400 B
+// to the fragments in whole 16-byte words. (The two-pass kernel above reads
+// every row twice: once for the sum of squares, once for the split.)
+template <int NB>
+__global__ __launch_bounds__(1024) void rmsnorm_split_mx_rows_kernel(uint8_t *xm, int64_t ldst, const float *x,
+                                                                     const float *w, int64_t wlen, int64_t len,
+                                                                     float eps, int gemma, int64_t n) {
+    __shared__ u32x4 stage_buf[16 * MX_BLOCK / 16];  // 16 stages of one phase, 100 KiB
+    const int64_t m16 = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r = m16 * 16 + wave;
+    const bool row_in = r < n;
+    const bool vec = (len % 4) == 0 && ((uintptr_t)x & 15) == 0;
+    float xv[NB][32];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int64_t k0 = (int64_t)(lane + 64 * j) * 32;
+        if (row_in && vec && k0 + 32 <= len) {
+#pragma unroll
+            for (int q = 0; q < 32; q += 4) {
+                const float4 a = *(const float4 *)(x + r * len + k0 + q);
+                xv[j][q] = a.x; xv[j][q + 1] = a.y; xv[j][q + 2] = a.z; xv[j][q + 3] = a.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 32; q++) xv[j][q] = row_in && k0 + q < len ? x[r * len + k0 + q] : 0.f;
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int q = 0; q < 32; q++) ss = __builtin_fmaf(xv[j][q], xv[j][q], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+    const float inv = row_in ? __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)len), eps))) : 0.f;
+    const int64_t nst = ldst;  // stages in the fragments
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int64_t st0 = 16 * j;
+        if (st0 >= nst) break;
+        // this lane's block: stage st0 + lane / 4, block lane % 4 of it
+        const int64_t k0 = (int64_t)(lane + 64 * j) * 32;
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 32; q += 4) {
+            float4 b = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (wlen > 0 && (wlen % 4) == 0 && k0 + q + 4 <= wlen) b = *(const float4 *)(w + k0 + q);
+            else if (wlen > 0) {
+                b.x = k0 + q < wlen ? w[k0 + q] : 1.f;
+                b.y = k0 + q + 1 < wlen ? w[k0 + q + 1] : 1.f;
+                b.z = k0 + q + 2 < wlen ? w[k0 + q + 2] : 1.f;
+                b.w = k0 + q + 3 < wlen ? w[k0 + q + 3] : 1.f;
+            }
+            const float wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float y = 0.f;
+                if (row_in && k0 + q + u < len) {
+                    y = __fmul_rn(xv[j][q + u], inv);
+                    if (wlen > 0) y = __fmul_rn(y, gemma ? __fadd_rn(1.0f, wb[u]) : wb[u]);
+                }
+                v[q + u] = y;
+            }
+        }
+        if (st0 + lane / 4 < nst)
+            mx_write_slot(v, (uint8_t *)stage_buf + (lane / 4) * MX_BLOCK, wave + 16 * (lane % 4));
+        __syncthreads();
+        const int64_t nphase = nst - st0 < 16 ? nst - st0 : 16;
+        u32x4 *dst = (u32x4 *)(xm + (m16 * ldst + st0) * MX_BLOCK);
+        for (int64_t i = threadIdx.x; i < nphase * (MX_BLOCK / 16); i += 1024) dst[i] = stage_buf[i];
+        __syncthreads();
+    }
+}
+
 __global__ void layernorm_kernel(float *out, const float *x, const float *w, int64_t wlen, const float *bias,
                                  int64_t len, float eps, int one_plus) {
     __shared__ float sh[8];
@@ -555,16 +731,25 @@ void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, con
                           int64_t len, float eps, int gemma, hipStream_t s) {
     if (n <= 0) return;
     DITCH_CHECK(ldk * 32 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split: fragments shorter than the row");
-    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (u32x4 *)xs, ldk, out, x,
-                       w, wlen, len, eps, gemma, n);
+    const dim3 grid((unsigned)((n + 15) / 16));
+    // rows up to 4096 columns (fragments up to 128 k tiles): one read of each row
+    if (ldk <= 32) hipLaunchKernelGGL(rmsnorm_split_rows_kernel<1>, grid, dim3(1024), 0, s, (u32x4 *)xs, ldk, out, x, w, wlen, len, eps, gemma, n);
+    else if (ldk <= 64) hipLaunchKernelGGL(rmsnorm_split_rows_kernel<2>, grid, dim3(1024), 0, s, (u32x4 *)xs, ldk, out, x, w, wlen, len, eps, gemma, n);
+    else if (ldk <= 128) hipLaunchKernelGGL(rmsnorm_split_rows_kernel<4>, grid, dim3(1024), 0, s, (u32x4 *)xs, ldk, out, x, w, wlen, len, eps, gemma, n);
+    else hipLaunchKernelGGL(rmsnorm_split_kernel, grid, dim3(256), 0, s, (u32x4 *)xs, ldk, out, x, w, wlen, len, eps, gemma, n);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_split_mx(void *xm, int64_t ldst, float *out, const float *x, const float *w, int64_t wlen,
                              int64_t n, int64_t len, float eps, int gemma, hipStream_t s) {
     if (n <= 0) return;
     DITCH_CHECK(ldst * 128 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split_mx: fragments shorter than the row");
-    hipLaunchKernelGGL(rmsnorm_split_mx_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (uint8_t *)xm, ldst,
-                       out, x, w, wlen, len, eps, gemma, n);
+    if (!out && ldst <= 32) {  // rows up to 4096 columns, no f32 copy asked: one read of each row
+        hipLaunchKernelGGL(rmsnorm_split_mx_rows_kernel<2>, dim3((unsigned)((n + 15) / 16)), dim3(1024), 0, s,
+                           (uint8_t *)xm, ldst, x, w, wlen, len, eps, gemma, n);
+    } else {
+        hipLaunchKernelGGL(rmsnorm_split_mx_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (uint8_t *)xm,
+                           ldst, out, x, w, wlen, len, eps, gemma, n);
+    }
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_strided(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len,
