@@ -445,20 +445,22 @@ constexpr int MX_BLOCK = 6400;  // bytes per 16 tokens x 128 k
 // slot `slot` of a fragment block (slot = token % 16 + 16 * block within the
 // stage); r is left holding the remainder. A NaN or infinity among the 32
 // values gives the slot E8M0 255 (NaN) in every term, so that every product
-// reading it is NaN.
+// reading it is NaN. SLOTS: the slots of the block (64 in a fragment block;
+// fewer for a staging copy that holds part of the slots in the same order).
+template <int SLOTS = 64>
 __device__ __forceinline__ void mx_write_slot(float (&r)[32], uint8_t *blk, int slot) {
     typedef float v16f_t __attribute__((ext_vector_type(16)));
-    u32x4 *lo = (u32x4 *)blk + slot;                // + 64 e
-    uint2 *hi = (uint2 *)(blk + 4096) + slot;        // + 64 e
-    uint32_t *scw = (uint32_t *)(blk + 6144) + slot;
+    u32x4 *lo = (u32x4 *)blk + slot;                                        // + SLOTS e
+    uint2 *hi = (uint2 *)(blk + 16 * MX_TERMS * SLOTS) + slot;              // + SLOTS e
+    uint32_t *scw = (uint32_t *)(blk + 24 * MX_TERMS * SLOTS) + slot;
     bool finite = true;
 #pragma unroll
     for (int j = 0; j < 32; j++) finite = finite && __builtin_isfinite(r[j]);
     if (!finite) {
 #pragma unroll
         for (int e = 0; e < MX_TERMS; e++) {
-            lo[64 * e] = u32x4{0, 0, 0, 0};
-            hi[64 * e] = make_uint2(0, 0);
+            lo[SLOTS * e] = u32x4{0, 0, 0, 0};
+            hi[SLOTS * e] = make_uint2(0, 0);
         }
         *scw = 0xffffffffu;
         return;
@@ -491,8 +493,8 @@ __device__ __forceinline__ void mx_write_slot(float (&r)[32], uint8_t *blk, int 
         const auto back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(d, sc);
 #pragma unroll
         for (int j = 0; j < 32; j++) r[j] = __fsub_rn(r[j], back[j]);
-        lo[64 * e] = u32x4{(uint32_t)d[0], (uint32_t)d[1], (uint32_t)d[2], (uint32_t)d[3]};
-        hi[64 * e] = make_uint2((uint32_t)d[4], (uint32_t)d[5]);
+        lo[SLOTS * e] = u32x4{(uint32_t)d[0], (uint32_t)d[1], (uint32_t)d[2], (uint32_t)d[3]};
+        hi[SLOTS * e] = make_uint2((uint32_t)d[4], (uint32_t)d[5]);
     }
     *scw = scales;
 }

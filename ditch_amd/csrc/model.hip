@@ -504,13 +504,19 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int32_t *counts, i
 
 // out[t] = x[t] + (sum over the token's experts in ascending index of
 // w * eo + shared) (moe.zig:1197-1227 then the residual add); ord holds each
-// token's selections in that order. Four columns per thread.
-__global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared, const int32_t *ord,
-                                   const float *selw, const int32_t *pair_of, int64_t n, int64_t k, int64_t hidden) {
+// token's selections in that order. Four columns per thread. UNI: a row is a
+// whole number of waves (hidden a multiple of 256), so a wave's token is
+// one value and its selections, weights and pair rows are scalar loads.
+template <bool UNI>
+__global__ void moe_combine_kernel(float *x, const float *eo, const float *eo_shared,
+                                   const int32_t *__restrict__ ord, const float *__restrict__ selw,
+                                   const int32_t *__restrict__ pair_of, int64_t n, int64_t k, int64_t hidden) {
     const int64_t h4 = (hidden + 3) / 4, total = n * h4;
     const bool vec = (hidden % 4) == 0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t t = i / h4, c0 = (i % h4) * 4;
+        int64_t t = i / h4;
+        if constexpr (UNI) t = (int64_t)__builtin_amdgcn_readfirstlane((int)t);
+        const int64_t c0 = (i % h4) * 4;
         // the token's k (<= 16) rows and weights first, then every row load
         // in flight together, added in the order ord gives (fixed-size
         // register arrays, entries j >= k unused)
@@ -1155,8 +1161,14 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         esh = m->e_shared.get<float>(n * hidden);
         mm(m, L.sh_down, esh, sgb, n, nullptr, 0, s);
     }
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(grid_for(n * ((hidden + 3) / 4))), dim3(256), 0, s, x, eo, esh, ord,
-                       selw, pair_of, n, k, hidden);
+    // a wave of 64 threads covers 256 columns; grid_for's block count keeps
+    // every grid-stride step a whole number of waves
+    if (hidden % 256 == 0 && n * (hidden / 4) < INT32_MAX)
+        hipLaunchKernelGGL(moe_combine_kernel<true>, dim3(grid_for(n * ((hidden + 3) / 4))), dim3(256), 0, s, x, eo,
+                           esh, ord, selw, pair_of, n, k, hidden);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel<false>, dim3(grid_for(n * ((hidden + 3) / 4))), dim3(256), 0, s, x, eo,
+                           esh, ord, selw, pair_of, n, k, hidden);
     DITCH_TRY_HIP(hipGetLastError());
 }
 

@@ -398,21 +398,26 @@ __global__ __launch_bounds__(1024) void rmsnorm_split_rows_kernel(u32x4 *xs, int
     }
 }
 
-// RMSNorm of 16 rows written as MX fragments, each row read once: wave w of
-// 16 holds row 16 m16 + w in registers (lane l: 32-column blocks l + 64 j,
-// j < NB), sums its squares with a butterfly over the wave, normalises, and
-// splits its blocks into fp6 terms into LDS in fragment order, 16 stages
-// (64 blocks) a phase; the workgroup then writes each phase's 16 x 6400 B
-// to the fragments in whole 16-byte words. (The two-pass kernel above reads
-// every row twice: once for the sum of squares, once for the split.)
+// RMSNorm of 8 rows written as MX fragments, each row read once: wave w of
+// 8 holds row 16 m16 + 8 h + w (h = blockIdx.x % 2: the two halves of a
+// 16-token block) in registers (lane l: 32-column blocks l + 64 j, j < NB),
+// sums its squares with a butterfly over the wave, normalises, and splits its
+// blocks into fp6 terms into LDS, 16 stages (64 blocks) a phase, in a copy
+// of the fragment layout that holds only the half's 32 slots; the workgroup
+// then writes them to their slots (128-byte runs). Two workgroups fit a CU,
+// so one's loads overlap the other's splits. (The two-pass kernel above
+// reads every row twice: once for the sum of squares, once for the split.)
 template <int NB>
-__global__ __launch_bounds__(1024) void rmsnorm_split_mx_rows_kernel(uint8_t *xm, int64_t ldst, const float *x,
-                                                                     const float *w, int64_t wlen, int64_t len,
-                                                                     float eps, int gemma, int64_t n) {
-    __shared__ u32x4 stage_buf[16 * MX_BLOCK / 16];  // 16 stages of one phase, 100 KiB
-    const int64_t m16 = blockIdx.x;
+__global__ __launch_bounds__(512) void rmsnorm_split_mx_rows_kernel(uint8_t *xm, int64_t ldst, const float *x,
+                                                                    const float *w, int64_t wlen, int64_t len,
+                                                                    float eps, int gemma, int64_t n) {
+    constexpr int HS = 32;                         // slots of a half block
+    constexpr int HB = 25 * MX_TERMS * HS;         // bytes of a half block: 16 + 8 per term and slot, + scale words
+    __shared__ u32x4 stage_buf[16 * HB / 16];      // 16 stages, 50 KiB
+    const int64_t m16 = blockIdx.x >> 1;
+    const int half = blockIdx.x & 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r = m16 * 16 + wave;
+    const int64_t r = m16 * 16 + half * 8 + wave;
     const bool row_in = r < n;
     const bool vec = (len % 4) == 0 && ((uintptr_t)x & 15) == 0;
     float xv[NB][32];
@@ -467,12 +472,26 @@ __global__ __launch_bounds__(1024) void rmsnorm_split_mx_rows_kernel(uint8_t *xm
                 v[q + u] = y;
             }
         }
+        // half slot: token wave, block lane % 4 (fragment slot 8 half + wave + 16 (lane % 4))
         if (st0 + lane / 4 < nst)
-            mx_write_slot(v, (uint8_t *)stage_buf + (lane / 4) * MX_BLOCK, wave + 16 * (lane % 4));
+            mx_write_slot<HS>(v, (uint8_t *)stage_buf + (lane / 4) * HB, wave + 8 * (lane % 4));
         __syncthreads();
-        const int64_t nphase = nst - st0 < 16 ? nst - st0 : 16;
-        u32x4 *dst = (u32x4 *)(xm + (m16 * ldst + st0) * MX_BLOCK);
-        for (int64_t i = threadIdx.x; i < nphase * (MX_BLOCK / 16); i += 1024) dst[i] = stage_buf[i];
+        const int nphase = (int)(nst - st0 < 16 ? nst - st0 : 16);
+        uint8_t *dst = xm + (m16 * ldst + st0) * MX_BLOCK;
+        const uint8_t *src = (const uint8_t *)stage_buf;
+        // per stage: 16 (term, block) runs of 8 slots in each of the two code
+        // parts, 4 runs of 8 scale words
+        for (int i = threadIdx.x; i < nphase * 16 * 8; i += 512) {
+            const int st = i >> 7, run = (i >> 3) & 15, t = i & 7;
+            const int e = run >> 2, kb = run & 3;
+            const int hs = 8 * kb + t, fs = 8 * half + 16 * kb + t;  // half-block and fragment slot
+            *(u32x4 *)(dst + st * MX_BLOCK + (64 * e + fs) * 16) = *(const u32x4 *)(src + st * HB + (HS * e + hs) * 16);
+            *(uint2 *)(dst + st * MX_BLOCK + 4096 + (64 * e + fs) * 8) =
+                *(const uint2 *)(src + st * HB + 16 * MX_TERMS * HS + (HS * e + hs) * 8);
+            if (e == 0)
+                *(uint32_t *)(dst + st * MX_BLOCK + 6144 + fs * 4) =
+                    *(const uint32_t *)(src + st * HB + 24 * MX_TERMS * HS + hs * 4);
+        }
         __syncthreads();
     }
 }
@@ -744,7 +763,7 @@ void launch_rmsnorm_split_mx(void *xm, int64_t ldst, float *out, const float *x,
     if (n <= 0) return;
     DITCH_CHECK(ldst * 128 >= len, DITCH_INVALID_ARGUMENT, "rmsnorm_split_mx: fragments shorter than the row");
     if (!out && ldst <= 32) {  // rows up to 4096 columns, no f32 copy asked: one read of each row
-        hipLaunchKernelGGL(rmsnorm_split_mx_rows_kernel<2>, dim3((unsigned)((n + 15) / 16)), dim3(1024), 0, s,
+        hipLaunchKernelGGL(rmsnorm_split_mx_rows_kernel<2>, dim3((unsigned)((n + 15) / 16 * 2)), dim3(512), 0, s,
                            (uint8_t *)xm, ldst, x, w, wlen, len, eps, gemma, n);
     } else {
         hipLaunchKernelGGL(rmsnorm_split_mx_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, (uint8_t *)xm,
