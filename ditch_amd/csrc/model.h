@@ -25,12 +25,14 @@ void host_mat_free(HostMat &hm);
 struct Mat {
     ditch_hip_tensor *t = nullptr;
     float *da = nullptr, *db = nullptr;  // delta A [rank][cols], B [rows][rank]
+    bool joint = false;                   // db lies in da's allocation (one allocation for both)
     int rank = 0;
     HostMat hm;
     void clear_delta() {
         dev_free(da);
-        dev_free(db);
+        if (!joint) dev_free(db);
         da = db = nullptr;
+        joint = false;
         rank = 0;
     }
     void release() {
@@ -148,6 +150,7 @@ struct ditch_hip_model {
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     ditch::DevBuf attn_dense;      // the attention's dense-rows flag
+    ditch::DevBuf edit_v, edit_part;  // the none-mode edit's directions and matvecT partial sums
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
     uint64_t expert_pinned = 0;    // host bytes of routed experts held pinned
     bool expert_pinned_exhausted = false;

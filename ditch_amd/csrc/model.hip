@@ -841,24 +841,27 @@ void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float
     Mat *mt = mat_slot(m, layer, slot, expert);
     DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "edit of an empty slot");
     hipStream_t s = m->h->stream;
-    DevBuf dv, part, staged;
+    DevBuf staged;
     TileView w = mt->t->v;
     if (mt->streamed()) {  // a streamed expert: the edit reads a device copy of its blob
         uint8_t *d = staged.get<uint8_t>(mt->hm.bytes);
         DITCH_TRY_HIP(hipMemcpyAsync(d, mt->hm.host, mt->hm.bytes, hipMemcpyHostToDevice, s));
         w = view_at(*mt, d);
     }
-    float *d_v = dv.get<float>(k * w.rows + k * w.cols);
-    float *d_a = d_v + k * w.rows;
+    // the directions and the partial sums in the model's edit scratch (an
+    // edit of thousands of matrices allocates and frees nothing per matrix
+    // there); a and b in one allocation, a written by the product itself
+    float *d_v = m->edit_v.get<float>(k * w.rows);
     DITCH_TRY_HIP(hipMemcpyAsync(d_v, v, k * w.rows * 4, hipMemcpyHostToDevice, s));
-    launch_matvecT(d_a, w, d_v, (int64_t)k, s, part.get<float>(matvecT_partials_floats(w, k)));
+    mt->clear_delta();
+    float *dab = (float *)dev_alloc((k * w.cols + w.rows * k) * 4);
+    mt->da = dab;
+    mt->db = dab + k * w.cols;
+    mt->joint = true;
+    launch_matvecT(mt->da, w, d_v, (int64_t)k, s, m->edit_part.get<float>(matvecT_partials_floats(w, k)));
     std::vector<float> b(w.rows * k);
     for (int64_t i = 0; i < w.rows; i++)
         for (uint64_t j = 0; j < k; j++) b[i * k + j] = -weight * v[j * w.rows + i];
-    mt->clear_delta();
-    mt->da = (float *)dev_alloc(k * w.cols * 4);
-    mt->db = (float *)dev_alloc(w.rows * k * 4);
-    DITCH_TRY_HIP(hipMemcpyAsync(mt->da, d_a, k * w.cols * 4, hipMemcpyDeviceToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(mt->db, b.data(), w.rows * k * 4, hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipStreamSynchronize(s));
     mt->rank = (int)k;

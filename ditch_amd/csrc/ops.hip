@@ -694,8 +694,12 @@ __global__ void row_norms_kernel(float *out, TileView w) {
 }
 
 // W^T y, first pass: block (column chunk, row chunk) -> partial sums
-// [row_chunk][q][cols]; the second pass adds the chunks in order.
-constexpr int MVT_ROWS = 256;
+// [row_chunk][q][cols]; the second pass adds the chunks in order. A row
+// chunk is 32 rows, decoded 8 at a time with every load of the 8 issued
+// before the first multiply-add (a chunk of hundreds of rows walked one
+// decode at a time waits for each load in turn, and gives a 2048 x 768
+// matrix 24 workgroups).
+constexpr int MVT_ROWS = 32;
 constexpr int MVT_MAXQ = 16;
 
 __global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q) {
@@ -706,12 +710,19 @@ __global__ void matvecT_partial_kernel(float *partials, TileView w, const float 
     float acc[MVT_MAXQ];
 #pragma unroll
     for (int j = 0; j < MVT_MAXQ; j++) acc[j] = 0.f;
-    for (int64_t r = r0; r < r1; r++) {
-        uint16_t b;
-        float v = tiled_element_f32(w, r, c, &b);
+    for (int64_t rb = r0; rb < r1; rb += 8) {
+        float v[8];
 #pragma unroll
-        for (int j = 0; j < MVT_MAXQ; j++)
-            if (j < q) acc[j] = __builtin_fmaf(y[j * w.rows + r], v, acc[j]);
+        for (int i = 0; i < 8; i++) {
+            uint16_t b;
+            v[i] = rb + i < r1 ? tiled_element_f32(w, rb + i, c, &b) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (rb + i < r1)
+#pragma unroll
+                for (int j = 0; j < MVT_MAXQ; j++)
+                    if (j < q) acc[j] = __builtin_fmaf(y[j * w.rows + rb + i], v[i], acc[j]);
     }
     for (int j = 0; j < q; j++) partials[(rc * q + j) * w.cols + c] = acc[j];
 }
