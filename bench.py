@@ -587,7 +587,7 @@ def main():
     ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c4-layers", type=int, default=48)
     ap.add_argument("--c5", action="store_true", help="run configs[4] (pins ~100 GB of host memory)")
-    ap.add_argument("--kernel-only", choices=["glu", "gemv", "copy", "c4", "c5"], default=None,
+    ap.add_argument("--kernel-only", choices=["glu", "gemv", "copy", "c1", "c4", "c5"], default=None,
                     help="run only one leg (for rocprofv3 runs)")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
@@ -613,6 +613,9 @@ def main():
         return
     if args.kernel_only == "copy":
         print(json.dumps({"kernel_only": "copy", "copy": copy_leg(dev, args.reps)}))
+        return
+    if args.kernel_only == "c1":
+        print(json.dumps({"kernel_only": "c1", "c1": c1_leg(dev, args.steps, args.warmup)}))
         return
     if args.kernel_only == "c4":
         print(json.dumps({"kernel_only": "c4", "c4": c4_leg(dev, args.steps, args.warmup, args.c4_layers)}))

@@ -184,11 +184,21 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
         // select: no branch inside the product loop)
         const float sc_bf = u2f(bits << 16), sc_h = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
         const float sc = w.scale_type == SC_BF16 ? sc_bf : sc_h;
-        const int32_t zf = (int32_t)(word >> 16);
+        // (q - z) s as q s - z s in one fused multiply-add: q s and z s are
+        // exact (4-bit integers times a 16-bit scale; upload keeps a bf16
+        // scale's magnitude under 2^120, so 15 s stays finite), their
+        // difference is (q - z) s, exact in f32, so the fused operation
+        // returns it unrounded; the nibbles are spread into bytes and
+        // converted by byte lane
+        const float zs = __fmul_rn((float)(int32_t)(word >> 16), sc);
         const uint32_t wd = c[0][t];
+        const uint32_t lo = wd & 0x0f0f0f0fu, hi = (wd >> 4) & 0x0f0f0f0fu;
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = __fmul_rn((float)((int32_t)((wd >> (4 * j)) & 0xfu) - zf), sc);
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xffu), sc, -zs);
+            v[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xffu), sc, -zs);
+        }
         f = u32x4{cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]), cvt_pk_bf16(v[4], v[5]), cvt_pk_bf16(v[6], v[7])};
     }
     return f;
@@ -382,8 +392,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         map_tile(blockIdx.x, G, tm, p.tiles_n, mt, nt);
     }
     const int32_t *gd = GR ? p.gdesc + 4 * mt : nullptr;
-    const TileView &w = GR ? p.gsegs[gd[0]].w : p.w;
-    const TileView &w2 = GR && GLU ? p.gsegs2[gd[0]].w : p.w2;
+    // the weights' descriptions by value: read through a reference into the
+    // segment table they would be loaded again at every stage (the copies
+    // and stores in the loop might, as far as the compiler knows, change
+    // them), and each stage's copies would wait for those loads
+    const TileView w = GR ? p.gsegs[gd[0]].w : p.w;
+    const TileView w2 = GR && GLU ? p.gsegs2[gd[0]].w : p.w2;
     TileOut to{p.out, p.ldo, p.n, w.rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank, p.delta_stride};
     int64_t tok0;  // token (within the output rows) of the tile's first block
     // row groups of this wave: WN of w, or (GLU) the same WN/2 output groups

@@ -565,8 +565,19 @@ static int fast_decode_ok(const ditch_weight *w, int tf) {
         return !special && finite_scales(w->scale, w->scale_rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
     }
     case TF_INT4:
-        // the tiled GEMM's side word holds a 16-bit scale
+        // the tiled GEMM's side word holds a 16-bit scale; its decode forms
+        // (q - z) s as q s - z s, which needs 15 s finite: bf16 scales below
+        // 2^120 in magnitude (every f16 scale is)
         if (w->group % 64 != 0 || (w->scale_dtype != DITCH_F16 && w->scale_dtype != DITCH_BF16)) return 0;
+        if (w->scale_dtype == DITCH_BF16) {
+            const size_t count = w->rows * w->scale_cols;
+            for (size_t i = 0; i < count; i++) {
+                uint16_t b;
+                memcpy(&b, (const uint8_t *)w->scale + 2 * i, 2);
+                if (((b >> 7) & 0xffu) >= 127 + 120) return 0;
+            }
+            return 1;
+        }
         return finite_scales(w->scale, w->rows * w->scale_cols, w->scale_dtype) ? 1 : 0;
     default: return 0;
     }
