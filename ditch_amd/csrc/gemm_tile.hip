@@ -117,13 +117,27 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
+// FP8 and INT4 index their scale column by 64-column steps: stage s entry j
+// is step s (FP8) or 2 s + j (INT4) over `per` = block_cols / 64 or
+// group / 64 steps a column; `sh` = log2(per) when per is a power of two,
+// else -1 (a 32-bit division: this runs once per copy and stage)
+struct SideStep {
+    uint32_t per;
+    int sh;
+};
 template <int TF>
-__device__ __forceinline__ const uint32_t *side_word(const TileView &w, const uint32_t *side, int64_t base, int64_t s,
-                                                     int j) {
-    if constexpr (TF == TF_MX4) return side + base + s;
-    else if constexpr (TF == TF_Q8) return side + base + s * 16;  // [group][unit][row % 16]
-    else if constexpr (TF == TF_FP8) return side + base + (s * 64) / w.block_cols;
-    else return side + base + (s * 128 + 64 * j) / w.group;
+__device__ __forceinline__ SideStep side_step(const TileView &w) {
+    const uint32_t per = TF == TF_FP8 ? (uint32_t)(w.block_cols / 64) : TF == TF_INT4 ? (uint32_t)(w.group / 64) : 1u;
+    return SideStep{per, (per & (per - 1)) == 0 ? __builtin_ctz(per) : -1};
+}
+template <int TF>
+__device__ __forceinline__ const uint32_t *side_word(const SideStep &st, const uint32_t *side, int64_t s, int j) {
+    if constexpr (TF == TF_MX4) return side + s;
+    else if constexpr (TF == TF_Q8) return side + s * 16;  // [group][unit][row % 16]
+    else {
+        const uint32_t u = TF == TF_FP8 ? (uint32_t)s : (uint32_t)(2 * s + j);
+        return side + (st.sh >= 0 ? u >> st.sh : u / st.per);
+    }
 }
 
 // Side row of this lane's weight row (FP8: its row of the scale grid).
@@ -471,6 +485,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         const TileView &wi = (GLU && i >= OG) ? w2 : w;
         return wi.codes + group_of(wq, i) * units * 1024;
     };
+    const SideStep sst = side_step<TF>(w);
     const uint32_t *ssrc[CS > 0 ? CS : 1];
 #pragma unroll
     for (int j = 0; j < CS; j++) {
@@ -501,7 +516,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                 constexpr int j = decltype(jc)::value, off = (j % 16) * 256;
                 const int q = ck * CS + j;
                 __builtin_amdgcn_global_load_lds(
-                    (const void *)((const char *)side_word<TF>(w, ssrc[j], 0, s, q % NS1) - off),
+                    (const void *)((const char *)side_word<TF>(sst, ssrc[j], s, q % NS1) - off),
                     (lds_void *)&Ss[(ck * CS + j / 16 * 16) * 64], 4, off, 0);
             });
         }
