@@ -206,7 +206,12 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
         // converted by byte lane
         const float zs = __fmul_rn((float)(int32_t)(word >> 16), sc);
         const uint32_t wd = c[0][t];
-        const uint32_t lo = wd & 0x0f0f0f0fu, hi = (wd >> 4) & 0x0f0f0f0fu;
+        // (the masks as instructions the compiler cannot see through: it
+        // would fold each byte's mask and shift into a bit-field extract,
+        // one instruction per nibble ahead of its conversion)
+        uint32_t lo, hi;
+        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(wd));
+        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(wd >> 4));
         float v[8];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
