@@ -563,7 +563,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         // A set, read again once k tile t's products have issued: its block-
         // scaled partial sums need the registers, and a kernel that spills
         // reloads its copy addresses behind a wait for every copy in flight.
-        constexpr int AS = TF == TF_Q8 ? 1 : 2;
+        constexpr int AS = TF == TF_Q8 || WM > 4 ? 1 : 2;
         u32x4 a[AS][WM][XT], bf[2][WN];
 #pragma unroll
         for (int m = 0; m < WM; m++)
@@ -1136,8 +1136,10 @@ static void launch_tile(TileGemmParams &p, hipStream_t s) {
     constexpr int BM = 16 * WM * WGM, BN = 16 * (GLU ? WN / 2 : WN) * WGN;
     p.tiles_m = (int)((p.n + BM - 1) / BM);
     p.tiles_n = (int)((p.w.rows + BN - 1) / BN);
-    static_assert(BM == 64 && (GLU || BN == 64 * tile_wgn(TF, XT)), "tile_ksplit_of sizes the same tile");
-    p.ksplit = GLU || !p.part ? 1 : tile_ksplit((int64_t)p.tiles_m * p.tiles_n, p.kt_total / TileCfg<TF>::TPS);
+    static_assert((BM == 64 || BM == 96) && (GLU || BN == 64 * tile_wgn(TF, XT)), "tile_ksplit_of sizes the same tile");
+    // 96-token tiles only where the 64-token ones take no k split (the
+    // partial-sum scratch is sized for those)
+    p.ksplit = GLU || !p.part || BM != 64 ? 1 : tile_ksplit((int64_t)p.tiles_m * p.tiles_n, p.kt_total / TileCfg<TF>::TPS);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)p.ksplit);
     hipLaunchKernelGGL((tile_gemm_kernel<TF, XT, WGM, WGN, WM, WN, GLU>), grid, dim3(WGM * WGN * 64), 0, s, p);
     if (p.ksplit > 1) {
@@ -1153,8 +1155,25 @@ static void launch_tile_tf(TileGemmParams &p, hipStream_t s) {
     // waves side by side, each 64 tokens x 64 rows with 64 accumulator
     // registers: 8 waves (two per SIMD, a 64 x 512 tile) where the stage
     // buffers fit in LDS, 4 otherwise
-    if constexpr (TF == TF_BF16 || XT == 3) launch_tile<TF, XT, 1, 4, 4, 4, GLU>(p, s);
-    else launch_tile<TF, XT, 1, 8, 4, 4, GLU>(p, s);
+    if constexpr (TF == TF_BF16 || XT == 3) {
+        launch_tile<TF, XT, 1, 4, 4, 4, GLU>(p, s);
+    } else if constexpr (TF == TF_FP8) {
+        // FP8 (64-column stages): 96-token waves where the grid stays full.
+        // The decode of a weight tile then feeds 12 MFMAs instead of 8, and
+        // the decode's vector instructions do not overlap the MFMAs; the
+        // tile is 1.5x the work, so it pays when the 96-token grid needs
+        // fewer rounds of one workgroup a CU (counted 10 % cheaper per unit
+        // of work) and the 64-token grid takes no k split.
+        const int64_t bn = 16 * (GLU ? 2 : 4) * 8;
+        const int64_t tn = (p.w.rows + bn - 1) / bn;
+        const int64_t t64 = (p.n + 63) / 64 * tn, t96 = (p.n + 95) / 96 * tn;
+        const bool split64 = !GLU && p.part && tile_ksplit(t64, p.kt_total / TileCfg<TF>::TPS) > 1;
+        const double r64 = (double)((t64 + 255) / 256), r96 = 1.35 * (double)((t96 + 255) / 256);
+        if (!split64 && r96 < r64) launch_tile<TF, XT, 1, 8, 6, 4, GLU>(p, s);
+        else launch_tile<TF, XT, 1, 8, 4, 4, GLU>(p, s);
+    } else {
+        launch_tile<TF, XT, 1, 8, 4, 4, GLU>(p, s);
+    }
 }
 
 template <bool GLU>
