@@ -202,8 +202,10 @@ __device__ __forceinline__ u32x4 decode_tile_lds(const TileView &w, const u32x4 
         // exact (4-bit integers times a 16-bit scale; upload keeps a bf16
         // scale's magnitude under 2^120, so 15 s stays finite), their
         // difference is (q - z) s, exact in f32, so the fused operation
-        // returns it unrounded; the nibbles are spread into bytes and
-        // converted by byte lane
+        // returns it unrounded (a zero weight, q = z, comes out +0 where the
+        // reference's product gives -0 under a negative scale: a product
+        // differs only in the sign of an all-zero sum); the nibbles are
+        // spread into bytes and converted by byte lane
         const float zs = __fmul_rn((float)(int32_t)(word >> 16), sc);
         const uint32_t wd = c[0][t];
         // (the masks as instructions the compiler cannot see through: it
