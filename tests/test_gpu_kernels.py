@@ -345,6 +345,34 @@ def test_matmul_device_two_term_bias_accumulate(dev, ref, kind):
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("exp_field", [246, 248])
+def test_int4_bf16_scales_at_the_fast_decode_bound(dev, ref, exp_field):
+    """INT4 with bf16 scales of magnitude 2^119 (the tiled product's decode,
+    q s - z s in one fused multiply-add, still takes them) and 2^121 (past
+    its 2^120 bound: the exact decoder's product), activations scaled down
+    to keep the sums finite, against the oracle."""
+    from ditch_amd import hipmem
+    rng = np.random.default_rng(exp_field)
+    n, rows, cols = 64, 136, 512
+    w = wg.int_random(rows, cols, rng, scale_kind="bf16")
+    sc = w.arrays[1]  # the bf16 scale bits (the weight points at this array)
+    sc[...] = (sc & 0x807F) | (exp_field << 7)
+    x = (rng.standard_normal((n, cols)) * 2.0 ** (127 - exp_field)).astype(np.float32)
+    t = dev.upload(w)
+    try:
+        bx, bo = hipmem.Buffer.from_array(x), hipmem.Buffer.from_array(np.zeros((n, rows), np.float32))
+        t.matmul_device(bo.ptr, bx.ptr, n)
+        dev.sync()
+        got = bo.download(np.float32, (n, rows))
+    finally:
+        t.free()
+    want = ref.matmulT(x, w).astype(np.float64)
+    assert np.isfinite(got).all()
+    split = split_bound("int4", x, dequant_f32(ref, w))
+    bad = np.abs(got - want) > TOL_MATMUL["atol"] + TOL_MATMUL["rtol"] * np.abs(want) + split
+    assert not bad.any(), f"{bad.sum()} outside the split bound"
+
+
 @pytest.mark.parametrize("n,rows,cols", [(1, 72, 512), (2, 1000, 2880), (3, 33, 4096), (4, 520, 8192), (4, 17, 256),
                                          (32, 72, 512), (33, 1000, 2880), (64, 520, 3072), (65, 136, 576),
                                          (128, 64, 4096), (129, 520, 1024), (200, 300, 640), (256, 1040, 2048)])
