@@ -465,8 +465,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
     // ck CA .., code pieces ck CB .., side words ck CS ..) and writes it in
     // 4 KiB windows: an LDS copy writes at M0 plus its instruction offset
     // (which moves the global address too, so the source pointer is lowered
-    // by it), and an M0 write stalls the wave until the previous copy has
-    // landed; one M0 value per window instead of one per copy.
+    // by it): one M0 write per window instead of one per copy, so the
+    // copies issue back to back (measured faster than an M0 write before
+    // every copy).
     const bool copier = wave >= WAVES - CW;
     const int ck = copier ? wave - (WAVES - CW) : 0;
     // sources: a uniform base per copy (scalar registers) plus the lane's 16
