@@ -26,6 +26,7 @@
 #include "decode.h"
 #include "gemm_common.h"
 #include "internal.h"
+#include "attention_rope.h"
 
 namespace ditch {
 
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(1024) void attn_dense_check_kernel(const ditch_row 
 }
 
 template <int HD>
-__global__ __launch_bounds__(512) void attn_prompt_kernel(AttnArgs a) {
+__global__ __launch_bounds__(512) void attn_prompt_kernel(AttnArgs a, AttnRope rope) {
     if (*a.dense == 0) return;  // the per-block kernel takes these rows
     constexpr int NW = 8, VD = HD, QS = HD / 32, VB = VD / 16, KB = AK / 16, NCH = PK / AK;
     constexpr int KRS = HD + 8, VRS = PK + 8;  // row strides (bf16), as in the per-block kernel
@@ -499,6 +500,7 @@ __global__ __launch_bounds__(512) void attn_prompt_kernel(AttnArgs a) {
         {
             const bool ok = row_pos >= 0;
             const float *q = a.q + ((ok ? r0 + c16 : r0) * a.heads + h) * a.hd + 8 * g;
+            float v[QS][8];
 #pragma unroll
             for (int st = 0; st < QS; st++) {
                 float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
@@ -506,9 +508,33 @@ __global__ __launch_bounds__(512) void attn_prompt_kernel(AttnArgs a) {
                     v0 = *(const float4 *)(q + 32 * st);
                     v1 = *(const float4 *)(q + 32 * st + 4);
                 }
-                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                split8_words(v, qh[st], ql[st]);
+                v[st][0] = v0.x; v[st][1] = v0.y; v[st][2] = v0.z; v[st][3] = v0.w;
+                v[st][4] = v1.x; v[st][5] = v1.y; v[st][6] = v1.z; v[st][7] = v1.w;
             }
+            if constexpr (HD == 128) {
+                // the query's RoPE: dims 8 g + 32 st + j (st = 0, 1) pair with
+                // the same lane's dims 64 further (st + 2), with the RoPE
+                // kernel's operations in its order
+                if (rope.cos_t && ok) {
+                    const int64_t rp = row_pos < rope.rope_len - 1 ? row_pos : rope.rope_len - 1;
+                    const float *cr = rope.cos_t + rp * 64 + 8 * g, *sr = rope.sin_t + rp * 64 + 8 * g;
+#pragma unroll
+                    for (int st = 0; st < 2; st++) {
+                        const float4 c0 = *(const float4 *)(cr + 32 * st), c1 = *(const float4 *)(cr + 32 * st + 4);
+                        const float4 s0 = *(const float4 *)(sr + 32 * st), s1 = *(const float4 *)(sr + 32 * st + 4);
+                        const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const float x0 = v[st][j], x1 = v[st + 2][j];
+                            v[st][j] = __fsub_rn(__fmul_rn(x0, c[j]), __fmul_rn(x1, sn[j]));
+                            v[st + 2][j] = __fadd_rn(__fmul_rn(x1, c[j]), __fmul_rn(x0, sn[j]));
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < QS; st++) split8_words(v[st], qh[st], ql[st]);
         }
 
         // scores of chunks 0 .. nch (transposed D layout), scaled and masked
@@ -627,19 +653,31 @@ void launch_attention_dense_check(const ditch_row *rows, int64_t n, int64_t T, i
 
 // With a.dense (set by launch_attention_dense_check for these rows), both
 // kernels are launched and the one the flag does not select exits at once.
-void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
+static void launch_attention(const AttnArgs &a, const AttnRope &rope, int64_t kv_heads, hipStream_t s) {
     if (a.dense) {
         DITCH_CHECK(!a.xs && attention_prompt_takes(a.hd, a.vd, a.T), DITCH_INVALID_ARGUMENT,
                     "attention: the whole-prompt kernel does not take this shape");
+        DITCH_CHECK(!rope.cos_t || a.hd == 128, DITCH_INVALID_ARGUMENT,
+                    "attention: the whole-prompt kernel rotates queries of head_dim 128 only");
         const dim3 grid((unsigned)((a.n + a.T - 1) / a.T), (unsigned)kv_heads);
-        if (a.hd == 64) hipLaunchKernelGGL(attn_prompt_kernel<64>, grid, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL(attn_prompt_kernel<128>, grid, dim3(512), 0, s, a);
+        if (a.hd == 64) hipLaunchKernelGGL(attn_prompt_kernel<64>, grid, dim3(512), 0, s, a, rope);
+        else hipLaunchKernelGGL(attn_prompt_kernel<128>, grid, dim3(512), 0, s, a, rope);
         DITCH_TRY_HIP(hipGetLastError());
     }
     if (a.hd == 64) launch_attn<64, 64>(a, kv_heads, s);
     else if (a.hd == 128) launch_attn<128, 128>(a, kv_heads, s);
     else launch_attn<192, 128>(a, kv_heads, s);
     DITCH_TRY_HIP(hipGetLastError());
+}
+
+void launch_attention_mfma(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
+    launch_attention(a, AttnRope{}, kv_heads, s);
+}
+
+void launch_attention_mfma_rope(const AttnArgs &a, const AttnRope &rope, int64_t kv_heads, hipStream_t s) {
+    DITCH_CHECK(a.dense && rope.cos_t && rope.sin_t && rope.rope_len > 0, DITCH_INVALID_ARGUMENT,
+                "attention: query rotation needs the dense flag and the rope tables");
+    launch_attention(a, rope, kv_heads, s);
 }
 
 }  // namespace ditch

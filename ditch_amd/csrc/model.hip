@@ -9,6 +9,7 @@
 
 #include "decode.h"
 #include "internal.h"
+#include "attention_rope.h"
 #include "tiled.h"
 #include "model.h"
 
@@ -67,6 +68,11 @@ struct RopeArgs {
     int64_t n, heads, kv_heads, hd, rope_off, rot, half, rope_len, T, kvd, nb;
     float eps;
     int style;
+    // the whole-prompt attention rotates the queries itself when *dense is
+    // set (q_in_attn: head_dim 128, whole-head neox, no query norm): the
+    // query heads are then left as they are
+    const int *dense;
+    int q_in_attn;
 };
 
 // One head vector: optional RMSNorm (x * inv * w, tensor.zig:1167-1179), then
@@ -116,12 +122,12 @@ __device__ void head_norm_rope(float *x, float *dst2, const float *nw, const Rop
 // every load of the group issued before the first use; the same operations
 // in the same order as head_norm_rope.
 template <int HB>
-__device__ void heads_rope_128(const RopeArgs &a, int64_t i, int64_t pos, float *kd) {
+__device__ void heads_rope_128(const RopeArgs &a, int64_t i, int64_t pos, float *kd, int64_t h_first) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int64_t H = a.heads + a.kv_heads;
     const int64_t p = pos < a.rope_len - 1 ? pos : a.rope_len - 1;
     const float c = a.cos_t[p * 64 + lane], sn = a.sin_t[p * 64 + lane];
-    for (int64_t h0 = (int64_t)wave * HB; h0 < H; h0 += (int64_t)nw * HB) {
+    for (int64_t h0 = h_first + (int64_t)wave * HB; h0 < H; h0 += (int64_t)nw * HB) {
         float x0[HB], x1[HB];
 #pragma unroll
         for (int j = 0; j < HB; j++) {
@@ -168,7 +174,8 @@ __global__ void qk_rope_cache_kernel(RopeArgs a) {
     if (b >= a.nb || pos >= a.T) return;  // outside the KV cache: the row is skipped
     float *kd = a.kc + (b * a.T + pos) * a.kvd, *vd = a.vc + (b * a.T + pos) * a.kvd;
     if (a.hd == 128 && a.rope_off == 0 && a.rot == 128 && a.half == 64 && a.style == DITCH_ROPE_NEOX) {
-        heads_rope_128<4>(a, i, pos, kd);
+        const bool keys_only = a.q_in_attn && *a.dense;
+        heads_rope_128<4>(a, i, pos, kd, keys_only ? a.heads : 0);
         for (int64_t d = threadIdx.x; d < a.kvd; d += blockDim.x) vd[d] = a.v[i * a.kvd + d];
         return;
     }
@@ -1269,6 +1276,20 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             kc = pc->k + li * B * T * kvd;
             vc = pc->v + li * B * T * kvd;
         }
+        // the attention kernels this layer takes; with the whole-prompt kernel
+        // (decided on the device by the dense check) and a whole-head neox
+        // RoPE of head_dim 128 without a query norm, that kernel rotates the
+        // queries as it loads them and the RoPE kernel leaves them alone
+        const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
+        const bool frag_epi = attn_split_fragments && frags && mfma_attn && (nh * vd) % 128 == 0 &&
+                              frag_only(L.o, n) && !mx_only(L.o, n);
+        const bool prompt_attn = mfma_attn && !frag_epi && attention_prompt_takes(hd, vd, T);
+        const bool q_rope_in_attn = prompt_attn && !c.mla && hd == 128 && c.rotary_dim == 128 &&
+                                    c.rope_style == DITCH_ROPE_NEOX && !c.qk_norm;
+        if (prompt_attn && !dense_checked) {
+            launch_attention_dense_check(d_rows, n, T, B, dense_flag, s);
+            dense_checked = true;
+        }
         RopeArgs ra{};
         ra.q = q;
         ra.k = kk;
@@ -1293,26 +1314,23 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
         ra.kvd = kvd;
         ra.eps = c.rms_eps;
         ra.style = c.rope_style;
+        ra.dense = q_rope_in_attn ? dense_flag : nullptr;
+        ra.q_in_attn = q_rope_in_attn ? 1 : 0;
         hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
         DITCH_TRY_HIP(hipGetLastError());
         AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0, B, nullptr};
-        const bool mfma_attn = attention_mfma_takes(hd, vd, nh / nkv);
         Act aact{att, nullptr, 0};
         // (the kernel's own bf16-fragment epilogue needs 34 KB more LDS a
         // workgroup, which halves its occupancy: the o product splitting the
         // f32 rows costs less)
-        if (attn_split_fragments && frags && mfma_attn && (nh * vd) % 128 == 0 && frag_only(L.o, n) &&
-            !mx_only(L.o, n)) {
+        if (frag_epi) {
             aa.ldk = split_ldk(nh * vd);
             aa.xs = m->atts.get<uint8_t>(split_bytes_ldk(n, aa.ldk, 2));
             aact = Act{att, aa.xs, aa.ldk};
         }
-        if (mfma_attn && !aa.xs && attention_prompt_takes(hd, vd, T)) {
-            if (!dense_checked) launch_attention_dense_check(d_rows, n, T, B, dense_flag, s);
-            dense_checked = true;
-            aa.dense = dense_flag;
-        }
-        if (mfma_attn) launch_attention_mfma(aa, nkv, s);
+        if (prompt_attn) aa.dense = dense_flag;
+        if (q_rope_in_attn) launch_attention_mfma_rope(aa, AttnRope{m->rope_cos, m->rope_sin, (int64_t)c.rope_len}, nkv, s);
+        else if (mfma_attn) launch_attention_mfma(aa, nkv, s);
         else hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((n * nh + 3) / 4)), dim3(256), 0, s, aa);
         DITCH_TRY_HIP(hipGetLastError());
         mm_act(m, L.o, x, aact, n, nullptr, 1, s);  // x += o(att)
