@@ -695,17 +695,25 @@ __global__ void row_norms_kernel(float *out, TileView w) {
 
 // W^T y, first pass: block (column chunk, row chunk) -> partial sums
 // [row_chunk][q][cols]; the second pass adds the chunks in order. A row
-// chunk is 32 rows, decoded 8 at a time with every load of the 8 issued
-// before the first multiply-add (a chunk of hundreds of rows walked one
-// decode at a time waits for each load in turn, and gives a 2048 x 768
-// matrix 24 workgroups).
+// chunk is 32 rows (taller, in steps of 32, where that would make more than
+// MVT_CHUNKS chunks: the partial sums stay near the weight's own size),
+// decoded 8 at a time with every load of the 8 issued before the first
+// multiply-add (a chunk of hundreds of rows walked one decode at a time
+// waits for each load in turn, and gives a 2048 x 768 matrix 24
+// workgroups).
 constexpr int MVT_ROWS = 32;
+constexpr int MVT_CHUNKS = 256;
 constexpr int MVT_MAXQ = 16;
 
-__global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q) {
+static int64_t mvt_chunk_rows(const TileView &w) {
+    const int64_t steps = (w.rows + MVT_ROWS * MVT_CHUNKS - 1) / (MVT_ROWS * MVT_CHUNKS);
+    return MVT_ROWS * (steps > 1 ? steps : 1);
+}
+
+__global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q, int64_t chunk_rows) {
     int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int64_t rc = blockIdx.y;
-    int64_t r0 = rc * MVT_ROWS, r1 = r0 + MVT_ROWS < w.rows ? r0 + MVT_ROWS : w.rows;
+    int64_t r0 = rc * chunk_rows, r1 = r0 + chunk_rows < w.rows ? r0 + chunk_rows : w.rows;
     if (c >= w.cols) return;
     float acc[MVT_MAXQ];
 #pragma unroll
@@ -888,14 +896,14 @@ void launch_row_norms(float *out, const TileView &w, hipStream_t s) {
     DITCH_TRY_HIP(hipGetLastError());
 }
 size_t matvecT_partials_floats(const TileView &w, int64_t q) {
-    int64_t chunks = (w.rows + MVT_ROWS - 1) / MVT_ROWS;
+    const int64_t cr = mvt_chunk_rows(w), chunks = (w.rows + cr - 1) / cr;
     return (size_t)chunks * q * w.cols;
 }
 void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials) {
     DITCH_CHECK(q >= 1 && q <= MVT_MAXQ, DITCH_UNSUPPORTED, "matvecTMulti: q must be 1..16");
-    int64_t chunks = (w.rows + MVT_ROWS - 1) / MVT_ROWS;
+    const int64_t cr = mvt_chunk_rows(w), chunks = (w.rows + cr - 1) / cr;
     dim3 grid((unsigned)((w.cols + 255) / 256), (unsigned)chunks);
-    hipLaunchKernelGGL(matvecT_partial_kernel, grid, dim3(256), 0, s, partials, w, y, q);
+    hipLaunchKernelGGL(matvecT_partial_kernel, grid, dim3(256), 0, s, partials, w, y, q, cr);
     DITCH_TRY_HIP(hipGetLastError());
     hipLaunchKernelGGL(matvecT_reduce_kernel, dim3(grid_1d(q * w.cols)), dim3(256), 0, s, out, partials, chunks,
                        q * w.cols);

@@ -214,6 +214,16 @@ def test_rownorms_matvecT(dev, ref):
         close(dev.matvecTMulti(w, y), ref.matvecTMulti(w, y), **TOL_MATMUL)
 
 
+@pytest.mark.parametrize("kind,rows", [("bf16", 8200), ("q8_0", 16411)])
+def test_matvecT_tall_row_chunks(dev, ref, kind, rows):
+    """matvecTMulti over more than 256 x 32 rows: row chunks taller than 32
+    (64 and 96 rows here, the last one ragged), five vectors."""
+    rng = np.random.default_rng(rows)
+    w = wg.make(kind, rows, 256, rng)
+    y = rng.standard_normal((5, rows)).astype(np.float32)
+    close(dev.matvecTMulti(w, y), ref.matvecTMulti(w, y), **TOL_MATMUL)
+
+
 def test_kl_rows(dev, ref):
     rng = np.random.default_rng(17)
     base = rng.standard_normal((4, 5000)).astype(np.float32) * 2
