@@ -371,10 +371,14 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
             if (e < a.E && !((kept_mask >> (e / per)) & 1ull)) ch[j] = -INFINITY;
         }
     }
-    // top k, in selection order
+    // top k, in selection order (k <= 16; the selections stay in registers:
+    // arrays indexed at run time would live in scratch memory)
     float sum = 0.f;
     int32_t selj[16];
-    for (int64_t jk = 0; jk < a.k; jk++) {
+    float pbs[16];
+#pragma unroll
+    for (int jk = 0; jk < 16; jk++) {
+        if (jk >= a.k) break;
         float v = -INFINITY;
         int idx = 0;
 #pragma unroll
@@ -389,28 +393,33 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
                 ch[j] = -INFINITY;
             }
         pb = __shfl(pb, best % 64, 64);
-        if (jk < 16) selj[jk] = best;
-        if (lane == 0) {
-            a.sel[t * a.k + jk] = best;
-            a.selw[t * a.k + jk] = pb;
-        }
+        selj[jk] = best;
+        pbs[jk] = pb;
         sum = __fadd_rn(sum, pb);
     }
-    if (lane == 0) {
-        if (a.norm_topk && sum > 0)
-            for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fdiv_rn(a.selw[t * a.k + j], sum);
-        if (a.scaling != 1.0f)
-            for (int64_t j = 0; j < a.k; j++) a.selw[t * a.k + j] = __fmul_rn(a.selw[t * a.k + j], a.scaling);
-        // the selections in ascending expert index (the combine's order)
-        int32_t order[16];
-        for (int64_t j = 0; j < a.k; j++) order[j] = (int32_t)j;
-        for (int64_t a1 = 1; a1 < a.k; a1++)
-            for (int64_t b1 = a1; b1 > 0 && selj[order[b1]] < selj[order[b1 - 1]]; b1--) {
-                const int32_t tmp = order[b1];
-                order[b1] = order[b1 - 1];
-                order[b1 - 1] = tmp;
-            }
-        for (int64_t j = 0; j < a.k; j++) a.ord[t * a.k + j] = order[j];
+    // lane j < k finishes selection j: its weight (renormalised by the sum,
+    // then scaled), and its place in ascending expert index (the combine's
+    // order: the experts are distinct, so the place is the count of smaller
+    // ones)
+    int32_t my_sel = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jk = 0; jk < 16; jk++)
+        if (lane == jk) {
+            my_sel = selj[jk];
+            my_w = pbs[jk];
+        }
+    if (lane < a.k) {
+        float w = my_w;
+        if (a.norm_topk && sum > 0) w = __fdiv_rn(w, sum);
+        if (a.scaling != 1.0f) w = __fmul_rn(w, a.scaling);
+        a.sel[t * a.k + lane] = my_sel;
+        a.selw[t * a.k + lane] = w;
+        int rank = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (i < a.k && selj[i] < my_sel) rank++;
+        a.ord[t * a.k + rank] = lane;
     }
 }
 
