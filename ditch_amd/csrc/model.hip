@@ -449,22 +449,43 @@ __global__ __launch_bounds__(LIST_WAVES * 64) void expert_list_kernel(const int3
     const int64_t nk = n * k;
     const int64_t seg = (nk + LIST_WAVES * 64 - 1) / (LIST_WAVES * 64) * 64;
     const int64_t lo = wave * seg, hi = lo + seg < nk ? lo + seg : nk;
+    // both passes take 8 steps of 64 selections at a time, their loads
+    // issued together (one step at a time waits for each load in turn)
+    constexpr int LU = 8;
     int32_t cnt = 0;
-    for (int64_t c = lo; c < hi; c += 64) cnt += __popcll(__ballot(c + lane < hi && sel[c + lane] == e));
+    for (int64_t c = lo; c < hi; c += 64 * LU) {
+        int32_t v[LU];
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int64_t i = c + 64 * u + lane;
+            v[u] = i < hi ? sel[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < LU; u++) cnt += __popcll(__ballot(v[u] == e));
+    }
     if (lane == 0) wave_cnt[wave] = cnt;
     __syncthreads();
     int32_t base = offsets[e];
     for (int w = 0; w < wave; w++) base += wave_cnt[w];
-    for (int64_t c = lo; c < hi; c += 64) {
-        const int64_t i = c + lane;
-        const bool hit = i < hi && sel[i] == e;
-        const unsigned long long ballot = __ballot(hit);
-        if (hit) {
-            const int32_t p = base + __popcll(ballot & ((1ull << lane) - 1ull));
-            pair_token[p] = (int32_t)(i / k);
-            pair_of[i] = p;
+    for (int64_t c = lo; c < hi; c += 64 * LU) {
+        int32_t v[LU];
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int64_t i = c + 64 * u + lane;
+            v[u] = i < hi ? sel[i] : -1;
         }
-        base += __popcll(ballot);
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int64_t i = c + 64 * u + lane;
+            const bool hit = v[u] == e;
+            const unsigned long long ballot = __ballot(hit);
+            if (hit) {
+                const int32_t p = base + __popcll(ballot & ((1ull << lane) - 1ull));
+                pair_token[p] = (int32_t)(i / k);
+                pair_of[i] = p;
+            }
+            base += __popcll(ballot);
+        }
     }
 }
 
