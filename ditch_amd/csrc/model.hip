@@ -499,21 +499,51 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int32_t *counts, i
                                                         int64_t max_blocks) {
     __shared__ int32_t cnt_s[ROUTE_MAXE], off_s[ROUTE_MAXE], base_s[ROUTE_MAXE], dbase_s[ROUTE_MAXE];
     __shared__ int32_t tot_blocks;
-    for (int64_t e = threadIdx.x; e < E; e += blockDim.x) cnt_s[e] = counts[e];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t o = 0, b = 0, d = 0;
-        for (int64_t e = 0; e < E; e++) {
-            const int32_t nb = (cnt_s[e] + 15) / 16;
-            off_s[e] = o;
-            base_s[e] = b;
-            dbase_s[e] = d;
-            o += cnt_s[e];
-            b += nb;
-            d += (nb + 3) / 4;
+    __shared__ int32_t wsum[3][16];
+    // exclusive prefix sums over the experts of their pairs, 16-row blocks
+    // and 4-block tile rows (thread e holds expert e, E <= 512 < 1024):
+    // inclusive scans within each wave, then the earlier waves' totals
+    {
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int64_t e = threadIdx.x;
+        const int32_t c = e < E ? counts[e] : 0, nb = (c + 15) / 16, nd = (nb + 3) / 4;
+        int32_t ic = c, ib = nb, id = nd;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t tc = __shfl_up(ic, o, 64), tb = __shfl_up(ib, o, 64), td = __shfl_up(id, o, 64);
+            if (lane >= o) {
+                ic += tc;
+                ib += tb;
+                id += td;
+            }
         }
-        tot_blocks = b;
-        *count = d;
+        if (lane == 63) {
+            wsum[0][wv] = ic;
+            wsum[1][wv] = ib;
+            wsum[2][wv] = id;
+        }
+        __syncthreads();
+        int32_t pc = 0, pb = 0, pd = 0;
+        for (int w = 0; w < wv; w++) {
+            pc += wsum[0][w];
+            pb += wsum[1][w];
+            pd += wsum[2][w];
+        }
+        if (e < E) {
+            cnt_s[e] = c;
+            off_s[e] = pc + ic - c;
+            base_s[e] = pb + ib - nb;
+            dbase_s[e] = pd + id - nd;
+        }
+        if (threadIdx.x == 0) {
+            int32_t b = 0, d = 0;
+            for (int w = 0; w < (int)(blockDim.x >> 6); w++) {
+                b += wsum[1][w];
+                d += wsum[2][w];
+            }
+            tot_blocks = b;
+            *count = d;
+        }
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < E; e += blockDim.x) {
