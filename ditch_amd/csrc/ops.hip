@@ -82,6 +82,48 @@ __global__ void rmsnorm_kernel(float *out, const float *x, const float *w, int64
     }
 }
 
+// rmsnorm_kernel for rows of 256 NV columns: a wave per row holds it in
+// registers (NV float4 a lane, one read of the row), sums its squares over
+// the wave and writes the normalised row; four rows a workgroup.
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float *out, const float *x, const float *w, int64_t wlen,
+                                                           int64_t n, float eps, int gemma, const int64_t *row_index,
+                                                           int64_t n_src) {
+    constexpr int64_t LEN = 256 * NV;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= n) return;
+    int64_t src = row_index ? row_index[r] : r;
+    src = (uint64_t)src < (uint64_t)n_src ? src : n_src - 1;  // the row lists are unsigned
+    const float4 *xr = (const float4 *)(x + src * LEN);
+    float4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) v[j] = xr[64 * j + lane];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        ss = __builtin_fmaf(v[j].x, v[j].x, ss);
+        ss = __builtin_fmaf(v[j].y, v[j].y, ss);
+        ss = __builtin_fmaf(v[j].z, v[j].z, ss);
+        ss = __builtin_fmaf(v[j].w, v[j].w, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)LEN), eps)));
+    float4 *o = (float4 *)(out + r * LEN);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int64_t i = 4 * (64 * j + lane);
+        float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            e[q] = __fmul_rn(e[q], inv);
+            if (wlen > 0) e[q] = __fmul_rn(e[q], gemma ? __fadd_rn(1.0f, w[i + q]) : w[i + q]);
+        }
+        o[64 * j + lane] = make_float4(e[0], e[1], e[2], e[3]);
+    }
+}
+
 // RMS norm of rows (tensor.zig:1167-1179) written straight into the tiled
 // GEMM's two-term bf16 A fragments ([n/16][ldk][2][64 lanes] x 16 bytes,
 // columns past len are zero) and, when `out` is given, as f32 rows too. One
@@ -761,8 +803,17 @@ __global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64
 void launch_rmsnorm(float *out, const float *x, const float *w, int64_t wlen, int64_t n, int64_t len, float eps,
                     int gemma, hipStream_t s, const int64_t *row_index, int64_t n_src) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, gemma, row_index,
-                       row_index ? n_src : n, len, len);
+    const int64_t ns = row_index ? n_src : n;
+    const dim3 g4((unsigned)((n + 3) / 4));
+    // rows of whole 256-column steps up to 4096, 16-byte aligned: a wave per row
+    const bool rows = len % 256 == 0 && len <= 4096 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0;
+    if (rows && len == 512) hipLaunchKernelGGL(rmsnorm_rows_kernel<2>, g4, dim3(256), 0, s, out, x, w, wlen, n, eps, gemma, row_index, ns);
+    else if (rows && len == 1024) hipLaunchKernelGGL(rmsnorm_rows_kernel<4>, g4, dim3(256), 0, s, out, x, w, wlen, n, eps, gemma, row_index, ns);
+    else if (rows && len == 2048) hipLaunchKernelGGL(rmsnorm_rows_kernel<8>, g4, dim3(256), 0, s, out, x, w, wlen, n, eps, gemma, row_index, ns);
+    else if (rows && len == 4096) hipLaunchKernelGGL(rmsnorm_rows_kernel<16>, g4, dim3(256), 0, s, out, x, w, wlen, n, eps, gemma, row_index, ns);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, s, out, x, w, wlen, len, eps, gemma,
+                           row_index, ns, len, len);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_rmsnorm_split(void *xs, int64_t ldk, float *out, const float *x, const float *w, int64_t wlen, int64_t n,
