@@ -16,14 +16,21 @@ Beside it, in the same JSON line:
                  events on the library's stream (roofline_fp8: the same for
                  the FP8 leg);
   gemv         - configs[1]: the Q8_0 14336x4096 dequant-fused product for
-                 M in {1, 4, 16, 64, 256}, achieved HBM GB/s vs 8 TB/s;
-  c1           - configs[0]: Qwen2.5-0.5B-shaped f32 forward, 16 x 64 tokens;
+                 M in {1, 4, 16, 64, 256}, achieved HBM GB/s vs 8 TB/s
+                 (gemv_cpu_baseline: the oracle's product for each M);
+  c1           - configs[0]: Qwen2.5-0.5B-shaped f32 forward, 16 x 64 tokens,
+                 its CPU baseline, and on the same model the rest of a
+                 search trial (`trial`: the residual-mean pass over 400
+                 prompts, greedy decode of 16 x 32 tokens, the none / pre /
+                 full edit apply) beside the reference's published figures;
   c4           - configs[3]: Qwen3-30B-A3B-shaped INT4 MoE, 48 layers, 32 x
                  128 tokens, then the rank-2 edit of every o_proj and expert
-                 down_proj (its apply time) and the edited forward;
-  c5           - configs[4] (with --c5 only: it pins ~100 GB of host memory):
-                 DeepSeek-V3-shaped FP8, 12 layers, 256 experts streamed
-                 through a 96 GB HBM cache, 16 x 256 tokens;
+                 down_proj (one batch call: its apply time) and the edited
+                 forward, with its CPU baseline (a layer sample, scaled);
+  c5           - configs[4] (`--no-c5` skips it; skipped with the reason when
+                 host memory is short): DeepSeek-V3-shaped FP8, 12 layers,
+                 256 experts streamed through a 96 GB HBM cache, 16 x 256
+                 tokens;
   cpu_baseline - the CPU oracle (oracle/cpu_ref.c, built -march=native on
                  this host) on a sample of the benchmark's prompts at the
                  full depth, with the GPU's logits compared on that sample.
@@ -71,6 +78,21 @@ def cpu_share():
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+# host bytes the C5 leg needs: 2 304 routed expert blobs of ~44 MB each plus
+# the trunk, with room for the rest of the process
+C5_HOST_BYTES = 120 * 10**9
+
+
+def host_mem_available():
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return None
 
 
 def cpu_model():
@@ -403,24 +425,189 @@ def gemv_leg(dev, reps):
     return out
 
 
-def c1_leg(dev, steps, warmup):
+def c1_leg(dev, steps, warmup, cpu=True, trial=True):
     from ditch_amd.hip import Model
     spec = c1_spec()
     model = Model(dev, spec)
     r = time_forward(dev, model, C1, steps, warmup)
+    tr = trial_leg(dev, model, spec) if trial else None
     model.free()
     n = C1["prompts"] * C1["tokens"]
-    return {"workload": "c1: Qwen2.5-0.5B-shaped, 24 layers, d 896, FFN 4864, GQA 14/2 x 64, vocab 151936, f32 "
-                        "weights N(0,0.02), q/k/v bias, tied embedding; 16 prompts x 64 tokens",
-            "ms_per_step": round(r["ms"], 3), "tokens_per_s": round(n / (r["ms"] * 1e-3), 1),
-            "outputs_finite": bool(np.isfinite(r["logprobs"]).all() and np.isfinite(r["res"]).all())}
+    out = {"workload": "c1: Qwen2.5-0.5B-shaped, 24 layers, d 896, FFN 4864, GQA 14/2 x 64, vocab 151936, f32 "
+                       "weights N(0,0.02), q/k/v bias, tied embedding; 16 prompts x 64 tokens",
+           "ms_per_step": round(r["ms"], 3), "tokens_per_s": round(n / (r["ms"] * 1e-3), 1),
+           "outputs_finite": bool(np.isfinite(r["logprobs"]).all() and np.isfinite(r["res"]).all()),
+           "trial": tr}
+    if cpu:
+        out["cpu_baseline"], out["parity_vs_cpu_sample"] = cpu_leg(spec, C1, r, prompts=4)
+    return out
 
 
-def c4_leg(dev, steps, warmup, layers=48):
+def trial_leg(dev, model, spec):
+    """The other timed parts of a search trial the reference publishes for
+    this model shape (tools/real-model-validation.md:56-66, Qwen2.5-0.5B),
+    on the C1 model: the residual-mean pass over 400 prompts
+    (engine.zig:314-438: forward with every layer entry's last-token
+    residual, the window mean and the f64 sums per entry; batches of 16
+    prompts of 32 tokens), greedy decode of 16 prompts x 32 tokens
+    (generateKeep, model.zig:5378-5444; prefill included), and the apply of
+    the none / pre / full edits of every layer's o_proj and down_proj with
+    one direction (abliterate.zig:148-210; full: lora rank 3)."""
+    from ditch_amd import abi, hipmem
+    c = C1
+    L, H, V = c["layers"], c["hidden"], c["vocab"]
+    rng = np.random.default_rng(77)
+    # residual-mean pass
+    B, T, NP = 16, 32, 400
+    E = L + 1
+    bres = hipmem.Buffer(E * B * H * 4)
+    blog = hipmem.Buffer(B * V * 4)
+    bsum = hipmem.Buffer(E * H * 8)
+    bsum.zero()
+    bvout = hipmem.Buffer(B * E * H * 4)
+    bmean = hipmem.Buffer(E * H * 4)
+    rows = np.array([(b, p) for b in range(B) for p in range(T)], dtype=np.uint32)
+    last = np.array([b * T + T - 1 for b in range(B)], dtype=np.uint64)
+    first = np.arange(B, dtype=np.uint32)
+    take = np.ones(B, dtype=np.uint32)
+    br, bl = hipmem.Buffer.from_array(rows), hipmem.Buffer.from_array(last)
+    bf, btk = hipmem.Buffer.from_array(first), hipmem.Buffer.from_array(take)
+    batches = [hipmem.Buffer.from_array(rng.integers(0, V, B * T).astype(np.uint32)) for _ in range(NP // B)]
+    dev.sync()
+    e0, e1 = hipmem.Event(), hipmem.Event()
+    t0 = time.perf_counter()
+    e0.record(dev.stream)
+    for bt in batches:
+        model.forward_device(bt.ptr, br.ptr, B * T, B, T, bl.ptr, B, bres.ptr, bl.ptr, B, blog.ptr)
+        dev.check(dev.lib.ditch_hip_residual_reduce_device(dev.h, bres.ptr, E, B, H, bf.ptr, btk.ptr, B, -1.0,
+                                                           bvout.ptr, bsum.ptr, None, None))
+    dev.check(dev.lib.ditch_hip_residual_mean_device(dev.h, bmean.ptr, bsum.ptr, NP, E * H, None))
+    e1.record(dev.stream)
+    e1.synchronize()
+    mean_pass_s = time.perf_counter() - t0
+    mean_pass_gpu_s = e0.elapsed_ms(e1) / 1e3
+    means = bmean.download(np.float32, (E, H))
+    # decode
+    prompts = [list(rng.integers(0, V, T)) for _ in range(B)]
+    cache = model.kv_cache(B, 2 * T + 8)
+    try:
+        model.generate(cache, prompts, 4)  # warm-up
+        dev.sync()
+        t0 = time.perf_counter()
+        outs, _ = model.generate(cache, prompts, T)
+        gen_s = time.perf_counter() - t0
+    finally:
+        model.kv_cache_free(cache)
+    new_tokens = sum(len(o) for o in outs)
+    # apply: every layer's o_proj and down_proj, one direction per layer
+    dirs = []
+    for li in range(L):
+        v = rng.standard_normal(H)
+        dirs.append(np.ascontiguousarray((v / np.linalg.norm(v))[None, :], dtype=np.float32))
+    targets = []
+    for li in range(L):
+        targets.append((li, abi.SLOT["O"], -1, dirs[li], 1.0))
+        targets.append((li, abi.SLOT["DOWN"], -1, dirs[li], 1.0))
+    apply_ms = {}
+    for mode in ("none", "pre", "full"):
+        runs = []
+        for rep in range(3):
+            model.reset_deltas()
+            dev.sync()
+            t0 = time.perf_counter()
+            if mode == "none":
+                model.edit_batch(targets, 1)
+            else:
+                for li, slot, e, v, wt in targets:
+                    model.edit_ex(li, slot, e, v, wt, mode=mode, lora_rank=3, seed=li)
+            dev.sync()
+            runs.append((time.perf_counter() - t0) * 1e3)
+        apply_ms[mode] = round(float(np.median(runs)), 3)
+    model.reset_deltas()
+    return {"workload": "c1 model (Qwen2.5-0.5B shape, f32 weights): the reference's per-trial timings "
+                        "(tools/real-model-validation.md:56-66: 4 vCPU, bf16 weights)",
+            "residual_mean_pass_s": round(mean_pass_s, 3), "residual_mean_pass_gpu_s": round(mean_pass_gpu_s, 3),
+            "residual_mean_pass_prompts": NP, "residual_mean_pass_tokens_per_prompt": T,
+            "residual_means_finite": bool(np.isfinite(means).all()),
+            "decode_tokens_per_s": round(new_tokens / gen_s, 1), "decode_prompts": B, "decode_new_tokens": T,
+            "decode_s_incl_prefill": round(gen_s, 4),
+            "apply_ms": apply_ms, "apply_matrices": len(targets),
+            "reference_cpu": {"residual_mean_pass_s": 36.55, "decode_tokens_per_s": 143.1,
+                              "apply_ms": {"none": 8.7, "pre": 16.1, "full": 293.8},
+                              "source": "tools/real-model-validation.md:63-65 (4 threads, bf16 Qwen2.5-0.5B)"}}
+
+
+def c4_cpu_leg(spec, cfg, fwd, layers_run=4):
+    """The oracle on configs[3]'s first prompt (128 tokens) through the first
+    `layers_run` layers (every layer has the same shapes; the experts kept
+    packed and decoded per use, the reference's streamed mode), scaled to
+    the full depth: tokens/s of the 48-layer forward on this host's cores."""
+    from oracle import ref as oref
+    cores = cpu_share()
+    tokens, rows, last = fwd["batch"]
+    T, L = cfg["tokens"], cfg["layers"]
+    with tempfile.TemporaryDirectory() as d:
+        so = os.path.join(d, "libcpu_ref_native.so")
+        try:
+            oref.build(so, arch="native")
+        except Exception:
+            so = oref.LIB
+        m = oref.RefModel(spec, path=so, threads=cores, keep_packed=True)
+        m.limit_layers(0, layers_run)
+        t0 = time.perf_counter()
+        m.forward(tokens[:T], [tuple(x) for x in rows[:T]], capture_rows=last[:1], logit_rows=last[:1])
+        secs = time.perf_counter() - t0
+        m.free()
+    full = secs * L / layers_run
+    return {"value": round(T / full, 3), "unit": "tokens/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+            "sample": (f"oracle/cpu_ref.c -O3 -march=native, {cores} threads: 1 prompt x {T} tokens through the "
+                       f"first {layers_run} of {L} layers with lm_head ({secs:.1f}s), scaled to {L} layers; "
+                       "INT4 experts decoded per use"),
+            "cpu_seconds": round(secs, 2)}
+
+
+def c2_cpu_leg(reps_s=2.0):
+    """The oracle's dequant-fused matmulT (tensor.zig:827-913 restated) on
+    configs[1]'s Q8_0 14336 x 4096 weight for each M, on this host's cores."""
+    import torch
+    from ditch_amd import synth
+    from oracle import ref as oref
+    cores = cpu_share()
+    rng = np.random.default_rng(3)
+    N, K = 14336, 4096
+    w = synth.q8_0_random(N, K, torch.Generator().manual_seed(11))
+    wbytes = N * (K // 32) * 34
+    out = []
+    with tempfile.TemporaryDirectory() as d:
+        so = os.path.join(d, "libcpu_ref_native.so")
+        try:
+            oref.build(so, arch="native")
+        except Exception:
+            so = oref.LIB
+        r = oref.Ref(path=so, threads=cores)
+        for m in (1, 4, 16, 64, 256):
+            x = rng.standard_normal((m, K)).astype(np.float32)
+            r.matmulT(x, w)
+            n, t0 = 0, time.perf_counter()
+            while True:
+                r.matmulT(x, w)
+                n += 1
+                el = time.perf_counter() - t0
+                if n >= 3 and el >= reps_s / 5:
+                    break
+            ms = el / n * 1e3
+            nbytes = wbytes + m * K * 2 + m * N * 4
+            out.append({"M": m, "ms": round(ms, 3), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 2),
+                        "GFLOP_s": round(2.0 * m * N * K / (ms * 1e-3) / 1e9, 1)})
+    return {"cores": cores, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"oracle ref_matmulT, Q8_0 {N}x{K}, {cores} threads, at least 3 calls per M", "per_M": out}
+
+
+def c4_leg(dev, steps, warmup, layers=48, cpu=True):
     """configs[3] at full depth: the forward, the rank-2 none-mode edit of
     every o_proj and every expert's down_proj (abliterate.zig:148-210,
-    264-280; R = QR of a 2048 x 2 Gaussian, lambda 1), timed as one apply,
-    then the edited forward."""
+    264-280; R = QR of a 2048 x 2 Gaussian, lambda 1) made by one batch
+    call and timed as one apply, then the edited forward."""
     from ditch_amd import abi
     from ditch_amd.hip import Model
     c = dict(C4, layers=layers)
@@ -435,28 +622,51 @@ def c4_leg(dev, steps, warmup, layers=48):
     rng = np.random.default_rng(14)
     v, _ = np.linalg.qr(rng.standard_normal((c["hidden"], 2)))
     v = np.ascontiguousarray(v.T, dtype=np.float32)
-    dev.sync()
-    t0 = time.perf_counter()
+    targets = []
     for li in range(layers):
-        model.edit(li, abi.SLOT["O"], -1, v, 1.0)
-        for e in range(c["experts"]):
-            model.edit(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0)
-    dev.sync()
-    apply_s = time.perf_counter() - t0
+        targets.append((li, abi.SLOT["O"], -1, v, 1.0))
+        targets += [(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0) for e in range(c["experts"])]
+    # one ditch_hip_model_edit_batch call per apply (abliterate.apply); the
+    # first apply pays the allocator's growth, the rest are timed
+    applies = []
+    for rep in range(4):
+        dev.sync()
+        t0 = time.perf_counter()
+        model.edit_batch(targets, 2)
+        dev.sync()
+        applies.append(time.perf_counter() - t0)
+    apply_s = float(np.median(applies[1:]))
+    # algorithmic bytes of one apply: the INT4 codes, f16 scales and 4-bit
+    # zero points of every edited matrix (read once), plus its delta
+    def int4_bytes(rows, cols):
+        groups = cols // 128
+        return rows * cols // 2 + rows * groups * 2 + rows * groups // 2 + 2 * 4 * (rows + cols)
+    apply_bytes = layers * (int4_bytes(c["hidden"], c["heads"] * c["head_dim"]) +
+                            c["experts"] * int4_bytes(c["hidden"], c["moe_inter"]))
+    stats1 = model.path_stats()
     edited = time_forward(dev, model, c, steps, warmup, batch=base["batch"])
+    stats2 = model.path_stats()
     model.free()
+    cpu_b = c4_cpu_leg(spec, c, base) if cpu else None
     n = c["prompts"] * c["tokens"]
     flops = 2.0 * n * c["top_k"] * 3 * c["hidden"] * c["moe_inter"] * layers
     return {"workload": f"c4: Qwen3-30B-A3B-shaped MoE, {layers} layers, d 2048, 128 experts top-8 of FFN 768, "
                         "INT4 g128 asymmetric, vocab 151936; 32 prompts x 128 tokens",
             "ms_per_step": round(base["ms"], 3), "tokens_per_s": round(n / (base["ms"] * 1e-3), 1),
             "routed_expert_tflops_over_step": round(flops / (base["ms"] * 1e-3) / 1e12, 2),
-            "edit_apply_s": round(apply_s, 3),
-            "edit_matrices": layers * (1 + c["experts"]),
+            "edit_apply_ms": round(apply_s * 1e3, 3),
+            "edit_apply_ms_runs": [round(a * 1e3, 3) for a in applies],
+            "edit_matrices": len(targets),
+            "edit_apply_bytes": int(apply_bytes),
+            "edit_apply_GB_s": round(apply_bytes / apply_s / 1e9, 1),
             "edited_ms_per_step": round(edited["ms"], 3),
             "edited_tokens_per_s": round(n / (edited["ms"] * 1e-3), 1),
+            "edited_over_unedited": round(edited["ms"] / base["ms"], 4),
             "moe_layers_device_planned_unedited": stats0["moe_device_planned"],
+            "moe_layers_device_planned_edited": stats2["moe_device_planned"] - stats1["moe_device_planned"],
+            "moe_layers_host_planned_edited": stats2["moe_host_planned"] - stats1["moe_host_planned"],
             "edit_changed_logits": bool(np.abs(edited["logits"] - base["logits"]).max() > 1e-4),
+            "cpu_baseline": cpu_b,
             "outputs_finite": bool(np.isfinite(base["logprobs"]).all() and np.isfinite(edited["logprobs"]).all())}
 
 
@@ -586,7 +796,9 @@ def main():
     ap.add_argument("--no-c1", action="store_true")
     ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c4-layers", type=int, default=48)
-    ap.add_argument("--c5", action="store_true", help="run configs[4] (pins ~100 GB of host memory)")
+    ap.add_argument("--no-c5", action="store_true", help="skip configs[4] (it pins ~48 GB and holds ~100 GB of "
+                                                         "host memory)")
+    ap.add_argument("--no-trial", action="store_true", help="skip the decode / residual-mean / apply timings")
     ap.add_argument("--kernel-only", choices=["glu", "gemv", "copy", "c1", "c4", "c5"], default=None,
                     help="run only one leg (for rocprofv3 runs)")
     ap.add_argument("--reps", type=int, default=20)
@@ -641,14 +853,28 @@ def main():
     if gemv:
         for g in gemv:
             log(f"gemv M={g['M']}: {g['avg_launch_us']} us, {g['GB_s']} GB/s ({g['frac_hbm_peak'] * 100:.1f}%)")
-    c1 = None if args.no_c1 else c1_leg(dev, args.steps, args.warmup)
+    c2_cpu = None if (args.no_gemv or args.no_cpu) else c2_cpu_leg()
+    if gemv and c2_cpu:
+        for g, cg in zip(gemv, c2_cpu["per_M"]):
+            g["cpu_ms"] = cg["ms"]
+            g["cpu_GB_s"] = cg["GB_s"]
+    c1 = None if args.no_c1 else c1_leg(dev, args.steps, args.warmup, cpu=not args.no_cpu, trial=not args.no_trial)
     if c1:
-        log(f"c1: {c1['ms_per_step']} ms/step, {c1['tokens_per_s']} tokens/s")
-    c4 = None if args.no_c4 else c4_leg(dev, args.steps, args.warmup, args.c4_layers)
+        log(f"c1: {c1['ms_per_step']} ms/step, {c1['tokens_per_s']} tokens/s; trial {c1['trial']}")
+    c4 = None if args.no_c4 else c4_leg(dev, args.steps, args.warmup, args.c4_layers, cpu=not args.no_cpu)
     if c4:
-        log(f"c4: {c4['ms_per_step']} ms/step ({c4['tokens_per_s']} tokens/s), edit apply {c4['edit_apply_s']} s, "
-            f"edited {c4['edited_ms_per_step']} ms/step")
-    c5 = c5_leg(dev, args.steps, args.warmup) if args.c5 else None
+        log(f"c4: {c4['ms_per_step']} ms/step ({c4['tokens_per_s']} tokens/s), edit apply {c4['edit_apply_ms']} ms "
+            f"({c4['edit_apply_GB_s']} GB/s), edited {c4['edited_ms_per_step']} ms/step")
+    c5 = None
+    if not args.no_c5:
+        avail = host_mem_available()
+        if avail is not None and avail < C5_HOST_BYTES:
+            c5 = {"skipped": f"host memory: {avail / 1e9:.0f} GB available, the C5 leg holds about "
+                             f"{C5_HOST_BYTES / 1e9:.0f} GB of expert blobs"}
+        else:
+            c5 = c5_leg(dev, args.steps, args.warmup)
+            log(f"c5: {c5['ms_per_step']} ms/step ({c5['tokens_per_s']} tokens/s), host->HBM "
+                f"{c5['host_to_hbm_GB_s_over_step']} GB/s over the step")
     cpu, parity = None, None
     if not args.no_cpu:
         t0 = time.time()
@@ -685,6 +911,7 @@ def main():
         f"c3_{other}": second,
         f"roofline_{other}": roof_other,
         "gemv": gemv,
+        "gemv_cpu_baseline": c2_cpu,
         "c1": c1,
         "c4": c4,
         "c5": c5,

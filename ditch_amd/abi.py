@@ -128,6 +128,12 @@ class EditOptions(C.Structure):
 ROWNORM = {"none": 0, "pre": 1, "full": 2}
 
 
+class EditTarget(C.Structure):
+    """`ditch_edit_target`: one matrix of a batch edit."""
+    _fields_ = [("layer", C.c_int32), ("slot", C.c_int32), ("expert", C.c_int32), ("weight", C.c_float),
+                ("v", C.c_void_p)]
+
+
 class Sampler(C.Structure):
     """`ditch_sampler` (model.Sampler)."""
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("seed", C.c_uint64)]
@@ -216,6 +222,7 @@ PROTOTYPES = {
     "ditch_hip_generate": (I32, [P, P, P, P, U64, U64, P, U64, P, P, P, P]),
     "ditch_hip_edit_delta": (I32, [P, P, P, P, P, U64, FLT]),
     "ditch_hip_model_edit": (I32, [P, I32, I32, I32, P, U64, FLT]),
+    "ditch_hip_model_edit_batch": (I32, [P, P, U64, U64]),
     "ditch_hip_logSoftmaxRows": (I32, [P, P, P, U64, U64]),
     "ditch_hip_klRows": (I32, [P, P, P, P, U64, U64]),
     "ditch_hip_edit_rank": (U64, [U64, U64, U64, P]),

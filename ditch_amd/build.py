@@ -8,6 +8,7 @@ import os
 import shutil
 import subprocess
 import sys
+import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -43,8 +44,24 @@ EXTRA = {"gemm_tile.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-disab
          "gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
+# sources compiled more than once: (object name, extra flags) per object
+# (gemv.hip: one object per tile format and activation term count, each
+# with those kernels, plus one with the dispatch; they compile in parallel)
+VARIANTS = {"gemv.hip": [("gemv", [])] + [(f"gemv_tf{tf}_x{xt}", [f"-DGEMV_TF={tf}", f"-DGEMV_XT={xt}"])
+                                           for tf in range(7) for xt in (2, 3) if xt == 2 or tf not in (1, 2)]}
+
+
 def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def jobs():
+    """(source, object name, extra flags) for every object of the library."""
+    out = []
+    for src in sources():
+        for name, flags in VARIANTS.get(src, [(src[:-len(".hip")], [])]):
+            out.append((src, name, flags))
+    return out
 
 
 def _includes(path, seen):
@@ -71,14 +88,19 @@ def _stale(src, obj):
     return any(os.path.getmtime(d) > t for d in deps)
 
 
-def _compile(src, build_dir, incremental=False):
-    obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+def _compile(job, build_dir, incremental=False):
+    src, name, flags = job
+    obj = os.path.join(build_dir, name + ".o")
     if incremental and not _stale(src, obj):
         return obj
-    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), *flags, "-c", os.path.join(CSRC, src), "-o", obj]
+    started = time.time()
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
+    # the object is as new as the sources the compiler read: an edit made
+    # while it ran leaves the object stale for the next incremental build
+    os.utime(obj, (started, started))
     return obj
 
 
@@ -87,9 +109,13 @@ def build(verbose=True, incremental=False):
     older than the source or a header) and links the library."""
     build_dir = os.path.join(CSRC, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, build_dir, incremental), srcs))
+    todo = jobs()
+    # the slowest objects first, so the long compiles overlap
+    order = sorted(range(len(todo)), key=lambda i: not todo[i][1].startswith(("gemv_tf", "gemm_tile")))
+    objs = [None] * len(todo)
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(todo))) as ex:
+        for i, obj in zip(order, ex.map(lambda i: _compile(todo[i], build_dir, incremental), order)):
+            objs[i] = obj
     tmp = OUT + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -97,7 +123,7 @@ def build(verbose=True, incremental=False):
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
     if verbose:
-        print(f"built {OUT} from {len(srcs)} sources")
+        print(f"built {OUT} from {len(sources())} sources ({len(todo)} objects)")
     return OUT
 
 

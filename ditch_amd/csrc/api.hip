@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <memory>
+#include <mutex>
 
 #include "internal.h"
 #include "model.h"
@@ -18,6 +19,7 @@ void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64
                      const float *b);
 void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight);
 void model_reset_deltas(ditch_hip_model *m);
+void model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint64_t n, uint64_t k);
 void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight,
                    int mode, int64_t lora_rank, uint64_t seed, int ablate);
 ditch_hip_kv_cache *kv_cache_create(ditch_hip_model *m, int64_t B, int64_t T);
@@ -78,6 +80,19 @@ using namespace ditch;
 static constexpr size_t STATIC_SCRATCH_BYTES = (size_t)64 << 20;
 static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
 
+// The order of the calls that share one GPU's scratch: each call's stream
+// waits for the event the previous call (any stream, any context) recorded
+// after its last kernel, and records it again after its own. The events are
+// created at context open, one per device, and kept for the life of the
+// process, like the scratch array.
+struct ScratchOrder {
+    std::mutex mu;
+    hipEvent_t last = nullptr;
+    bool recorded = false;
+};
+static constexpr int MAX_DEVICES = 64;
+static ScratchOrder scratch_order[MAX_DEVICES];
+
 extern "C" {
 
 ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
@@ -112,6 +127,18 @@ ditch_hip *ditch_hip_open(int32_t device, char *err, size_t err_len) {
         h->static_scratch = nullptr;
         h->scratch_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se);
         (void)hipGetLastError();
+    } else if (device >= MAX_DEVICES) {
+        h->static_scratch = nullptr;
+        h->scratch_error = "device index beyond the scratch ordering table";
+    } else {
+        ScratchOrder &o = scratch_order[device];
+        std::lock_guard<std::mutex> lk(o.mu);
+        if (!o.last && hipEventCreateWithFlags(&o.last, hipEventDisableTiming) != hipSuccess) {
+            o.last = nullptr;
+            h->static_scratch = nullptr;
+            h->scratch_error = "hipEventCreate for the scratch ordering failed";
+            (void)hipGetLastError();
+        }
     }
     return h;
 }
@@ -180,9 +207,9 @@ int32_t ditch_hip_matvecTMulti(ditch_hip *h, float *out, const ditch_weight *w, 
         hipStream_t s = h->stream;
         WeightRef t;
         acquire_weight(h, w, s, t);
-        Tmp dy(q * w->rows * 4), dout(q * w->cols * 4), part(matvecT_partials_floats(t->v, q) * 4);
+        Tmp dy(q * w->rows * 4), dout(q * w->cols * 4);
         h2d(dy.p, y, q * w->rows * 4, s);
-        launch_matvecT(dout.as<float>(), t->v, dy.as<float>(), (int64_t)q, s, part.as<float>());
+        launch_matvecT(dout.as<float>(), t->v, dy.as<float>(), (int64_t)q, s);
         d2h(out, dout.p, q * w->cols * 4, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
     });
@@ -388,7 +415,19 @@ int32_t ditch_hip_matmulT_device_noalloc(ditch_hip *h, float *d_out, uint64_t ou
         ep.bias = d_bias;
         ep.accumulate = accumulate;
         DevBuf ws(h->static_scratch, STATIC_SCRATCH_BYTES);  // never allocates: too large a need is refused
-        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, stream ? (hipStream_t)stream : h->stream, nullptr, &ws);
+        hipStream_t st = stream ? (hipStream_t)stream : h->stream;
+        // after the previous call's kernels on this GPU, whatever its stream
+        // (a stream under graph capture takes its order from the graph)
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        DITCH_TRY_HIP(hipStreamIsCapturing(st, &cap));
+        ScratchOrder &o = scratch_order[h->device];
+        std::lock_guard<std::mutex> lk(o.mu);
+        if (cap == hipStreamCaptureStatusNone && o.recorded) DITCH_TRY_HIP(hipStreamWaitEvent(st, o.last, 0));
+        launch_matmul(w->v, d_out, d_x, (int64_t)n, ep, st, nullptr, &ws);
+        if (cap == hipStreamCaptureStatusNone) {
+            DITCH_TRY_HIP(hipEventRecord(o.last, st));
+            o.recorded = true;
+        }
     });
 }
 
@@ -729,9 +768,9 @@ int32_t ditch_hip_edit_delta(ditch_hip *h, float *a, float *b, const ditch_weigh
         hipStream_t s = h->stream;
         WeightRef t;
         acquire_weight(h, w, s, t);
-        Tmp dv(k * w->rows * 4), da(k * w->cols * 4), part(matvecT_partials_floats(t->v, k) * 4);
+        Tmp dv(k * w->rows * 4), da(k * w->cols * 4);
         h2d(dv.p, v, k * w->rows * 4, s);
-        launch_matvecT(da.as<float>(), t->v, dv.as<float>(), (int64_t)k, s, part.as<float>());
+        launch_matvecT(da.as<float>(), t->v, dv.as<float>(), (int64_t)k, s);
         d2h(a, da.p, k * w->cols * 4, s);
         DITCH_TRY_HIP(hipStreamSynchronize(s));
         for (uint64_t i = 0; i < w->rows; i++)
@@ -745,6 +784,14 @@ int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot, in
     return guarded(m->h, [&] {
         DITCH_CHECK(v && k > 0, DITCH_INVALID_ARGUMENT, "edit arguments");
         model_edit(m, layer, slot, expert, v, k, weight);
+    });
+}
+
+int32_t ditch_hip_model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint64_t n, uint64_t k) {
+    if (!m) return DITCH_INVALID_ARGUMENT;
+    return guarded(m->h, [&] {
+        DITCH_CHECK(targets && n > 0 && k > 0, DITCH_INVALID_ARGUMENT, "edit batch arguments");
+        model_edit_batch(m, targets, n, k);
     });
 }
 

@@ -296,9 +296,10 @@ struct StTensor {
     size_t begin = 0, end = 0;  // absolute offsets in the file
     const uint8_t *data() const { return file->base + begin; }
     size_t bytes() const { return end - begin; }
-    int64_t numel() const {
+    int64_t numel() const {  // -1 when a dimension is negative or the product overflows
         int64_t n = 1;
-        for (int64_t d : shape) n *= d;
+        for (int64_t d : shape)
+            if (d < 0 || __builtin_mul_overflow(n, d, &n)) return -1;
         return n;
     }
 };
@@ -332,7 +333,8 @@ static void read_safetensors(const Mapped &f, std::map<std::string, StTensor> &o
         st.begin = base + (size_t)off->arr[0].num;
         st.end = base + (size_t)off->arr[1].num;
         const size_t eb = st_elem_bytes(st.dtype);
-        DITCH_CHECK(eb && st.begin <= st.end && st.end <= f.size && st.bytes() == (size_t)st.numel() * eb,
+        DITCH_CHECK(eb && st.numel() >= 0 && st.begin <= st.end && st.end <= f.size &&
+                        (uint64_t)st.numel() <= UINT64_MAX / eb && st.bytes() == (size_t)st.numel() * eb,
                     DITCH_INVALID_ARGUMENT, "safetensors: entry " + kv.first + " out of range or of unknown dtype");
         out[kv.first] = st;
     }
@@ -462,9 +464,12 @@ static void read_gguf(const Mapped &f, std::map<std::string, GgufMeta> &meta, st
         in.off = r.take<uint64_t>();
         DITCH_CHECK(gguf_block(tt, in.type, in.bs, in.bb), DITCH_UNSUPPORTED,
                     "gguf: tensor type " + std::to_string(tt) + " of " + in.name);
+        DITCH_CHECK(dims[0] < (1ull << 40), DITCH_INVALID_ARGUMENT, "gguf: dimensions of " + in.name);
         in.cols = (int64_t)dims[0];
         in.rows = 1;
-        for (uint32_t d = 1; d < nd; d++) in.rows *= (int64_t)dims[d];
+        for (uint32_t d = 1; d < nd; d++)
+            DITCH_CHECK(dims[d] < (1ull << 40) && !__builtin_mul_overflow(in.rows, (int64_t)dims[d], &in.rows),
+                        DITCH_INVALID_ARGUMENT, "gguf: dimensions of " + in.name);
         infos.push_back(in);
     }
     uint64_t align = 32;
@@ -478,8 +483,12 @@ static void read_gguf(const Mapped &f, std::map<std::string, GgufMeta> &meta, st
         g.type = in.type;
         g.rows = in.rows;
         g.cols = in.cols;
-        g.bytes = (size_t)(in.rows * (in.cols / in.bs) * in.bb);
-        DITCH_CHECK(base + in.off <= f.size && g.bytes <= f.size - base - in.off, DITCH_INVALID_ARGUMENT,
+        int64_t nb = 0;
+        DITCH_CHECK(in.rows >= 0 && in.cols >= 0 && !__builtin_mul_overflow(in.rows, in.cols / in.bs, &nb) &&
+                        !__builtin_mul_overflow(nb, in.bb, &nb),
+                    DITCH_INVALID_ARGUMENT, "gguf: size of tensor " + in.name + " overflows");
+        g.bytes = (size_t)nb;
+        DITCH_CHECK(in.off <= f.size && base <= f.size - in.off && g.bytes <= f.size - base - in.off, DITCH_INVALID_ARGUMENT,
                     "gguf: tensor " + in.name + " past the end of the file");
         g.data = f.base + base + in.off;
         out[in.name] = g;
@@ -522,6 +531,18 @@ static const uint8_t *stage_copy(PinnedStage &ps, const uint8_t *src, size_t n) 
     return d;
 }
 
+// The bytes the upload will read from each piece of w (its shape and
+// quantisation description) must lie inside what was staged for it, or a
+// checkpoint whose tensors disagree with each other would be read past the
+// end of the staging buffer.
+static ditch_weight staged_checked(const ditch_weight &w, const std::string &prefix, size_t data, size_t scale = 0,
+                                   size_t zero = 0, size_t gidx = 0) {
+    const RawSizes z = raw_sizes(&w);
+    DITCH_CHECK(z.data <= data && z.scale <= scale && z.zero <= zero && z.gidx <= gidx, DITCH_INVALID_ARGUMENT,
+                "checkpoint: " + prefix + ": the tensors hold fewer bytes than its shape needs");
+    return w;
+}
+
 // The matrix at `prefix` (...proj): plain, FP8, pack-quantized INT or
 // mxfp4-pack-quantized, its pieces in `ps`.
 static ditch_weight hf_weight(const HfWeights &hw, const std::string &prefix, PinnedStage &ps) {
@@ -540,13 +561,14 @@ static ditch_weight hf_weight(const HfWeights &hw, const std::string &prefix, Pi
             w.data = stage_copy(ps, packed->data(), packed->bytes());
             w.scale = stage_copy(ps, sc.data(), sc.bytes());
             w.scale_dtype = DITCH_E8M0;
-            return w;
+            return staged_checked(w, prefix, packed->bytes(), sc.bytes());
         }
         const StTensor &shape = hw.at(prefix + ".weight_shape");
         DITCH_CHECK(shape.dtype == "I64" && shape.numel() == 2 && sc.shape.size() == 2, DITCH_INVALID_ARGUMENT,
                     "checkpoint: pack-quantized tensor " + prefix);
         int64_t rc[2];
         memcpy(rc, shape.data(), 16);
+        DITCH_CHECK(rc[0] > 0 && rc[1] > 0, DITCH_INVALID_ARGUMENT, "checkpoint: weight_shape of " + prefix);
         const StTensor *zp = hw.find(prefix + ".weight_zero_point"), *gi = hw.find(prefix + ".weight_g_idx");
         ps.reserve(packed->bytes() + sc.bytes() + (zp ? zp->bytes() : 0) + (gi ? gi->bytes() : 0) + 2048);
         w.dtype = DITCH_INT_PACKED;
@@ -566,7 +588,8 @@ static ditch_weight hf_weight(const HfWeights &hw, const std::string &prefix, Pi
                         "checkpoint: g_idx of " + prefix);
             w.g_idx = (const int32_t *)stage_copy(ps, gi->data(), gi->bytes());
         }
-        return w;
+        DITCH_CHECK(w.scale_rows >= w.rows, DITCH_INVALID_ARGUMENT, "checkpoint: scale rows of " + prefix);
+        return staged_checked(w, prefix, packed->bytes(), sc.bytes(), zp ? zp->bytes() : 0, gi ? gi->bytes() : 0);
     }
     const StTensor &wt = hw.at(prefix + ".weight");
     DITCH_CHECK(wt.shape.size() == 2, DITCH_INVALID_ARGUMENT, "checkpoint: " + prefix + " is not a matrix");
@@ -587,13 +610,13 @@ static ditch_weight hf_weight(const HfWeights &hw, const std::string &prefix, Pi
         w.scale_cols = (uint64_t)sc->shape[1];
         w.block_rows = hw.fp8_block_rows ? (uint64_t)hw.fp8_block_rows : (w.rows + w.scale_rows - 1) / w.scale_rows;
         w.block_cols = hw.fp8_block_cols ? (uint64_t)hw.fp8_block_cols : (w.cols + w.scale_cols - 1) / w.scale_cols;
-        return w;
+        return staged_checked(w, prefix, wt.bytes(), sc->bytes());
     }
     w.dtype = st_plain_dtype(wt.dtype);
     DITCH_CHECK(w.dtype >= 0, DITCH_UNSUPPORTED, "checkpoint: dtype " + wt.dtype + " of " + prefix);
     ps.reserve(wt.bytes() + 256);
     w.data = stage_copy(ps, wt.data(), wt.bytes());
-    return w;
+    return staged_checked(w, prefix, wt.bytes());
 }
 
 // A norm or bias vector widened to f32 in pinned memory.
@@ -826,6 +849,71 @@ static ditch_hip_model *load_hf(ditch_hip *h, const std::string &dir, uint64_t e
         const ditch_weight w = st_vec(hw.at(name), ps);
         model_set(m, layer, slot, -1, &w);
     };
+    // Routed experts stored as two stacked tensors (Layout.fused /
+    // .fused_transposed, moe.zig:83-93, detection and slicing at
+    // moe.zig:688-770): `experts.gate_up_proj` [E, 2I, hidden] with
+    // `experts.down_proj` [E, hidden, I], each expert a contiguous row-major
+    // block whose rows 0..I are the gate and I..2I the up projection; or
+    // [E, hidden, 2I] with [E, I, hidden], each block transposed on load
+    // (columns 0..I the gate, I..2I the up). Plain dtypes (the stacked
+    // tensors are sliced element-wise).
+    auto set_fused_experts = [&](int layer, const std::string &mp, const StTensor &gu) {
+        const StTensor *dn = hw.find(mp + "experts.down_proj");
+        if (!dn) dn = hw.find(mp + "experts.down_proj.weight");
+        DITCH_CHECK(dn != nullptr, DITCH_INVALID_ARGUMENT, "checkpoint: " + mp + "experts.down_proj missing");
+        const int64_t E = n_exp, I = (int64_t)c.moe_inter, H = (int64_t)hidden;
+        const int32_t dt = st_plain_dtype(gu.dtype);
+        DITCH_CHECK(dt >= 0 && st_plain_dtype(dn->dtype) == dt, DITCH_UNSUPPORTED,
+                    "checkpoint: stacked experts of " + mp + " in dtype " + gu.dtype + " (F32, F16, BF16)");
+        DITCH_CHECK(gu.shape.size() == 3 && dn->shape.size() == 3 && gu.shape[0] == E && dn->shape[0] == E,
+                    DITCH_INVALID_ARGUMENT, "checkpoint: stacked experts of " + mp + ": expert count");
+        bool transposed;
+        if (gu.shape[1] == 2 * I && gu.shape[2] == H) {
+            transposed = false;
+            DITCH_CHECK(dn->shape[1] == H && dn->shape[2] == I, DITCH_INVALID_ARGUMENT,
+                        "checkpoint: " + mp + "experts.down_proj shape");
+        } else if (gu.shape[1] == H && gu.shape[2] == 2 * I) {
+            transposed = true;
+            DITCH_CHECK(dn->shape[1] == I && dn->shape[2] == H, DITCH_INVALID_ARGUMENT,
+                        "checkpoint: " + mp + "experts.down_proj shape");
+        } else {
+            throw Error{DITCH_INVALID_ARGUMENT, "checkpoint: unexpected stacked expert shape in " + mp};
+        }
+        const size_t es = st_elem_bytes(gu.dtype);
+        // rows x cols of the matrix [rows][cols] whose element (r, c) lies at
+        // src + (r * rs + c * cs) * es
+        auto put = [&](int slot, int e, const uint8_t *src, int64_t rows, int64_t cols, int64_t rs, int64_t cs) {
+            ps.reset();
+            ps.reserve((size_t)(rows * cols) * es + 256);
+            uint8_t *d = ps.take((size_t)(rows * cols) * es);
+            if (cs == 1)
+                for (int64_t r = 0; r < rows; r++) memcpy(d + (size_t)(r * cols) * es, src + (size_t)(r * rs) * es, cols * es);
+            else
+                for (int64_t r = 0; r < rows; r++)
+                    for (int64_t k = 0; k < cols; k++)
+                        memcpy(d + (size_t)(r * cols + k) * es, src + (size_t)(r * rs + k * cs) * es, es);
+            ditch_weight w{};
+            w.dtype = dt;
+            w.rows = (uint64_t)rows;
+            w.cols = (uint64_t)cols;
+            w.data = d;
+            model_set(m, layer, slot, e, &w);
+        };
+        for (int64_t e = 0; e < E; e++) {
+            const uint8_t *g = gu.data() + (size_t)(e * 2 * I * H) * es, *dw = dn->data() + (size_t)(e * H * I) * es;
+            if (!transposed) {
+                put(DITCH_SLOT_EXPERT_GATE, (int)e, g, I, H, H, 1);
+                put(DITCH_SLOT_EXPERT_UP, (int)e, g + (size_t)(I * H) * es, I, H, H, 1);
+                put(DITCH_SLOT_EXPERT_DOWN, (int)e, dw, H, I, I, 1);
+            } else {
+                // block [H][2I]: gate (r, k) = block[k][r], up (r, k) = block[k][I + r]
+                put(DITCH_SLOT_EXPERT_GATE, (int)e, g, I, H, 1, 2 * I);
+                put(DITCH_SLOT_EXPERT_UP, (int)e, g + (size_t)I * es, I, H, 1, 2 * I);
+                // block [I][H]: down (r, k) = block[k][r]
+                put(DITCH_SLOT_EXPERT_DOWN, (int)e, dw, H, I, 1, H);
+            }
+        }
+    };
     set_plain(-1, DITCH_SLOT_EMBED, "model.embed_tokens.weight");
     set_vec(-1, DITCH_SLOT_FINAL_NORM, "model.norm.weight");
     if (hw.find("lm_head.weight")) set_plain(-1, DITCH_SLOT_LM_HEAD, "lm_head.weight");
@@ -867,12 +955,16 @@ static ditch_hip_model *load_hf(ditch_hip *h, const std::string &dir, uint64_t e
             set_plain(li, DITCH_SLOT_ROUTER, mp + "gate.weight");
             if (hw.find(mp + "gate.e_score_correction_bias"))
                 set_vec(li, DITCH_SLOT_ROUTER_CORRECTION, mp + "gate.e_score_correction_bias");
-            for (int e = 0; e < (int)n_exp; e++) {
-                const std::string ep = mp + "experts." + std::to_string(e) + ".";
-                set_mat(li, DITCH_SLOT_EXPERT_GATE, e, ep + "gate_proj");
-                set_mat(li, DITCH_SLOT_EXPERT_UP, e, ep + "up_proj");
-                set_mat(li, DITCH_SLOT_EXPERT_DOWN, e, ep + "down_proj");
-            }
+            const StTensor *fgu = hw.find(mp + "experts.gate_up_proj");
+            if (!fgu) fgu = hw.find(mp + "experts.gate_up_proj.weight");
+            if (fgu) set_fused_experts(li, mp, *fgu);
+            else
+                for (int e = 0; e < (int)n_exp; e++) {
+                    const std::string ep = mp + "experts." + std::to_string(e) + ".";
+                    set_mat(li, DITCH_SLOT_EXPERT_GATE, e, ep + "gate_proj");
+                    set_mat(li, DITCH_SLOT_EXPERT_UP, e, ep + "up_proj");
+                    set_mat(li, DITCH_SLOT_EXPERT_DOWN, e, ep + "down_proj");
+                }
             if (hw.find(mp + "shared_experts.gate_proj.weight") || hw.find(mp + "shared_experts.gate_proj.weight_packed")) {
                 set_mat(li, DITCH_SLOT_SHARED_GATE, -1, mp + "shared_experts.gate_proj");
                 set_mat(li, DITCH_SLOT_SHARED_UP, -1, mp + "shared_experts.up_proj");

@@ -297,7 +297,7 @@ int64_t edit_rank(int64_t rows, int64_t cols, int64_t k, int mode, int64_t lora_
 }
 
 struct EditWork {
-    DevBuf v, norms, vn, a, bp, wa, gram, c, d, omega, qy, qx, cy, part, dots, bbt, evecs, xs, xa, wu;
+    DevBuf v, norms, vn, a, bp, wa, gram, c, d, omega, qy, qx, cy, dots, bbt, evecs, xs, xa, wu;
 };
 
 // b[i][0..r) = bp[i][0..r), b[i][r + j] = -lambda wu[j][i]  (abliterate.zig:252-257)
@@ -325,12 +325,9 @@ static void edit_matmul(const TileView &w, float *out, const float *x, int64_t n
     launch_matmul(w, out, x, n, ep, s, nullptr, ws);
 }
 
-// W^T y for q vectors, 16 at a time
-static void edit_matvecT(const TileView &w, float *out, const float *y, int64_t q, hipStream_t s, DevBuf *part) {
-    for (int64_t j0 = 0; j0 < q; j0 += 16) {
-        const int64_t qq = q - j0 < 16 ? q - j0 : 16;
-        launch_matvecT(out + j0 * w.cols, w, y + j0 * w.rows, qq, s, part->get<float>(matvecT_partials_floats(w, qq)));
-    }
+// W^T y for q vectors
+static void edit_matvecT(const TileView &w, float *out, const float *y, int64_t q, hipStream_t s) {
+    launch_matvecT(out, w, y, q, s);
 }
 
 static void edit_orth(float *vecs, int64_t q, int64_t n, hipStream_t s) {
@@ -364,7 +361,7 @@ void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weig
         float *norms = nullptr;
         float *a = A;  // none / pre: the output-side A is the first k rows of A
         if (mode == 0) {
-            edit_matvecT(w, a, v, k, s, &W.part);
+            edit_matvecT(w, a, v, k, s);
         } else {
             norms = W.norms.get<float>(rows);
             launch_row_norms(norms, w, s);
@@ -372,7 +369,7 @@ void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weig
             hipLaunchKernelGGL(edit_vn_kernel, dim3(ed_grid(k * rows)), dim3(256), 0, s, vn, v, norms, k, rows);
             DITCH_TRY_HIP(hipGetLastError());
             if (mode == 2) a = W.a.get<float>(k * cols);
-            edit_matvecT(w, a, vn, k, s, &W.part);
+            edit_matvecT(w, a, vn, k, s);
         }
         if (mode != 2) {
             hipLaunchKernelGGL(edit_b_kernel, dim3(ed_grid(k * rows)), dim3(256), 0, s, Bp, v, mode == 1 ? norms : nullptr,
@@ -409,7 +406,7 @@ void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weig
             auto applyT = [&](float *out, const float *y) {  // out [q][cols] = (D^T Y)^T
                 hipLaunchKernelGGL(edit_scale_rows_kernel, dim3(ed_grid(q * rows)), dim3(256), 0, s, cy, y, c, q, rows);
                 DITCH_TRY_HIP(hipGetLastError());
-                edit_matvecT(w, out, cy, q, s, &W.part);
+                edit_matvecT(w, out, cy, q, s);
                 edit_dots(dots, d, k, y, q, rows, s);
                 hipLaunchKernelGGL(edit_applyT_kernel, dim3(ed_grid(q * cols)), dim3(256), 0, s, out, a, dots, q, k,
                                    cols);
@@ -436,7 +433,7 @@ void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weig
             // U = orth(W^T V) [k][cols]; W' U through the primary delta; the
             // rank grows by k (abliterate.zig:234-261)
             float *u = A + r_out * cols;
-            edit_matvecT(w, u, v, k, s, &W.part);
+            edit_matvecT(w, u, v, k, s);
             edit_orth(u, k, cols, s);
             float *wu = W.wu.get<float>(k * rows);
             float *xa = W.xa.get<float>(k * r_out);

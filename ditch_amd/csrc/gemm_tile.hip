@@ -1373,9 +1373,9 @@ void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const
 // (GroupedDevPlan): the grid covers plan.max_desc tile rows and the rows past
 // *plan.count exit at once; no host copy of the counts.
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
-                                 const TileView &up0, uint32_t act, void *xs_out, int64_t ldk_out, const float *x,
-                                 int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan, DevBuf *ws,
-                                 hipStream_t s) {
+                                 const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
+                                 const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
+                                 DevBuf *ws, hipStream_t s) {
     DITCH_CHECK(tile_glu_takes(gate0, up0, 128), DITCH_INVALID_ARGUMENT, "grouped GLU: gate and up must share format and shape");
     DITCH_CHECK(!xs_out || ldk_out * 32 >= gate0.rows, DITCH_INVALID_ARGUMENT, "grouped GLU: output fragments too short");
     const int64_t kt = split_k_tiles(gate0);
@@ -1393,6 +1393,7 @@ void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, c
     p.ldk = kt;
     p.xs_out = (u32x4 *)xs_out;
     p.ldk_out = ldk_out;
+    p.out = out;
     p.ldo = gate0.rows;
     p.gsegs = d_gate;
     p.gsegs2 = d_up;
@@ -1403,9 +1404,12 @@ void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, c
 }
 
 void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,
-                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s) {
+                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s, const float *delta_xa,
+                                  int delta_stride) {
     TileGemmParams p{};
     p.w = w0;
+    p.delta_xa = delta_xa;
+    p.delta_stride = delta_stride;
     p.xs = (const u32x4 *)xs;
     p.kt_total = split_k_tiles(w0);
     p.ldk = p.kt_total;

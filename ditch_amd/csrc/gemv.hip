@@ -384,11 +384,28 @@ static void gemv_launch(const GemmParams &p, int64_t rows, unsigned nseg, bool l
     } else hipLaunchKernelGGL((gemv_kernel<TF, NT, XT, D, W, false>), grid, dim3(64 * W), 0, s, p);
 }
 
-template <int TF>
-static void gemv_launch_xt(const GemmParams &p, int64_t rows, unsigned nseg, bool lx, int xt, hipStream_t s) {
-    if (Fmt<TF>::fp32 || xt == 2) gemv_launch<TF, 2>(p, rows, nseg, lx, s);
-    else gemv_launch<TF, 3>(p, rows, nseg, lx, s);
-}
+// The build compiles this file once per tile format and activation term
+// count with GEMV_TF and GEMV_XT set (each object holds those kernels: the
+// fully unrolled register rings make every format a long compile, and the
+// objects build in parallel) and once without them (the split kernel and
+// the dispatch). f16 and f32 weights take two f32 terms only.
+#define GEMV_ENTRY_NAME(tf, xt) gemv_launch_tf##tf##_x##xt
+#define GEMV_ENTRY(tf, xt) GEMV_ENTRY_NAME(tf, xt)
+#define GEMV_ENTRY_ARGS const GemmParams &p, int64_t rows, unsigned nseg, bool lx, hipStream_t s
+
+#ifdef GEMV_TF
+void GEMV_ENTRY(GEMV_TF, GEMV_XT)(GEMV_ENTRY_ARGS) { gemv_launch<GEMV_TF, GEMV_XT>(p, rows, nseg, lx, s); }
+#else
+#define GEMV_DECLARE(tf) void GEMV_ENTRY(tf, 2)(GEMV_ENTRY_ARGS); void GEMV_ENTRY(tf, 3)(GEMV_ENTRY_ARGS);
+GEMV_DECLARE(0)
+GEMV_DECLARE(3)
+GEMV_DECLARE(4)
+GEMV_DECLARE(5)
+GEMV_DECLARE(6)
+void GEMV_ENTRY(1, 2)(GEMV_ENTRY_ARGS);
+void GEMV_ENTRY(2, 2)(GEMV_ENTRY_ARGS);
+static_assert(TF_BF16 == 0 && TF_F16 == 1 && TF_F32 == 2 && TF_Q8 == 3 && TF_FP8 == 4 && TF_MX4 == 5 && TF_INT4 == 6,
+              "one GEMV object per tile format 0..6");
 
 void launch_gemv(GemmParams &p, int tf, int64_t rows, int64_t cols, bool exact, unsigned nseg, DevBuf *ws,
                  hipStream_t s) {
@@ -418,17 +435,19 @@ void launch_gemv(GemmParams &p, int tf, int64_t rows, int64_t cols, bool exact, 
         p.xn = q.xn;
         p.xf_seg = q.xf_seg;
     }
+    const bool x3 = xt == 3;
     switch (tf) {
-    case TF_BF16: gemv_launch_xt<TF_BF16>(p, rows, nseg, lx, xt, s); break;
-    case TF_F16: gemv_launch_xt<TF_F16>(p, rows, nseg, lx, xt, s); break;
-    case TF_F32: gemv_launch_xt<TF_F32>(p, rows, nseg, lx, xt, s); break;
-    case TF_Q8: gemv_launch_xt<TF_Q8>(p, rows, nseg, lx, xt, s); break;
-    case TF_FP8: gemv_launch_xt<TF_FP8>(p, rows, nseg, lx, xt, s); break;
-    case TF_MX4: gemv_launch_xt<TF_MX4>(p, rows, nseg, lx, xt, s); break;
-    case TF_INT4: gemv_launch_xt<TF_INT4>(p, rows, nseg, lx, xt, s); break;
+    case TF_BF16: x3 ? GEMV_ENTRY(0, 3)(p, rows, nseg, lx, s) : GEMV_ENTRY(0, 2)(p, rows, nseg, lx, s); break;
+    case TF_F16: GEMV_ENTRY(1, 2)(p, rows, nseg, lx, s); break;
+    case TF_F32: GEMV_ENTRY(2, 2)(p, rows, nseg, lx, s); break;
+    case TF_Q8: x3 ? GEMV_ENTRY(3, 3)(p, rows, nseg, lx, s) : GEMV_ENTRY(3, 2)(p, rows, nseg, lx, s); break;
+    case TF_FP8: x3 ? GEMV_ENTRY(4, 3)(p, rows, nseg, lx, s) : GEMV_ENTRY(4, 2)(p, rows, nseg, lx, s); break;
+    case TF_MX4: x3 ? GEMV_ENTRY(5, 3)(p, rows, nseg, lx, s) : GEMV_ENTRY(5, 2)(p, rows, nseg, lx, s); break;
+    case TF_INT4: x3 ? GEMV_ENTRY(6, 3)(p, rows, nseg, lx, s) : GEMV_ENTRY(6, 2)(p, rows, nseg, lx, s); break;
     default: throw Error{DITCH_UNSUPPORTED, "tile format"};
     }
     DITCH_TRY_HIP(hipGetLastError());
 }
+#endif
 
 }  // namespace ditch

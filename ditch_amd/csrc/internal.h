@@ -193,6 +193,12 @@ namespace ditch {
 
 // tiles.hip
 ditch_hip_tensor *upload_weight(ditch_hip *h, const ditch_weight *w, hipStream_t s);
+// The bytes an upload of w reads from each of its host pieces (refused when
+// the description is inconsistent or its sizes overflow).
+struct RawSizes {
+    size_t data, scale, zero, gidx;
+};
+RawSizes raw_sizes(const ditch_weight *w);
 void free_tensor(ditch_hip_tensor *t);
 // A per-call weight: the residency cache's copy (owned = false) or a fresh
 // upload the caller frees (owned = true).
@@ -308,12 +314,16 @@ struct GroupedDevPlan {
     int32_t *prow, *desc, *count;
     int64_t max_blocks, max_desc;
 };
+// out (may be NULL): act(gate) * up as f32 rows in the grouped row order
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
-                                 const TileView &up0, uint32_t act, void *xs_out, int64_t ldk_out, const float *x,
-                                 int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan, DevBuf *ws,
-                                 hipStream_t s);
+                                 const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
+                                 const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
+                                 DevBuf *ws, hipStream_t s);
+// delta_xa [rows][delta_stride]: the x . A^T of the segments' deltas (their
+// B and rank in the segment table), or NULL
 void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,
-                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s);
+                                  const void *xs, const GroupedDevPlan &plan, hipStream_t s,
+                                  const float *delta_xa = nullptr, int delta_stride = 0);
 // Routed gate/up in one tiled product: act(x gate_z^T) * (x up_z^T) per
 // segment z, as f32 rows of out (may be NULL) and as the down product's
 // activation fragments xs_out (ldk_out k tiles, grouped row order)
@@ -395,8 +405,8 @@ void launch_attention_scores(float *scores, int64_t n_keys, const float *q, int6
 void launch_attention_values(float *out, int64_t vd, const float *scores, int64_t n_keys, const float *v,
                              int64_t stride, hipStream_t s);
 void launch_row_norms(float *out, const TileView &w, hipStream_t s);
-void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials);
-size_t matvecT_partials_floats(const TileView &w, int64_t q);
+// out[q][cols] = y[q][rows] . W over the resident tiles (edit_batch.hip)
+void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s);
 void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank,
                      hipStream_t s);
 

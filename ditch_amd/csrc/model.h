@@ -1,6 +1,7 @@
 // model.h — host-side state of a resident model (not part of the ABI).
 #pragma once
 #include <cstdint>
+#include <memory>
 #include <unordered_map>
 #include <vector>
 
@@ -26,11 +27,15 @@ struct Mat {
     ditch_hip_tensor *t = nullptr;
     float *da = nullptr, *db = nullptr;  // delta A [rank][cols], B [rows][rank]
     bool joint = false;                   // db lies in da's allocation (one allocation for both)
+    std::shared_ptr<void> arena;          // else: da and db lie in a batch edit's allocation, shared
     int rank = 0;
     HostMat hm;
     void clear_delta() {
-        dev_free(da);
-        if (!joint) dev_free(db);
+        if (arena) arena.reset();  // the allocation goes with its last matrix
+        else {
+            dev_free(da);
+            if (!joint) dev_free(db);
+        }
         da = db = nullptr;
         joint = false;
         rank = 0;
@@ -150,7 +155,7 @@ struct ditch_hip_model {
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)
     ditch::DevBuf attn_dense;      // the attention's dense-rows flag
-    ditch::DevBuf edit_v, edit_part;  // the none-mode edit's directions and matvecT partial sums
+    ditch::DevBuf edit_v, edit_part;  // the none-mode edits' directions and the edit batch's tables
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
     uint64_t expert_pinned = 0;    // host bytes of routed experts held pinned
     bool expert_pinned_exhausted = false;

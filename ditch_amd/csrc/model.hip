@@ -399,8 +399,11 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     }
     // lane j < k finishes selection j: its weight (renormalised by the sum,
     // then scaled), and its place in ascending expert index (the combine's
-    // order: the experts are distinct, so the place is the count of smaller
-    // ones)
+    // order): the count of smaller experts plus the earlier selections of
+    // the same expert. Experts repeat when fewer than k choices are above
+    // -inf (NaN router scores, or group-limited routing that keeps fewer
+    // than k experts): the argmax then returns expert 0 again, as topk
+    // does (moe.zig:971-985), and the repeats keep their selection order.
     int32_t my_sel = 0;
     float my_w = 0.f;
 #pragma unroll
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
         int rank = 0;
 #pragma unroll
         for (int i = 0; i < 16; i++)
-            if (i < a.k && selj[i] < my_sel) rank++;
+            if (i < a.k && (selj[i] < my_sel || (selj[i] == my_sel && i < lane))) rank++;
         a.ord[t * a.k + rank] = lane;
     }
 }
@@ -671,6 +674,31 @@ __global__ void grouped_delta_xa_kernel(float *xa, const float *x, const int32_t
     if (lane == 0) xa[p * max_rank + j] = acc;
 }
 
+// The same for a routed layer planned on the device (every expert a
+// segment, off / cnt written by moe_plan_kernel): one wave per (pair p,
+// direction j); p's expert is the last whose pair offset is <= p (offsets
+// are non-decreasing in expert order and cover every pair); a[e] is expert
+// e's delta A, or NULL for an expert without a delta (its rows are unused).
+__global__ void plan_delta_xa_kernel(float *xa, const float *x, const GroupSeg *segs, const float *const *a,
+                                     int64_t E, int64_t cols, int max_rank, int64_t P) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= P * max_rank) return;
+    const int64_t p = t / max_rank, j = t % max_rank;
+    int64_t lo = 0, hi = E - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) / 2;
+        if (segs[mid].off <= p) lo = mid;
+        else hi = mid - 1;
+    }
+    const float *ae = a[lo];
+    float acc = 0.f;
+    if (ae && j < segs[lo].delta_rank)
+        for (int64_t c = lane; c < cols; c += 64) acc = __builtin_fmaf(ae[j * cols + c], x[p * cols + c], acc);
+    acc = wave_sum64(acc);
+    if (lane == 0) xa[p * max_rank + j] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 
@@ -882,6 +910,8 @@ static void check_delta_slot(int slot) {
                 DITCH_UNSUPPORTED, "a delta on the embedding or a routed expert's gate/up projection is not applied "
                                    "by the forward");
 }
+void check_edit_slot(int slot) { check_delta_slot(slot); }
+Mat *mat_slot_of(ditch_hip_model *m, int layer, int slot, int expert) { return mat_slot(m, layer, slot, expert); }
 
 void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64_t rank, const float *a,
                      const float *b) {
@@ -925,7 +955,7 @@ void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float
     mt->da = dab;
     mt->db = dab + k * w.cols;
     mt->joint = true;
-    launch_matvecT(mt->da, w, d_v, (int64_t)k, s, m->edit_part.get<float>(matvecT_partials_floats(w, k)));
+    launch_matvecT(mt->da, w, d_v, (int64_t)k, s);
     std::vector<float> b(w.rows * k);
     for (int64_t i = 0; i < w.rows; i++)
         for (uint64_t j = 0; j < k; j++) b[i * k + j] = -weight * v[j * w.rows + i];
@@ -1035,14 +1065,15 @@ static bool mx_only(const Mat &mt, int64_t n) { return mt.ok() && mt.rank == 0 &
 
 // Whether a routed layer's grouped products can be planned on the device:
 // every expert resident (no cache), gate/up/down of one tiled format and
-// shape (the fused GLU then the down product), no down delta, and enough
-// pairs per expert on average for the 16-token blocks.
+// shape (the fused GLU then the down product, whose epilogue adds each
+// expert's down delta), and enough pairs per expert on average for the
+// 16-token blocks.
 static bool moe_device_plan(ditch_hip_model *m, const Layer &L, int64_t n) {
     const ditch_model_config &c = m->c;
     const int64_t E = (int64_t)c.n_experts, k = (int64_t)c.top_k;
     if (E <= 0 || E > ROUTE_MAXE || n * k < 16 * E) return false;
     for (int64_t e = 0; e < E; e++) {
-        if (!L.eg[e].ok() || !L.eu[e].ok() || !L.ed[e].ok() || L.eg[e].streamed() || L.ed[e].rank != 0) return false;
+        if (!L.eg[e].ok() || !L.eu[e].ok() || !L.ed[e].ok() || L.eg[e].streamed()) return false;
         const TileView &g = L.eg[e].t->v, &u = L.eu[e].t->v, &d = L.ed[e].t->v, &g0 = L.eg[0].t->v,
                        &d0 = L.ed[0].t->v;
         if (!tile_gemm_takes(g, 128) || !tile_gemm_takes(d, 128) || !tile_glu_takes(g, u, 128) || g.tf != g0.tf ||
@@ -1076,18 +1107,20 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     int32_t *pair_of = m->r_pair_of.get<int32_t>(n * k);
     float *eo = nullptr;
     if (moe_device_plan(m, L, n)) {
-        // every expert resident and on the tiled product, no down delta:
-        // the grouped products are planned on the device
+        // every expert resident and on the tiled product: the grouped
+        // products are planned on the device
         m->moe_device_planned++;
         const int64_t P = n * k, max_blocks = (P + 15) / 16 + E, max_desc = (max_blocks + 3) / 4 + E;
         int32_t *offsets = m->r_offsets.get<int32_t>(E);
         int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
         eo = m->e_out.get<float>(P * hidden);
         std::vector<GroupSeg> tab((size_t)(3 * E));
+        int max_rank = 0;
         for (int64_t e = 0; e < E; e++) {
             tab[e] = GroupSeg{L.eg[e].t->v, 0, 0, nullptr, 0};
             tab[E + e] = GroupSeg{L.eu[e].t->v, 0, 0, nullptr, 0};
-            tab[2 * E + e] = GroupSeg{L.ed[e].t->v, 0, 0, nullptr, 0};
+            tab[2 * E + e] = GroupSeg{L.ed[e].t->v, 0, 0, L.ed[e].db, L.ed[e].rank};
+            max_rank = std::max(max_rank, L.ed[e].rank);
         }
         GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * E);
         DITCH_TRY_HIP(hipMemcpyAsync(dsegs, tab.data(), tab.size() * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
@@ -1103,9 +1136,22 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         const TileView &vd = L.ed[0].t->v;
         const int64_t ldk_d = split_k_tiles(vd);
         void *fr = m->acts.get<uint8_t>(split_bytes_ldk(max_blocks * 16, ldk_d, 2));
-        launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, fr, ldk_d, h, hidden, pair_token,
-                                    plan, &m->xsplit, s);
-        launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s);
+        // with down deltas the GLU writes act(g) * u as f32 rows too, for
+        // the deltas' x . A^T
+        float *act = max_rank > 0 ? m->e_gate.get<float>(P * inter) : nullptr, *dxa = nullptr;
+        launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, act, fr, ldk_d, h, hidden,
+                                    pair_token, plan, &m->xsplit, s);
+        if (max_rank > 0) {
+            std::vector<const float *> das((size_t)E);
+            for (int64_t e = 0; e < E; e++) das[e] = L.ed[e].rank ? L.ed[e].da : nullptr;
+            const float **dda = m->segd.get<const float *>(E);
+            DITCH_TRY_HIP(hipMemcpyAsync(dda, das.data(), E * sizeof(float *), hipMemcpyHostToDevice, s));
+            dxa = m->e_xa.get<float>(P * max_rank);
+            hipLaunchKernelGGL(plan_delta_xa_kernel, dim3((unsigned)((P * max_rank + 3) / 4)), dim3(256), 0, s, dxa,
+                               act, dsegs + 2 * E, dda, E, inter, max_rank, P);
+            DITCH_TRY_HIP(hipGetLastError());
+        }
+        launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s, dxa, max_rank);
     } else {
     m->moe_host_planned++;
     std::vector<int32_t> hc(E), ho(E);

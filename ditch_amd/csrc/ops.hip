@@ -735,56 +735,6 @@ __global__ void row_norms_kernel(float *out, TileView w) {
     if (threadIdx.x == 0) out[r] = __fsqrt_rn(s);
 }
 
-// W^T y, first pass: block (column chunk, row chunk) -> partial sums
-// [row_chunk][q][cols]; the second pass adds the chunks in order. A row
-// chunk is 32 rows (taller, in steps of 32, where that would make more than
-// MVT_CHUNKS chunks: the partial sums stay near the weight's own size),
-// decoded 8 at a time with every load of the 8 issued before the first
-// multiply-add (a chunk of hundreds of rows walked one decode at a time
-// waits for each load in turn, and gives a 2048 x 768 matrix 24
-// workgroups).
-constexpr int MVT_ROWS = 32;
-constexpr int MVT_CHUNKS = 256;
-constexpr int MVT_MAXQ = 16;
-
-static int64_t mvt_chunk_rows(const TileView &w) {
-    const int64_t steps = (w.rows + MVT_ROWS * MVT_CHUNKS - 1) / (MVT_ROWS * MVT_CHUNKS);
-    return MVT_ROWS * (steps > 1 ? steps : 1);
-}
-
-__global__ void matvecT_partial_kernel(float *partials, TileView w, const float *y, int64_t q, int64_t chunk_rows) {
-    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t rc = blockIdx.y;
-    int64_t r0 = rc * chunk_rows, r1 = r0 + chunk_rows < w.rows ? r0 + chunk_rows : w.rows;
-    if (c >= w.cols) return;
-    float acc[MVT_MAXQ];
-#pragma unroll
-    for (int j = 0; j < MVT_MAXQ; j++) acc[j] = 0.f;
-    for (int64_t rb = r0; rb < r1; rb += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint16_t b;
-            v[i] = rb + i < r1 ? tiled_element_f32(w, rb + i, c, &b) : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (rb + i < r1)
-#pragma unroll
-                for (int j = 0; j < MVT_MAXQ; j++)
-                    if (j < q) acc[j] = __builtin_fmaf(y[j * w.rows + rb + i], v[i], acc[j]);
-    }
-    for (int j = 0; j < q; j++) partials[(rc * q + j) * w.cols + c] = acc[j];
-}
-
-__global__ void matvecT_reduce_kernel(float *out, const float *partials, int64_t chunks, int64_t qc) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= qc) return;
-    float s = 0.f;
-    for (int64_t k = 0; k < chunks; k++) s += partials[k * qc + i];
-    out[i] = s;
-}
-
 // xa[i][j] = dot(a_j, x_i) for the low-rank delta (tensor.zig:1036-1042)
 __global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank) {
     int lane = threadIdx.x & 63;
@@ -944,20 +894,6 @@ void launch_attention_values(float *out, int64_t vd, const float *scores, int64_
 void launch_row_norms(float *out, const TileView &w, hipStream_t s) {
     if (w.rows <= 0) return;
     hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)w.rows), dim3(256), 0, s, out, w);
-    DITCH_TRY_HIP(hipGetLastError());
-}
-size_t matvecT_partials_floats(const TileView &w, int64_t q) {
-    const int64_t cr = mvt_chunk_rows(w), chunks = (w.rows + cr - 1) / cr;
-    return (size_t)chunks * q * w.cols;
-}
-void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hipStream_t s, float *partials) {
-    DITCH_CHECK(q >= 1 && q <= MVT_MAXQ, DITCH_UNSUPPORTED, "matvecTMulti: q must be 1..16");
-    const int64_t cr = mvt_chunk_rows(w), chunks = (w.rows + cr - 1) / cr;
-    dim3 grid((unsigned)((w.cols + 255) / 256), (unsigned)chunks);
-    hipLaunchKernelGGL(matvecT_partial_kernel, grid, dim3(256), 0, s, partials, w, y, q, cr);
-    DITCH_TRY_HIP(hipGetLastError());
-    hipLaunchKernelGGL(matvecT_reduce_kernel, dim3(grid_1d(q * w.cols)), dim3(256), 0, s, out, partials, chunks,
-                       q * w.cols);
     DITCH_TRY_HIP(hipGetLastError());
 }
 void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank, hipStream_t s) {

@@ -435,30 +435,39 @@ static int32_t scale_type_code(int32_t st) {
 }
 
 // Validates `w` and fills the raw view plus the byte sizes of its pieces.
-struct RawSizes {
-    size_t data, scale, zero, gidx;
-};
+// a * b for sizes taken from a caller's description: refused when either is
+// negative or the product does not fit
+static int64_t mul_sz(int64_t a, int64_t b) {
+    int64_t r;
+    DITCH_CHECK(a >= 0 && b >= 0 && !__builtin_mul_overflow(a, b, &r), DITCH_INVALID_ARGUMENT,
+                "weight size overflows");
+    return r;
+}
 
-static RawSizes raw_sizes(const ditch_weight *w) {
+RawSizes raw_sizes(const ditch_weight *w) {
     RawSizes z{0, 0, 0, 0};
+    DITCH_CHECK(w->rows < (1ull << 40) && w->cols < (1ull << 40), DITCH_INVALID_ARGUMENT, "weight shape too large");
     int64_t rows = (int64_t)w->rows, cols = (int64_t)w->cols;
     DITCH_CHECK(w->data != nullptr, DITCH_INVALID_ARGUMENT, "weight data is NULL");
+    const int64_t rc = mul_sz(rows, cols);
     switch (w->dtype) {
-    case DITCH_F32: z.data = rows * cols * 4; break;
-    case DITCH_F16: case DITCH_BF16: z.data = rows * cols * 2; break;
+    case DITCH_F32: z.data = mul_sz(rc, 4); break;
+    case DITCH_F16: case DITCH_BF16: z.data = mul_sz(rc, 2); break;
     case DITCH_Q8_0: case DITCH_Q4_0: case DITCH_Q4_1: case DITCH_Q5_0: case DITCH_Q5_1:
     case DITCH_Q4_K: case DITCH_Q6_K: case DITCH_Q8_K: {
         int bs = gguf_block_size(w->dtype);
         DITCH_CHECK(cols % bs == 0, DITCH_INVALID_ARGUMENT, "GGUF row length is not a whole number of blocks");
-        z.data = rows * (cols / bs) * gguf_block_bytes(w->dtype);
+        z.data = mul_sz(mul_sz(rows, cols / bs), gguf_block_bytes(w->dtype));
         break;
     }
     case DITCH_FP8:
         DITCH_CHECK(w->scale && w->block_rows > 0 && w->block_cols > 0 && w->scale_cols > 0 && w->scale_rows > 0,
                     DITCH_INVALID_ARGUMENT, "FP8 weight needs a scale grid and block sizes");
         DITCH_CHECK(scale_elem_bytes(w->scale_dtype) > 0, DITCH_INVALID_ARGUMENT, "FP8 scale dtype");
-        z.data = rows * cols;
-        z.scale = w->scale_rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
+        DITCH_CHECK(w->scale_rows < (1ull << 40) && w->scale_cols < (1ull << 40), DITCH_INVALID_ARGUMENT,
+                    "FP8 scale grid too large");
+        z.data = rc;
+        z.scale = mul_sz(mul_sz((int64_t)w->scale_rows, (int64_t)w->scale_cols), scale_elem_bytes(w->scale_dtype));
         {
             // the grid must cover every row (dequant.zig:471-475) and column block
             int64_t last = rows - 1, sr;
@@ -473,25 +482,26 @@ static RawSizes raw_sizes(const ditch_weight *w) {
         break;
     case DITCH_MXFP4:
         DITCH_CHECK(cols % 32 == 0 && w->scale, DITCH_INVALID_ARGUMENT, "MXFP4 needs cols % 32 == 0 and scales");
-        z.data = rows * cols / 2;
-        z.scale = rows * cols / 32;
+        z.data = rc / 2;
+        z.scale = rc / 32;
         break;
     case DITCH_MXFP4_T:
         DITCH_CHECK(rows % 32 == 0 && w->scale, DITCH_INVALID_ARGUMENT, "transposed MXFP4 needs rows % 32 == 0 and scales");
-        z.data = cols * rows / 2;
-        z.scale = cols * rows / 32;
+        z.data = rc / 2;
+        z.scale = rc / 32;
         break;
     case DITCH_INT_PACKED: {
         DITCH_CHECK(w->bits >= 1 && w->bits <= 8 && w->scale && w->scale_cols > 0, DITCH_INVALID_ARGUMENT,
                     "pack-quantized weight needs 1..8 bits and scales");
         DITCH_CHECK(w->g_idx || w->group > 0, DITCH_INVALID_ARGUMENT, "pack-quantized weight needs a group size");
         DITCH_CHECK(scale_elem_bytes(w->scale_dtype) > 1, DITCH_INVALID_ARGUMENT, "pack-quantized scale dtype");
+        DITCH_CHECK(w->scale_cols < (1ull << 40), DITCH_INVALID_ARGUMENT, "pack-quantized scale grid too large");
         int64_t wpr = (cols * w->bits + 31) / 32;
-        z.data = rows * wpr * 4;
-        z.scale = rows * w->scale_cols * scale_elem_bytes(w->scale_dtype);
-        if (w->zero) z.zero = ((rows * w->bits + 31) / 32) * w->scale_cols * 4;
+        z.data = mul_sz(mul_sz(rows, wpr), 4);
+        z.scale = mul_sz(mul_sz(rows, (int64_t)w->scale_cols), scale_elem_bytes(w->scale_dtype));
+        if (w->zero) z.zero = mul_sz(mul_sz((rows * w->bits + 31) / 32, (int64_t)w->scale_cols), 4);
         if (w->g_idx) {
-            z.gidx = cols * 4;
+            z.gidx = mul_sz(cols, 4);
             for (int64_t c = 0; c < cols; c++)
                 DITCH_CHECK(w->g_idx[c] >= 0 && (uint64_t)w->g_idx[c] < w->scale_cols, DITCH_INVALID_ARGUMENT,
                             "g_idx names a group beyond the scales");

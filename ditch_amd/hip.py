@@ -347,6 +347,18 @@ class Model:
         v = _f32(v)
         self.dev.check(self.dev.lib.ditch_hip_model_edit(self.h, layer, slot, expert, _p(v), v.shape[0], weight))
 
+    def edit_batch(self, targets, k):
+        """targets: [(layer, slot, expert, v [k][rows] f32 array, weight)];
+        one call edits them all (ditch_hip_model_edit_batch)."""
+        keep = []
+        arr = (abi.EditTarget * len(targets))()
+        for i, (layer, slot, expert, v, weight) in enumerate(targets):
+            v = _f32(v)
+            assert v.shape[0] == k
+            keep.append(v)
+            arr[i] = abi.EditTarget(layer, slot, expert, weight, v.ctypes.data)
+        self.dev.check(self.dev.lib.ditch_hip_model_edit_batch(self.h, ctypes.byref(arr), len(targets), k))
+
     def edit_ex(self, layer, slot, expert, v, weight, mode="full", lora_rank=3, seed=0, ablate=False):
         v = _f32(v)
         o = abi.EditOptions(abi.ROWNORM[mode], lora_rank, seed, int(ablate))

@@ -32,6 +32,8 @@ def hip():
         "hipMemset": [P, ctypes.c_int, S],
         "hipDeviceSynchronize": [],
         "hipStreamSynchronize": [P],
+        "hipStreamCreateWithFlags": [ctypes.POINTER(P), ctypes.c_uint],
+        "hipStreamDestroy": [P],
         "hipEventCreate": [ctypes.POINTER(P)],
         "hipEventDestroy": [P],
         "hipEventRecord": [P, P],

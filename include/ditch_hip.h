@@ -240,8 +240,13 @@ int32_t ditch_hip_matmulT_device(ditch_hip *h, float *d_out, uint64_t out_bytes,
  * each GPU holds for the life of the process: the call allocates nothing.
  * A call needing more scratch than that is refused (InvalidArgument) before
  * anything is launched; when only the split-K partial sums do not fit, the
- * product runs unsplit. Every call on one GPU shares that GPU's array, so
- * calls that overlap on one GPU (different streams) race: serialise them. */
+ * product runs unsplit. Every call on one GPU shares that GPU's array: the
+ * calls are ordered on the device in the order they are made (each call's
+ * stream first waits for an event the previous call recorded after its last
+ * kernel, whatever its stream or context), so calls on different streams
+ * do not overlap (under graph capture the graph orders the captured calls:
+ * make them depend on each other). The array keeps the last call's
+ * contents.                                                               */
 int32_t ditch_hip_matmulT_device_noalloc(ditch_hip *h, float *d_out,
                                          uint64_t out_bytes, const float *d_x,
                                          uint64_t x_bytes, uint64_t n,
@@ -593,6 +598,24 @@ int32_t ditch_hip_model_edit(ditch_hip_model *m, int32_t layer, int32_t slot,
                              int32_t expert, const float *v, uint64_t k,
                              float weight);
 
+/* One matrix of a batch edit: the slot (expert -1 for a dense slot), the
+ * edit's weight and its k directions v [k][rows] (host memory, rows = the
+ * matrix's rows; several targets may share one v).                        */
+typedef struct ditch_edit_target {
+    int32_t layer, slot, expert;
+    float weight;
+    const float *v;
+} ditch_edit_target;
+/* ditch_hip_model_edit for n matrices in one call (abliterate.apply's loop
+ * over layers, components and experts, abliterate.zig:148-210, `none`
+ * mode): every resident matrix's a = V^T W in one grouped launch over the
+ * resident tiles, every b = -weight V in another, all deltas in one device
+ * allocation (freed with the last of them); a streamed expert is staged on
+ * the device on its own. Returns when the deltas are installed.           */
+int32_t ditch_hip_model_edit_batch(ditch_hip_model *m,
+                                   const ditch_edit_target *targets, uint64_t n,
+                                   uint64_t k);
+
 /* The edit in every row-normalisation mode (abliterate.computeDelta,
  * abliterate.zig:223-350; Options abliterate.zig:63-84): `none` as above,
  * `pre` (directions over the row-normalised matrix, B scaled by the row
@@ -638,7 +661,10 @@ int32_t ditch_hip_klRows(ditch_hip *h, double *kl, const float *base_logprobs,
                          const float *trial_logits, uint64_t n, uint64_t vocab);
 /* The same two on device memory, enqueued on `stream` (NULL = the context
  * stream) and not waited for: the scorer's inputs stay in HBM after
- * ditch_hip_forward_device. d_out may equal d_x (in place).               */
+ * ditch_hip_forward_device. d_out may equal d_x (in place). These take no
+ * buffer lengths: d_out and d_x hold n * len floats, d_base_logprobs and
+ * d_trial_logits n * vocab floats, d_kl n doubles (a shorter buffer is
+ * written or read past its end).                                          */
 int32_t ditch_hip_logSoftmaxRows_device(ditch_hip *h, float *d_out,
                                         const float *d_x, uint64_t n,
                                         uint64_t len, void *stream);
@@ -649,7 +675,11 @@ int32_t ditch_hip_klRows_device(ditch_hip *h, double *d_kl,
 
 /* ------------------------------------------------------------------------ */
 /* The step after residual capture, on device memory (enqueued on `stream`,
- * NULL = the context stream, not waited for).                              */
+ * NULL = the context stream, not waited for). These take no buffer
+ * lengths: every device buffer must hold the elements its shape below
+ * names (d_first and d_take: prompts entries each; d_mean and d_sum: n;
+ * d_dirs, d_good_means, d_bad_means, d_first (basis), d_center: entries *
+ * hidden, d_dirs of the basis entries * k * hidden).                       */
 
 /* Engine.forEachResidual's per-batch reduction (engine.zig:414-431): for
  * prompt b and layer entry l, v = mean of the prompt's take[b] captured rows

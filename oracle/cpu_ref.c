@@ -955,6 +955,7 @@ struct ref_model {
     float *rope_cos, *rope_sin;
     int threads;
     size_t first_layer, n_layers_run;
+    int keep_packed;  /* quantised weights referenced as given, decoded per row at use */
 };
 
 ref_model *ref_model_create(const ditch_model_config *cfg) {
@@ -1004,6 +1005,12 @@ void ref_model_free(ref_model *m) {
 }
 
 void ref_set_threads(ref_model *m, int threads) { m->threads = threads < 1 ? 1 : threads; }
+/* Streamed mode (WeightStore + Dequant.readRange, dequant.zig:427-456): the
+ * virtual-bf16 formats (FP8, MXFP4, INT pack-quantized) set after this call
+ * keep pointing at the caller's packed pieces, which must outlive the
+ * model, and each product decodes the rows it multiplies (ref_weight_row:
+ * the same bf16 value as the mapped mode's one-time decode). */
+void ref_model_keep_packed(ref_model *m, int on) { m->keep_packed = on; }
 void ref_model_limit_layers(ref_model *m, size_t first, size_t count) { m->first_layer = first; m->n_layers_run = count; }
 
 static int is_vector_slot(int slot) {
@@ -1078,6 +1085,7 @@ int ref_model_set(ref_model *m, int layer, int slot, int expert, const ditch_wei
         return ref_weight_row(&flat, 0, t->vec);
     }
     t->w = *w;
+    if (is_bf16_virtual(w->dtype) && m->keep_packed) return 0;  /* borrowed, decoded per row */
     if (is_bf16_virtual(w->dtype)) {
         /* mapped mode: the virtual bf16 tensor decoded once (dequant.zig:841-845) */
         uint16_t *buf = (uint16_t *)malloc(w->rows * w->cols * 2);
@@ -1213,12 +1221,17 @@ static int moe_forward(ref_model *m, rlayer *L, float *out, const float *h, size
             for (size_t j = 0; j < k; j++) selw[t * k + j] = selw[t * k + j] * c->routed_scaling;
     }
     memset(out, 0, n * hidden * sizeof(float));
-    float *xg = (float *)malloc(n * hidden * sizeof(float));
-    float *gate = (float *)malloc(n * (inter > c->shared_inter ? inter : c->shared_inter) * sizeof(float));
-    float *up = (float *)malloc(n * (inter > c->shared_inter ? inter : c->shared_inter) * sizeof(float));
-    float *eo = (float *)malloc(n * hidden * sizeof(float));
-    size_t *tok = (size_t *)malloc(n * sizeof(size_t));
-    float *wts = (float *)malloc(n * sizeof(float));
+    /* an expert takes up to n * k pairs: a token selects expert 0 more than
+     * once when fewer than k choices are above -inf (topk's argmax returns
+     * index 0 then, moe.zig:971-985) */
+    size_t np_ = n * k;
+    size_t wi = inter > c->shared_inter ? inter : c->shared_inter;
+    float *xg = (float *)malloc(np_ * hidden * sizeof(float));
+    float *gate = (float *)malloc((np_ > n ? np_ : n) * wi * sizeof(float));
+    float *up = (float *)malloc((np_ > n ? np_ : n) * wi * sizeof(float));
+    float *eo = (float *)malloc((np_ > n ? np_ : n) * hidden * sizeof(float));
+    size_t *tok = (size_t *)malloc(np_ * sizeof(size_t));
+    float *wts = (float *)malloc(np_ * sizeof(float));
     uint8_t *used = (uint8_t *)calloc(ne_all, 1);
     for (size_t i = 0; i < n * k; i++) used[sel[i]] = 1;
     int rc = 0;

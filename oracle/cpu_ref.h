@@ -132,6 +132,7 @@ int ref_forward(ref_model *m, const uint32_t *tokens, const ditch_row *rows,
  * bounded CPU sample); count 0 = all layers. */
 void ref_model_limit_layers(ref_model *m, size_t first, size_t count);
 void ref_set_threads(ref_model *m, int threads);
+void ref_model_keep_packed(ref_model *m, int on);
 const char *ref_last_error(void);
 
 #ifdef __cplusplus

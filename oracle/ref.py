@@ -49,6 +49,7 @@ PROTOS = {
     "ref_forward": (ctypes.c_int, [P, P, P, SZ, P, SZ, P, P, SZ, P]),
     "ref_model_limit_layers": (None, [P, SZ, SZ]),
     "ref_set_threads": (None, [P, ctypes.c_int]),
+    "ref_model_keep_packed": (None, [P, ctypes.c_int]),
     "ref_last_error": (ctypes.c_char_p, []),
     "ref_residual_reduce": (ctypes.c_int, [P, SZ, SZ, SZ, P, P, SZ, FLT, P, P, P]),
     "ref_directions": (None, [P, P, P, SZ, SZ, ctypes.c_int]),
@@ -294,12 +295,16 @@ class Ref:
 class RefModel:
     """The oracle's model.forward over a ModelSpec."""
 
-    def __init__(self, spec, path=LIB, threads=8):
+    def __init__(self, spec, path=LIB, threads=8, keep_packed=False):
+        """keep_packed: FP8 / MXFP4 / INT weights stay in the spec's packed
+        arrays (held by this object) and are decoded row by row at use, as
+        the reference's streamed mode does, instead of once to bf16."""
         self.lib = load(path)
         self.spec = spec
         self.cfg = spec.config_struct()
         self.h = self.lib.ref_model_create(ctypes.byref(self.cfg))
         self.lib.ref_set_threads(self.h, threads)
+        self.lib.ref_model_keep_packed(self.h, int(keep_packed))
         for (layer, slot, expert), w in spec.tensors.items():
             if self.lib.ref_model_set(self.h, layer, slot, expert, w.ref()) != 0:
                 raise OracleError(self.lib.ref_last_error().decode())

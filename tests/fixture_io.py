@@ -302,7 +302,11 @@ def spec_from_hf(name):
             spec.set("ROUTER", _w_plain(tensors[m + "gate.weight"]), li)
             if m + "gate.e_score_correction_bias" in tensors:
                 spec.set("ROUTER_CORRECTION", _vec(tensors[m + "gate.e_score_correction_bias"]), li)
-            for e in range(n_exp):
+            fused = tensors.get(m + "experts.gate_up_proj") or tensors.get(m + "experts.gate_up_proj.weight")
+            if fused is not None:
+                _set_fused_experts(spec, li, fused, tensors.get(m + "experts.down_proj")
+                                   or tensors[m + "experts.down_proj.weight"], c["moe_inter"], hidden)
+            for e in range(n_exp if fused is None else 0):
                 ep = f"{m}experts.{e}."
                 spec.set("EXPERT_GATE", _quant_weight(tensors, ep + "gate_proj", qc), li, e)
                 spec.set("EXPERT_UP", _quant_weight(tensors, ep + "up_proj", qc), li, e)
@@ -317,6 +321,26 @@ def spec_from_hf(name):
             spec.set("UP", _quant_weight(tensors, m + "up_proj", qc), li)
             spec.set("DOWN", _quant_weight(tensors, m + "down_proj", qc), li)
     return spec
+
+
+def _set_fused_experts(spec, li, gate_up, down, inter, hidden):
+    """Stacked routed experts (moe.zig:83-93): gate_up [E, 2I, H] with down
+    [E, H, I] (gate = rows :I, up = rows I:), or the transposed pair
+    gate_up [E, H, 2I] with down [E, I, H]."""
+    gu, dn = as_array(gate_up), as_array(down)
+    dt = gate_up[0]
+    wrap = {"BF16": HostWeight.bf16, "F32": HostWeight.f32, "F16": HostWeight.f16}[dt]
+    if gu.shape[1:] == (2 * inter, hidden):
+        gates, ups, downs = gu[:, :inter, :], gu[:, inter:, :], dn
+    else:
+        assert gu.shape[1:] == (hidden, 2 * inter) and dn.shape[1:] == (inter, hidden)
+        gates = gu[:, :, :inter].transpose(0, 2, 1)
+        ups = gu[:, :, inter:].transpose(0, 2, 1)
+        downs = dn.transpose(0, 2, 1)
+    for e in range(gu.shape[0]):
+        spec.set("EXPERT_GATE", wrap(np.ascontiguousarray(gates[e])), li, e)
+        spec.set("EXPERT_UP", wrap(np.ascontiguousarray(ups[e])), li, e)
+        spec.set("EXPERT_DOWN", wrap(np.ascontiguousarray(downs[e])), li, e)
 
 
 def _gguf_weight(entry):

@@ -21,7 +21,8 @@ from ditch_amd.hip import DeviceError, Model
 
 pytestmark = pytest.mark.gpu
 
-HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "deepseek_v3"]
+HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "qwen3_moe_fused",
+      "qwen3_moe_fused_t", "qwen3_moe_big", "deepseek_v3"]
 GGUF = ["qwen2_gguf", "llama_gguf"]
 
 
@@ -216,4 +217,54 @@ def test_load_failures_are_reported(dev):
         f.write(b"GGUF" + struct.pack("<I", 3) + b"\x00" * 4)
         f.flush()
         with pytest.raises(DeviceError, match="truncated"):
+            Model.load(dev, f.name)
+
+
+def _gguf_string(s):
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def test_inconsistent_checkpoints_are_refused_on_the_host(dev):
+    """Tensors that disagree with each other are refused before anything is
+    uploaded: pack-quantized codes narrower than weight_shape needs, MXFP4
+    scales shorter than the codes need, a GGUF tensor whose size
+    overflows."""
+    spec = mg.dense("int4", hidden=256, inter=512, layers=1, heads=4, kv_heads=2, head_dim=64, vocab=300, seed=3,
+                    tie=False)
+    with tempfile.TemporaryDirectory() as d:
+        write_checkpoint(d, spec, "llama", QC["int4"])
+        shard = [f for f in sorted(os.listdir(d)) if f.endswith(".safetensors")]
+        tensors = {}
+        for f in shard:
+            tensors.update({k: (dt, fx.as_array((dt, shp, raw))) for k, (dt, shp, raw) in
+                            fx.read_safetensors(os.path.join(d, f)).items()})
+            os.remove(os.path.join(d, f))
+        name = "model.layers.0.mlp.down_proj.weight_packed"
+        tensors[name] = ("I32", np.ascontiguousarray(tensors[name][1][:, :-1]))
+        write_safetensors(os.path.join(d, "model.safetensors"), tensors)
+        with pytest.raises(DeviceError, match="fewer bytes"):
+            Model.load(dev, d)
+    spec = mg.dense("mxfp4", hidden=256, inter=512, layers=1, heads=4, kv_heads=2, head_dim=64, vocab=300, seed=3,
+                    tie=False)
+    with tempfile.TemporaryDirectory() as d:
+        write_checkpoint(d, spec, "llama", QC["mxfp4"])
+        tensors = {}
+        for f in [f for f in sorted(os.listdir(d)) if f.endswith(".safetensors")]:
+            tensors.update({k: (dt, fx.as_array((dt, shp, raw))) for k, (dt, shp, raw) in
+                            fx.read_safetensors(os.path.join(d, f)).items()})
+            os.remove(os.path.join(d, f))
+        name = "model.layers.0.self_attn.o_proj.weight_scale"
+        tensors[name] = ("U8", np.ascontiguousarray(tensors[name][1][:, :-1]))
+        write_safetensors(os.path.join(d, "model.safetensors"), tensors)
+        with pytest.raises(DeviceError, match="fewer bytes"):
+            Model.load(dev, d)
+    with tempfile.NamedTemporaryFile(suffix=".gguf") as f:
+        hdr = b"GGUF" + struct.pack("<IQQ", 3, 1, 1)
+        hdr += _gguf_string("general.architecture") + struct.pack("<I", 8) + _gguf_string("llama")
+        # Q8_0 (type 8) tensor of 2^39 x 2^39: its byte count overflows 64 bits
+        hdr += _gguf_string("token_embd.weight") + struct.pack("<IQQIQ", 2, 1 << 39, 1 << 39, 8, 0)
+        f.write(hdr + b"\x00" * 64)
+        f.flush()
+        with pytest.raises(DeviceError, match="overflows"):
             Model.load(dev, f.name)

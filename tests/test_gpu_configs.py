@@ -97,6 +97,50 @@ def test_c4_layer_at_full_batch_takes_the_device_plan(dev, ref):
     check_parity(ref, rg, lg, rc, lc, "c4 layer full batch")
 
 
+def test_c4_layer_edited_in_one_batch_stays_on_the_device_plan(dev, ref):
+    """The same layer with the rank-2 none-mode edit of o_proj and all 128
+    expert down projections made by one ditch_hip_model_edit_batch call
+    (abliterate.apply, abliterate.zig:148-210): the deltas equal those of
+    one ditch_hip_model_edit per matrix (the same forward, bit for bit), the
+    edited routed layer is still planned on the device (its down deltas in
+    the device segment table), and the forward matches the oracle doing the
+    same edit."""
+    spec = mg.moe_c4(layers=1, seed=51)
+    tokens, rows, last = mg.batch(32, [128], spec.config["vocab"], seed=52)
+    rng = np.random.default_rng(53)
+    v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+    v = np.ascontiguousarray(v.T.astype(np.float32))
+    E = spec.config["n_experts"]
+    targets = [(0, abi.SLOT["O"], -1, v, 0.8)] + [(0, abi.SLOT["EXPERT_DOWN"], e, v, 1.0) for e in range(E)]
+    cm = RefModel(spec, threads=16)
+    try:
+        for layer, slot, e, vv, wt in targets:
+            cm.edit(layer, slot, e, vv, wt)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        cm.free()
+    gm = Model(dev, spec)
+    try:
+        gm.edit_batch(targets, 2)
+        before = gm.path_stats()
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        after = gm.path_stats()
+        assert after["moe_device_planned"] - before["moe_device_planned"] == 1, after
+        assert after["moe_host_planned"] == before["moe_host_planned"], after
+        gm.reset_deltas()
+        for layer, slot, e, vv, wt in targets:
+            gm.edit(layer, slot, e, vv, wt)
+        rg1, lg1 = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        gm.reset_deltas()
+        _, l0 = gm.forward(tokens, rows, logit_rows=last)
+    finally:
+        gm.free()
+    np.testing.assert_array_equal(lg, lg1)
+    np.testing.assert_array_equal(rg, rg1)
+    check_parity(ref, rg, lg, rc, lc, "c4 layer edited in one batch")
+    assert np.abs(l0 - lg).max() > 1e-4  # the edit changed the model
+
+
 def test_mla_attention_256_keys(dev, ref):
     """MLA (head dims 192 / 128) over prompts of C5's 256 tokens: the
     attention kernel's uncached two-pass path (more than 128 keys)."""

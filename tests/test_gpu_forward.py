@@ -18,7 +18,8 @@ from oracle.ref import RefModel
 
 pytestmark = pytest.mark.gpu
 
-HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "deepseek_v3"]
+HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "qwen3_moe_fused",
+      "qwen3_moe_fused_t", "qwen3_moe_big", "deepseek_v3"]
 GGUF = ["qwen2_gguf", "llama_gguf"]
 
 
@@ -87,6 +88,15 @@ SYNTH = {
     "moe_fp8_sigmoid_groups": lambda: mg.moe("fp8", sigmoid=True, n_group=4, topk_group=2, shared=128, scaling=2.5,
                                              dense_first=1),
     "mla_fp8": lambda: mg.mla("fp8"),
+    # group-limited routing that keeps 2 experts for top-4: every token's
+    # last selections repeat expert 0 (moe.zig:971-985 returns index 0 when
+    # nothing is above -inf), so the combine must order repeats stably
+    # hidden 512 and q_lora 512: the norms take the wave-per-row kernel (the
+    # final norm through the logit rows' index, MLA's q_a norm in place)
+    "dense_bf16_h512": lambda: mg.dense("bf16", hidden=512, inter=1024, heads=8, kv_heads=2, head_dim=64),
+    "mla_fp8_qlora512": lambda: mg.mla("fp8", q_lora=512),
+    "moe_int4_repeated_selections": lambda: mg.moe("int4", experts=8, top_k=4, sigmoid=True, n_group=4,
+                                                   topk_group=1),
 }
 
 
@@ -330,6 +340,55 @@ def test_streamed_expert_edit_matches_oracle(dev, ref):
     finally:
         gm.free()
         cm.free()
+
+
+@pytest.mark.parametrize("streamed", [False, True])
+def test_edit_batch_matches_per_matrix_edits_and_oracle(dev, ref, streamed):
+    """One ditch_hip_model_edit_batch call over every layer's o_proj (layer
+    0's in bf16, the rest INT4: two tile formats in one batch), the dense
+    layer's down_proj and every routed expert's down_proj, with a direction
+    set and weight per layer (abliterate.apply, abliterate.zig:148-210):
+    the same forward, bit for bit, as one ditch_hip_model_edit per matrix,
+    and the oracle's forward after the same edits; with the experts
+    streamed, their blobs are staged on the device one at a time."""
+    spec = mg.moe("int4", dense_first=1, seed=12)
+    gen_o = np.random.default_rng(13)
+    from ditch_amd import synth
+    import torch
+    spec.set("O", synth.bf16_weight(torch.from_numpy(gen_o.normal(0, 0.02, (256, 256)).astype(np.float32))), 0)
+    rng = np.random.default_rng(14)
+    L, E = spec.config["layers"], spec.config["n_experts"]
+    targets = []
+    for li in range(L):
+        v, _ = np.linalg.qr(rng.standard_normal((spec.config["hidden"], 2)))
+        v = np.ascontiguousarray(v.T.astype(np.float32))
+        targets.append((li, abi.SLOT["O"], -1, v, 0.5 + 0.25 * li))
+        if spec.moe_layers[li]:
+            targets += [(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0) for e in range(E)]
+        else:
+            targets.append((li, abi.SLOT["DOWN"], -1, v, 0.9))
+    tokens, rows, last = mg.batch(3, [30, 12, 64], spec.config["vocab"], seed=15)
+    budget = 0
+    if streamed:
+        slot, _ = _cache_geometry(dev, spec, tokens, rows, last)
+        budget = 3 * slot
+    gm = Model(dev, spec, expert_cache_bytes=budget)
+    cm = RefModel(spec)
+    try:
+        gm.edit_batch(targets, 2)
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        gm.reset_deltas()
+        for layer, slot_, e, v, wt in targets:
+            gm.edit(layer, slot_, e, v, wt)
+            cm.edit(layer, slot_, e, v, wt)
+        rg1, lg1 = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    np.testing.assert_array_equal(lg, lg1)
+    np.testing.assert_array_equal(rg, rg1)
+    check_parity(ref, rg, lg, rc, lc, "edit batch")
 
 
 def test_expert_cache_rejects_late_budget_and_tiny_budget(dev):

@@ -170,6 +170,19 @@ def test_rmsnorm_layernorm_softmax(dev, ref):
     close(dev.logSoftmaxRows(x * 4), ref.log_softmax_rows(x * 4), **TOL_ELEM)
 
 
+@pytest.mark.parametrize("length", [512, 1024, 2048, 4096])
+def test_rmsnorm_rows_held_in_registers(dev, ref, length):
+    """Rows of 512-4096 columns take the wave-per-row kernel (the row held in
+    registers, one read): with and without a weight, gemma's (1 + w), and a
+    row count that leaves the last workgroup partly empty."""
+    rng = np.random.default_rng(length)
+    x = (rng.standard_normal((7, length)) * 3).astype(np.float32)
+    w = rng.standard_normal(length).astype(np.float32)
+    close(dev.rmsnormRows(x, w, 1e-6), ref.rmsnorm_rows(x, w, 1e-6), **TOL_ELEM)
+    close(dev.rmsnormRows(x, None, 1e-5), ref.rmsnorm_rows(x, None, 1e-5), **TOL_ELEM)
+    close(dev.rmsnormRows(x, w, 1e-6, gemma_style=True), ref.rmsnorm_rows(x, w, 1e-6, gemma=True), **TOL_ELEM)
+
+
 @pytest.mark.parametrize("act", range(6))
 def test_gated_activation(dev, ref, act):
     rng = np.random.default_rng(13 + act)

@@ -12,7 +12,8 @@ import pytest
 import fixture_io as fx
 from oracle.ref import RefModel
 
-HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "deepseek_v3"]
+HF = ["qwen2", "llama", "qwen2_fp8", "qwen2_int4", "qwen2_int4_actorder", "qwen3_moe", "qwen3_moe_fused",
+      "qwen3_moe_fused_t", "qwen3_moe_big", "deepseek_v3"]
 GGUF = ["qwen2_gguf", "llama_gguf"]
 TOL = 2e-3  # model_test.zig:62
 
@@ -53,3 +54,44 @@ def test_plant_a_mistake_in_the_oracle_fails():
     ids = case["ids"]
     _, logits = model.forward(ids, fx.case_rows(ids), logit_rows=[len(ids) - 1])
     assert np.abs(logits[0] - np.asarray(case["last_logits"])).max() > TOL
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "int4"])
+def test_packed_mode_matches_decoded_mode(fmt):
+    """The oracle's streamed mode (packed weights decoded row by row at use,
+    dequant.zig:427-456) gives the same forward, bit for bit, as its mapped
+    mode (each weight decoded to bf16 once)."""
+    import model_gen as mg
+    spec = mg.moe(fmt, hidden=128, layers=2, heads=2, kv_heads=1, head_dim=64, vocab=300, experts=8, top_k=2,
+                  moe_inter=128, seed=5)
+    tokens, rows, last = mg.batch(2, [9, 5], 300, seed=6)
+    outs = []
+    for packed in (False, True):
+        m = RefModel(spec, keep_packed=packed)
+        try:
+            outs.append(m.forward(tokens, rows, capture_rows=last, logit_rows=last))
+        finally:
+            m.free()
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+
+
+def test_oracle_routes_repeated_selections():
+    """Group-limited routing that keeps 2 experts for top-4 makes every
+    token select expert 0 more than once (moe.zig:971-985 returns index 0
+    when nothing is above -inf): the expert then takes more pairs than
+    there are tokens, and the oracle's per-expert buffers must hold them
+    (buffers sized by the token count were overrun); two runs agree bit for
+    bit and stay finite."""
+    import model_gen as mg
+    spec = mg.moe("int4", hidden=128, layers=1, heads=2, kv_heads=1, head_dim=64, vocab=300, experts=8, top_k=4,
+                  moe_inter=128, sigmoid=True, n_group=4, topk_group=1, seed=9)
+    tokens, rows, last = mg.batch(3, [20, 7, 33], 300, seed=10)
+    m = RefModel(spec)
+    try:
+        r1 = m.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        r2 = m.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        m.free()
+    assert np.isfinite(r1[1]).all()
+    np.testing.assert_array_equal(r1[1], r2[1])

@@ -6,6 +6,8 @@ the scaled-MFMA product, and a product whose split-K partial sums do not fit
 the scratch, which then runs unsplit). The bar is the product tolerance of
 the VTable products (abs 1e-4, rel 1e-3 of the output scale); where the two
 calls pick the same kernels the outputs are identical."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -81,3 +83,43 @@ def test_noalloc_refuses_more_than_the_scratch(dev):
         np.testing.assert_array_equal(o2.download(np.float32, (40, rows)), o1.download(np.float32, (40, rows)))
     finally:
         t.free()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """Calls alternating between two streams with different inputs (and
+    different weights) share the one scratch array: each call's stream waits
+    for the previous call's kernels, so every output equals the allocating
+    product's on the same inputs."""
+    from ditch_amd.hipmem import hip
+    lib = hip()
+    streams = []
+    for _ in range(2):
+        s = ctypes.c_void_p()
+        assert lib.hipStreamCreateWithFlags(ctypes.byref(s), 1) == 0  # non-blocking, default priority
+        streams.append(s)
+    ts = [dev.upload(_weight("fp8", 4096, 4096, 11)), dev.upload(_weight("int4", 1536, 2048, 12))]
+    try:
+        rng = np.random.default_rng(13)
+        jobs = []
+        for i in range(6):
+            t = ts[i % 2]
+            rows, cols = (4096, 4096) if i % 2 == 0 else (1536, 2048)
+            n = (64, 200, 48, 33, 96, 130)[i]
+            x = rng.standard_normal((n, cols)).astype(np.float32)
+            bx = hipmem.Buffer.from_array(x)
+            want, got = hipmem.Buffer(n * rows * 4), hipmem.Buffer(n * rows * 4)
+            jobs.append((t, n, rows, bx, want, got, streams[i % 2]))
+        for t, n, rows, bx, want, got, s in jobs:
+            t.matmul_device_noalloc(got.ptr, bx.ptr, n, stream=s.value)
+        for s in streams:
+            assert lib.hipStreamSynchronize(s) == 0
+        for t, n, rows, bx, want, got, s in jobs:
+            t.matmul_device(want.ptr, bx.ptr, n)
+        dev.sync()
+        for t, n, rows, bx, want, got, s in jobs:
+            np.testing.assert_array_equal(got.download(np.float32, (n, rows)), want.download(np.float32, (n, rows)))
+    finally:
+        for t in ts:
+            t.free()
+        for s in streams:
+            lib.hipStreamDestroy(s)
