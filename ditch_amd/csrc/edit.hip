@@ -343,11 +343,13 @@ static void edit_dots(float *out, const float *p, int64_t np, const float *x, in
 // The delta of abliterate.computeDelta for the resident weight w and host
 // directions v [k][rows]: device buffers da [rank][cols], db [rows][rank]
 // (allocated here, owned by the caller), *rank set.
-void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weight, int mode, int64_t lora_rank,
-                       uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out, int64_t *rank_out) {
+void edit_delta_device(ditch_hip *h, const TileView &w, const float *hv, int64_t k, float weight, int mode,
+                       int64_t lora_rank, uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out,
+                       int64_t *rank_out) {
     const int64_t rows = w.rows, cols = w.cols;
     DITCH_CHECK(k >= 1 && k <= 16 && mode >= 0 && mode <= 2, DITCH_INVALID_ARGUMENT, "edit: 1..16 directions, mode 0..2");
-    EditWork W;
+    if (!h->edit_work) h->edit_work = std::make_shared<EditWork>();
+    EditWork &W = *static_cast<EditWork *>(h->edit_work.get());
     float *v = W.v.get<float>(k * rows);
     DITCH_TRY_HIP(hipMemcpyAsync(v, hv, k * rows * 4, hipMemcpyHostToDevice, s));
     const int64_t rank = edit_rank(rows, cols, k, mode, lora_rank, ablate);

@@ -15,8 +15,11 @@
 // launch, and the result does not depend on timing. Like the reference, a
 // row whose y is 0 contributes nothing (0 times a non-finite weight
 // included).
+#include <map>
+
 #include "gemm_common.h"
 #include "model.h"
+#include "tile_decode.h"
 
 namespace ditch {
 
@@ -54,8 +57,10 @@ template <int TF> struct WtySide {
     int zp[Fmt<TF>::tiles];
 };
 
+// (kq: the lane's 8-column quarter of each 32-column k tile; a scale block
+// of FP8 / INT4 narrower than the unit covers the lane's 8 columns whole)
 template <int TF>
-__device__ __forceinline__ void wty_side(const TileView &w, int64_t row, int64_t unit, WtySide<TF> &sd) {
+__device__ __forceinline__ void wty_side(const TileView &w, int64_t row, int64_t unit, int kq, WtySide<TF> &sd) {
     constexpr int TL = Fmt<TF>::tiles, UK = 32 * TL;
     if constexpr (TF == TF_Q8 || TF == TF_MX4) {
         sd.word = load_side<TF>(w, row, unit).word;
@@ -73,7 +78,7 @@ __device__ __forceinline__ void wty_side(const TileView &w, int64_t row, int64_t
 #pragma unroll
             for (int t = 0; t < TL; t++) {
                 sd.zp[t] = 0;
-                sd.s[t] = tile_scale_of<TF>(w, row, unit * UK + 32 * t, &sd.zp[t]);
+                sd.s[t] = tile_scale_of<TF>(w, row, unit * UK + 32 * t + 8 * kq, &sd.zp[t]);
             }
         }
     }
@@ -116,9 +121,20 @@ __device__ __forceinline__ void wty_decode(const TileView &w, const Raw &raw, co
     }
 }
 
-template <int TF, int QB>
+// FAST (FP8, MXFP4, INT4 tensors whose every element the conversion
+// instructions decode exactly, TileView::fast): the tiled GEMM's decode from
+// the per-row side words, and every weight finite, so a row whose y is 0
+// adds exactly 0 without a test.
+template <int TF> constexpr bool wty_has_fast() { return TF == TF_FP8 || TF == TF_MX4 || TF == TF_INT4; }
+template <int TF, bool FAST> constexpr int wty_side_words() {
+    if constexpr (FAST) return TileCfg<TF>::NS;
+    else return 1;
+}
+
+template <int TF, int QB, bool FAST>
 __global__ __launch_bounds__(WTY_WAVES * 64) void wty_kernel(WtyArgs a) {
     constexpr int TL = Fmt<TF>::tiles, UK = 32 * TL, NV = 8 * TL;
+    constexpr int NS = wty_side_words<TF, FAST>();
     __shared__ float red[WTY_WAVES][QB][UK];
     int64_t unit;
     const WtySeg *sp = &a.one;
@@ -141,9 +157,12 @@ __global__ __launch_bounds__(WTY_WAVES * 64) void wty_kernel(WtyArgs a) {
 #pragma unroll
         for (int v = 0; v < NV; v++) acc[j][v] = 0.f;
 
+    SideStep st{1u, 0};
+    if constexpr (FAST) st = side_step<TF>(w);
     for (int64_t g0 = (int64_t)wave * WTY_STEP; g0 < groups; g0 += WTY_WAVES * WTY_STEP) {
         Raw raw[WTY_STEP];
         WtySide<TF> sd[WTY_STEP];
+        uint32_t sw[WTY_STEP][NS];
         float yv[WTY_STEP][QB];
         // every load of the step first
 #pragma unroll
@@ -151,7 +170,13 @@ __global__ __launch_bounds__(WTY_WAVES * 64) void wty_kernel(WtyArgs a) {
             const int64_t g = g0 + i < groups ? g0 + i : groups - 1;
             const int64_t row = g * 16 + r16;
             raw[i] = load_raw<TF>(w, g, unit, lane);
-            wty_side<TF>(w, row, unit, sd[i]);
+            if constexpr (FAST) {
+                const uint32_t *base = w.side + side_row(w, g, lane);
+#pragma unroll
+                for (int j = 0; j < NS; j++) sw[i][j] = gload<uint32_t>(side_word<TF>(st, base, unit, j));
+            } else {
+                wty_side<TF>(w, row, unit, kq, sd[i]);
+            }
 #pragma unroll
             for (int j = 0; j < QB; j++)
                 yv[i][j] = (g0 + i < groups && row < w.rows && j < a.q) ? y[(a.q0 + j) * w.rows + row] : 0.f;
@@ -161,13 +186,27 @@ __global__ __launch_bounds__(WTY_WAVES * 64) void wty_kernel(WtyArgs a) {
 #pragma unroll
             for (int t = 0; t < TL; t++) {
                 float f[8];
-                wty_decode<TF>(w, raw[i], sd[i], t, f);
+                if constexpr (FAST) {
+                    const u32x4 c[1] = {u32x4{raw[i].a.x, raw[i].a.y, raw[i].a.z, raw[i].a.w}};
+                    const u32x4 bh = decode_tile_lds<TF>(w, c, sw[i], t, true);
 #pragma unroll
-                for (int j = 0; j < QB; j++)
+                    for (int q = 0; q < 4; q++) {
+                        f[2 * q] = u2f(bh[q] << 16);
+                        f[2 * q + 1] = u2f(bh[q] & 0xffff0000u);
+                    }
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        acc[j][8 * t + e] = yv[i][j] != 0.f ? __builtin_fmaf(yv[i][j], f[e], acc[j][8 * t + e])
-                                                            : acc[j][8 * t + e];
+                    for (int j = 0; j < QB; j++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[j][8 * t + e] = __builtin_fmaf(yv[i][j], f[e], acc[j][8 * t + e]);
+                } else {
+                    wty_decode<TF>(w, raw[i], sd[i], t, f);
+#pragma unroll
+                    for (int j = 0; j < QB; j++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            acc[j][8 * t + e] = yv[i][j] != 0.f ? __builtin_fmaf(yv[i][j], f[e], acc[j][8 * t + e])
+                                                                : acc[j][8 * t + e];
+                }
             }
         }
     }
@@ -191,27 +230,44 @@ __global__ __launch_bounds__(WTY_WAVES * 64) void wty_kernel(WtyArgs a) {
     }
 }
 
-template <int TF>
+template <int TF, bool FAST>
 static void wty_launch_q(const WtyArgs &a, unsigned blocks, hipStream_t s) {
-    if (a.q == 1) hipLaunchKernelGGL((wty_kernel<TF, 1>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
-    else if (a.q == 2) hipLaunchKernelGGL((wty_kernel<TF, 2>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
-    else hipLaunchKernelGGL((wty_kernel<TF, 4>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
+    if (a.q == 1) hipLaunchKernelGGL((wty_kernel<TF, 1, FAST>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
+    else if (a.q == 2) hipLaunchKernelGGL((wty_kernel<TF, 2, FAST>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
+    else hipLaunchKernelGGL((wty_kernel<TF, 4, FAST>), dim3(blocks), dim3(WTY_WAVES * 64), 0, s, a);
+}
+
+template <int TF>
+static void wty_launch_fast(const WtyArgs &a, bool fast, unsigned blocks, hipStream_t s) {
+    if constexpr (wty_has_fast<TF>()) {
+        if (fast) return wty_launch_q<TF, true>(a, blocks, s);
+    }
+    wty_launch_q<TF, false>(a, blocks, s);
+}
+
+// The kind of kernel a tensor takes: its tile format, and whether it takes
+// the side-word decode.
+static int wty_kind(const TileView &w) {
+    const bool fast = w.fast && w.side && (w.tf == TF_FP8 || w.tf == TF_MX4 || w.tf == TF_INT4);
+    return w.tf * 2 + (fast ? 1 : 0);
 }
 
 // q directions in passes of at most 4 (the accumulators of one pass stay in
 // registers)
-static void wty_launch(int tf, WtyArgs a, int64_t q, unsigned blocks, hipStream_t s) {
+static void wty_launch(int kind, WtyArgs a, int64_t q, unsigned blocks, hipStream_t s) {
+    const int tf = kind / 2;
+    const bool fast = kind % 2;
     for (int64_t q0 = 0; q0 < q; q0 += 4) {
         a.q0 = q0;
         a.q = q - q0 < 4 ? q - q0 : 4;
         switch (tf) {
-        case TF_BF16: wty_launch_q<TF_BF16>(a, blocks, s); break;
-        case TF_F16: wty_launch_q<TF_F16>(a, blocks, s); break;
-        case TF_F32: wty_launch_q<TF_F32>(a, blocks, s); break;
-        case TF_Q8: wty_launch_q<TF_Q8>(a, blocks, s); break;
-        case TF_FP8: wty_launch_q<TF_FP8>(a, blocks, s); break;
-        case TF_MX4: wty_launch_q<TF_MX4>(a, blocks, s); break;
-        case TF_INT4: wty_launch_q<TF_INT4>(a, blocks, s); break;
+        case TF_BF16: wty_launch_fast<TF_BF16>(a, fast, blocks, s); break;
+        case TF_F16: wty_launch_fast<TF_F16>(a, fast, blocks, s); break;
+        case TF_F32: wty_launch_fast<TF_F32>(a, fast, blocks, s); break;
+        case TF_Q8: wty_launch_fast<TF_Q8>(a, fast, blocks, s); break;
+        case TF_FP8: wty_launch_fast<TF_FP8>(a, fast, blocks, s); break;
+        case TF_MX4: wty_launch_fast<TF_MX4>(a, fast, blocks, s); break;
+        case TF_INT4: wty_launch_fast<TF_INT4>(a, fast, blocks, s); break;
         default: throw Error{DITCH_UNSUPPORTED, "matvecTMulti: tile format"};
         }
         DITCH_TRY_HIP(hipGetLastError());
@@ -223,7 +279,7 @@ void launch_matvecT(float *out, const TileView &w, const float *y, int64_t q, hi
     if (w.rows <= 0 || w.cols <= 0) return;
     WtyArgs a{};
     a.one = WtySeg{w, y, out};
-    wty_launch(w.tf, a, q, (unsigned)w.units_k, s);
+    wty_launch(wty_kind(w), a, q, (unsigned)w.units_k, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -311,8 +367,8 @@ void model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint
     std::vector<EditB> eb(resident.size());
     std::vector<int64_t> item(items);
     int64_t it = 0;
-    int tf = -1;
-    bool one_tf = true;
+    int kind = -1;
+    bool one_kind = true;
     for (size_t r = 0; r < resident.size(); r++) {
         const ditch_edit_target &t = targets[resident[r]];
         const TileView &w = mats[resident[r]]->t->v;
@@ -321,8 +377,8 @@ void model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint
         segs[r] = WtySeg{w, v, da};
         eb[r] = EditB{db, v, w.rows, t.weight};
         for (int64_t u = 0; u < w.units_k; u++) item[it++] = ((int64_t)r << 32) | u;
-        if (tf < 0) tf = w.tf;
-        one_tf = one_tf && w.tf == tf;
+        if (kind < 0) kind = wty_kind(w);
+        one_kind = one_kind && wty_kind(w) == kind;
     }
     // the tables in one staging allocation, freed when the work has run
     const size_t seg_b = segs.size() * sizeof(WtySeg), eb_b = eb.size() * sizeof(EditB), it_b = item.size() * 8;
@@ -333,18 +389,18 @@ void model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint
     DITCH_TRY_HIP(hipMemcpyAsync(dsegs, segs.data(), seg_b, hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(deb, eb.data(), eb_b, hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(ditems, item.data(), it_b, hipMemcpyHostToDevice, s));
-    if (one_tf) {
+    if (one_kind) {
         WtyArgs a{};
         a.segs = dsegs;
         a.items = ditems;
-        wty_launch(tf, a, (int64_t)k, (unsigned)items, s);
+        wty_launch(kind, a, (int64_t)k, (unsigned)items, s);
     } else {
-        // matrices of several tile formats: one launch per format over its
-        // items (the segment table is shared)
-        std::unordered_map<int, std::vector<int64_t>> by_tf;
-        for (int64_t i = 0; i < items; i++) by_tf[segs[item[i] >> 32].w.tf].push_back(item[i]);
+        // matrices of several tile formats (or decodes): one launch per kind
+        // over its items (the segment table is shared)
+        std::map<int, std::vector<int64_t>> by_kind;
+        for (int64_t i = 0; i < items; i++) by_kind[wty_kind(segs[item[i] >> 32].w)].push_back(item[i]);
         int64_t *dst = ditems;
-        for (auto &kv : by_tf) {
+        for (auto &kv : by_kind) {
             DITCH_TRY_HIP(hipMemcpyAsync(dst, kv.second.data(), kv.second.size() * 8, hipMemcpyHostToDevice, s));
             WtyArgs a{};
             a.segs = dsegs;

@@ -4,6 +4,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -166,6 +167,9 @@ struct ditch_hip {
     ditch::DevBuf rowred;
     // scratch of the direction pipeline (projections, basis columns)
     ditch::DevBuf dirtmp;
+    // the edit's workspace (edit.hip), kept across calls: an edit of
+    // thousands of matrices allocates and frees nothing per matrix
+    std::shared_ptr<void> edit_work;
     // this device's copy of the static scratch array (api.hip), resolved
     // with hipGetSymbolAddress when the context opens
     void *static_scratch = nullptr;
@@ -377,8 +381,10 @@ void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, c
 // edit.hip
 void edit_gaussian(float *out, size_t n, uint64_t seed);
 int64_t edit_rank(int64_t rows, int64_t cols, int64_t k, int mode, int64_t lora_rank, int ablate);
-void edit_delta_device(const TileView &w, const float *hv, int64_t k, float weight, int mode, int64_t lora_rank,
-                       uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out, int64_t *rank_out);
+// (h: the context whose edit workspace the passes use)
+void edit_delta_device(ditch_hip *h, const TileView &w, const float *hv, int64_t k, float weight, int mode,
+                       int64_t lora_rank, uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out,
+                       int64_t *rank_out);
 
 // directions.hip
 void launch_residual_reduce(const float *res, int64_t entries, int64_t n_capture, int64_t hidden,

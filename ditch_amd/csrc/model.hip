@@ -675,16 +675,18 @@ __global__ void grouped_delta_xa_kernel(float *xa, const float *x, const int32_t
 }
 
 // The same for a routed layer planned on the device (every expert a
-// segment, off / cnt written by moe_plan_kernel): one wave per (pair p,
-// direction j); p's expert is the last whose pair offset is <= p (offsets
-// are non-decreasing in expert order and cover every pair); a[e] is expert
-// e's delta A, or NULL for an expert without a delta (its rows are unused).
+// segment, off / cnt written by moe_plan_kernel): one wave per pair p and 4
+// directions (the pair's row read once for the four); p's expert is the
+// last whose pair offset is <= p (offsets are non-decreasing in expert
+// order and cover every pair); a[e] is expert e's delta A, or NULL for an
+// expert without a delta (its rows are unused).
 __global__ void plan_delta_xa_kernel(float *xa, const float *x, const GroupSeg *segs, const float *const *a,
                                      int64_t E, int64_t cols, int max_rank, int64_t P) {
     const int lane = threadIdx.x & 63;
+    const int64_t nb = (max_rank + 3) / 4;
     const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (t >= P * max_rank) return;
-    const int64_t p = t / max_rank, j = t % max_rank;
+    if (t >= P * nb) return;
+    const int64_t p = t / nb, j0 = (t % nb) * 4;
     int64_t lo = 0, hi = E - 1;
     while (lo < hi) {
         const int64_t mid = (lo + hi + 1) / 2;
@@ -692,11 +694,14 @@ __global__ void plan_delta_xa_kernel(float *xa, const float *x, const GroupSeg *
         else hi = mid - 1;
     }
     const float *ae = a[lo];
-    float acc = 0.f;
-    if (ae && j < segs[lo].delta_rank)
-        for (int64_t c = lane; c < cols; c += 64) acc = __builtin_fmaf(ae[j * cols + c], x[p * cols + c], acc);
-    acc = wave_sum64(acc);
-    if (lane == 0) xa[p * max_rank + j] = acc;
+    const int rank = ae ? segs[lo].delta_rank : 0;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j0 < rank) delta_dot4(x + p * cols, ae, cols, j0, rank, lane, acc);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        const float v = wave_sum64(acc[jj]);
+        if (lane == 0 && j0 + jj < max_rank) xa[p * max_rank + j0 + jj] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -981,7 +986,7 @@ void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const fl
     }
     float *da = nullptr, *db = nullptr;
     int64_t rank = 0;
-    edit_delta_device(w, v, (int64_t)k, weight, mode, lora_rank, seed, ablate, s, &da, &db, &rank);
+    edit_delta_device(m->h, w, v, (int64_t)k, weight, mode, lora_rank, seed, ablate, s, &da, &db, &rank);
     mt->clear_delta();
     mt->da = da;
     mt->db = db;
@@ -1147,8 +1152,9 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
             const float **dda = m->segd.get<const float *>(E);
             DITCH_TRY_HIP(hipMemcpyAsync(dda, das.data(), E * sizeof(float *), hipMemcpyHostToDevice, s));
             dxa = m->e_xa.get<float>(P * max_rank);
-            hipLaunchKernelGGL(plan_delta_xa_kernel, dim3((unsigned)((P * max_rank + 3) / 4)), dim3(256), 0, s, dxa,
-                               act, dsegs + 2 * E, dda, E, inter, max_rank, P);
+            const int64_t waves = P * ((max_rank + 3) / 4);
+            hipLaunchKernelGGL(plan_delta_xa_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, dxa, act,
+                               dsegs + 2 * E, dda, E, inter, max_rank, P);
             DITCH_TRY_HIP(hipGetLastError());
         }
         launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s, dxa, max_rank);

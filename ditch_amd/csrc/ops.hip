@@ -736,15 +736,20 @@ __global__ void row_norms_kernel(float *out, TileView w) {
 }
 
 // xa[i][j] = dot(a_j, x_i) for the low-rank delta (tensor.zig:1036-1042)
+// (a wave per row and 4 directions: delta_dot4)
 __global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank) {
     int lane = threadIdx.x & 63;
+    const int64_t nb = (rank + 3) / 4;
     int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (t >= n * rank) return;
-    int64_t i = t / rank, j = t % rank;
-    float s = 0.f;
-    for (int64_t c = lane; c < cols; c += 64) s = __builtin_fmaf(a[j * cols + c], x[i * cols + c], s);
-    s = wave_sum(s);
-    if (lane == 0) xa[t] = s;
+    if (t >= n * nb) return;
+    const int64_t i = t / nb, j0 = (t % nb) * 4;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    delta_dot4(x + i * cols, a, cols, j0, rank, lane, s);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        const float v = wave_sum(s[jj]);
+        if (lane == 0 && j0 + jj < rank) xa[i * rank + j0 + jj] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -898,7 +903,8 @@ void launch_row_norms(float *out, const TileView &w, hipStream_t s) {
 }
 void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank, hipStream_t s) {
     if (n * rank <= 0) return;
-    hipLaunchKernelGGL(delta_xa_kernel, dim3((unsigned)((n * rank + 3) / 4)), dim3(256), 0, s, xa, x, a, n, cols, rank);
+    const int64_t waves = n * ((rank + 3) / 4);
+    hipLaunchKernelGGL(delta_xa_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, xa, x, a, n, cols, rank);
     DITCH_TRY_HIP(hipGetLastError());
 }
 

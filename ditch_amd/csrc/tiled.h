@@ -98,4 +98,43 @@ __device__ float tiled_element_f32(const TileView &v, int64_t n, int64_t k, uint
     }
 }
 
+// One wave's part of x_row . a_j for the low-rank deltas' products
+// (tensor.zig:1036-1042), directions j0 .. j0 + 3 below `rank` at once: the
+// row is read once for the four, 16 bytes a lane with four such loads in
+// flight (rows of whole, aligned float4s; else one float a lane). Lane sums
+// in s, to be added over the wave.
+__device__ __forceinline__ void delta_dot4(const float *xr, const float *a, int64_t cols, int64_t j0, int64_t rank,
+                                           int lane, float (&s)[4]) {
+    if ((cols & 3) == 0 && (((uintptr_t)xr | (uintptr_t)a) & 15) == 0) {
+        constexpr int U = 4;
+        for (int64_t c0 = 4 * lane; c0 < cols; c0 += 256 * U) {
+            float4 xv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                xv[u] = c0 + 256 * u < cols ? *(const float4 *)(xr + c0 + 256 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                if (j0 + jj >= rank) continue;
+                const float *ar = a + (j0 + jj) * cols;
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    if (c0 + 256 * u >= cols) continue;
+                    const float4 av = *(const float4 *)(ar + c0 + 256 * u);
+                    s[jj] = __builtin_fmaf(av.x, xv[u].x, s[jj]);
+                    s[jj] = __builtin_fmaf(av.y, xv[u].y, s[jj]);
+                    s[jj] = __builtin_fmaf(av.z, xv[u].z, s[jj]);
+                    s[jj] = __builtin_fmaf(av.w, xv[u].w, s[jj]);
+                }
+            }
+        }
+    } else {
+        for (int64_t c = lane; c < cols; c += 64) {
+            const float xv = xr[c];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                if (j0 + jj < rank) s[jj] = __builtin_fmaf(a[(j0 + jj) * cols + c], xv, s[jj]);
+        }
+    }
+}
+
 }  // namespace ditch

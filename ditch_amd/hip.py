@@ -347,17 +347,25 @@ class Model:
         v = _f32(v)
         self.dev.check(self.dev.lib.ditch_hip_model_edit(self.h, layer, slot, expert, _p(v), v.shape[0], weight))
 
-    def edit_batch(self, targets, k):
-        """targets: [(layer, slot, expert, v [k][rows] f32 array, weight)];
-        one call edits them all (ditch_hip_model_edit_batch)."""
-        keep = []
+    @staticmethod
+    def edit_targets(targets, k):
+        """The ditch_edit_target array of [(layer, slot, expert, v [k][rows]
+        f32 array, weight)] (with the arrays it points into)."""
+        keep = {}
         arr = (abi.EditTarget * len(targets))()
         for i, (layer, slot, expert, v, weight) in enumerate(targets):
-            v = _f32(v)
-            assert v.shape[0] == k
-            keep.append(v)
-            arr[i] = abi.EditTarget(layer, slot, expert, weight, v.ctypes.data)
-        self.dev.check(self.dev.lib.ditch_hip_model_edit_batch(self.h, ctypes.byref(arr), len(targets), k))
+            if id(v) not in keep:
+                keep[id(v)] = _f32(v)
+            vv = keep[id(v)]
+            assert vv.shape[0] == k
+            arr[i] = abi.EditTarget(layer, slot, expert, weight, vv.ctypes.data)
+        return (arr, list(keep.values()), k)
+
+    def edit_batch(self, targets, k=None):
+        """One call edits every target (ditch_hip_model_edit_batch): a list as
+        for edit_targets, or what edit_targets returned."""
+        arr, keep, k = targets if isinstance(targets, tuple) else self.edit_targets(targets, k)
+        self.dev.check(self.dev.lib.ditch_hip_model_edit_batch(self.h, ctypes.byref(arr), len(arr), k))
 
     def edit_ex(self, layer, slot, expert, v, weight, mode="full", lora_rank=3, seed=0, ablate=False):
         v = _f32(v)

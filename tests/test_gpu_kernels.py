@@ -237,6 +237,41 @@ def test_matvecT_tall_row_chunks(dev, ref, kind, rows):
     close(dev.matvecTMulti(w, y), ref.matvecTMulti(w, y), **TOL_MATMUL)
 
 
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16", "q8_0", "fp8", "fp8_16x8", "mxfp4", "int4", "int4_g16",
+                                  "int4_sym", "int8"])
+@pytest.mark.parametrize("rows,cols,q", [(2048, 768, 2), (203, 1024, 9)])
+def test_matvecT_formats_and_shapes(dev, ref, kind, rows, cols, q):
+    """W^T y over every tile format, with the side-word decode (FP8 128 x 128,
+    MXFP4, INT4 group 128) and the element decode (FP8 16 x 8, INT4 group
+    16, INT8, symmetric INT4 ...): C4's expert down_proj shape with the
+    rank-2 edit's q, and a ragged matrix with q = 9 (three passes of the
+    accumulators); a row whose y is 0 in every direction contributes
+    nothing."""
+    rng = np.random.default_rng(rows + cols + q)
+    w = wg.make(kind, rows, cols, rng)
+    y = rng.standard_normal((q, rows)).astype(np.float32)
+    y[:, 5] = 0.0
+    close(dev.matvecTMulti(w, y), ref.matvecTMulti(w, y), **TOL_MATMUL)
+
+
+def test_matvecT_skips_zero_rows_of_non_finite_weights(dev, ref):
+    """A row of NaN / infinite weights (MXFP4 scale byte 255) whose y is 0
+    in every direction is skipped, as tensor.matvecTMulti skips it
+    (tensor.zig:1056-1094): the product stays finite; with y non-zero there
+    it is not finite."""
+    rng = np.random.default_rng(31)
+    rows, cols = 96, 256
+    w = wg.mxfp4_random(rows, cols, rng)
+    w.arrays[1][7, 2] = 255
+    y = rng.standard_normal((2, rows)).astype(np.float32)
+    y[:, 7] = 0.0
+    got = dev.matvecTMulti(w, y)
+    assert np.isfinite(got).all()
+    close(got, ref.matvecTMulti(w, y), **TOL_MATMUL)
+    y[1, 7] = 1.0
+    assert not np.isfinite(dev.matvecTMulti(w, y)[1]).all()
+
+
 def test_kl_rows(dev, ref):
     rng = np.random.default_rng(17)
     base = rng.standard_normal((4, 5000)).astype(np.float32) * 2
