@@ -135,8 +135,17 @@ class EditTarget(C.Structure):
 
 
 class Sampler(C.Structure):
-    """`ditch_sampler` (model.Sampler)."""
-    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("seed", C.c_uint64)]
+    """`ditch_sampler` (model.Sampler): set it with `sampler(lib, ...)`."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("reserved", C.c_uint32),
+                ("rng", C.c_uint64 * 4)]
+
+
+def sampler(lib, seed=0, temperature=1.0, top_k=50, top_p=0.95):
+    """Sampler.init (model.zig:5216-5218) through ditch_hip_sampler_init."""
+    s = Sampler()
+    if lib.ditch_hip_sampler_init(C.byref(s), seed, temperature, top_k, top_p) != 0:
+        raise ValueError("ditch_hip_sampler_init failed")
+    return s
 
 
 class PathStats(C.Structure):
@@ -218,7 +227,8 @@ PROTOTYPES = {
     "ditch_hip_kv_cache_create": (P, [P, U32, U32]),
     "ditch_hip_kv_cache_free": (None, [P]),
     "ditch_hip_forward_cached": (I32, [P, P, P, P, U64, P, U64, P, U64]),
-    "ditch_hip_pick_tokens_device": (I32, [P, P, P, U64, U64, P, U64, P, P]),
+    "ditch_hip_sampler_init": (I32, [P, U64, FLT, U64, FLT]),
+    "ditch_hip_pick_tokens_device": (I32, [P, P, P, U64, U64, P, P]),
     "ditch_hip_generate": (I32, [P, P, P, P, U64, U64, P, U64, P, P, P, P]),
     "ditch_hip_edit_delta": (I32, [P, P, P, P, P, U64, FLT]),
     "ditch_hip_model_edit": (I32, [P, I32, I32, I32, P, U64, FLT]),

@@ -25,7 +25,7 @@ void model_edit_ex(ditch_hip_model *m, int layer, int slot, int expert, const fl
 ditch_hip_kv_cache *kv_cache_create(ditch_hip_model *m, int64_t B, int64_t T);
 ditch_hip_model *model_load(ditch_hip *h, const char *path, uint64_t expert_cache);
 void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens, const uint64_t *lens, int64_t B,
-              int64_t max_new, const uint32_t *eos, int64_t n_eos, const ditch_sampler *smp, uint32_t *out_tokens,
+              int64_t max_new, const uint32_t *eos, int64_t n_eos, ditch_sampler *smp, uint32_t *out_tokens,
               uint64_t *out_lens, float *first_logits);
 uint64_t model_bytes(const ditch_hip_model *m);
 void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row *d_rows, int64_t n, int64_t B,
@@ -728,19 +728,23 @@ int32_t ditch_hip_forward_cached(ditch_hip_model *m, ditch_hip_kv_cache *c, cons
     });
 }
 
+int32_t ditch_hip_sampler_init(ditch_sampler *s, uint64_t seed, float temperature, uint64_t top_k, float top_p) {
+    if (!s) return DITCH_INVALID_ARGUMENT;
+    sampler_init(s, seed, temperature, top_k, top_p);
+    return DITCH_OK;
+}
+
 int32_t ditch_hip_pick_tokens_device(ditch_hip *h, uint32_t *d_out, const float *d_logits, uint64_t n, uint64_t vocab,
-                                     const ditch_sampler *sampler, uint64_t step, const uint32_t *d_row_ids,
-                                     void *stream) {
+                                     ditch_sampler *sampler, void *stream) {
     return guarded(h, [&] {
         DITCH_CHECK(d_out && d_logits, DITCH_INVALID_ARGUMENT, "NULL argument");
-        launch_pick(d_out, d_logits, (int64_t)n, (int64_t)vocab, sampler, step, d_row_ids,
-                    stream ? (hipStream_t)stream : h->stream);
+        launch_pick(d_out, d_logits, (int64_t)n, (int64_t)vocab, sampler, stream ? (hipStream_t)stream : h->stream);
     });
 }
 
 int32_t ditch_hip_generate(ditch_hip_model *m, ditch_hip_kv_cache *c, const uint32_t *tokens,
                            const uint64_t *prompt_lens, uint64_t n_prompts, uint64_t max_new_tokens,
-                           const uint32_t *eos_ids, uint64_t n_eos, const ditch_sampler *sampler, uint32_t *out_tokens,
+                           const uint32_t *eos_ids, uint64_t n_eos, ditch_sampler *sampler, uint32_t *out_tokens,
                            uint64_t *out_lens, float *first_logits) {
     if (!m) return DITCH_INVALID_ARGUMENT;
     return guarded(m->h, [&] {

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "zig_random.h"
 
 namespace ditch {
 
@@ -147,6 +148,95 @@ __global__ __launch_bounds__(1024) void edit_orthonormalize_kernel(float *vecs, 
     }
 }
 
+// The same Gram-Schmidt with the vector being orthonormalised held in
+// registers (EPT elements a thread, element m * 1024 + tid): each step reads
+// only v_j, whose successor is loaded before the step's reduction, and each
+// reduction takes one barrier that waits on LDS alone (the wave sums
+// alternate between two LDS slots, so a fast wave cannot overwrite sums a
+// slow wave is still reading). Per element the arithmetic is the kernel
+// above's: f64 dot rounded to f32, then v_i + (-p) v_j rounded twice.
+template <int CTRL>
+__device__ __forceinline__ double ed_dpp(double v) {
+    const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xf, 0xf, false);
+    return __hiloint2double(hi, lo);
+}
+
+// the sum of a wave's 64 values, the same in every lane: DPP butterflies
+// within each row of 16 lanes (quad swaps, half-row and row mirrors), then
+// the four row sums read as scalars
+__device__ __forceinline__ double ed_wave_total(double v) {
+    v += ed_dpp<0xB1>(v);
+    v += ed_dpp<0x4E>(v);
+    v += ed_dpp<0x141>(v);
+    v += ed_dpp<0x140>(v);
+    double r = 0.0;
+#pragma unroll
+    for (int row = 0; row < 4; row++)
+        r += __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), 16 * row),
+                              __builtin_amdgcn_readlane(__double2loint(v), 16 * row));
+    return r;
+}
+
+__device__ __forceinline__ void ed_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int EPT>
+__global__ __launch_bounds__(1024) void edit_orth_reg_kernel(float *vecs, int64_t q, int64_t n) {
+    __shared__ double sh[2][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int slot = 0;
+    auto block_dot = [&](const float *a, const float *b) -> float {
+        double acc = 0.0;
+#pragma unroll
+        for (int m = 0; m < EPT; m++) acc += (double)a[m] * (double)b[m];
+        acc = ed_wave_total(acc);
+        if (lane == 0) sh[slot][wave] = acc;
+        ed_lds_barrier();
+        double r = 0.0;
+#pragma unroll
+        for (int w = 0; w < 16; w++) r += sh[slot][w];
+        slot ^= 1;
+        return (float)r;
+    };
+    auto load = [&](float *dst, const float *src) {
+#pragma unroll
+        for (int m = 0; m < EPT; m++) {
+            const int64_t t = (int64_t)m * 1024 + tid;
+            dst[m] = t < n ? src[t] : 0.f;
+        }
+    };
+    for (int64_t i = 0; i < q; i++) {
+        float *vi_g = vecs + i * n;
+        float vi[EPT], vj[EPT], vn[EPT];
+        load(vi, vi_g);
+        if (i > 0) load(vj, vecs);
+        for (int pass = 0; pass < 2; pass++)
+            for (int64_t j = 0; j < i; j++) {
+                const int64_t nj = j + 1 < i ? j + 1 : (pass == 0 ? 0 : -1);
+                if (nj >= 0) load(vn, vecs + nj * n);
+                const float p = block_dot(vi, vj);
+#pragma unroll
+                for (int m = 0; m < EPT; m++) vi[m] = __fadd_rn(vi[m], __fmul_rn(-p, vj[m]));
+                if (nj >= 0) {
+#pragma unroll
+                    for (int m = 0; m < EPT; m++) vj[m] = vn[m];
+                }
+            }
+        const float nrm = __fsqrt_rn(block_dot(vi, vi));
+        const float s = nrm > 1e-20f ? __fdiv_rn(1.0f, nrm) : 0.f;
+#pragma unroll
+        for (int m = 0; m < EPT; m++) {
+            const int64_t t = (int64_t)m * 1024 + tid;
+            if (t < n) vi_g[t] = nrm > 1e-20f ? __fmul_rn(vi[m], s) : 0.f;
+        }
+        __syncthreads();  // v_i (global) is read by the later vectors
+    }
+}
+
 constexpr int ED_MAXQ = 64;
 
 // abliterate.jacobiEigen (abliterate.zig:427-469): cyclic Jacobi in f32 on the
@@ -262,26 +352,12 @@ static int ed_grid(int64_t total) {
     return (int)(g < 1 ? 1 : g > 16384 ? 16384 : g);
 }
 
-// The full mode's random test matrix: q x cols standard normals from a
-// counter-based generator (splitmix64 of seed and index, Box-Muller in
-// f64), so any caller can reproduce it. The reference draws it from Zig's
-// Xoshiro256 (abliterate.zig:476-481); the SVD it seeds converges to the
-// same subspace.
-static uint64_t splitmix64(uint64_t x) {
-    x += 0x9E3779B97F4A7C15ull;
-    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
-    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
-    return x ^ (x >> 31);
-}
-
+// The full mode's random test matrix: the first n draws of
+// Random.floatNorm(f32) from std.Random.DefaultPrng.init(seed), in the
+// order the reference fills omega (abliterate.zig:474-479).
 void edit_gaussian(float *out, size_t n, uint64_t seed) {
-    for (size_t t = 0; t < n; t++) {
-        const uint64_t r1 = splitmix64(seed ^ (2 * (uint64_t)t) * 0xD1B54A32D192ED03ull);
-        const uint64_t r2 = splitmix64(seed ^ (2 * (uint64_t)t + 1) * 0xD1B54A32D192ED03ull);
-        const double u1 = ((double)(r1 >> 11) + 1.0) * 0x1.0p-53;  // (0, 1]
-        const double u2 = (double)(r2 >> 11) * 0x1.0p-53;          // [0, 1)
-        out[t] = (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
-    }
+    ZigRandom rng(seed);
+    for (size_t t = 0; t < n; t++) out[t] = rng.norm_f32();
 }
 
 int64_t edit_rank(int64_t rows, int64_t cols, int64_t k, int mode, int64_t lora_rank, int ablate) {
@@ -331,7 +407,19 @@ static void edit_matvecT(const TileView &w, float *out, const float *y, int64_t 
 }
 
 static void edit_orth(float *vecs, int64_t q, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(edit_orthonormalize_kernel, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    const int64_t ept = (n + 1023) / 1024;
+    if (ept <= 2)
+        hipLaunchKernelGGL(edit_orth_reg_kernel<2>, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    else if (ept <= 4)
+        hipLaunchKernelGGL(edit_orth_reg_kernel<4>, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    else if (ept <= 8)
+        hipLaunchKernelGGL(edit_orth_reg_kernel<8>, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    else if (ept <= 16)
+        hipLaunchKernelGGL(edit_orth_reg_kernel<16>, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    else if (ept <= 24)
+        hipLaunchKernelGGL(edit_orth_reg_kernel<24>, dim3(1), dim3(1024), 0, s, vecs, q, n);
+    else  // vectors above 24 576 elements: the global-memory form
+        hipLaunchKernelGGL(edit_orthonormalize_kernel, dim3(1), dim3(1024), 0, s, vecs, q, n);
     DITCH_TRY_HIP(hipGetLastError());
 }
 

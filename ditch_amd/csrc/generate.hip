@@ -4,7 +4,8 @@
 // the active prompts' rows through the resident forward, and the next token
 // of every row is picked on the device: the first maximum (model.zig:
 // 5194-5204), or the Sampler's temperature / top-k / top-p draw (model.zig:
-// 5208-5264) with a counter-based uniform per (seed, step, prompt).
+// 5208-5264), whose uniform draws come from the Sampler's own Zig
+// DefaultPrng on the host, one per sampled row in row order.
 #include <math.h>
 #include <string.h>
 
@@ -12,6 +13,7 @@
 
 #include "internal.h"
 #include "model.h"
+#include "zig_random.h"
 
 namespace ditch {
 
@@ -20,15 +22,15 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
                    int64_t n_logit, float *d_logits, ditch_hip_kv_cache *pc);
 
 constexpr int PICK_MAXK = 256;  // Sampler.max_top_k
+constexpr int PICK_ROWS = 256;  // rows per launch: their draws travel in the arguments
 
 struct PickArgs {
     uint32_t *out;
     const float *logits;
-    const uint32_t *row_ids;  // the prompt of each row (RNG stream), NULL = the row index
-    int64_t n, vocab;
+    int64_t vocab;
     float temperature, top_p;
     int top_k;
-    uint64_t seed, step;
+    double u[PICK_ROWS];  // each row's Random.float(f64) draw
 };
 
 // floats ordered as unsigned keys (larger key = larger value)
@@ -38,13 +40,6 @@ __device__ __forceinline__ uint32_t pick_key(float f) {
 }
 __device__ __forceinline__ float pick_val(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-__device__ __forceinline__ uint64_t pick_mix(uint64_t x) {
-    x += 0x9E3779B97F4A7C15ull;
-    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
-    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
-    return x ^ (x >> 31);
 }
 
 // One block per logit row.
@@ -198,9 +193,7 @@ __global__ __launch_bounds__(1024) void pick_kernel(PickArgs a) {
             kept++;
             if (kept_mass >= (double)a.top_p * total) break;
         }
-        const uint64_t pid = a.row_ids ? a.row_ids[row] : (uint64_t)row;
-        const uint64_t h = pick_mix(a.seed ^ pick_mix(a.step * 0x100000001B3ull ^ pick_mix(pid + 0x51ED27ull)));
-        double u = (double)(h >> 11) * 0x1.0p-53 * kept_mass;
+        double u = a.u[row] * kept_mass;
         uint32_t id = ~(uint32_t)(cand[kept - 1] & 0xFFFFFFFFu);
         for (int i = 0; i < kept; i++) {
             u -= probs[i];
@@ -213,26 +206,48 @@ __global__ __launch_bounds__(1024) void pick_kernel(PickArgs a) {
     }
 }
 
-void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, const ditch_sampler *smp,
-                 uint64_t step, const uint32_t *row_ids, hipStream_t s) {
+void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, ditch_sampler *smp, hipStream_t s) {
     if (n <= 0) return;
     DITCH_CHECK(vocab > 0 && n <= INT32_MAX, DITCH_INVALID_ARGUMENT, "pick: empty rows");
-    PickArgs a{out, logits, row_ids, n, vocab, 0.f, 1.f, 1, 0, step};
-    if (smp && smp->temperature > 0.f) {
+    const bool sample = smp && smp->temperature > 0.f;
+    ZigRandom rng;
+    PickArgs a{};
+    a.vocab = vocab;
+    a.temperature = 0.f;
+    a.top_p = 1.f;
+    a.top_k = 1;
+    if (sample) {
+        rng = ZigRandom::from_state(smp->rng);
         a.temperature = smp->temperature;
         a.top_p = smp->top_p;
         a.top_k = (int)(smp->top_k < 1 ? 1 : smp->top_k > (uint32_t)PICK_MAXK ? PICK_MAXK : smp->top_k);
-        a.seed = smp->seed;
     }
-    hipLaunchKernelGGL(pick_kernel, dim3((unsigned)n), dim3(1024), 0, s, a);
-    DITCH_TRY_HIP(hipGetLastError());
+    for (int64_t r0 = 0; r0 < n; r0 += PICK_ROWS) {
+        const int64_t rows = n - r0 < PICK_ROWS ? n - r0 : PICK_ROWS;
+        a.out = out + r0;
+        a.logits = logits + r0 * vocab;
+        for (int64_t i = 0; i < rows; i++) a.u[i] = sample ? rng.float64() : 0.0;
+        hipLaunchKernelGGL(pick_kernel, dim3((unsigned)rows), dim3(1024), 0, s, a);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
+    if (sample)
+        for (int i = 0; i < 4; i++) smp->rng[i] = rng.s[i];
+}
+
+void sampler_init(ditch_sampler *smp, uint64_t seed, float temperature, uint64_t top_k, float top_p) {
+    const ZigRandom rng(seed);
+    smp->temperature = temperature;
+    smp->top_k = (uint32_t)(top_k < 1 ? 1 : top_k > (uint64_t)PICK_MAXK ? PICK_MAXK : top_k);
+    smp->top_p = top_p;
+    smp->reserved = 0;
+    for (int i = 0; i < 4; i++) smp->rng[i] = rng.s[i];
 }
 
 // ---------------------------------------------------------------------------
 // the generation loop (generateKeep, model.zig:5378-5444)
 
 void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens, const uint64_t *lens, int64_t B,
-              int64_t max_new, const uint32_t *eos, int64_t n_eos, const ditch_sampler *smp, uint32_t *out_tokens,
+              int64_t max_new, const uint32_t *eos, int64_t n_eos, ditch_sampler *smp, uint32_t *out_tokens,
               uint64_t *out_lens, float *first_logits) {
     const ditch_model_config &c = m->c;
     hipStream_t s = m->h->stream;
@@ -258,17 +273,17 @@ void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens
         last[b] = (uint64_t)idx - 1;
     }
     const int64_t cap = total > B ? total : B;
-    DevBuf d_tok, d_rows, d_lr, d_log, d_pick, d_ids;
+    DevBuf d_tok, d_rows, d_lr, d_log, d_pick;
     uint32_t *dt = d_tok.get<uint32_t>(cap);
     ditch_row *dr = d_rows.get<ditch_row>(cap);
     uint64_t *dl = d_lr.get<uint64_t>(B);
     float *dlog = d_log.get<float>((size_t)B * V);
-    uint32_t *dp = d_pick.get<uint32_t>(B), *di = d_ids.get<uint32_t>(B);
+    uint32_t *dp = d_pick.get<uint32_t>(B);
     DITCH_TRY_HIP(hipMemcpyAsync(dt, tokens, total * 4, hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(dr, rows.data(), total * sizeof(ditch_row), hipMemcpyHostToDevice, s));
     DITCH_TRY_HIP(hipMemcpyAsync(dl, last.data(), B * 8, hipMemcpyHostToDevice, s));
     model_forward(m, dt, dr, total, kc->B, kc->T, nullptr, 0, nullptr, dl, B, dlog, kc);
-    launch_pick(dp, dlog, B, V, smp, 0, nullptr, s);
+    launch_pick(dp, dlog, B, V, smp, s);
     std::vector<uint32_t> picked(B), ids;
     DITCH_TRY_HIP(hipMemcpyAsync(picked.data(), dp, B * 4, hipMemcpyDeviceToHost, s));
     if (first_logits) DITCH_TRY_HIP(hipMemcpyAsync(first_logits, dlog, (size_t)B * V * 4, hipMemcpyDeviceToHost, s));
@@ -309,9 +324,8 @@ void generate(ditch_hip_model *m, ditch_hip_kv_cache *kc, const uint32_t *tokens
         DITCH_TRY_HIP(hipMemcpyAsync(dt, step_tok.data(), n * 4, hipMemcpyHostToDevice, s));
         DITCH_TRY_HIP(hipMemcpyAsync(dr, step_rows.data(), n * sizeof(ditch_row), hipMemcpyHostToDevice, s));
         DITCH_TRY_HIP(hipMemcpyAsync(dl, step_lr.data(), n * 8, hipMemcpyHostToDevice, s));
-        DITCH_TRY_HIP(hipMemcpyAsync(di, ids.data(), n * 4, hipMemcpyHostToDevice, s));
         model_forward(m, dt, dr, n, kc->B, kc->T, nullptr, 0, nullptr, dl, n, dlog, kc);
-        launch_pick(dp, dlog, n, V, smp, (uint64_t)step, di, s);
+        launch_pick(dp, dlog, n, V, smp, s);
         DITCH_TRY_HIP(hipMemcpyAsync(picked.data(), dp, n * 4, hipMemcpyDeviceToHost, s));
         DITCH_TRY_HIP(hipStreamSynchronize(s));
         for (int64_t i = 0; i < n; i++) {

@@ -375,8 +375,8 @@ void launch_layernorm(float *out, const float *x, const float *w, int64_t wlen, 
                       int64_t len, float eps, int one_plus, hipStream_t s);
 void launch_softmax_rows(float *x, int64_t n, int64_t len, hipStream_t s);
 // generate.hip
-void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, const ditch_sampler *smp,
-                 uint64_t step, const uint32_t *row_ids, hipStream_t s);
+void launch_pick(uint32_t *out, const float *logits, int64_t n, int64_t vocab, ditch_sampler *smp, hipStream_t s);
+void sampler_init(ditch_sampler *smp, uint64_t seed, float temperature, uint64_t top_k, float top_p);
 
 // edit.hip
 void edit_gaussian(float *out, size_t n, uint64_t seed);

@@ -414,8 +414,10 @@ class Model:
         self.dev.lib.ditch_hip_kv_cache_free(c)
 
     def generate(self, cache, prompts, max_new_tokens, eos=(), sampler=None, first_logits=False):
-        """generateKeep: prompts = list of token-id lists; returns (list of
-        generated token lists, first-token logits [prompts][vocab] or None)."""
+        """generateKeep: prompts = list of token-id lists; sampler = None
+        (greedy), a dict (a new Sampler) or an abi.Sampler (advanced in place
+        by its draws); returns (list of generated token lists, first-token
+        logits [prompts][vocab] or None)."""
         lens = np.array([len(p) for p in prompts], dtype=np.uint64)
         toks = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts]))
         B = len(prompts)
@@ -423,10 +425,10 @@ class Model:
         out_lens = np.zeros(B, dtype=np.uint64)
         eos_a = np.ascontiguousarray(eos, dtype=np.uint32)
         fl = np.empty((B, self.spec.config["vocab"]), dtype=np.float32) if first_logits else None
-        smp = None
-        if sampler is not None:
-            smp = abi.Sampler(sampler.get("temperature", 1.0), sampler.get("top_k", 50), sampler.get("top_p", 0.95),
-                              sampler.get("seed", 0))
+        smp = sampler
+        if isinstance(sampler, dict):
+            smp = abi.sampler(self.dev.lib, sampler.get("seed", 0), sampler.get("temperature", 1.0),
+                              sampler.get("top_k", 50), sampler.get("top_p", 0.95))
         self.dev.check(self.dev.lib.ditch_hip_generate(
             self.h, cache, _p(toks), _p(lens), B, max_new_tokens, _p(eos_a) if eos_a.size else None, eos_a.size,
             ctypes.byref(smp) if smp is not None else None, _p(out), _p(out_lens), _p(fl) if fl is not None else None))

@@ -558,32 +558,39 @@ int32_t ditch_hip_forward_cached(ditch_hip_model *m, ditch_hip_kv_cache *c,
                                  uint64_t n_logit, float *d_logits,
                                  uint64_t logits_bytes);
 /* model.Sampler (model.zig:5208-5264): temperature <= 0 is greedy; top_k is
- * clamped to 1..256. The draw is a uniform from splitmix64 of (seed, step,
- * prompt) (the reference draws from Zig's Xoshiro256 stream), so sampled
- * tokens follow the same distribution, not the same sequence.             */
+ * clamped to 1..256; rng is the state of the Sampler's
+ * std.Random.DefaultPrng (Xoshiro256++), set by ditch_hip_sampler_init
+ * (Sampler.init, model.zig:5216-5218). Every sampled pick takes one
+ * Random.float(f64) draw from it, in row order, so a sampler used for the
+ * same logits in the same order picks the reference's tokens.             */
 typedef struct ditch_sampler {
     float temperature;
     uint32_t top_k;
     float top_p;
-    uint64_t seed;
+    uint32_t reserved;
+    uint64_t rng[4];
 } ditch_sampler;
+/* Sampler.init(seed, temperature, top_k, top_p). Host only.               */
+int32_t ditch_hip_sampler_init(ditch_sampler *s, uint64_t seed, float temperature,
+                               uint64_t top_k, float top_p);
 /* The next token of each of n logit rows on the device: the first maximum
- * (argmax, model.zig:5194-5204) when `sampler` is NULL or greedy, else the
- * Sampler's pick. d_row_ids (may be NULL) names the prompt of each row.    */
+ * (argmax, model.zig:5194-5204) when `sampler` is NULL or greedy, else
+ * Sampler.pick of each row in order, advancing sampler->rng by the rows'
+ * draws (taken on the host when the call is made).                        */
 int32_t ditch_hip_pick_tokens_device(ditch_hip *h, uint32_t *d_out, const float *d_logits,
                                      uint64_t n, uint64_t vocab,
-                                     const ditch_sampler *sampler, uint64_t step,
-                                     const uint32_t *d_row_ids, void *stream);
+                                     ditch_sampler *sampler, void *stream);
 /* generateKeep: prefill of n_prompts prompts (tokens flattened, prompt_lens
  * each), then up to max_new_tokens tokens per prompt, a prompt stopping at
  * an EOS id or a full cache. Host buffers: out_tokens [n_prompts]
  * [max_new_tokens], out_lens [n_prompts], first_logits (NULL or
- * [n_prompts][vocab], the prefill's next-token logits).                    */
+ * [n_prompts][vocab], the prefill's next-token logits). A sampler's rng
+ * advances by one draw per sampled token, as the reference's does.        */
 int32_t ditch_hip_generate(ditch_hip_model *m, ditch_hip_kv_cache *c,
                            const uint32_t *tokens, const uint64_t *prompt_lens,
                            uint64_t n_prompts, uint64_t max_new_tokens,
                            const uint32_t *eos_ids, uint64_t n_eos,
-                           const ditch_sampler *sampler, uint32_t *out_tokens,
+                           ditch_sampler *sampler, uint32_t *out_tokens,
                            uint64_t *out_lens, float *first_logits);
 
 /* ------------------------------------------------------------------------ */
@@ -624,10 +631,8 @@ int32_t ditch_hip_model_edit_batch(ditch_hip_model *m,
  * iterations, abliterate.zig:282-349, 473-538), and the input-side
  * ablation that widens the delta by k (abliterate.zig:234-261). All passes
  * over W run on the device over the resident (quantised) weight.
- * The SVD's Gaussian test matrix is ditch_hip_edit_gaussian(q * cols, seed)
- * (splitmix64 of seed and index, Box-Muller): the reference draws its own
- * from Zig's Xoshiro256, so the two deltas agree to the SVD's accuracy,
- * not bit for bit.                                                          */
+ * The SVD's Gaussian test matrix is ditch_hip_edit_gaussian(q * cols, seed),
+ * the reference's own draws (abliterate.zig:474-479).                      */
 enum { DITCH_ROWNORM_NONE = 0, DITCH_ROWNORM_PRE = 1, DITCH_ROWNORM_FULL = 2 };
 typedef struct ditch_edit_options {
     int32_t row_normalization; /* DITCH_ROWNORM_*                              */
@@ -649,6 +654,10 @@ int32_t ditch_hip_edit_delta_ex(ditch_hip *h, float *a, uint64_t a_len, float *b
 int32_t ditch_hip_model_edit_ex(ditch_hip_model *m, int32_t layer, int32_t slot,
                                 int32_t expert, const float *v, uint64_t k,
                                 float weight, const ditch_edit_options *opts);
+/* The first n draws of Random.floatNorm(f32) from Zig's
+ * std.Random.DefaultPrng.init(seed) (Xoshiro256++ seeded by SplitMix64, the
+ * ziggurat normal): the full edit's test matrix, and, with seed ^
+ * 0x5eedd1ec7105, the sketch's (directions.zig:65-67). Host only.         */
 void ditch_hip_edit_gaussian(float *out, uint64_t n, uint64_t seed);
 
 /* ------------------------------------------------------------------------ */

@@ -1741,23 +1741,183 @@ int ref_basis(float *dirs, const float *first, const float *good_means, size_t e
  * abliterate.computeDelta / computeOutputDelta / ablateInputs /
  * DeltaOperator / randomizedSvd / jacobiEigen (abliterate.zig:223-538).    */
 
-static uint64_t splitmix64_ref(uint64_t x) {
-    x += 0x9E3779B97F4A7C15ull;
-    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
-    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
-    return x ^ (x >> 31);
+/* Zig's std.Random as the reference uses it (test oracle; Zig 0.16 std,
+ * the reference's minimum_zig_version, build.zig.zon): DefaultPrng is
+ * Xoshiro256++ whose state is four SplitMix64 outputs of the seed
+ * (lib/std/Random/Xoshiro256.zig, SplitMix64.zig); Random.float(f64) takes
+ * the exponent from a draw's leading zeros (lib/std/Random.zig); floatNorm
+ * is the 256-layer ziggurat of lib/std/Random/ziggurat.zig with
+ * r = 3.6541528853610088, v = 0.00492867323399. The reference draws from
+ * it in randomizedSvd (abliterate.zig:473-479), Sketch.init
+ * (directions.zig:65-67) and Sampler.pick (model.zig:5256).               */
+static uint64_t zig_splitmix(uint64_t *x) {
+    uint64_t z = (*x += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
 }
 
-/* The full mode's test matrix: standard normals from splitmix64 of the seed
- * and index, Box-Muller in f64 (the reference draws them from Zig's
- * Xoshiro256, abliterate.zig:476-481; any Gaussian start converges). */
+void ref_zig_init(uint64_t st[4], uint64_t seed) {
+    uint64_t x = seed;
+    st[0] = zig_splitmix(&x);
+    st[1] = zig_splitmix(&x);
+    st[2] = zig_splitmix(&x);
+    st[3] = zig_splitmix(&x);
+}
+
+static uint64_t zig_rotl(uint64_t x, unsigned k) { return (x << k) | (x >> (64 - k)); }
+
+uint64_t ref_zig_next(uint64_t st[4]) {
+    uint64_t out = zig_rotl(st[0] + st[3], 23) + st[0];
+    uint64_t t = st[1] << 17;
+    st[2] ^= st[0];
+    st[3] ^= st[1];
+    st[1] ^= st[2];
+    st[0] ^= st[3];
+    st[2] ^= t;
+    st[3] = zig_rotl(st[3], 45);
+    return out;
+}
+
+static unsigned zig_clz64(uint64_t x) { return x ? (unsigned)__builtin_clzll(x) : 64u; }
+
+double ref_zig_float64(uint64_t st[4]) {
+    uint64_t r = ref_zig_next(st);
+    uint64_t lz = zig_clz64(r);
+    if (lz >= 12) { /* the top 12 bits are zero: more draws extend the run */
+        lz = 12;
+        for (;;) {
+            uint64_t more = zig_clz64(ref_zig_next(st));
+            lz += more;
+            if (more != 64) break;
+            if (lz >= 1022) { lz = 1022; break; }
+        }
+    }
+    uint64_t bits = ((1022 - lz) << 52) | (r & ((1ull << 52) - 1));
+    double d;
+    memcpy(&d, &bits, sizeof d);
+    return d;
+}
+
+static double zig_norm_f(double x) { return exp(-x * x / 2.0); }
+
+static double zig_tx[257], zig_tf[257];
+static int zig_tables_ready;
+
+void ref_zig_norm_tables(double *x, double *f) {
+    if (!zig_tables_ready) {
+        const double r = 3.6541528853610088, v = 0.00492867323399;
+        zig_tx[0] = v / zig_norm_f(r);
+        zig_tx[1] = r;
+        for (int i = 2; i < 256; i++) {
+            double prev = zig_tx[i - 1];
+            zig_tx[i] = sqrt(-2.0 * log(v / prev + zig_norm_f(prev)));
+        }
+        zig_tx[256] = 0;
+        for (int i = 0; i < 257; i++) zig_tf[i] = zig_norm_f(zig_tx[i]);
+        zig_tables_ready = 1;
+    }
+    if (x) memcpy(x, zig_tx, sizeof zig_tx);
+    if (f) memcpy(f, zig_tf, sizeof zig_tf);
+}
+
+double ref_zig_norm(uint64_t st[4]) {
+    const double r = 3.6541528853610088;
+    ref_zig_norm_tables(NULL, NULL);
+    for (;;) {
+        uint64_t bits = ref_zig_next(st);
+        unsigned i = (unsigned)(bits & 255u);
+        uint64_t repr = (0x400ull << 52) | (bits >> 12); /* [2, 4) */
+        double u;
+        memcpy(&u, &repr, sizeof u);
+        u -= 3.0; /* [-1, 1) */
+        double x = u * zig_tx[i];
+        if (fabs(x) < zig_tx[i + 1]) return x;
+        if (i == 0) { /* the tail beyond r */
+            double tx = 1, ty = 0;
+            while (-2.0 * ty < tx * tx) {
+                tx = log(ref_zig_float64(st)) / r;
+                ty = log(ref_zig_float64(st));
+            }
+            return u < 0 ? tx - r : r - tx;
+        }
+        if (zig_tf[i + 1] + (zig_tf[i] - zig_tf[i + 1]) * ref_zig_float64(st) < zig_norm_f(x)) return x;
+    }
+}
+
+/* n draws of one kind (0 int(u64), 1 float(f64), 2 floatNorm(f64)) from
+ * DefaultPrng.init(seed) */
+void ref_zig_draws(void *out, size_t n, uint64_t seed, int kind) {
+    uint64_t st[4];
+    ref_zig_init(st, seed);
+    for (size_t i = 0; i < n; i++) {
+        if (kind == 0) ((uint64_t *)out)[i] = ref_zig_next(st);
+        else if (kind == 1) ((double *)out)[i] = ref_zig_float64(st);
+        else ((double *)out)[i] = ref_zig_norm(st);
+    }
+}
+
+/* The full mode's test matrix: Random.floatNorm(f32) draws of
+ * DefaultPrng.init(seed) in omega's order (abliterate.zig:474-479). */
 void ref_edit_gaussian(float *out, size_t n, uint64_t seed) {
-    for (size_t t = 0; t < n; t++) {
-        uint64_t r1 = splitmix64_ref(seed ^ (2 * (uint64_t)t) * 0xD1B54A32D192ED03ull);
-        uint64_t r2 = splitmix64_ref(seed ^ (2 * (uint64_t)t + 1) * 0xD1B54A32D192ED03ull);
-        double u1 = ((double)(r1 >> 11) + 1.0) * 0x1.0p-53;
-        double u2 = (double)(r2 >> 11) * 0x1.0p-53;
-        out[t] = (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+    uint64_t st[4];
+    ref_zig_init(st, seed);
+    for (size_t t = 0; t < n; t++) out[t] = (float)ref_zig_norm(st);
+}
+
+/* Sampler.pick (model.zig:5222-5263) for n rows in order, st the Sampler's
+ * DefaultPrng state (Sampler.init, model.zig:5216-5218), advanced. */
+void ref_sampler_pick(uint32_t *out, const float *logits, size_t n, size_t vocab, uint64_t st[4],
+                      float temperature, size_t top_k, float top_p) {
+    size_t kk = top_k < 1 ? 1 : top_k > 256 ? 256 : top_k;
+    for (size_t row = 0; row < n; row++) {
+        const float *x = logits + row * vocab;
+        if (temperature <= 0) { /* argmax: the first maximum */
+            size_t best = 0;
+            for (size_t i = 1; i < vocab; i++)
+                if (x[i] > x[best]) best = i;
+            out[row] = (uint32_t)best;
+            continue;
+        }
+        uint32_t ids[256];
+        float vals[256];
+        double probs[256];
+        size_t k = kk < vocab ? kk : vocab, m = 0;
+        for (size_t i = 0; i < vocab; i++) {
+            if (m < k) {
+                ids[m] = (uint32_t)i;
+                vals[m] = x[i];
+                m++;
+            } else if (x[i] > vals[m - 1]) {
+                ids[m - 1] = (uint32_t)i;
+                vals[m - 1] = x[i];
+            } else {
+                continue;
+            }
+            for (size_t j = m - 1; j > 0 && vals[j] > vals[j - 1]; j--) {
+                float tv = vals[j]; vals[j] = vals[j - 1]; vals[j - 1] = tv;
+                uint32_t ti = ids[j]; ids[j] = ids[j - 1]; ids[j - 1] = ti;
+            }
+        }
+        double total = 0;
+        for (size_t i = 0; i < m; i++) {
+            probs[i] = exp((double)(vals[i] - vals[0]) / (double)temperature);
+            total += probs[i];
+        }
+        size_t kept = 0;
+        double mass = 0;
+        while (kept < m) {
+            mass += probs[kept];
+            kept++;
+            if (mass >= (double)top_p * total) break;
+        }
+        double r = ref_zig_float64(st) * mass;
+        uint32_t id = ids[kept - 1];
+        for (size_t i = 0; i < kept; i++) {
+            r -= probs[i];
+            if (r <= 0) { id = ids[i]; break; }
+        }
+        out[row] = id;
     }
 }
 

@@ -12,6 +12,11 @@
  * 676-687), no other contraction (built with -ffp-contract=off), f64 where
  * the reference uses f64. The lane width of the dot products is VL = 16, the
  * reference's AVX-512 build (tensor.zig:628-669).
+ *
+ * Parity unpinned: ref_zig_float64's extra draws when a draw's top 12 bits
+ * are zero (Zig 0.16's Random.float, restated without a Zig toolchain to
+ * run it); the rest of the Zig stream is pinned by Zig's own sequence tests
+ * and the xoshiro256 jump polynomial.
  */
 #ifndef DITCH_CPU_REF_H
 #define DITCH_CPU_REF_H
@@ -110,6 +115,16 @@ int ref_basis(float *dirs, const float *first, const float *good_means, size_t e
  * 2 full (rank-r randomised SVD seeded by ref_edit_gaussian), optional
  * input-side ablation; a [rank][cols], b [rows][rank] (rank <= 64)         */
 void ref_edit_gaussian(float *out, size_t n, uint64_t seed);
+/* Zig's std.Random stream (DefaultPrng, float(f64), floatNorm) and the
+ * Sampler's pick over it                                                   */
+void ref_zig_init(uint64_t st[4], uint64_t seed);
+uint64_t ref_zig_next(uint64_t st[4]);
+double ref_zig_float64(uint64_t st[4]);
+double ref_zig_norm(uint64_t st[4]);
+void ref_zig_norm_tables(double *x, double *f);
+void ref_zig_draws(void *out, size_t n, uint64_t seed, int kind);
+void ref_sampler_pick(uint32_t *out, const float *logits, size_t n, size_t vocab, uint64_t st[4],
+                      float temperature, size_t top_k, float top_p);
 void ref_jacobi_f32(float *m, float *vecs, size_t n);
 int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_weight *w, const float *v, size_t k,
                       float weight, int mode, size_t lora_rank, uint64_t seed, int ablate, int threads);

@@ -58,6 +58,10 @@ PROTOS = {
     "ref_symmetric_eigen": (None, [P, P, SZ]),
     "ref_basis": (ctypes.c_int, [P, P, P, SZ, SZ, SZ, ctypes.c_int, P, P, SZ]),
     "ref_edit_gaussian": (None, [P, SZ, U64]),
+    "ref_zig_init": (None, [P, U64]),
+    "ref_zig_draws": (None, [P, SZ, U64, ctypes.c_int]),
+    "ref_zig_norm_tables": (None, [P, P]),
+    "ref_sampler_pick": (None, [P, P, SZ, SZ, P, FLT, SZ, FLT]),
     "ref_jacobi_f32": (None, [P, P, SZ]),
     "ref_edit_delta_ex": (ctypes.c_int, [P, P, P, P, P, SZ, FLT, ctypes.c_int, SZ, U64, ctypes.c_int, ctypes.c_int]),
 }
@@ -270,6 +274,33 @@ class Ref:
     def edit_gaussian(self, n, seed):
         out = np.empty(n, dtype=np.float32)
         self.lib.ref_edit_gaussian(_p(out), n, seed)
+        return out
+
+    def zig_draws(self, n, seed, kind):
+        """n draws of Zig's DefaultPrng.init(seed): kind 'u64' (int(u64)),
+        'f64' (float(f64)) or 'norm' (floatNorm(f64))."""
+        k = {"u64": 0, "f64": 1, "norm": 2}[kind]
+        out = np.empty(n, dtype=np.uint64 if k == 0 else np.float64)
+        self.lib.ref_zig_draws(_p(out), n, seed, k)
+        return out
+
+    def zig_norm_tables(self):
+        x, f = np.empty(257), np.empty(257)
+        self.lib.ref_zig_norm_tables(_p(x), _p(f))
+        return x, f
+
+    def sampler_init(self, seed):
+        """Sampler.init's DefaultPrng state (4 x u64)."""
+        st = np.empty(4, dtype=np.uint64)
+        self.lib.ref_zig_init(_p(st), seed)
+        return st
+
+    def sampler_pick(self, logits, state, temperature, top_k, top_p):
+        """Sampler.pick of each row in order; `state` advances in place."""
+        logits = _f32(logits)
+        n, V = logits.shape
+        out = np.empty(n, dtype=np.uint32)
+        self.lib.ref_sampler_pick(_p(out), _p(logits), n, V, _p(state), temperature, top_k, top_p)
         return out
 
     def jacobi_f32(self, m):

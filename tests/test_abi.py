@@ -31,11 +31,11 @@ def test_struct_layouts_match_the_header():
 #include <stddef.h>
 #include "ditch_hip.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(ditch_weight), sizeof(ditch_model_config), sizeof(ditch_row),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(ditch_weight), sizeof(ditch_model_config), sizeof(ditch_row),
          offsetof(ditch_model_config, moe_layers), offsetof(ditch_weight, g_idx), sizeof(ditch_expert_cache_stats),
          sizeof(ditch_edit_options), offsetof(ditch_edit_options, seed), sizeof(ditch_model_path_stats),
          sizeof(ditch_residency_stats), sizeof(ditch_hot_expert), sizeof(ditch_edit_target),
-         offsetof(ditch_edit_target, v));
+         offsetof(ditch_edit_target, v), sizeof(ditch_sampler), offsetof(ditch_sampler, rng));
   return 0;
 }
 """
@@ -50,7 +50,7 @@ int main(void) {
                    abi.ModelConfig.moe_layers.offset, abi.Weight.g_idx.offset, ctypes.sizeof(abi.ExpertCacheStats),
                    ctypes.sizeof(abi.EditOptions), abi.EditOptions.seed.offset, ctypes.sizeof(abi.PathStats),
                    ctypes.sizeof(abi.ResidencyStats), ctypes.sizeof(abi.HotExpert), ctypes.sizeof(abi.EditTarget),
-                   abi.EditTarget.v.offset]
+                   abi.EditTarget.v.offset, ctypes.sizeof(abi.Sampler), abi.Sampler.rng.offset]
 
 
 def test_open_without_a_gpu_fails_cleanly():

@@ -22,6 +22,16 @@ from test_oracle_edit import MODES, exact_full, materialize, orthonormal_rows
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("seed", [0, 9, (1 << 63) + 5])
+def test_edit_gaussian_is_the_oracle_stream(dev, ref, seed):
+    """The full edit's test matrix: Zig's floatNorm(f32) stream of
+    DefaultPrng.init(seed), bit for bit the oracle's."""
+    n = 200000
+    out = np.empty(n, dtype=np.float32)
+    dev.lib.ditch_hip_edit_gaussian(out.ctypes.data, n, seed)
+    np.testing.assert_array_equal(out, ref.edit_gaussian(n, seed))
+
+
 @pytest.mark.parametrize("k", [1, 2])
 @pytest.mark.parametrize("mode", ["none", "pre", "full"])
 def test_device_edit_reference_invariants_6x5(dev, k, mode):

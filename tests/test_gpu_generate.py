@@ -1,6 +1,7 @@
 """Generation on the device (generateKeep, model.zig:5378-5444): the token
-picker against the reference's sampler test (model.zig:5270-5286) and
-numpy's top-k / top-p distribution, the persistent KV cache against the
+picker against the reference's sampler test (model.zig:5270-5286),
+numpy's top-k / top-p distribution and the oracle's Sampler over the same
+Zig random stream (token for token), the persistent KV cache against the
 one-shot forward, greedy generation checked against the oracle by teacher
 forcing (each generated token is the oracle's most likely next token, up to
 near-ties at the logit tolerance), EOS and full-cache stops, and seeded
@@ -16,18 +17,20 @@ from oracle.ref import RefModel
 pytestmark = pytest.mark.gpu
 
 
-def pick(dev, logits, sampler=None, step=0, row_ids=None):
+def make_sampler(dev, sampler):
+    return abi.sampler(dev.lib, sampler.get("seed", 0), sampler["temperature"], sampler["top_k"], sampler["top_p"])
+
+
+def pick(dev, logits, sampler=None):
+    """Device picks of the rows in order; `sampler` a dict (a new Sampler)
+    or an abi.Sampler (advanced in place)."""
+    import ctypes
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     n, V = logits.shape
     bl, bo = hipmem.Buffer.from_array(logits), hipmem.Buffer(n * 4)
-    bi = hipmem.Buffer.from_array(np.asarray(row_ids, dtype=np.uint32)) if row_ids is not None else None
-    smp = None
-    if sampler is not None:
-        smp = abi.Sampler(sampler["temperature"], sampler["top_k"], sampler["top_p"], sampler.get("seed", 0))
-    import ctypes
+    smp = make_sampler(dev, sampler) if isinstance(sampler, dict) else sampler
     dev.check(dev.lib.ditch_hip_pick_tokens_device(dev.h, bo.ptr, bl.ptr, n, V,
-                                                   ctypes.byref(smp) if smp is not None else None, step,
-                                                   bi.ptr if bi is not None else None, None))
+                                                   ctypes.byref(smp) if smp is not None else None, None))
     dev.sync()
     return bo.download(np.uint32, (n,))
 
@@ -76,12 +79,38 @@ def test_sampling_distribution_matches_numpy(dev, top_k, top_p, temp):
     kept = min(kept, top_k)
     probs = p[:kept] / p[:kept].sum()
     n = 20000
-    got = pick(dev, np.tile(row, (n, 1)), {"temperature": temp, "top_k": top_k, "top_p": top_p, "seed": 3},
-               row_ids=np.arange(n))
+    got = pick(dev, np.tile(row, (n, 1)), {"temperature": temp, "top_k": top_k, "top_p": top_p, "seed": 3})
     allowed = set(order[:kept].tolist())
     assert set(got.tolist()) <= allowed
     freq = np.array([(got == t).mean() for t in order[:kept]])
     assert np.abs(freq - probs).max() < 0.02
+
+
+@pytest.mark.parametrize("top_k,top_p,temp", [(40, 0.9, 0.8), (256, 1.0, 1.5), (1, 1.0, 1.0)])
+def test_pick_matches_the_oracle_sampler(dev, ref, top_k, top_p, temp):
+    """The Sampler's picks, token for token, against the oracle's Sampler
+    over the same Zig stream: 300 rows (two launches), one call of 300 and
+    calls of 120 + 180 rows continuing one sampler; the samplers' states
+    agree afterwards."""
+    rng = np.random.default_rng(top_k)
+    logits = (rng.standard_normal((300, 32000)) * 3).astype(np.float32)
+    st = ref.sampler_init(21)
+    want = ref.sampler_pick(logits, st, temp, top_k, top_p)
+    cfg = {"temperature": temp, "top_k": top_k, "top_p": top_p, "seed": 21}
+    s1 = make_sampler(dev, cfg)
+    np.testing.assert_array_equal(pick(dev, logits, s1), want)
+    assert list(s1.rng) == [int(x) for x in st]
+    s2 = make_sampler(dev, cfg)
+    got = np.concatenate([pick(dev, logits[:120], s2), pick(dev, logits[120:], s2)])
+    np.testing.assert_array_equal(got, want)
+    assert list(s2.rng) == list(s1.rng)
+
+
+def test_greedy_pick_draws_nothing(dev):
+    s = make_sampler(dev, {"temperature": 0.0, "top_k": 50, "top_p": 1.0, "seed": 4})
+    before = list(s.rng)
+    pick(dev, np.random.default_rng(0).standard_normal((5, 100)).astype(np.float32), s)
+    assert list(s.rng) == before
 
 
 def _teacher_forcing_ok(ref, spec, prompts, outs):
@@ -201,3 +230,72 @@ def test_sampled_generation_is_seeded(dev):
     finally:
         gm.kv_cache_free(cache)
         gm.free()
+
+
+def test_sampled_generation_matches_the_oracle_sampler(dev, ref):
+    """generateKeep with a Sampler (model.zig:5378-5444): the oracle's logits
+    at every generated position (teacher forcing on the device's tokens),
+    picked by the oracle's Sampler over the same Zig stream in the
+    reference's order (prompt order within a step), give the device's
+    tokens, up to what the logit tolerance leaves open (near-equal logits
+    that sort either way: at least 90 % of the picks are exact); the
+    caller's sampler ends where the oracle's does."""
+    spec = GEN_MODELS["dense_mxfp4"]()
+    rng = np.random.default_rng(12)
+    prompts = [list(rng.integers(0, 3000, n)) for n in (6, 12, 9)]
+    steps = 10
+    cfg = {"temperature": 0.9, "top_k": 40, "top_p": 0.95, "seed": 77}
+    gm = Model(dev, spec)
+    cache = gm.kv_cache(3, 64)
+    try:
+        smp = make_sampler(dev, cfg)
+        outs, _ = gm.generate(cache, prompts, steps, sampler=smp)
+    finally:
+        gm.kv_cache_free(cache)
+        gm.free()
+    assert [len(o) for o in outs] == [steps] * 3
+    cm = RefModel(spec)
+    try:
+        per_prompt = []
+        for p, gen in zip(prompts, outs):
+            seq = list(p) + list(gen[:-1])
+            rows = [(0, i) for i in range(len(seq))]
+            _, lc = cm.forward(np.asarray(seq, np.uint32), rows, logit_rows=list(range(len(p) - 1, len(seq))))
+            per_prompt.append(lc)
+    finally:
+        cm.free()
+    st = ref.sampler_init(cfg["seed"])
+    draws = ref.zig_draws(3 * steps, cfg["seed"], "f64")  # one float(f64) per pick
+    exact = 0
+    for t in range(steps):
+        rows = np.stack([per_prompt[b][t] for b in range(3)])
+        want = ref.sampler_pick(rows, st, cfg["temperature"], cfg["top_k"], cfg["top_p"])
+        for b in range(3):
+            got = outs[b][t]
+            exact += got == want[b]
+            assert got in _near_picks(rows[b], draws[3 * t + b], cfg), (t, b, got, want[b])
+    assert exact >= 0.9 * 3 * steps, exact
+    assert list(smp.rng) == [int(x) for x in st]
+
+
+def _near_picks(x, u, cfg):
+    """Sampler.pick's token for the draw u over logits x, and every token a
+    perturbation of x within the logit tolerance (1e-3 of max |logit|) can
+    give instead: near-equal logits that may sort either way, and the
+    neighbours of a cumulative boundary the draw lies within the tolerance
+    of."""
+    tol = 1e-3 * float(np.abs(x).max())
+    order = np.argsort(-x.astype(np.float64), kind="stable")[:cfg["top_k"]]
+    vals = x[order]
+    p = np.exp((vals - vals[0]).astype(np.float64) / cfg["temperature"])
+    cs = np.cumsum(p)
+    kept = int(np.searchsorted(cs, cfg["top_p"] * cs[-1], side="left")) + 1
+    r = u * cs[kept - 1]
+    i = min(int(np.searchsorted(cs[:kept], r, side="left")), kept - 1)
+    near = {int(order[i])}
+    near |= {int(order[j]) for j in range(len(order)) if abs(float(vals[j]) - float(vals[i])) <= 2 * tol}
+    slack = 4 * tol / cfg["temperature"] * cs[kept - 1]
+    for j in (i - 1, i + 1):
+        if 0 <= j < len(order) and (abs(cs[i] - r) <= slack or (i > 0 and abs(cs[i - 1] - r) <= slack)):
+            near.add(int(order[j]))
+    return near
