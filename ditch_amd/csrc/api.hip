@@ -955,7 +955,7 @@ int32_t ditch_hip_basis_device(ditch_hip *h, float *d_dirs, const float *d_first
     return guarded(h, [&] {
         DITCH_CHECK(d_dirs && d_first && d_good_means && (k <= 1 || (d_y && d_w)), DITCH_INVALID_ARGUMENT,
                     "NULL argument");
-        DITCH_CHECK(k >= 1 && k <= 8, DITCH_UNSUPPORTED, "basis: 1 to 8 directions");
+        DITCH_CHECK(k >= 1, DITCH_INVALID_ARGUMENT, "basis: no directions");
         DITCH_CHECK(entries <= 65535, DITCH_UNSUPPORTED, "basis: more than 65535 entries");
         launch_basis(d_dirs, d_first, d_good_means, (int64_t)entries, (int64_t)hidden, (int64_t)k, orthogonalize, d_y,
                      d_w, (int64_t)m, pick(h, stream), &h->dirtmp);

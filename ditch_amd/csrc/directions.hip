@@ -19,7 +19,7 @@
 namespace ditch {
 
 constexpr int DIR_MAX_HIDDEN = 16384;  // |v| keys of one vector in LDS
-constexpr int DIR_MAX_M = 32;          // sketch width (4 x 8 directions)
+constexpr int DIR_LDS_M = 96;          // sketch widths whose basis works in LDS
 
 // ---------------------------------------------------------------------------
 // block reductions (blockDim.x a multiple of 64, at most 1024)
@@ -221,7 +221,8 @@ __global__ void sketch_accum_kernel(double *y, double *w, const double *proj, in
 // Basis (Sketch.factor + computeBasisFrom), one block per entry
 
 // directions.symmetricEigen (directions.zig:463-500): cyclic Jacobi in f64 on
-// an n x n matrix in LDS (overwritten by its diagonalisation), eigenvectors
+// an n x n matrix in LDS or global memory (overwritten by its
+// diagonalisation), eigenvectors
 // in the columns of vecs; the rotation's rows and columns are updated by the
 // block's threads in the reference's operation order.
 __device__ void dir_symmetric_eigen(double *mat, double *vecs, int n, double *flag) {
@@ -251,8 +252,7 @@ __device__ void dir_symmetric_eigen(double *mat, double *vecs, int n, double *fl
                 const double t = theta == 0 ? 1.0 : sg / (fabs(theta) + sqrt(theta * theta + 1.0));
                 const double cs = 1.0 / sqrt(t * t + 1.0), sn = t * cs;
                 __syncthreads();  // every thread has read the pivot before it changes
-                if (tid < n) {
-                    const int k = tid;
+                for (int k = tid; k < n; k += blockDim.x) {
                     const double akp = mat[k * n + p], akq = mat[k * n + q];
                     mat[k * n + p] = cs * akp - sn * akq;
                     mat[k * n + q] = sn * akp + cs * akq;
@@ -261,8 +261,7 @@ __device__ void dir_symmetric_eigen(double *mat, double *vecs, int n, double *fl
                     vecs[k * n + q] = sn * vkp + cs * vkq;
                 }
                 __syncthreads();
-                if (tid < n) {
-                    const int k = tid;
+                for (int k = tid; k < n; k += blockDim.x) {
                     const double apk = mat[p * n + k], aqk = mat[q * n + k];
                     mat[p * n + k] = cs * apk - sn * aqk;
                     mat[q * n + k] = sn * apk + cs * aqk;
@@ -283,15 +282,21 @@ struct BasisArgs {
     float *gd;             // scratch [entries][hidden]
     int64_t hidden, k, m;
     int orthogonalize;
+    // the sketch's m x m matrices and index lists: in dynamic LDS (lds = 1)
+    // or, for wide sketches, per entry in `work` (2 m^2 doubles + 2 m ints)
+    int lds;
+    double *work;
 };
 
 __global__ __launch_bounds__(256) void basis_kernel(BasisArgs a) {
-    __shared__ double wm[DIR_MAX_M * DIR_MAX_M], vecs[DIR_MAX_M * DIR_MAX_M];
+    extern __shared__ double dir_dyn[];
     __shared__ double sh[16], flag[1];
-    __shared__ int valid[DIR_MAX_M], order[DIR_MAX_M];
     __shared__ int r_sh;
     const int64_t e = blockIdx.x, H = a.hidden, K = a.k;
     const int m = (int)a.m, tid = threadIdx.x;
+    double *wm = a.lds ? dir_dyn : a.work + e * (2 * a.m * a.m + a.m);
+    double *vecs = wm + m * m;
+    int *valid = (int *)(vecs + m * m), *order = valid + m;
     float *basis = a.dirs + e * K * H;
     float *gd = a.gd + e * H;
     double *bf = a.bf + e * a.m * H;
@@ -455,7 +460,7 @@ void launch_directions(float *dirs, const float *good, const float *bad, int64_t
 void launch_sketch_add(double *y, double *w, const float *omega, int64_t m, const float *center, const float *v,
                        int64_t prompts, int64_t entries, int64_t hidden, hipStream_t s, DevBuf *tmp) {
     if (prompts <= 0 || entries <= 0) return;
-    DITCH_CHECK(m >= 1 && m <= DIR_MAX_M, DITCH_UNSUPPORTED, "sketch: width above 32");
+    DITCH_CHECK(m >= 1, DITCH_INVALID_ARGUMENT, "sketch: width 0");
     double *proj = tmp->get<double>((size_t)(prompts * entries * m));
     hipLaunchKernelGGL(sketch_proj_kernel, dim3((unsigned)prompts, (unsigned)entries), dim3(256), 0, s, proj, omega,
                        m, center, v, entries, hidden);
@@ -468,14 +473,27 @@ void launch_sketch_add(double *y, double *w, const float *omega, int64_t m, cons
 void launch_basis(float *dirs, const float *first, const float *good, int64_t entries, int64_t hidden, int64_t k,
                   int orthogonalize, const double *y, const double *w, int64_t m, hipStream_t s, DevBuf *tmp) {
     if (entries <= 0) return;
-    DITCH_CHECK(k >= 1 && m >= 1 && m <= DIR_MAX_M, DITCH_UNSUPPORTED, "basis: sketch width above 32");
+    DITCH_CHECK(k >= 1 && m >= 1, DITCH_INVALID_ARGUMENT, "basis: no directions or an empty sketch");
+    DITCH_CHECK(m <= 46340, DITCH_UNSUPPORTED, "basis: sketch width above 46340");
     if (k == 1) {
         DITCH_TRY_HIP(hipMemcpyAsync(dirs, first, (size_t)(entries * hidden) * 4, hipMemcpyDeviceToDevice, s));
         return;
     }
-    double *bf = tmp->get<double>((size_t)(entries * m * hidden + (entries * hidden + 1) / 2));
-    BasisArgs a{dirs, first, good, y, w, bf, (float *)(bf + entries * m * hidden), hidden, k, m, orthogonalize};
-    hipLaunchKernelGGL(basis_kernel, dim3((unsigned)entries), dim3(256), 0, s, a);
+    // per entry: 2 m^2 doubles and 2 m ints (m doubles' room) of eigen-solver state
+    const int64_t per = 2 * m * m + m;
+    const bool lds = m <= DIR_LDS_M;
+    double *bf = tmp->get<double>((size_t)(entries * m * hidden + (entries * hidden + 1) / 2 + (lds ? 0 : entries * per)));
+    BasisArgs a{dirs, first, good, y, w, bf, (float *)(bf + entries * m * hidden), hidden, k, m, orthogonalize,
+                lds ? 1 : 0, lds ? nullptr : bf + entries * m * hidden + (entries * hidden + 1) / 2};
+    const size_t shmem = lds ? (size_t)per * 8 : 0;
+    if (lds) {
+        static const bool attr = [] {
+            return hipFuncSetAttribute((const void *)basis_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (2 * DIR_LDS_M * DIR_LDS_M + DIR_LDS_M) * 8) == hipSuccess;
+        }();
+        DITCH_CHECK(attr, DITCH_DEVICE_FAILED, "basis: the kernel's LDS size was refused");
+    }
+    hipLaunchKernelGGL(basis_kernel, dim3((unsigned)entries), dim3(256), shmem, s, a);
     DITCH_TRY_HIP(hipGetLastError());
     hipLaunchKernelGGL(orient_kernel, dim3(1), dim3(1024), 0, s, dirs, entries, k, hidden);
     DITCH_TRY_HIP(hipGetLastError());

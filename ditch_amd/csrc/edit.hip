@@ -237,18 +237,22 @@ __global__ __launch_bounds__(1024) void edit_orth_reg_kernel(float *vecs, int64_
     }
 }
 
-constexpr int ED_MAXQ = 64;
+// SVD widths up to ED_LDS_Q keep the Jacobi's two q x q matrices in LDS;
+// wider ones work on them in place in global memory.
+constexpr int ED_LDS_Q = 128;
 
 // abliterate.jacobiEigen (abliterate.zig:427-469): cyclic Jacobi in f32 on the
 // q x q matrix m (in place: its diagonal ends as the eigenvalues),
 // eigenvectors in the columns of vecs. One block; the rotation's updates
 // are spread over the block's threads in the reference's order.
-__global__ __launch_bounds__(256) void edit_jacobi_kernel(float *m_g, float *vecs_g, int n) {
-    __shared__ float m[ED_MAXQ * ED_MAXQ], vecs[ED_MAXQ * ED_MAXQ];
+template <bool LDS>
+__global__ __launch_bounds__(1024) void edit_jacobi_kernel(float *m_g, float *vecs_g, int n) {
+    extern __shared__ float ed_dyn[];
     __shared__ int stop;
-    const int tid = threadIdx.x;
-    for (int t = tid; t < n * n; t += blockDim.x) {
-        m[t] = m_g[t];
+    float *m = LDS ? ed_dyn : m_g, *vecs = LDS ? ed_dyn + n * n : vecs_g;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int t = tid; t < n * n; t += nt) {
+        if (LDS) m[t] = m_g[t];
         vecs[t] = (t / n == t % n) ? 1.f : 0.f;
     }
     __syncthreads();
@@ -274,8 +278,7 @@ __global__ __launch_bounds__(256) void edit_jacobi_kernel(float *m_g, float *vec
                 const float cs = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fmul_rn(tf, tf), 1.0f)));
                 const float sn = __fmul_rn(tf, cs);
                 __syncthreads();  // every thread has read the pivot before it changes
-                if (tid < n) {
-                    const int k = tid;
+                for (int k = tid; k < n; k += nt) {
                     const float akp = m[k * n + p], akq = m[k * n + q];
                     m[k * n + p] = __fsub_rn(__fmul_rn(cs, akp), __fmul_rn(sn, akq));
                     m[k * n + q] = __fadd_rn(__fmul_rn(sn, akp), __fmul_rn(cs, akq));
@@ -284,8 +287,7 @@ __global__ __launch_bounds__(256) void edit_jacobi_kernel(float *m_g, float *vec
                     vecs[k * n + q] = __fadd_rn(__fmul_rn(sn, vkp), __fmul_rn(cs, vkq));
                 }
                 __syncthreads();
-                if (tid < n) {
-                    const int k = tid;
+                for (int k = tid; k < n; k += nt) {
                     const float apk = m[p * n + k], aqk = m[q * n + k];
                     m[p * n + k] = __fsub_rn(__fmul_rn(cs, apk), __fmul_rn(sn, aqk));
                     m[q * n + k] = __fadd_rn(__fmul_rn(sn, apk), __fmul_rn(cs, aqk));
@@ -294,10 +296,11 @@ __global__ __launch_bounds__(256) void edit_jacobi_kernel(float *m_g, float *vec
             }
     }
     __syncthreads();
-    for (int t = tid; t < n * n; t += blockDim.x) {
-        m_g[t] = m[t];
-        vecs_g[t] = vecs[t];
-    }
+    if (LDS)
+        for (int t = tid; t < n * n; t += nt) {
+            m_g[t] = m[t];
+            vecs_g[t] = vecs[t];
+        }
 }
 
 // The SVD's factors and the LoRA pair (abliterate.zig:514-547): eigenvalues
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(256) void edit_svd_out_kernel(float *a, float *b, c
                                                            const float *evecs, const float *qy, const float *bt,
                                                            int q, int64_t rows, int64_t cols, int64_t rank,
                                                            int64_t ldb, int64_t b_off) {
-    __shared__ int order[ED_MAXQ];
+    extern __shared__ int order[];  // q entries
     const int t = blockIdx.x;
     if (threadIdx.x == 0) {
         for (int i = 0; i < q; i++) order[i] = i;
@@ -423,6 +426,23 @@ static void edit_orth(float *vecs, int64_t q, int64_t n, hipStream_t s) {
     DITCH_TRY_HIP(hipGetLastError());
 }
 
+static void edit_jacobi(float *m, float *vecs, int64_t q, hipStream_t s) {
+    DITCH_CHECK(q <= 46340, DITCH_UNSUPPORTED, "edit: SVD width above 46340");
+    const dim3 block(q <= 256 ? 256 : 1024);
+    if (q <= ED_LDS_Q) {
+        static const bool attr = [] {
+            return hipFuncSetAttribute((const void *)edit_jacobi_kernel<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       2 * ED_LDS_Q * ED_LDS_Q * 4) == hipSuccess;
+        }();
+        DITCH_CHECK(attr, DITCH_DEVICE_FAILED, "edit: the Jacobi kernel's LDS size was refused");
+        hipLaunchKernelGGL(edit_jacobi_kernel<true>, dim3(1), block, (size_t)(2 * q * q * 4), s, m, vecs, (int)q);
+    } else {
+        hipLaunchKernelGGL(edit_jacobi_kernel<false>, dim3(1), block, 0, s, m, vecs, (int)q);
+    }
+    DITCH_TRY_HIP(hipGetLastError());
+}
+
 static void edit_dots(float *out, const float *p, int64_t np, const float *x, int64_t nx, int64_t len, hipStream_t s) {
     hipLaunchKernelGGL(edit_dots_kernel, dim3((unsigned)np, (unsigned)nx), dim3(256), 0, s, out, p, x, np, len);
     DITCH_TRY_HIP(hipGetLastError());
@@ -435,14 +455,13 @@ void edit_delta_device(ditch_hip *h, const TileView &w, const float *hv, int64_t
                        int64_t lora_rank, uint64_t seed, int ablate, hipStream_t s, float **da_out, float **db_out,
                        int64_t *rank_out) {
     const int64_t rows = w.rows, cols = w.cols;
-    DITCH_CHECK(k >= 1 && k <= 16 && mode >= 0 && mode <= 2, DITCH_INVALID_ARGUMENT, "edit: 1..16 directions, mode 0..2");
+    DITCH_CHECK(k >= 1 && mode >= 0 && mode <= 2, DITCH_INVALID_ARGUMENT, "edit: at least one direction, mode 0..2");
     if (!h->edit_work) h->edit_work = std::make_shared<EditWork>();
     EditWork &W = *static_cast<EditWork *>(h->edit_work.get());
     float *v = W.v.get<float>(k * rows);
     DITCH_TRY_HIP(hipMemcpyAsync(v, hv, k * rows * 4, hipMemcpyHostToDevice, s));
     const int64_t rank = edit_rank(rows, cols, k, mode, lora_rank, ablate);
     const int64_t r_out = rank - (ablate ? k : 0);  // the output-side edit's rank
-    DITCH_CHECK(rank <= 64, DITCH_UNSUPPORTED, "edit: delta rank above 64");
     float *A = (float *)dev_alloc(rank * cols * 4), *B = (float *)dev_alloc(rows * rank * 4);
     try {
         // the output-side B, [rows][r_out] (a separate buffer when the input
@@ -479,7 +498,6 @@ void edit_delta_device(ditch_hip *h, const TileView &w, const float *hv, int64_t
             int64_t q = 2 * rr + 4;
             q = q < rows ? q : rows;
             q = q < cols ? q : cols;
-            DITCH_CHECK(q <= ED_MAXQ, DITCH_UNSUPPORTED, "edit: SVD width above 64");
             std::vector<float> om((size_t)(q * cols));
             edit_gaussian(om.data(), om.size(), seed);
             float *omega = W.omega.get<float>(q * cols);
@@ -513,10 +531,9 @@ void edit_delta_device(ditch_hip *h, const TileView &w, const float *hv, int64_t
             applyT(qx, qy);  // B^T = (Q^T D)^T
             float *bbt = W.bbt.get<float>(q * q), *evecs = W.evecs.get<float>(q * q);
             edit_dots(bbt, qx, q, qx, q, cols, s);
-            hipLaunchKernelGGL(edit_jacobi_kernel, dim3(1), dim3(256), 0, s, bbt, evecs, (int)q);
-            DITCH_TRY_HIP(hipGetLastError());
-            hipLaunchKernelGGL(edit_svd_out_kernel, dim3((unsigned)r_out), dim3(256), 0, s, A, Bp, bbt, evecs, qy, qx,
-                               (int)q, rows, cols, r_out, r_out, (int64_t)0);
+            edit_jacobi(bbt, evecs, q, s);
+            hipLaunchKernelGGL(edit_svd_out_kernel, dim3((unsigned)r_out), dim3(256), (size_t)q * 4, s, A, Bp, bbt,
+                               evecs, qy, qx, (int)q, rows, cols, r_out, r_out, (int64_t)0);
             DITCH_TRY_HIP(hipGetLastError());
         }
         if (ablate) {

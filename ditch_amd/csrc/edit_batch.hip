@@ -307,7 +307,7 @@ void check_edit_slot(int slot);                                          // mode
 void model_edit(ditch_hip_model *m, int layer, int slot, int expert, const float *v, uint64_t k, float weight);
 
 void model_edit_batch(ditch_hip_model *m, const ditch_edit_target *targets, uint64_t n, uint64_t k) {
-    DITCH_CHECK(targets && n > 0 && k >= 1 && k <= 64, DITCH_INVALID_ARGUMENT, "edit batch arguments");
+    DITCH_CHECK(targets && n > 0 && k >= 1 && k <= (uint64_t)INT32_MAX, DITCH_INVALID_ARGUMENT, "edit batch arguments");
     hipStream_t s = m->h->stream;
     // the resident matrices go through the grouped product; a streamed
     // expert's blob is staged on the device one matrix at a time

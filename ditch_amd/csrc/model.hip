@@ -923,7 +923,7 @@ void model_set_delta(ditch_hip_model *m, int layer, int slot, int expert, uint64
     if (rank > 0) check_delta_slot(slot);
     Mat *mt = mat_slot(m, layer, slot, expert);
     DITCH_CHECK(mt->ok(), DITCH_INVALID_ARGUMENT, "delta on an empty slot");
-    DITCH_CHECK(rank <= 64, DITCH_UNSUPPORTED, "delta rank above 64");
+    DITCH_CHECK(rank <= (uint64_t)INT32_MAX, DITCH_UNSUPPORTED, "delta rank above 2^31");
     mt->clear_delta();
     if (rank == 0) return;
     hipStream_t s = m->h->stream;

@@ -640,7 +640,7 @@ typedef struct ditch_edit_options {
     uint64_t seed;             /* `full`: the test matrix's seed                */
     int32_t ablate_inputs;     /* nonzero: the input-side ablation as well      */
 } ditch_edit_options;
-/* Rank of the delta for a rows x cols matrix and k directions (<= 64).     */
+/* Rank of the delta for a rows x cols matrix and k directions.            */
 uint64_t ditch_hip_edit_rank(uint64_t rows, uint64_t cols, uint64_t k,
                              const ditch_edit_options *opts);
 /* Host buffers: a [rank][cols], b [rows][rank] with rank = ditch_hip_edit_rank
@@ -718,7 +718,8 @@ int32_t ditch_hip_directions_device(ditch_hip *h, float *d_dirs, const float *d_
  * residuals d_v [prompts][entries][hidden] (ditch_hip_residual_reduce's
  * d_vout): z = v - center, p = Omega^T z, Y += z p^T, W += p p^T in f64.
  * d_y [entries][m][hidden], d_w [entries][m][m], d_omega [m][hidden] (the
- * caller's Gaussian test matrix), m <= 32.                                 */
+ * caller's Gaussian test matrix: the reference's is m = min(max(4k, 8),
+ * hidden) rows of ditch_hip_edit_gaussian with seed ^ 0x5eedd1ec7105).     */
 int32_t ditch_hip_sketch_add_device(ditch_hip *h, double *d_y, double *d_w,
                                     const float *d_omega, uint64_t m,
                                     const float *d_center, const float *d_v,
@@ -726,7 +727,8 @@ int32_t ditch_hip_sketch_add_device(ditch_hip *h, double *d_y, double *d_w,
                                     uint64_t hidden, void *stream);
 /* directions.computeBasisFrom with Sketch.factor (directions.zig:108-134,
  * 371-455): the [entries][k][hidden] orthonormal bases from the first
- * directions, the good means and the sketch; k <= 8 (m <= 32).             */
+ * directions, the good means and the sketch (any k and m; sketches of up
+ * to 96 columns keep the eigen-solver in LDS, wider ones in global scratch). */
 int32_t ditch_hip_basis_device(ditch_hip *h, float *d_dirs, const float *d_first,
                                const float *d_good_means, uint64_t entries,
                                uint64_t hidden, uint64_t k, int32_t orthogonalize,

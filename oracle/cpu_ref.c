@@ -2004,7 +2004,8 @@ static int dop_applyT(const dop *o, float *out, const float *y, size_t q) {
 int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_weight *w, const float *v, size_t k,
                       float weight, int mode, size_t lora_rank, uint64_t seed, int ablate, int threads) {
     size_t rows = w->rows, cols = w->cols, r_out = k;
-    float *pa = (float *)malloc(64 * cols * sizeof(float)), *pb = (float *)malloc(rows * 64 * sizeof(float));
+    size_t cap = lora_rank > k ? lora_rank : k; /* the output-side rank's bound */
+    float *pa = (float *)malloc(cap * cols * sizeof(float)), *pb = (float *)malloc(rows * cap * sizeof(float));
     int rc = 0;
     if (mode == 0) {
         rc = ref_matvecTMulti(pa, w, v, k, threads);
@@ -2060,7 +2061,7 @@ int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_
             for (size_t i = 0; i < q; i++)
                 for (size_t j = 0; j < q; j++) bbt[i * q + j] = ref_dot(qx + i * cols, qx + j * cols, cols);
             ref_jacobi_f32(bbt, ev, q);
-            size_t order[64];
+            size_t *order = (size_t *)malloc(q * sizeof(size_t));
             for (size_t i = 0; i < q; i++) order[i] = i;
             for (size_t i = 1; i < q; i++) {
                 size_t ov = order[i], j = i;
@@ -2090,7 +2091,7 @@ int ref_edit_delta_ex(float *a_out, float *b_out, size_t *rank_out, const ditch_
                 for (size_t j = 0; j < cols; j++) pa[t * cols + j] = sq * vk[j];
                 for (size_t i = 0; i < rows; i++) pb[i * r_out + t] = uk[i] * sq;
             }
-            free(uk); free(vk); free(bbt); free(ev); free(omega); free(qy); free(qx);
+            free(uk); free(vk); free(bbt); free(ev); free(omega); free(qy); free(qx); free(order);
             free(wa); free(gram); free(c); free(d);
         }
         free(norms); free(vn); free(a);

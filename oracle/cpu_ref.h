@@ -113,7 +113,7 @@ int ref_basis(float *dirs, const float *first, const float *good_means, size_t e
 
 /* the edit in every mode (abliterate.zig:223-538): mode 0 none, 1 pre,
  * 2 full (rank-r randomised SVD seeded by ref_edit_gaussian), optional
- * input-side ablation; a [rank][cols], b [rows][rank] (rank <= 64)         */
+ * input-side ablation; a [rank][cols], b [rows][rank]                      */
 void ref_edit_gaussian(float *out, size_t n, uint64_t seed);
 /* Zig's std.Random stream (DefaultPrng, float(f64), floatNorm) and the
  * Sampler's pick over it                                                   */

@@ -314,8 +314,9 @@ class Ref:
         1 pre, 2 full."""
         v = _f32(v)
         k = v.shape[0]
-        a = np.empty((64, w.cols), dtype=np.float32)
-        b = np.empty((w.rows * 64,), dtype=np.float32)
+        cap = max(lora_rank, k) + k
+        a = np.empty((cap, w.cols), dtype=np.float32)
+        b = np.empty((w.rows * cap,), dtype=np.float32)
         rank = ctypes.c_size_t()
         self._check(self.lib.ref_edit_delta_ex(_p(a), _p(b), ctypes.byref(rank), w.ref(), _p(v), k, weight, mode,
                                                lora_rank, seed, int(ablate), self.threads))

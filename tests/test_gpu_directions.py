@@ -81,8 +81,11 @@ def dev_sketch_basis(dev, center, v, first, good, k, orth, omega):
     return by.download(np.float64, (E, m, H)), bw.download(np.float64, (E, m, m)), bd.download(np.float32, (E, k, H))
 
 
-@pytest.mark.parametrize("k,orth", [(2, False), (3, True), (8, False)])
+@pytest.mark.parametrize("k,orth", [(2, False), (3, True), (8, False), (16, False), (28, True)])
 def test_sketch_and_basis_match_oracle(dev, ref, k, orth):
+    """Sketch widths m = min(max(4k, 8), hidden) as the reference sizes them
+    (directions.zig:62): 8 to 64 columns keep the basis's eigen-solver in
+    LDS, 112 (k = 28) works in global scratch."""
     good, bad, bad_res, d1, d2 = planted_case(11 + k, entries=4, hidden=512, n=200)
     E, H = good.shape
     m = min(max(4 * k, 8), H)

@@ -93,6 +93,35 @@ def test_device_edit_matches_oracle(dev, ref, fmt, rows, cols, k, mode, ablate):
         assert np.linalg.norm(dstar - gd) <= 1.10 * best + 1e-6 * np.linalg.norm(dstar)
 
 
+WIDE = [("f32", 300, 400, 2, "full", 40), ("bf16", 320, 400, 3, "full", 70), ("int4", 384, 512, 20, "pre", 3),
+        ("fp8", 384, 1024, 24, "none", 3)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols,k,mode,lora", WIDE, ids=[f"{c[0]}-{c[4]}-k{c[3]}-r{c[5]}" for c in WIDE])
+def test_device_edit_wide_ranks_match_oracle(dev, ref, fmt, rows, cols, k, mode, lora):
+    """Ranks and direction counts the reference allows without a cap: the
+    full edit at lora rank 40 (SVD width 84, Jacobi in LDS) and 70 (width
+    144, Jacobi in global memory, delta rank above 64), and 20 / 24
+    directions."""
+    w = _weight(fmt, rows, cols, rows + k)
+    rng = np.random.default_rng(rows + k)
+    v = orthonormal_rows(rng, k, rows)
+    ga, gb = dev.edit_delta_ex(w, v, 1.0, mode, lora_rank=lora, seed=3)
+    ca, cb = ref.edit_delta_ex(w, v, 1.0, MODES[mode], lora_rank=lora, seed=3)
+    assert ga.shape == ca.shape and gb.shape == cb.shape
+    gd = gb.astype(np.float64) @ ga.astype(np.float64)
+    cd = cb.astype(np.float64) @ ca.astype(np.float64)
+    scale = np.linalg.norm(cd)
+    assert np.linalg.norm(gd - cd) <= (1e-2 if mode == "full" else 1e-4) * scale, np.linalg.norm(gd - cd) / scale
+    if mode == "full":
+        dense = ref.dequant(w)
+        dense = ((dense.astype(np.uint32) << 16).view(np.float32) if dense.dtype == np.uint16 else dense)
+        dstar = exact_full(dense, v) - dense.astype(np.float64)
+        s = np.linalg.svd(dstar, compute_uv=False)
+        best = np.sqrt((s[lora:] ** 2).sum())
+        assert np.linalg.norm(dstar - gd) <= 1.10 * best + 1e-6 * np.linalg.norm(dstar)
+
+
 @pytest.mark.parametrize("mode", ["pre", "full"])
 def test_model_edit_ex_then_forward(dev, ref, mode):
     """Edits of every o_proj, dense down_proj and routed expert down_proj

@@ -168,6 +168,38 @@ def test_edit_then_forward(dev, ref):
         cm.free()
 
 
+@pytest.mark.parametrize("lens", [[3, 1], [30, 12, 64]])
+def test_high_rank_deltas_then_forward(dev, ref, lens):
+    """Deltas of rank 80 and 130 (no cap in the reference's setDelta,
+    tensor.zig:588-592) on o_proj, the dense down_proj and every routed
+    expert's down_proj, at decode-sized and tiled row counts."""
+    spec = mg.moe("int4", dense_first=1)
+    c = spec.config
+    tokens, rows, last = mg.batch(len(lens), lens, c["vocab"], seed=7)
+    gm = Model(dev, spec)
+    cm = RefModel(spec)
+    rng = np.random.default_rng(sum(lens))
+    try:
+        for li in range(c["layers"]):
+            slots = [(abi.SLOT["O"], -1, c["hidden"], c["heads"] * c["head_dim"], 80)]
+            if spec.moe_layers[li]:
+                slots += [(abi.SLOT["EXPERT_DOWN"], e, c["hidden"], c["moe_inter"], 130 if e % 2 else 80)
+                          for e in range(c["n_experts"])]
+            else:
+                slots.append((abi.SLOT["DOWN"], -1, c["hidden"], c["inter"], 130))
+            for slot, e, r, k, rank in slots:
+                a = (rng.standard_normal((rank, k)) * 0.02).astype(np.float32)
+                b = (rng.standard_normal((r, rank)) * 0.02).astype(np.float32)
+                gm.set_delta(li, slot, e, a, b)
+                cm.set_delta(li, slot, e, a, b)
+        rg, lg = gm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+        rc, lc = cm.forward(tokens, rows, capture_rows=last, logit_rows=last)
+    finally:
+        gm.free()
+        cm.free()
+    check_parity(ref, rg, lg, rc, lc, "high_rank")
+
+
 @pytest.mark.parametrize("lens", [[20, 28], [130, 82]])
 def test_edit_split_k_products(dev, ref, lens):
     """Rank-2 edits of o_proj and down_proj on a dense FP8 model whose
