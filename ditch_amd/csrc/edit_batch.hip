@@ -39,15 +39,6 @@ struct WtyArgs {
 constexpr int WTY_WAVES = 4;
 constexpr int WTY_STEP = 4;  // row groups whose loads are in flight together
 
-// Sum over the 16 lanes of a DPP row (the 16 rows of a tile group): quad
-// swaps, then the half-row and row mirrors; lane 16 r holds the total.
-__device__ __forceinline__ float row16_sum(float v) {
-    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0xB1, 0xf, 0xf, false)));
-    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x4E, 0xf, 0xf, false)));
-    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x141, 0xf, 0xf, false)));
-    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x140, 0xf, 0xf, false)));
-    return v;
-}
 
 // Side data of one (row, unit): the Q8 / MXFP4 scale word, or the FP8 /
 // INT4 scale (and INT4 zero point) of each k tile.

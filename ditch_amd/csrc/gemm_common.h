@@ -499,4 +499,14 @@ __device__ __forceinline__ void mx_write_slot(float (&r)[32], uint8_t *blk, int 
     *scw = scales;
 }
 
+// Sum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15): quad swaps,
+// then the half-row and row mirrors; every lane of the row holds the total.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0xB1, 0xf, 0xf, false)));
+    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x4E, 0xf, 0xf, false)));
+    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x141, 0xf, 0xf, false)));
+    v = __fadd_rn(v, u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x140, 0xf, 0xf, false)));
+    return v;
+}
+
 }  // namespace ditch

@@ -118,6 +118,17 @@ struct TileGemmParams {
     // and stores its raw sums in part[y][n][rows]; ksplit_reduce_kernel adds them
     int ksplit;
     float *part;
+    // GLU, grouped: the routed down projections' delta products x . A^T
+    // formed from act(gate) * up in the epilogue: segment z's delta A
+    // [rank][rows of w] is xa_a[z] with rank xa_segs[z].delta_rank; each
+    // wave writes the sums over its 32 output columns to xa_part[((tile
+    // column * WGN + wave) * xa_pairs + pair) * xa_stride + j], for
+    // xa_reduce_kernel to add
+    const float *const *xa_a;
+    const GroupSeg *xa_segs;
+    float *xa_part;
+    int64_t xa_pairs;
+    int xa_parts, xa_stride;
 };
 
 // Where a tile's outputs go: a plain product's, or a routed segment's
@@ -168,15 +179,43 @@ __device__ __forceinline__ void tile_store(const TileOut &p, int64_t tok, int64_
 // element, each read of an output waits for the store before it (the
 // addresses may alias), and the residual add then pays one memory latency
 // per element.
-template <int NM, int NI>
+// The lane's rows' delta factors of the first four directions (loaded when
+// the kernel starts: the epilogue of each round of workgroups then waits on
+// no load for them).
+template <int NI>
+__device__ __forceinline__ void delta_b_first(const TileOut &p, const int64_t (&rw)[NI], float (&b0)[4][NI]) {
+    const int nj0 = p.delta_rank < 4 ? p.delta_rank : 4;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            b0[jj][i] = jj < nj0 && rw[i] < p.rows ? p.delta_b[rw[i] * p.delta_rank + jj] : 0.f;
+}
+
+template <int NM, int NI, bool PRE = false>
 __device__ __forceinline__ void tile_store_block(const TileOut &p, const int64_t (&tb)[NM], const int64_t (&rw)[NI],
-                                                 floatx4 (&acc)[NM][NI]) {
+                                                 floatx4 (&acc)[NM][NI], const float (*b0)[NI] = nullptr) {
     bool rin[NI];
     float bias[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         rin[i] = rw[i] < p.rows;
         bias[i] = p.bias && rin[i] ? p.bias[rw[i]] : 0.f;
+    }
+    // PRE: every block's tokens' first four x . A^T values, loaded before
+    // the first store (a store may alias them, so loads after it wait)
+    float x0[PRE ? NM : 1][4][4];
+    if constexpr (PRE) {
+        if (p.delta_rank > 0) {
+            const int nj0 = p.delta_rank < 4 ? p.delta_rank : 4;
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        x0[m][jj][r] = jj < nj0 && tb[m] + r < p.n ? p.delta_xa[(tb[m] + r) * p.delta_stride + jj] : 0.f;
+        }
     }
 #pragma unroll
     for (int m = 0; m < NM; m++) {
@@ -190,16 +229,45 @@ __device__ __forceinline__ void tile_store_block(const TileOut &p, const int64_t
             floatx4 d[NI];
 #pragma unroll
             for (int i = 0; i < NI; i++) d[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-            for (int j = 0; j < p.delta_rank; j++) {
-                float bj[NI], xj[4];
+            if constexpr (PRE) {
+                // four directions' factors a load round (the first four:
+                // b0, loaded when the kernel started, and x0)
+                for (int j0 = 0; j0 < p.delta_rank; j0 += 4) {
+                    const int nj = p.delta_rank - j0 < 4 ? p.delta_rank - j0 : 4;
+                    float bj[4][NI], xj[4][4];
 #pragma unroll
-                for (int i = 0; i < NI; i++) bj[i] = rin[i] ? p.delta_b[rw[i] * p.delta_rank + j] : 0.f;
+                    for (int jj = 0; jj < 4; jj++) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) xj[r] = tin[r] ? p.delta_xa[(tb[m] + r) * p.delta_stride + j] : 0.f;
+                        for (int i = 0; i < NI; i++)
+                            bj[jj][i] = j0 == 0 ? b0[jj][i]
+                                                : (jj < nj && rin[i] ? p.delta_b[rw[i] * p.delta_rank + j0 + jj] : 0.f);
 #pragma unroll
-                for (int i = 0; i < NI; i++)
+                        for (int r = 0; r < 4; r++)
+                            xj[jj][r] = j0 == 0 ? x0[m][jj][r]
+                                                : (jj < nj && tin[r] ? p.delta_xa[(tb[m] + r) * p.delta_stride + j0 + jj]
+                                                                     : 0.f);
+                    }
 #pragma unroll
-                    for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[i], xj[r]));
+                    for (int jj = 0; jj < 4; jj++) {
+                        if (jj >= nj) break;
+#pragma unroll
+                        for (int i = 0; i < NI; i++)
+#pragma unroll
+                            for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[jj][i], xj[jj][r]));
+                    }
+                }
+            } else {
+                for (int j = 0; j < p.delta_rank; j++) {
+                    float bj[NI], xj[4];
+#pragma unroll
+                    for (int i = 0; i < NI; i++) bj[i] = rin[i] ? p.delta_b[rw[i] * p.delta_rank + j] : 0.f;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) xj[r] = tin[r] ? p.delta_xa[(tb[m] + r) * p.delta_stride + j] : 0.f;
+#pragma unroll
+                    for (int i = 0; i < NI; i++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[i], xj[r]));
+                }
             }
 #pragma unroll
             for (int i = 0; i < NI; i++)
@@ -311,6 +379,33 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         to = TileOut{p.part + (int64_t)ks * p.n * w.rows, w.rows, p.n, w.rows, nullptr, 0, nullptr, nullptr, 0, 0};
     }
     const int64_t units = w.units_k;
+    // the grouped epilogues' delta factors that depend on the rows only,
+    // loaded now (routed products: the first four directions' B of the
+    // wave's rows; grouped GLU: the first four directions' A of the routed
+    // down delta over the wave's columns)
+    float b0[4][WN];
+    float xa0[4][OG];
+    int xa_rank = 0;
+    if constexpr (!GLU && GR) {
+        if (to.delta_rank > 0) {
+            int64_t rw0[WN];
+#pragma unroll
+            for (int i = 0; i < WN; i++) rw0[i] = (g0 + i) * 16 + (lane & 15);
+            delta_b_first(to, rw0, b0);
+        }
+    } else if constexpr (GR) {
+        xa_rank = p.xa_part ? p.xa_segs[gd[0]].delta_rank : 0;
+        if (xa_rank > 0) {
+            const float *A = p.xa_a[gd[0]];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                for (int i = 0; i < OG; i++) {
+                    const int64_t col = (g0 + i) * 16 + (lane & 15);
+                    xa0[jj][i] = jj < xa_rank && col < w.rows ? A[(int64_t)jj * w.rows + col] : 0.f;
+                }
+        }
+    }
 
     // Copies: a global_load_lds stalls the issuing wave while the texture
     // unit's queue is full, so with two waves per SIMD only the younger one
@@ -529,7 +624,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         for (int m = 0; m < WM; m++) tb[m] = tok0 + (wave_m * WM + m) * 16 + 4 * kq;
 #pragma unroll
         for (int i = 0; i < WN; i++) rw[i] = (g0 + i) * 16 + (lane & 15);
-        tile_store_block(to, tb, rw, acc);
+        if constexpr (GR) tile_store_block<WM, WN, true>(to, tb, rw, acc, b0);
+        else tile_store_block(to, tb, rw, acc);
     } else {
         // act(gate) * up (tensor.gatedActivation), as f32 rows and/or as the
         // A fragments of the next product: each 16-token block of the wave's
@@ -578,6 +674,72 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
                 }
             }
         }
+        if constexpr (GR) {
+            // the routed delta's x . A^T over this wave's 32 columns: per
+            // token, the 16 lanes of a DPP row hold 16 columns of each of
+            // the wave's two groups (y as stored above)
+            const int rank = xa_rank;
+            if (rank > 0) {
+                const float *A = p.xa_a[gd[0]];
+                const int64_t base = p.gsegs[gd[0]].off;
+                float *xp = p.xa_part + (int64_t)(nt * WGN + wave_n) * p.xa_pairs * p.xa_stride;
+                float y[WM][OG][4];
+#pragma unroll
+                for (int m = 0; m < WM; m++)
+#pragma unroll
+                    for (int i = 0; i < OG; i++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
+                            const int64_t col = (g0 + i) * 16 + (lane & 15);
+                            y[m][i][r] = tok >= to.n || col >= w.rows ? 0.f : __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
+                        }
+                for (int j0 = 0; j0 < rank; j0 += 4) {
+                    float aj[4][OG];
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                        for (int i = 0; i < OG; i++) {
+                            const int64_t col = (g0 + i) * 16 + (lane & 15);
+                            aj[jj][i] = j0 == 0 ? xa0[jj][i]
+                                                : (j0 + jj < rank && col < w.rows ? A[(int64_t)(j0 + jj) * w.rows + col] : 0.f);
+                        }
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        if (j0 + jj >= rank) break;
+#pragma unroll
+                        for (int m = 0; m < WM; m++)
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
+                                float sum = 0.f;
+#pragma unroll
+                                for (int i = 0; i < OG; i++) sum = __builtin_fmaf(y[m][i][r], aj[jj][i], sum);
+                                sum = row16_sum(sum);
+                                if ((lane & 15) == 0 && tok < to.n) xp[(base + tok) * p.xa_stride + j0 + jj] = sum;
+                            }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// xa[p][j] = the sum of the parts' entries for pair p in part order (part
+// k's [P][stride] slab at k P stride; j below a segment's rank only is used)
+__global__ void xa_reduce_kernel(float *xa, const float *part, int64_t P, int parts, int stride) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < P * stride;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        float sum = 0.f;
+        for (int k0 = 0; k0 < parts; k0 += 8) {  // eight parts' loads in flight, then their sums in order
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = k0 + k < parts ? part[(int64_t)(k0 + k) * P * stride + t] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (k0 + k < parts) sum = __fadd_rn(sum, v[k]);
+        }
+        xa[t] = sum;
     }
 }
 
@@ -1235,7 +1397,7 @@ void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
                                  const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
                                  const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
-                                 DevBuf *ws, hipStream_t s) {
+                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx) {
     DITCH_CHECK(tile_glu_takes(gate0, up0, 128), DITCH_INVALID_ARGUMENT, "grouped GLU: gate and up must share format and shape");
     DITCH_CHECK(!xs_out || ldk_out * 32 >= gate0.rows, DITCH_INVALID_ARGUMENT, "grouped GLU: output fragments too short");
     const int64_t kt = split_k_tiles(gate0);
@@ -1260,7 +1422,23 @@ void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, c
     p.gdesc = plan.desc;
     p.gcount = plan.count;
     p.tiles_m = (int)plan.max_desc;
+    if (dx) {
+        // the launch's tile columns times its waves: the parts of each pair
+        const int wgn = gate0.tf == TF_BF16 ? 4 : 8, bn = 16 * 2 * wgn;
+        p.xa_a = dx->a;
+        p.xa_segs = dx->segs;
+        p.xa_stride = dx->max_rank;
+        p.xa_parts = (int)((gate0.rows + bn - 1) / bn) * wgn;
+        p.xa_pairs = dx->pairs;
+        p.xa_part = (float *)dx->ws->get<float>((size_t)dx->pairs * p.xa_parts * dx->max_rank);
+    }
     launch_tile_grouped_any<true>(p, s);
+    if (dx) {
+        const int64_t total = dx->pairs * dx->max_rank;
+        hipLaunchKernelGGL(xa_reduce_kernel, dim3((unsigned)std::min<int64_t>((total + 255) / 256, 4096)), dim3(256),
+                           0, s, dx->xa, p.xa_part, dx->pairs, p.xa_parts, dx->max_rank);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
 }
 
 void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,

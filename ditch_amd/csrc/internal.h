@@ -115,6 +115,21 @@ struct DevBuf {
     DevBuf(void *mem, size_t cap) : p(mem), bytes(cap), borrowed(true) {}
     DevBuf(const DevBuf &) = delete;
     DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : p(o.p), bytes(o.bytes), borrowed(o.borrowed) {
+        o.p = nullptr;
+        o.bytes = 0;
+    }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        if (this != &o) {
+            if (!borrowed) dev_free(p);
+            p = o.p;
+            bytes = o.bytes;
+            borrowed = o.borrowed;
+            o.p = nullptr;
+            o.bytes = 0;
+        }
+        return *this;
+    }
     ~DevBuf() {
         if (!borrowed) dev_free(p);
     }
@@ -318,11 +333,24 @@ struct GroupedDevPlan {
     int32_t *prow, *desc, *count;
     int64_t max_blocks, max_desc;
 };
-// out (may be NULL): act(gate) * up as f32 rows in the grouped row order
+// The routed down projections' delta products, formed by the grouped GLU:
+// xa [pairs][max_rank] = act(gate) * up . A_z^T for each pair's segment z
+// (a[z] the down projection's delta A, segs[z].delta_rank its rank, 0: no
+// delta); ws holds the per-wave partial sums.
+struct GroupedDeltaXa {
+    const float *const *a;
+    const GroupSeg *segs;
+    float *xa;
+    int64_t pairs;
+    int max_rank;
+    DevBuf *ws;
+};
+// out (may be NULL): act(gate) * up as f32 rows in the grouped row order;
+// dx (may be NULL): the delta products as well
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
                                  const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
                                  const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
-                                 DevBuf *ws, hipStream_t s);
+                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx = nullptr);
 // delta_xa [rows][delta_stride]: the x . A^T of the segments' deltas (their
 // B and rank in the segment table), or NULL
 void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,

@@ -125,6 +125,12 @@ struct Layer {
     Vec attn_norm, q_bias, k_bias, v_bias, q_norm, k_norm, ffn_norm, corr, q_a_norm, kv_a_norm;
     Mat q, k, v, o, gate, up, down, router, sh_gate, sh_up, sh_down, q_a, q_b, kv_a, kv_b;
     std::vector<Mat> eg, eu, ed;
+    // the device-planned routed products' segment tables (gate, up, down)
+    // and the down deltas' A pointers, uploaded again only when what they
+    // are built from changes (plan_key: the tensors, delta factors and
+    // ranks, and the model's weights version)
+    DevBuf plan_tab, plan_da;
+    std::vector<uintptr_t> plan_key;
 };
 
 }  // namespace ditch
@@ -144,13 +150,14 @@ struct ditch_hip_model {
     ditch_model_config c{};
     std::vector<uint8_t> moe_layers;
     std::vector<ditch::Layer> layers;
+    uint64_t weights_version = 0;  // bumped whenever a matrix slot gets a new tensor
     ditch::Mat embed, lm_head;
     ditch::Vec final_norm;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     // workspace
     ditch::DevBuf x, hbuf, q, k, v, att, o, g, u, kc, vc, rowsb, xa, logit_h, mla_a, mla_b, mla_c;
     ditch::DevBuf r_logits, r_sel, r_selw, r_ord, r_counts, r_offsets, r_pair_token, r_pair_of, e_gate, e_up, e_out, e_shared,
-        segs, segd, e_xa;
+        segs, segd, e_xa, e_xa_part;
     ditch::DevBuf xsplit;  // split activations of the tiled GEMM
     ditch::DevBuf gmeta;   // row map and tile table of the grouped tiled GEMM
     ditch::DevBuf hs, atts, acts;  // A fragments written by the producers (norm, attention, gate/up)

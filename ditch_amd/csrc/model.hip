@@ -674,36 +674,6 @@ __global__ void grouped_delta_xa_kernel(float *xa, const float *x, const int32_t
     if (lane == 0) xa[p * max_rank + j] = acc;
 }
 
-// The same for a routed layer planned on the device (every expert a
-// segment, off / cnt written by moe_plan_kernel): one wave per pair p and 4
-// directions (the pair's row read once for the four); p's expert is the
-// last whose pair offset is <= p (offsets are non-decreasing in expert
-// order and cover every pair); a[e] is expert e's delta A, or NULL for an
-// expert without a delta (its rows are unused).
-__global__ void plan_delta_xa_kernel(float *xa, const float *x, const GroupSeg *segs, const float *const *a,
-                                     int64_t E, int64_t cols, int max_rank, int64_t P) {
-    const int lane = threadIdx.x & 63;
-    const int64_t nb = (max_rank + 3) / 4;
-    const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (t >= P * nb) return;
-    const int64_t p = t / nb, j0 = (t % nb) * 4;
-    int64_t lo = 0, hi = E - 1;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) / 2;
-        if (segs[mid].off <= p) lo = mid;
-        else hi = mid - 1;
-    }
-    const float *ae = a[lo];
-    const int rank = ae ? segs[lo].delta_rank : 0;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (j0 < rank) delta_dot4(x + p * cols, ae, cols, j0, rank, lane, acc);
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-        const float v = wave_sum64(acc[jj]);
-        if (lane == 0 && j0 + jj < max_rank) xa[p * max_rank + j0 + jj] = v;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Host side
 
@@ -899,6 +869,7 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
     ditch_hip_tensor *t = upload_weight(m->h, w, s);
     mt->release();
     mt->t = t;
+    m->weights_version++;
     if (m->expert_budget > 0 &&
         (slot == DITCH_SLOT_EXPERT_GATE || slot == DITCH_SLOT_EXPERT_UP || slot == DITCH_SLOT_EXPERT_DOWN)) {
         DITCH_CHECK(!m->cache, DITCH_INVALID_ARGUMENT, "expert registered after the expert cache was built");
@@ -1119,16 +1090,30 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         int32_t *offsets = m->r_offsets.get<int32_t>(E);
         int32_t *pair_token = m->r_pair_token.get<int32_t>(P);
         eo = m->e_out.get<float>(P * hidden);
-        std::vector<GroupSeg> tab((size_t)(3 * E));
         int max_rank = 0;
+        std::vector<uintptr_t> key;
+        key.reserve((size_t)(6 * E + 1));
+        key.push_back((uintptr_t)m->weights_version);
         for (int64_t e = 0; e < E; e++) {
-            tab[e] = GroupSeg{L.eg[e].t->v, 0, 0, nullptr, 0};
-            tab[E + e] = GroupSeg{L.eu[e].t->v, 0, 0, nullptr, 0};
-            tab[2 * E + e] = GroupSeg{L.ed[e].t->v, 0, 0, L.ed[e].db, L.ed[e].rank};
+            key.insert(key.end(), {(uintptr_t)L.eg[e].t, (uintptr_t)L.eu[e].t, (uintptr_t)L.ed[e].t,
+                                   (uintptr_t)L.ed[e].db, (uintptr_t)L.ed[e].da, (uintptr_t)L.ed[e].rank});
             max_rank = std::max(max_rank, L.ed[e].rank);
         }
-        GroupSeg *dsegs = m->segs.get<GroupSeg>(3 * E);
-        DITCH_TRY_HIP(hipMemcpyAsync(dsegs, tab.data(), tab.size() * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+        GroupSeg *dsegs = L.plan_tab.get<GroupSeg>(3 * E);
+        const float **dda = L.plan_da.get<const float *>(E);
+        if (key != L.plan_key) {
+            std::vector<GroupSeg> tab((size_t)(3 * E));
+            std::vector<const float *> das((size_t)E);
+            for (int64_t e = 0; e < E; e++) {
+                tab[e] = GroupSeg{L.eg[e].t->v, 0, 0, nullptr, 0};
+                tab[E + e] = GroupSeg{L.eu[e].t->v, 0, 0, nullptr, 0};
+                tab[2 * E + e] = GroupSeg{L.ed[e].t->v, 0, 0, L.ed[e].db, L.ed[e].rank};
+                das[e] = L.ed[e].rank ? L.ed[e].da : nullptr;
+            }
+            DITCH_TRY_HIP(hipMemcpyAsync(dsegs, tab.data(), tab.size() * sizeof(GroupSeg), hipMemcpyHostToDevice, s));
+            DITCH_TRY_HIP(hipMemcpyAsync(dda, das.data(), E * sizeof(float *), hipMemcpyHostToDevice, s));
+            L.plan_key = std::move(key);
+        }
         int32_t *meta = m->gmeta.get<int32_t>(max_blocks * 16 + max_desc * 4 + 1);
         const GroupedDevPlan plan{meta, meta + max_blocks * 16, meta + max_blocks * 16 + max_desc * 4, max_blocks,
                                   max_desc};
@@ -1141,22 +1126,15 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         const TileView &vd = L.ed[0].t->v;
         const int64_t ldk_d = split_k_tiles(vd);
         void *fr = m->acts.get<uint8_t>(split_bytes_ldk(max_blocks * 16, ldk_d, 2));
-        // with down deltas the GLU writes act(g) * u as f32 rows too, for
-        // the deltas' x . A^T
-        float *act = max_rank > 0 ? m->e_gate.get<float>(P * inter) : nullptr, *dxa = nullptr;
-        launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, act, fr, ldk_d, h, hidden,
-                                    pair_token, plan, &m->xsplit, s);
+        // routed down deltas: their x . A^T formed by the GLU's epilogue
+        float *dxa = nullptr;
+        GroupedDeltaXa dx{};
         if (max_rank > 0) {
-            std::vector<const float *> das((size_t)E);
-            for (int64_t e = 0; e < E; e++) das[e] = L.ed[e].rank ? L.ed[e].da : nullptr;
-            const float **dda = m->segd.get<const float *>(E);
-            DITCH_TRY_HIP(hipMemcpyAsync(dda, das.data(), E * sizeof(float *), hipMemcpyHostToDevice, s));
             dxa = m->e_xa.get<float>(P * max_rank);
-            const int64_t waves = P * ((max_rank + 3) / 4);
-            hipLaunchKernelGGL(plan_delta_xa_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, dxa, act,
-                               dsegs + 2 * E, dda, E, inter, max_rank, P);
-            DITCH_TRY_HIP(hipGetLastError());
+            dx = GroupedDeltaXa{dda, dsegs + 2 * E, dxa, P, max_rank, &m->e_xa_part};
         }
+        launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, nullptr, fr, ldk_d, h, hidden,
+                                    pair_token, plan, &m->xsplit, s, max_rank > 0 ? &dx : nullptr);
         launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s, dxa, max_rank);
     } else {
     m->moe_host_planned++;

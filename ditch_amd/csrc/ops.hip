@@ -752,6 +752,31 @@ __global__ void delta_xa_kernel(float *xa, const float *x, const float *a, int64
     }
 }
 
+// The same with A staged in LDS once per workgroup of 8 rows (one wave a
+// row and its 4-direction blocks): the waves then read A from LDS instead
+// of all of them fetching the same lines from L2.
+__global__ __launch_bounds__(512) void delta_xa_lds_kernel(float *xa, const float *x, const float *a, int64_t n,
+                                                           int64_t cols, int64_t rank) {
+    extern __shared__ float4 a_lds4[];
+    const float4 *a4 = (const float4 *)a;
+    const int64_t n4 = rank * cols / 4;
+    for (int64_t t = threadIdx.x; t < n4; t += blockDim.x) a_lds4[t] = a4[t];
+    __syncthreads();
+    const float *al = (const float *)a_lds4;
+    const int lane = threadIdx.x & 63;
+    const int64_t i = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (i >= n) return;
+    for (int64_t j0 = 0; j0 < rank; j0 += 4) {
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        delta_dot4(x + i * cols, al, cols, j0, rank, lane, s);
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const float v = wave_sum(s[jj]);
+            if (lane == 0 && j0 + jj < rank) xa[i * rank + j0 + jj] = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Launchers
 
@@ -903,6 +928,19 @@ void launch_row_norms(float *out, const TileView &w, hipStream_t s) {
 }
 void launch_delta_xa(float *xa, const float *x, const float *a, int64_t n, int64_t cols, int64_t rank, hipStream_t s) {
     if (n * rank <= 0) return;
+    const size_t abytes = (size_t)(rank * cols) * 4;
+    if (n >= 64 && (cols & 3) == 0 && (((uintptr_t)x | (uintptr_t)a) & 15) == 0 && abytes <= 65536) {
+        static const bool attr = [] {
+            return hipFuncSetAttribute((const void *)delta_xa_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       65536) == hipSuccess;
+        }();
+        if (attr) {
+            hipLaunchKernelGGL(delta_xa_lds_kernel, dim3((unsigned)((n + 7) / 8)), dim3(512), abytes, s, xa, x, a, n,
+                               cols, rank);
+            DITCH_TRY_HIP(hipGetLastError());
+            return;
+        }
+    }
     const int64_t waves = n * ((rank + 3) / 4);
     hipLaunchKernelGGL(delta_xa_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, xa, x, a, n, cols, rank);
     DITCH_TRY_HIP(hipGetLastError());
