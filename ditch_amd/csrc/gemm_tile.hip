@@ -85,6 +85,35 @@ __global__ __launch_bounds__(256) void split_kernel(SplitParams p) {
     for (int e = 0; e < XT; e++) p.xs[(f * XT + e) * 64 + lane] = w[e];
 }
 
+// Token-major activation terms for the routed products: out[token][k tile]
+// [term][k quarter] (16 bytes each, the same words split_kernel writes for
+// the token's fragment lanes), so that a routed tile gathers each pair's
+// pieces from its token's row (64 contiguous bytes per k tile and term)
+// instead of a copy of the row per pair.
+template <int XT>
+__global__ __launch_bounds__(256) void split_tok_kernel(u32x4 *out, const float *x, int64_t n, int64_t ldx, int64_t K,
+                                                        int64_t kt_total) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= n * kt_total * 4) return;
+    const int kq = (int)(t & 3);
+    const int64_t kt = (t >> 2) % kt_total, tok = (t >> 2) / kt_total;
+    const int64_t k0 = kt * 32 + 8 * kq;
+    const float *xr = x + tok * ldx;
+    float v[8];
+    if (k0 + 8 <= K && ((((uintptr_t)(xr + k0)) & 15) == 0)) {
+        const float4 a = *(const float4 *)(xr + k0), b = *(const float4 *)(xr + k0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = k0 + j < K ? xr[k0 + j] : 0.f;
+    }
+    u32x4 w[XT];
+    a_words<false, XT>(v, w);
+#pragma unroll
+    for (int e = 0; e < XT; e++) out[((tok * kt_total + kt) * XT + e) * 4 + kq] = w[e];
+}
+
 // ---------------------------------------------------------------------------
 
 struct TileGemmParams {
@@ -129,6 +158,12 @@ struct TileGemmParams {
     float *xa_part;
     int64_t xa_pairs;
     int xa_parts, xa_stride;
+    // GLU, grouped: the A fragments gathered from token-major terms
+    // (split_tok_kernel) instead of xs: fragment row r of the plan is pair
+    // a_prow[r] (-1: padding), token a_map[pair]; a_tok_stride bytes a token
+    const u32x4 *a_tok;
+    const int32_t *a_prow, *a_map;
+    int64_t a_tok_stride;
 };
 
 // Where a tile's outputs go: a plain product's, or a routed segment's
@@ -457,14 +492,39 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         ssrc[j] = wi.side + side_row(wi, group_of(wq, i), lane);
     }
 
+    // gathered A (grouped GLU with token-major terms): copier ck copies
+    // every fragment of block m16_0 + ck (CA == TPS * XT), so each lane
+    // keeps one pointer: its row's token, its k quarter
+    constexpr bool GATHER = GR && GLU && TF != TF_Q8;  // (Q8: no registers to spare)
+    const char *gsrc = nullptr;
+    if constexpr (GATHER) {
+        static_assert(CA == TPS * XT, "one copier per token block of the tile");
+        if (p.a_tok && copier) {
+            int64_t mb = m16_0 + ck;
+            mb = mb < m16_n ? mb : m16_n - 1;
+            const int32_t pr = p.a_prow[mb * 16 + (lane & 15)];
+            const int64_t tok = pr >= 0 ? (int64_t)p.a_map[pr] : 0;
+            gsrc = (const char *)p.a_tok + tok * p.a_tok_stride + (lane >> 4) * 16;
+        }
+    }
     auto copy_stage = [&](int64_t s, u32x4 *As, u32x4 *Bs, uint32_t *Ss) {
         if (!copier) return;
         // copy j of a run of 1 KiB pieces: window j / 4, offset (j % 4) KiB
-        static_for<CA>([&](auto jc) {
-            constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
-            __builtin_amdgcn_global_load_lds((const void *)(asrc(j) + (TPS * s * XT * 64 * 16 - off) + lofs),
-                                             (lds_void *)&As[(ck * CA + j / 4 * 4) * 64], 16, off, 0);
-        });
+        if (GATHER && gsrc) {
+            // fragment (k tile s TPS + j / XT, term j % XT): 64 bytes of the
+            // token's row per k tile and term
+            static_for<CA>([&](auto jc) {
+                constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
+                __builtin_amdgcn_global_load_lds((const void *)(gsrc + (TPS * s * XT * 64 + j * 64 - off)),
+                                                 (lds_void *)&As[(ck * CA + j / 4 * 4) * 64], 16, off, 0);
+            });
+        } else {
+            static_for<CA>([&](auto jc) {
+                constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
+                __builtin_amdgcn_global_load_lds((const void *)(asrc(j) + (TPS * s * XT * 64 * 16 - off) + lofs),
+                                                 (lds_void *)&As[(ck * CA + j / 4 * 4) * 64], 16, off, 0);
+            });
+        }
         static_for<CB>([&](auto jc) {
             constexpr int j = decltype(jc)::value, off = (j % 4) * 1024;
             const int q = ck * CB + j, u = q % NU;
@@ -1397,16 +1457,31 @@ void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
                                  const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
                                  const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
-                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx) {
+                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx, int64_t n_tok) {
     DITCH_CHECK(tile_glu_takes(gate0, up0, 128), DITCH_INVALID_ARGUMENT, "grouped GLU: gate and up must share format and shape");
     DITCH_CHECK(!xs_out || ldk_out * 32 >= gate0.rows, DITCH_INVALID_ARGUMENT, "grouped GLU: output fragments too short");
     const int64_t kt = split_k_tiles(gate0);
-    void *xs = ws->get<uint8_t>(split_bytes_ldk(plan.max_blocks * 16, kt, 2));
-    SplitParams sp{(u32x4 *)xs, x, row_index, plan.prow, plan.max_blocks * 16, ldx, gate0.cols, kt, plan.max_blocks};
-    const int64_t total = plan.max_blocks * kt * 64;
-    hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
-    DITCH_TRY_HIP(hipGetLastError());
     TileGemmParams p{};
+    void *xs = nullptr;
+    if (n_tok > 0 && gate0.tf != TF_Q8) {
+        // the tokens' terms once, token-major; the tiles gather each pair's
+        // pieces (x: the n_tok token rows, row_index: pair -> token)
+        xs = ws->get<uint8_t>((size_t)(n_tok * kt * 2 * 64));
+        const int64_t total = n_tok * kt * 4;
+        hipLaunchKernelGGL(split_tok_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (u32x4 *)xs, x,
+                           n_tok, ldx, gate0.cols, kt);
+        DITCH_TRY_HIP(hipGetLastError());
+        p.a_tok = (const u32x4 *)xs;
+        p.a_prow = plan.prow;
+        p.a_map = row_index;
+        p.a_tok_stride = kt * 2 * 64;
+    } else {
+        xs = ws->get<uint8_t>(split_bytes_ldk(plan.max_blocks * 16, kt, 2));
+        SplitParams sp{(u32x4 *)xs, x, row_index, plan.prow, plan.max_blocks * 16, ldx, gate0.cols, kt, plan.max_blocks};
+        const int64_t total = plan.max_blocks * kt * 64;
+        hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
     p.w = gate0;
     p.w2 = up0;
     p.act = act;

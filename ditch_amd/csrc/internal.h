@@ -346,11 +346,13 @@ struct GroupedDeltaXa {
     DevBuf *ws;
 };
 // out (may be NULL): act(gate) * up as f32 rows in the grouped row order;
-// dx (may be NULL): the delta products as well
+// dx (may be NULL): the delta products as well; n_tok > 0: x holds n_tok
+// token rows split once token-major and gathered by the tiles (row_index:
+// pair -> token), else the pairs' rows are split in fragment order
 void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, const TileView &gate0,
                                  const TileView &up0, uint32_t act, float *out, void *xs_out, int64_t ldk_out,
                                  const float *x, int64_t ldx, const int32_t *row_index, const GroupedDevPlan &plan,
-                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx = nullptr);
+                                 DevBuf *ws, hipStream_t s, const GroupedDeltaXa *dx = nullptr, int64_t n_tok = 0);
 // delta_xa [rows][delta_stride]: the x . A^T of the segments' deltas (their
 // B and rank in the segment table), or NULL
 void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, float *out, int64_t ldo,

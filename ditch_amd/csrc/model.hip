@@ -1134,7 +1134,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
             dx = GroupedDeltaXa{dda, dsegs + 2 * E, dxa, P, max_rank, &m->e_xa_part};
         }
         launch_tile_glu_grouped_dev(dsegs, dsegs + E, L.eg[0].t->v, L.eu[0].t->v, 0, nullptr, fr, ldk_d, h, hidden,
-                                    pair_token, plan, &m->xsplit, s, max_rank > 0 ? &dx : nullptr);
+                                    pair_token, plan, &m->xsplit, s, max_rank > 0 ? &dx : nullptr, n);
         launch_tile_gemm_grouped_dev(dsegs + 2 * E, vd, eo, hidden, fr, plan, s, dxa, max_rank);
     } else {
     m->moe_host_planned++;
