@@ -340,6 +340,129 @@ __host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// The grouped and plain GLU epilogue of a wave's tile: act(gate) * up
+// (tensor.gatedActivation), as f32 rows and/or as the A fragments of the
+// next product; each 16-token block of the wave's 32-column k tile goes
+// through the wave's LDS patch [16][32] (the stage buffers are idle: the
+// last stage ended with a barrier). Grouped: tokens and output rows within
+// the segment, fragment blocks in the padded order of the row map, and the
+// routed down delta's x . A^T partial sums over the wave's columns (part
+// `part`; xa0: the first four directions' A of its columns). tokb: the
+// token of the wave's first row (within the output rows), mblk0 its block.
+template <int WM, int OG, bool GR>
+__device__ __forceinline__ void glu_epilogue(const TileGemmParams &p, const TileOut &to, int64_t rows,
+                                             floatx4 (&acc)[WM][2 * OG], int64_t tokb, int64_t mblk0, int64_t m16_n,
+                                             int64_t g0, float *patch, int lane, int seg, int part, int xa_rank,
+                                             const float (&xa0)[4][OG]) {
+    const int kq = lane >> 4;
+    // the gates' activation first, the activation's switch outside the loops
+    with_act(p.act, [&](auto ac) {
+        constexpr int A = decltype(ac)::value;
+#pragma unroll
+        for (int m = 0; m < WM; m++)
+#pragma unroll
+            for (int i = 0; i < OG; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[m][i][r] = act_fused<A>(acc[m][i][r]);
+    });
+#pragma unroll
+    for (int m = 0; m < WM; m++) {
+        const int64_t mblk = mblk0 + m;
+#pragma unroll
+        for (int i = 0; i < OG; i++) {
+            const int64_t col = (g0 + i) * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int64_t tok = tokb + m * 16 + 4 * kq + r;
+                float y = __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
+                if (tok >= to.n || col >= rows) y = 0.f;
+                else if (p.out) to.out[tok * to.ldo + col] = y;
+                patch[(4 * kq + r) * 32 + (i & 1) * 16 + (lane & 15)] = y;
+            }
+            if ((i & 1) && p.xs_out && mblk < m16_n && ((g0 + i - 1) * 16) / 32 < p.ldk_out) {
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = patch[(lane & 15) * 32 + 8 * kq + j];
+                u32x4 words[2];
+                a_words<false, 2>(v, words);
+                const int64_t kt = ((g0 + i - 1) * 16) / 32;
+#pragma unroll
+                for (int e = 0; e < 2; e++) p.xs_out[((mblk * p.ldk_out + kt) * 2 + e) * 64 + lane] = words[e];
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            }
+        }
+    }
+    if constexpr (GR) {
+        // the routed delta's x . A^T over this wave's columns: per token,
+        // the 16 lanes of a DPP row hold 16 columns of each of the wave's
+        // groups (y as stored above)
+        const int rank = xa_rank;
+        if (rank > 0) {
+            const float *A = p.xa_a[seg];
+            const int64_t base = p.gsegs[seg].off;
+            float *xp = p.xa_part + (int64_t)part * p.xa_pairs * p.xa_stride;
+            float y[WM][OG][4];
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int i = 0; i < OG; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int64_t tok = tokb + m * 16 + 4 * kq + r;
+                        const int64_t col = (g0 + i) * 16 + (lane & 15);
+                        y[m][i][r] = tok >= to.n || col >= rows ? 0.f : __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
+                    }
+            for (int j0 = 0; j0 < rank; j0 += 4) {
+                float aj[4][OG];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                    for (int i = 0; i < OG; i++) {
+                        const int64_t col = (g0 + i) * 16 + (lane & 15);
+                        aj[jj][i] = j0 == 0 ? xa0[jj][i]
+                                            : (j0 + jj < rank && col < rows ? A[(int64_t)(j0 + jj) * rows + col] : 0.f);
+                    }
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    if (j0 + jj >= rank) break;
+#pragma unroll
+                    for (int m = 0; m < WM; m++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int64_t tok = tokb + m * 16 + 4 * kq + r;
+                            float sum = 0.f;
+#pragma unroll
+                            for (int i = 0; i < OG; i++) sum = __builtin_fmaf(y[m][i][r], aj[jj][i], sum);
+                            sum = row16_sum(sum);
+                            if ((lane & 15) == 0 && tok < to.n) xp[(base + tok) * p.xa_stride + j0 + jj] = sum;
+                        }
+                }
+            }
+        }
+    }
+}
+
+// the A of the routed down delta over a wave's columns, first four directions
+template <int OG>
+__device__ __forceinline__ int xa_first(const TileGemmParams &p, int seg, int64_t g0, int64_t rows, int lane,
+                                        float (&xa0)[4][OG]) {
+    const int rank = p.xa_part ? p.xa_segs[seg].delta_rank : 0;
+    if (rank > 0) {
+        const float *A = p.xa_a[seg];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int i = 0; i < OG; i++) {
+                const int64_t col = (g0 + i) * 16 + (lane & 15);
+                xa0[jj][i] = jj < rank && col < rows ? A[(int64_t)jj * rows + col] : 0.f;
+            }
+    }
+    return rank;
+}
+
 // Every operand of a stage travels global -> LDS by DMA (global_load_lds:
 // lane l's bytes land at the destination + l * size), two stage buffers:
 // stage s + 1 is copied while stage s is computed, and a stage ends with
@@ -429,17 +552,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
             delta_b_first(to, rw0, b0);
         }
     } else if constexpr (GR) {
-        xa_rank = p.xa_part ? p.xa_segs[gd[0]].delta_rank : 0;
-        if (xa_rank > 0) {
-            const float *A = p.xa_a[gd[0]];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-                for (int i = 0; i < OG; i++) {
-                    const int64_t col = (g0 + i) * 16 + (lane & 15);
-                    xa0[jj][i] = jj < xa_rank && col < w.rows ? A[(int64_t)jj * w.rows + col] : 0.f;
-                }
-        }
+        xa_rank = xa_first<OG>(p, gd[0], g0, w.rows, lane, xa0);
     }
 
     // Copies: a global_load_lds stalls the issuing wave while the texture
@@ -687,101 +800,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void tile_gemm_kernel(TileGemmParam
         if constexpr (GR) tile_store_block<WM, WN, true>(to, tb, rw, acc, b0);
         else tile_store_block(to, tb, rw, acc);
     } else {
-        // act(gate) * up (tensor.gatedActivation), as f32 rows and/or as the
-        // A fragments of the next product: each 16-token block of the wave's
-        // 32-column k tile goes through a per-wave LDS patch [16][32] (the
-        // stage buffers are idle: the last stage ended with a barrier)
-        // (grouped: tokens and output rows within the segment, fragment
-        // blocks in the padded order of the row map)
-        float *patch = (float *)As0 + wave * 16 * 32;
-        // the gates' activation first, the activation's switch outside the loops
-        with_act(p.act, [&](auto ac) {
-            constexpr int A = decltype(ac)::value;
-#pragma unroll
-            for (int m = 0; m < WM; m++)
-#pragma unroll
-                for (int i = 0; i < OG; i++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[m][i][r] = act_fused<A>(acc[m][i][r]);
-        });
-#pragma unroll
-        for (int m = 0; m < WM; m++) {
-            const int64_t mblk = m16_0 + wave_m * WM + m;
-#pragma unroll
-            for (int i = 0; i < OG; i++) {
-                const int64_t col = (g0 + i) * 16 + (lane & 15);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
-                    float y = __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
-                    if (tok >= to.n || col >= w.rows) y = 0.f;
-                    else if (p.out) to.out[tok * to.ldo + col] = y;
-                    patch[(4 * kq + r) * 32 + (i & 1) * 16 + (lane & 15)] = y;
-                }
-                if ((i & 1) && p.xs_out && mblk < m16_n && ((g0 + i - 1) * 16) / 32 < p.ldk_out) {
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    float v[8];
-#pragma unroll
-                    for (int j = 0; j < 8; j++) v[j] = patch[(lane & 15) * 32 + 8 * kq + j];
-                    u32x4 words[2];
-                    a_words<false, 2>(v, words);
-                    const int64_t kt = ((g0 + i - 1) * 16) / 32;
-#pragma unroll
-                    for (int e = 0; e < 2; e++) p.xs_out[((mblk * p.ldk_out + kt) * 2 + e) * 64 + lane] = words[e];
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                }
-            }
-        }
-        if constexpr (GR) {
-            // the routed delta's x . A^T over this wave's 32 columns: per
-            // token, the 16 lanes of a DPP row hold 16 columns of each of
-            // the wave's two groups (y as stored above)
-            const int rank = xa_rank;
-            if (rank > 0) {
-                const float *A = p.xa_a[gd[0]];
-                const int64_t base = p.gsegs[gd[0]].off;
-                float *xp = p.xa_part + (int64_t)(nt * WGN + wave_n) * p.xa_pairs * p.xa_stride;
-                float y[WM][OG][4];
-#pragma unroll
-                for (int m = 0; m < WM; m++)
-#pragma unroll
-                    for (int i = 0; i < OG; i++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
-                            const int64_t col = (g0 + i) * 16 + (lane & 15);
-                            y[m][i][r] = tok >= to.n || col >= w.rows ? 0.f : __fmul_rn(acc[m][i][r], acc[m][i + OG][r]);
-                        }
-                for (int j0 = 0; j0 < rank; j0 += 4) {
-                    float aj[4][OG];
-#pragma unroll
-                    for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-                        for (int i = 0; i < OG; i++) {
-                            const int64_t col = (g0 + i) * 16 + (lane & 15);
-                            aj[jj][i] = j0 == 0 ? xa0[jj][i]
-                                                : (j0 + jj < rank && col < w.rows ? A[(int64_t)(j0 + jj) * w.rows + col] : 0.f);
-                        }
-#pragma unroll
-                    for (int jj = 0; jj < 4; jj++) {
-                        if (j0 + jj >= rank) break;
-#pragma unroll
-                        for (int m = 0; m < WM; m++)
-#pragma unroll
-                            for (int r = 0; r < 4; r++) {
-                                const int64_t tok = tok0 + (wave_m * WM + m) * 16 + 4 * kq + r;
-                                float sum = 0.f;
-#pragma unroll
-                                for (int i = 0; i < OG; i++) sum = __builtin_fmaf(y[m][i][r], aj[jj][i], sum);
-                                sum = row16_sum(sum);
-                                if ((lane & 15) == 0 && tok < to.n) xp[(base + tok) * p.xa_stride + j0 + jj] = sum;
-                            }
-                    }
-                }
-            }
-        }
+        glu_epilogue<WM, OG, GR>(p, to, w.rows, acc, tok0 + wave_m * WM * 16, m16_0 + wave_m * WM, m16_n, g0,
+                                 (float *)As0 + wave * 16 * 32, lane, GR ? gd[0] : 0, nt * WGN + wave_n, xa_rank, xa0);
     }
 }
 
@@ -1499,7 +1519,7 @@ void launch_tile_glu_grouped_dev(const GroupSeg *d_gate, const GroupSeg *d_up, c
     p.tiles_m = (int)plan.max_desc;
     if (dx) {
         // the launch's tile columns times its waves: the parts of each pair
-        const int wgn = gate0.tf == TF_BF16 ? 4 : 8, bn = 16 * 2 * wgn;
+        const int wgn = gate0.tf == TF_BF16 ? 4 : 8, bn = 16 * 2 * wgn;  // the grouped GLU's tile columns
         p.xa_a = dx->a;
         p.xa_segs = dx->segs;
         p.xa_stride = dx->max_rank;
