@@ -403,6 +403,32 @@ def forward_leg(dev, fmt, cfg, steps, warmup):
     return r
 
 
+def gemm_leg(dev, fmt, cfg, reps):
+    """The forward's plain large-batch product at the FFN gate shape (N =
+    14336 rows over K = 4096) on the forward's 8192 tokens, its input
+    fragments split once before the timed region (ditch_hip_split_device),
+    then ditch_hip_matmulT_frags_device: the launch the q, o and down
+    projections make."""
+    import torch
+    from ditch_amd import hipmem, synth
+    gen = torch.Generator().manual_seed(7)
+    n, ff, h = cfg["prompts"] * cfg["tokens"], cfg["inter"], cfg["hidden"]
+    w = dev.upload(synth.QUANTIZERS[fmt](torch.randn(ff, h, generator=gen) * 0.02))
+    x = hipmem.Buffer.from_array(np.random.default_rng(3).standard_normal((n, h)).astype(np.float32))
+    fb = w.frag_bytes(n)
+    assert fb, "the large-batch product does not take the FFN shape"
+    xs, out = hipmem.Buffer(fb), hipmem.Buffer(n * ff * 4)
+    w.split_device(xs.ptr, fb, x.ptr, n)
+    ms = time_launches(dev, lambda: w.matmul_frags_device(out.ptr, xs.ptr, n, frag_bytes=fb), reps)
+    w.free()
+    flops = 2.0 * n * ff * h
+    achieved = flops / (ms * 1e-3) / 1e12
+    peak = FP6_FP4_PEAK_TFLOPS if fmt == "mxfp4" else BF16_PEAK_TFLOPS
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic_for(f"gemm_{fmt}"), "avg_launch_ms": round(ms, 4),
+            "algorithmic_flops_per_launch": flops, "kernel": f"large-batch {fmt} product {n}x{ff}x{h}"}
+
+
 def gemv_leg(dev, reps):
     """Q8_0 14336 x 4096 times [M, 4096] activations."""
     import torch
@@ -802,7 +828,7 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip configs[4] (it pins ~48 GB and holds ~100 GB of "
                                                          "host memory)")
     ap.add_argument("--no-trial", action="store_true", help="skip the decode / residual-mean / apply timings")
-    ap.add_argument("--kernel-only", choices=["glu", "gemv", "copy", "c1", "c4", "c5"], default=None,
+    ap.add_argument("--kernel-only", choices=["glu", "gemm", "gemv", "copy", "c1", "c4", "c5"], default=None,
                     help="run only one leg (for rocprofv3 runs)")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
@@ -822,6 +848,9 @@ def main():
 
     if args.kernel_only == "glu":
         print(json.dumps({"kernel_only": "glu", "roofline": roofline_leg(dev, fmt, cfg, args.reps)}))
+        return
+    if args.kernel_only == "gemm":
+        print(json.dumps({"kernel_only": "gemm", "roofline": gemm_leg(dev, fmt, cfg, args.reps)}))
         return
     if args.kernel_only == "gemv":
         print(json.dumps({"kernel_only": "gemv", "gemv": gemv_leg(dev, args.reps)}))
