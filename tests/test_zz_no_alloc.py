@@ -5,7 +5,10 @@ and without term staging, the generic GEMM, the tiled product with split-K,
 the scaled-MFMA product, and a product whose split-K partial sums do not fit
 the scratch, which then runs unsplit). The bar is the product tolerance of
 the VTable products (abs 1e-4, rel 1e-3 of the output scale); where the two
-calls pick the same kernels the outputs are identical."""
+calls pick the same kernels the outputs are identical. Calls on two streams
+are ordered through the one scratch array, and calls captured into a HIP
+graph (global capture mode: an allocation would end the capture with an
+error) give, on every replay, the allocating product's outputs."""
 import ctypes
 
 import numpy as np
@@ -123,3 +126,64 @@ def test_noalloc_calls_on_two_streams_are_ordered(dev):
             t.free()
         for s in streams:
             lib.hipStreamDestroy(s)
+
+
+# (format, rows, cols, n): the tiled product with split-K partial sums in the
+# scratch, the scaled-MFMA product, the GEMV with term staging
+GRAPH_CASES = [("fp8", 4096, 4096, 64), ("mxfp4", 2048, 4096, 256), ("bf16", 1000, 2048, 12)]
+
+
+@pytest.mark.parametrize("first,second", [(0, 1), (1, 2)])
+def test_noalloc_products_replayed_from_a_graph(dev, first, second):
+    """Two products (different weights, inputs and paths) captured on one
+    stream, the graph replayed three times with new inputs uploaded between
+    the replays: every replay equals the allocating product on its inputs."""
+    from ditch_amd.hipmem import hip
+    lib = hip()
+    P = ctypes.c_void_p
+    for name, args in {"hipStreamBeginCapture": [P, ctypes.c_int], "hipStreamEndCapture": [P, ctypes.POINTER(P)],
+                       "hipGraphInstantiate": [ctypes.POINTER(P), P, P, P, ctypes.c_size_t],
+                       "hipGraphLaunch": [P, P], "hipGraphExecDestroy": [P], "hipGraphDestroy": [P]}.items():
+        getattr(lib, name).argtypes = args
+        getattr(lib, name).restype = ctypes.c_int
+    stream = ctypes.c_void_p()
+    assert lib.hipStreamCreateWithFlags(ctypes.byref(stream), 1) == 0  # non-blocking, default priority
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    cases = [GRAPH_CASES[first], GRAPH_CASES[second]]
+    ts = [dev.upload(_weight(f, r, c, 20 + i)) for i, (f, r, c, n) in enumerate(cases)]
+    try:
+        rng = np.random.default_rng(21)
+        bufs = []
+        for (f, r, c, n) in cases:
+            bx = hipmem.Buffer(n * c * 4)
+            bx.upload(rng.standard_normal((n, c)).astype(np.float32))
+            bias = hipmem.Buffer.from_array(rng.standard_normal(r).astype(np.float32))
+            bufs.append((bx, bias, hipmem.Buffer(n * r * 4), hipmem.Buffer(n * r * 4)))
+        dev.sync()
+        assert lib.hipStreamBeginCapture(stream, 0) == 0  # hipStreamCaptureModeGlobal
+        for t, (f, r, c, n), (bx, bias, got, want) in zip(ts, cases, bufs):
+            t.matmul_device_noalloc(got.ptr, bx.ptr, n, d_bias=bias.ptr, stream=stream.value)
+        assert lib.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for replay in range(3):
+            # new inputs (eager, on the library stream), then the graph
+            for (f, r, c, n), (bx, bias, got, want) in zip(cases, bufs):
+                bx.upload(rng.standard_normal((n, c)).astype(np.float32))
+                got.zero()
+            assert lib.hipDeviceSynchronize() == 0
+            assert lib.hipGraphLaunch(exe, stream) == 0
+            assert lib.hipStreamSynchronize(stream) == 0
+            for t, (f, r, c, n), (bx, bias, got, want) in zip(ts, cases, bufs):
+                t.matmul_device(want.ptr, bx.ptr, n, d_bias=bias.ptr)
+            dev.sync()
+            for (f, r, c, n), (bx, bias, got, want) in zip(cases, bufs):
+                np.testing.assert_array_equal(got.download(np.float32, (n, r)), want.download(np.float32, (n, r)),
+                                              err_msg=f"{f} {r}x{c} n={n}, replay {replay}")
+    finally:
+        if exe.value:
+            lib.hipGraphExecDestroy(exe)
+        if graph.value:
+            lib.hipGraphDestroy(graph)
+        for t in ts:
+            t.free()
+        lib.hipStreamDestroy(stream)
