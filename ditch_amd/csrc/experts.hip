@@ -162,22 +162,30 @@ static int find_slot(const ExpertCache &c, int64_t layer, int64_t e) {
     return -1;
 }
 
-// Victim for a fill during layer `cur`: an unpinned slot, empty first, then
-// the one whose layer the forward reaches last from `cur` (the layers just
-// computed), then the least recently used.
+// Victim for a fill during layer `cur`: an unpinned slot, empty first; then
+// one whose expert reloads by DMA from pinned host memory if there is any
+// (so in the steady state of a cache smaller than the experts, the pageable
+// ones stay resident and the shortfall cycles through pinned ones); among
+// those, the one whose layer the forward reaches last from `cur` (the layers
+// just computed), then the least recently used.
 static int victim(const ExpertCache &c, int64_t cur, int64_t nlayers) {
     int best = -1;
     int64_t best_d = -1;
     uint64_t best_stamp = 0;
+    bool best_cheap = false;
     for (size_t i = 0; i < c.slots.size(); i++) {
         const auto &sl = c.slots[i];
         if (sl.pins > 0) continue;
         if (sl.layer < 0) return (int)i;
         const int64_t d = ((sl.layer - cur - 1) % nlayers + nlayers) % nlayers;
-        if (d > best_d || (d == best_d && sl.stamp < best_stamp)) {
+        const bool better = best < 0 || (sl.cheap != best_cheap
+                                             ? sl.cheap
+                                             : (d > best_d || (d == best_d && sl.stamp < best_stamp)));
+        if (better) {
             best = (int)i;
             best_d = d;
             best_stamp = sl.stamp;
+            best_cheap = sl.cheap;
         }
     }
     return best;
@@ -224,6 +232,7 @@ static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64
     DITCH_TRY_HIP(hipEventRecord(sl.loaded, c.copy));
     sl.layer = layer;
     sl.expert = e;
+    sl.cheap = L.eg[e].hm.pinned && L.eu[e].hm.pinned && L.ed[e].hm.pinned;
     sl.used_pending = false;
     sl.prefetched = false;
     sl.stamp = ++c.clock;
@@ -238,15 +247,27 @@ void expert_views(ExpertCache &c, int i, const Layer &L, int64_t e, TileView &g,
 
 // Makes as many of `experts` (from `from` on) resident and pinned as the
 // slots allow; the compute stream `s` waits for their copies. Returns the
-// slots in the order of `experts` (chunk = the prefix that fits).
+// slots in the order of `experts` (chunk = the prefix that fits). The
+// resident ones are pinned first, so that a miss never takes the slot of an
+// expert the same chunk is about to use (the victim rule counts the current
+// layer's other slots as the farthest in the cycle).
 std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts, size_t from,
                                hipStream_t s) {
     ExpertCache &c = cache_of(m);
     std::vector<int> got;
     const int64_t nl = (int64_t)m->layers.size();
+    std::vector<int> resident(experts.size(), -1);
     for (size_t k = from; k < experts.size(); k++) {
+        const int i = find_slot(c, layer, experts[k]);
+        if (i >= 0) {
+            resident[k] = i;
+            c.slots[i].pins++;
+        }
+    }
+    size_t k = from;
+    for (; k < experts.size(); k++) {
         const int64_t e = experts[k];
-        int i = find_slot(c, layer, e);
+        int i = resident[k];
         c.uses[(uint64_t)layer << 32 | (uint64_t)e]++;
         if (i >= 0) {
             // an expert filled ahead of use was still a read (expert_cache.zig:403-410)
@@ -255,16 +276,31 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
             c.slots[i].prefetched = false;
         } else {
             i = victim(c, layer, nl);
-            if (i < 0) break;  // every slot pinned by this chunk
+            // every slot holds an expert this chunk uses later and none is
+            // acquired yet: give those up from the last, so the chunk starts
+            for (size_t j = experts.size(); i < 0 && got.empty() && j-- > k + 1;) {
+                if (resident[j] < 0) continue;
+                c.slots[resident[j]].pins--;
+                resident[j] = -1;
+                i = victim(c, layer, nl);
+            }
+            if (i < 0) {
+                c.uses[(uint64_t)layer << 32 | (uint64_t)e]--;
+                break;  // every slot pinned by this chunk
+            }
             fill(c, m, i, layer, e);
             c.misses++;
+            c.slots[i].pins++;
         }
         auto &sl = c.slots[i];
-        sl.pins++;
         sl.stamp = ++c.clock;
         DITCH_TRY_HIP(hipStreamWaitEvent(s, sl.loaded, 0));
         got.push_back(i);
     }
+    // the resident experts past the chunk: unpinned again (a later chunk
+    // takes them)
+    for (; k < experts.size(); k++)
+        if (resident[k] >= 0) c.slots[resident[k]].pins--;
     DITCH_CHECK(!got.empty(), DITCH_DEVICE_FAILED, "expert cache: no slot free for a chunk");
     return got;
 }
@@ -281,32 +317,35 @@ void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_
     }
 }
 
-// After layer `layer`: copy ahead the experts the next routed layer used in
-// the previous forward, into slots that hold nothing nearer in the cycle.
+// After layer `layer`: copy ahead the experts the next routed layers (up to
+// PREFETCH_LAYERS of them, nearest first) used in the previous forward, into
+// slots that hold nothing nearer in the cycle than the layer copied for. Two
+// layers ahead: the copies for the next one start only once the host has
+// planned this one (its expert counts read back), which leaves them about
+// one layer's compute, less than a layer's refills take.
 void cache_prefetch_next(ditch_hip_model *m, int64_t layer) {
     if (!m->cache) return;
     ExpertCache &c = *m->cache;
+    constexpr int PREFETCH_LAYERS = 2;
     const int64_t nl = (int64_t)m->layers.size();
-    int64_t next = -1;
-    for (int64_t d = 1; d < nl; d++) {
-        const int64_t l = (layer + d) % nl;
-        if (!m->layers[l].eg.empty() && m->moe_layers[l] && m->layers[l].eg[0].streamed()) {
-            next = l;
-            break;
+    int done = 0;
+    for (int64_t d = 1; d < nl && done < PREFETCH_LAYERS; d++) {
+        const int64_t next = (layer + d) % nl;
+        if (m->layers[next].eg.empty() || !m->moe_layers[next] || !m->layers[next].eg[0].streamed()) continue;
+        done++;
+        if ((size_t)next >= c.last_used.size()) continue;
+        const int64_t dist_next = d - 1;
+        for (int32_t e : c.last_used[next]) {
+            if (find_slot(c, next, e) >= 0) continue;
+            const int i = victim(c, layer, nl);
+            if (i < 0) return;
+            const auto &sl = c.slots[i];
+            // never displace an expert the forward needs before `next`
+            if (sl.layer >= 0 && ((sl.layer - layer - 1) % nl + nl) % nl <= dist_next) return;
+            fill(c, m, i, next, e);
+            c.slots[i].prefetched = true;
+            c.prefetches++;
         }
-    }
-    if (next < 0 || (size_t)next >= c.last_used.size()) return;
-    const int64_t dist_next = ((next - layer - 1) % nl + nl) % nl;
-    for (int32_t e : c.last_used[next]) {
-        if (find_slot(c, next, e) >= 0) continue;
-        const int i = victim(c, layer, nl);
-        if (i < 0) return;
-        const auto &sl = c.slots[i];
-        // never displace an expert the forward needs before `next`
-        if (sl.layer >= 0 && ((sl.layer - layer - 1) % nl + nl) % nl <= dist_next) return;
-        fill(c, m, i, next, e);
-        c.slots[i].prefetched = true;
-        c.prefetches++;
     }
 }
 

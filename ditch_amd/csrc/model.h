@@ -75,7 +75,9 @@ TileView view_at(const Mat &mt, const uint8_t *base);
 // slots holding an expert's gate, up and down blobs, filled from pinned host
 // memory by hipMemcpyAsync on a copy stream of its own. Keyed by (layer,
 // expert); pinned while a chunk of a layer computes with them; victims are
-// the unpinned entries whose layer comes back last in the layer cycle (the
+// the unpinned entries whose blobs sit in pinned host memory (their refill
+// is a DMA; a pageable blob goes through the host copy of the staging ring),
+// among those the one whose layer comes back last in the layer cycle (the
 // forward visits layers in order), least recently used among equals.
 struct ExpertCache {
     struct Slot {
@@ -84,6 +86,7 @@ struct ExpertCache {
         uint64_t stamp = 0;
         bool used_pending = false;  // `used` recorded since the last load
         bool prefetched = false;    // filled ahead of use (prefetch, warm): its first use counts as a miss
+        bool cheap = false;         // its three blobs are in pinned host memory: a refill is DMA only
         hipEvent_t used = nullptr;   // the compute stream's last use
         hipEvent_t loaded = nullptr; // the copy stream's last fill
     };

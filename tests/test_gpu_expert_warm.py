@@ -90,7 +90,9 @@ def test_pageable_experts_through_the_staging_ring(dev, monkeypatch):
             np.testing.assert_array_equal(rq, rp)
         sp, sq = pinned.expert_cache_stats(), paged.expert_cache_stats()
         assert sp["bytes_staged"] == 0 and sq["bytes_staged"] > 0
-        assert sq["bytes_staged"] < sq["bytes_read"] == sp["bytes_read"]
+        # the pageable experts stay resident where pinned ones can go (a
+        # pinned expert's refill is one DMA): fewer bytes staged than read
+        assert sq["bytes_staged"] < sq["bytes_read"]
     finally:
         pinned.free()
         paged.free()
