@@ -65,7 +65,12 @@ __device__ __forceinline__ floatx4 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl,
 // (g, c16) holds row c16's scores of keys 4 g + r and 16 + 4 g + r of the
 // chunk. P.V: A = P (row c16, k = those 8 keys), B = V (the same 8 keys,
 // dim c16 of a 16-dim block), D = out rows 4 g + r, dim c16.
-template <int HD, int VD, int NW, bool SPLIT>
+// RB (one query head a KV head, groups == 1): the NW waves take NW
+// consecutive 16-row blocks of the one head instead of NW query heads of one
+// block, so every staged chunk serves 16 NW rows. A row's arithmetic is the
+// same either way: chunks past its own last key give it scores of -inf,
+// exp 0 and no change to its sums.
+template <int HD, int VD, int NW, bool SPLIT, bool RB = false>
 __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     constexpr int KRS = HD + 8;  // K row stride (bf16): 16 keys of one read hit distinct banks
     constexpr int VRS = AK + 8;  // transposed V row stride (bf16)
@@ -75,7 +80,9 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     static_assert(HD % 32 == 0 && VD % 16 == 0, "head dims");
     __shared__ __attribute__((aligned(16))) uint16_t Kh[AK * KRS], Kl[AK * KRS];
     __shared__ __attribute__((aligned(16))) uint16_t Vh[VD * VRS], Vl[VD * VRS];
-    __shared__ int32_t rb[16], rp[16];
+    constexpr int NR = RB ? 16 * NW : 16;  // rows of the workgroup
+    static_assert(NR <= 64, "row masks are 64-bit");
+    __shared__ int32_t rb[NR], rp[NR];
     __shared__ floatx4 Sc[NW][CACHED * KB][64];  // pass 1's scores, [wave][chunk, key block][lane]
     // SPLIT: the block's finished output rows per wave, for the fragments
     constexpr int OS = VD + 4;
@@ -84,13 +91,14 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     if (a.dense && *a.dense) return;  // the whole-prompt kernel took these rows
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int64_t r0 = (int64_t)blockIdx.x * 16;
+    const int wr = RB ? 16 * wave : 0;                   // the wave's first row within the workgroup's
+    const int64_t r0 = (int64_t)blockIdx.x * NR + wr;    // the wave's first row
     const int64_t hkv = blockIdx.y;
-    const int64_t hq = (int64_t)blockIdx.z * NW + wave;  // query head within the group
+    const int64_t hq = RB ? 0 : (int64_t)blockIdx.z * NW + wave;  // query head within the group
     const bool head_ok = hq < a.groups;
     const int64_t h = hkv * a.groups + (head_ok ? hq : 0);
-    if (threadIdx.x < 16) {
-        int64_t r = r0 + threadIdx.x;
+    if (threadIdx.x < NR) {
+        int64_t r = (int64_t)blockIdx.x * NR + threadIdx.x;
         // rows outside the KV cache are skipped like the padding rows
         const bool in = r < a.n && (int64_t)a.rows[r].b < a.nb && (int64_t)a.rows[r].pos < a.T;
         rb[threadIdx.x] = in ? (int32_t)a.rows[r].b : -1;
@@ -242,30 +250,31 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
         }
     };
 
-    int done = 0;
+    uint64_t done = 0;
     for (;;) {
-        // the next prompt among the block's rows
+        // the next prompt among the workgroup's rows
         int first = -1;
-        for (int i = 0; i < 16; i++)
+        for (int i = 0; i < NR; i++)
             if (!((done >> i) & 1) && rb[i] >= 0) {
                 first = i;
                 break;
             }
         if (first < 0) break;
         const int64_t b = rb[first];
-        int in_mask = 0, kmax = -1;
-        for (int i = 0; i < 16; i++)
+        uint64_t in_mask = 0;
+        int kmax = -1;
+        for (int i = 0; i < NR; i++)
             if (rb[i] == b) {
-                in_mask |= 1 << i;
+                in_mask |= (uint64_t)1 << i;
                 kmax = rp[i] > kmax ? rp[i] : kmax;
             }
         done |= in_mask;
         // this lane's row (c16) position, and those of its four output rows
-        const int row_pos = ((in_mask >> c16) & 1) ? rp[c16] : -1;
+        const int row_pos = ((in_mask >> (wr + c16)) & 1) ? rp[wr + c16] : -1;
         int pos[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int row = 4 * g + r;
+            const int row = wr + 4 * g + r;
             pos[r] = ((in_mask >> row) & 1) ? rp[row] : -1;
         }
         const int nch = (kmax + AK) / AK;
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
                 a_words<false, 2>(v, words);
                 const int64_t ktg = (h * VD) / 32 + kt;
 #pragma unroll
-                for (int e = 0; e < 2; e++) xs[(((int64_t)blockIdx.x * a.ldk + ktg) * 2 + e) * 64 + lane] = words[e];
+                for (int e = 0; e < 2; e++) xs[((r0 / 16 * a.ldk + ktg) * 2 + e) * 64 + lane] = words[e];
             }
         }
     }
@@ -632,12 +641,27 @@ static void launch_attn_nw(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
     }
 }
 
+// one query head a KV head (MHA, MLA): four waves on four 16-row blocks of
+// the head, sharing each staged chunk
+template <int HD, int VD>
+static void launch_attn_rows(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
+    constexpr int NW = 4;
+    dim3 grid((unsigned)((a.n + 16 * NW - 1) / (16 * NW)), (unsigned)kv_heads, 1);
+    if (a.xs) {
+        DITCH_CHECK((a.heads * VD) % 128 == 0 && a.ldk * 32 >= a.heads * VD, DITCH_INVALID_ARGUMENT,
+                    "attention: fragment output needs heads * v_head_dim a multiple of 128");
+        hipLaunchKernelGGL((attn_mfma_kernel<HD, VD, NW, true, true>), grid, dim3(NW * 64), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((attn_mfma_kernel<HD, VD, NW, false, true>), grid, dim3(NW * 64), 0, s, a);
+    }
+}
+
 // one wave per query head of the group, up to four per workgroup
 template <int HD, int VD>
 static void launch_attn(const AttnArgs &a, int64_t kv_heads, hipStream_t s) {
     if (a.groups >= 4) launch_attn_nw<HD, VD, 4>(a, kv_heads, s);
     else if (a.groups == 2 || a.groups == 3) launch_attn_nw<HD, VD, 2>(a, kv_heads, s);
-    else launch_attn_nw<HD, VD, 1>(a, kv_heads, s);
+    else launch_attn_rows<HD, VD>(a, kv_heads, s);
 }
 
 // Whether the whole-prompt kernel can take a forward's attention (head dims
