@@ -31,7 +31,7 @@ void host_mat_free(HostMat &hm) {
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-void stream_out(Mat &mt, uint64_t &pinned_bytes, bool &pinned_exhausted) {
+void stream_out(Mat &mt, uint64_t &pinned_bytes, uint64_t pinned_limit, uint64_t &pinned_total, bool &pinned_exhausted) {
     ditch_hip_tensor *t = mt.t;
     DITCH_CHECK(t, DITCH_INVALID_ARGUMENT, "stream_out of an empty slot");
     void *parts[6] = {t->codes, t->scale, t->zero, t->side, t->mx, t->mx_scales};
@@ -42,12 +42,11 @@ void stream_out(Mat &mt, uint64_t &pinned_bytes, bool &pinned_exhausted) {
     }
     HostMat hm;
     const size_t alloc = total ? total : 256;
-    uint64_t limit = EXPERT_PINNED_LIMIT;
-    if (const char *ev = getenv("DITCH_HIP_EXPERT_PINNED_LIMIT")) limit = strtoull(ev, nullptr, 10);
-    if (!pinned_exhausted && pinned_bytes + alloc <= limit) {
+    if (!pinned_exhausted && pinned_bytes + alloc <= pinned_limit) {
         if (hipHostMalloc((void **)&hm.host, alloc, hipHostMallocDefault) == hipSuccess) {
             hm.pinned = true;
             pinned_bytes += alloc;
+            pinned_total += alloc;
         } else {
             (void)hipGetLastError();
             hm.host = nullptr;
@@ -148,6 +147,7 @@ static ExpertCache &cache_of(ditch_hip_model *m) {
         }
         DITCH_TRY_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking));
         c->last_used.resize(m->layers.size());
+        c->resident_layer.assign(m->layers.size(), 0);
     } catch (...) {
         delete c;
         throw;
@@ -156,36 +156,70 @@ static ExpertCache &cache_of(ditch_hip_model *m) {
     return *c;
 }
 
+static uint64_t slot_key(int64_t layer, int64_t e) { return (uint64_t)layer << 32 | (uint64_t)e; }
+
 static int find_slot(const ExpertCache &c, int64_t layer, int64_t e) {
-    for (size_t i = 0; i < c.slots.size(); i++)
-        if (c.slots[i].layer == layer && c.slots[i].expert == e) return (int)i;
-    return -1;
+    const auto it = c.where.find(slot_key(layer, e));
+    return it == c.where.end() ? -1 : it->second;
+}
+
+// Routed layers copied ahead after each routed layer (see cache_prefetch_next).
+constexpr int PREFETCH_LAYERS = 2;
+
+// Experts layer `l` routed in the last forward that are not resident.
+static int64_t hole_of(const ExpertCache &c, int64_t l) {
+    return (int64_t)c.last_used[l].size() - c.resident_layer[l];
+}
+
+// The most experts a layer may be missing once the copies ahead have made
+// room: the shortfall (experts the routed layers used last minus slots)
+// spread over the routed layers that are not being copied ahead. A cache
+// short by D experts then refills about D / (routed - PREFETCH_LAYERS) of
+// them for each routed layer, a steady stream of copies under the compute,
+// where letting the whole shortfall sit in one layer makes that layer wait
+// for all of it. 0: no shortfall, no cap.
+static int64_t hole_cap(const ExpertCache &c, const ditch_hip_model *m) {
+    int64_t want = 0, routed = 0;
+    for (size_t l = 0; l < c.last_used.size(); l++)
+        if (m->moe_layers[l]) {
+            routed++;
+            want += (int64_t)c.last_used[l].size();
+        }
+    const int64_t short_by = want - (int64_t)c.slots.size(), spread = routed - PREFETCH_LAYERS;
+    if (short_by <= 0 || spread <= 0) return 0;
+    return (short_by + spread - 1) / spread;
 }
 
 // Victim for a fill during layer `cur`: an unpinned slot, empty first; then
-// one whose expert reloads by DMA from pinned host memory if there is any
-// (so in the steady state of a cache smaller than the experts, the pageable
-// ones stay resident and the shortfall cycles through pinned ones); among
-// those, the one whose layer the forward reaches last from `cur` (the layers
-// just computed), then the least recently used.
-static int victim(const ExpertCache &c, int64_t cur, int64_t nlayers) {
+// the slot whose layer the forward reaches last from `cur` (the layers just
+// computed), among that layer's slots one whose expert reloads by DMA from
+// pinned host memory (so the pageable ones stay resident), then the least
+// recently used. A copy ahead for a layer `ahead` routed layers on passes
+// `cap` > 0: layers further than that whose missing experts are below the
+// cap come first, so the shortfall spreads over the layers.
+static int victim(const ExpertCache &c, int64_t cur, int64_t nlayers, int64_t cap = 0, int64_t ahead = -1) {
     int best = -1;
     int64_t best_d = -1;
     uint64_t best_stamp = 0;
-    bool best_cheap = false;
+    bool best_cheap = false, best_open = false;
     for (size_t i = 0; i < c.slots.size(); i++) {
         const auto &sl = c.slots[i];
         if (sl.pins > 0) continue;
         if (sl.layer < 0) return (int)i;
         const int64_t d = ((sl.layer - cur - 1) % nlayers + nlayers) % nlayers;
-        const bool better = best < 0 || (sl.cheap != best_cheap
-                                             ? sl.cheap
-                                             : (d > best_d || (d == best_d && sl.stamp < best_stamp)));
+        const bool open = cap > 0 && d > ahead && hole_of(c, sl.layer) < cap;
+        bool better;
+        if (best < 0) better = true;
+        else if (open != best_open) better = open;
+        else if (d != best_d) better = d > best_d;
+        else if (sl.cheap != best_cheap) better = sl.cheap;
+        else better = sl.stamp < best_stamp;
         if (better) {
             best = (int)i;
             best_d = d;
             best_stamp = sl.stamp;
             best_cheap = sl.cheap;
+            best_open = open;
         }
     }
     return best;
@@ -230,8 +264,14 @@ static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64
         off += align256(mt->hm.bytes);
     }
     DITCH_TRY_HIP(hipEventRecord(sl.loaded, c.copy));
+    if (sl.layer >= 0) {
+        c.where.erase(slot_key(sl.layer, sl.expert));
+        c.resident_layer[sl.layer]--;
+    }
     sl.layer = layer;
     sl.expert = e;
+    c.where[slot_key(layer, e)] = i;
+    c.resident_layer[layer]++;
     sl.cheap = L.eg[e].hm.pinned && L.eu[e].hm.pinned && L.ed[e].hm.pinned;
     sl.used_pending = false;
     sl.prefetched = false;
@@ -319,15 +359,16 @@ void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_
 
 // After layer `layer`: copy ahead the experts the next routed layers (up to
 // PREFETCH_LAYERS of them, nearest first) used in the previous forward, into
-// slots that hold nothing nearer in the cycle than the layer copied for. Two
-// layers ahead: the copies for the next one start only once the host has
-// planned this one (its expert counts read back), which leaves them about
-// one layer's compute, less than a layer's refills take.
+// slots that hold nothing nearer in the cycle than the layer copied for,
+// taking them from the layers whose missing experts are under hole_cap().
+// Two layers ahead: a copy into a slot of the layer just computed starts
+// once that layer's products are done with it, which leaves it about one
+// layer's compute.
 void cache_prefetch_next(ditch_hip_model *m, int64_t layer) {
     if (!m->cache) return;
     ExpertCache &c = *m->cache;
-    constexpr int PREFETCH_LAYERS = 2;
     const int64_t nl = (int64_t)m->layers.size();
+    const int64_t cap = hole_cap(c, m);
     int done = 0;
     for (int64_t d = 1; d < nl && done < PREFETCH_LAYERS; d++) {
         const int64_t next = (layer + d) % nl;
@@ -337,7 +378,7 @@ void cache_prefetch_next(ditch_hip_model *m, int64_t layer) {
         const int64_t dist_next = d - 1;
         for (int32_t e : c.last_used[next]) {
             if (find_slot(c, next, e) >= 0) continue;
-            const int i = victim(c, layer, nl);
+            const int i = victim(c, layer, nl, cap, dist_next);
             if (i < 0) return;
             const auto &sl = c.slots[i];
             // never displace an expert the forward needs before `next`

@@ -60,13 +60,14 @@ struct Vec {
     }
 };
 
-// Moves an uploaded matrix to pinned host memory (frees its device parts).
-// Moves a registered routed expert matrix to host memory: pinned while the
-// model's pinned bytes stay under EXPERT_PINNED_LIMIT and the allocation
-// succeeds, pageable after that (systems cap pinned memory; these GPU hosts
-// pin about 65 GiB).
+// Moves a registered routed expert matrix to host memory (frees its device
+// parts): pinned while its layer's pinned bytes stay under `pinned_limit`
+// and the allocation succeeds, pageable after that (systems cap pinned
+// memory; these GPU hosts pin about 65 GiB). The model's EXPERT_PINNED_LIMIT
+// is shared evenly by its routed layers, so every layer has experts whose
+// refill is one DMA.
 constexpr uint64_t EXPERT_PINNED_LIMIT = (uint64_t)48 << 30;
-void stream_out(Mat &mt, uint64_t &pinned_bytes, bool &pinned_exhausted);
+void stream_out(Mat &mt, uint64_t &pinned_bytes, uint64_t pinned_limit, uint64_t &pinned_total, bool &pinned_exhausted);
 // The matrix's TileView with its device pointers inside a copy of its host
 // blob at `base`.
 TileView view_at(const Mat &mt, const uint8_t *base);
@@ -75,10 +76,12 @@ TileView view_at(const Mat &mt, const uint8_t *base);
 // slots holding an expert's gate, up and down blobs, filled from pinned host
 // memory by hipMemcpyAsync on a copy stream of its own. Keyed by (layer,
 // expert); pinned while a chunk of a layer computes with them; victims are
-// the unpinned entries whose blobs sit in pinned host memory (their refill
-// is a DMA; a pageable blob goes through the host copy of the staging ring),
-// among those the one whose layer comes back last in the layer cycle (the
-// forward visits layers in order), least recently used among equals.
+// the unpinned entries whose layer comes back last in the layer cycle (the
+// forward visits layers in order), among those one whose blobs sit in pinned
+// host memory (a refill by DMA; a pageable blob goes through the host copy
+// of the staging ring), least recently used among equals. Copies ahead
+// spread the shortfall over the layers (a cap on each layer's missing
+// experts).
 struct ExpertCache {
     struct Slot {
         int64_t layer = -1, expert = -1;
@@ -97,6 +100,8 @@ struct ExpertCache {
     uint64_t hits = 0, misses = 0, prefetches = 0, bytes_read = 0, evictions = 0;
     std::vector<std::vector<int32_t>> last_used;  // per layer: experts routed by the last forward
     std::unordered_map<uint64_t, uint64_t> uses;   // (layer << 32 | expert) -> acquisitions
+    std::unordered_map<uint64_t, int> where;       // (layer << 32 | expert) -> its slot
+    std::vector<int64_t> resident_layer;           // per layer: slots holding one of its experts
     uint64_t warmed = 0;
     // pinned staging ring for pageable blobs: a buffer is refilled once the
     // copy stream has passed its last copy
@@ -168,6 +173,7 @@ struct ditch_hip_model {
     ditch::DevBuf edit_v, edit_part;  // the none-mode edits' directions and the edit batch's tables
     uint64_t expert_budget = 0;    // > 0: routed experts stream from pinned host memory
     uint64_t expert_pinned = 0;    // host bytes of routed experts held pinned
+    std::vector<uint64_t> expert_pinned_layer;  // the same per layer
     bool expert_pinned_exhausted = false;
     // routed layers run with the grouped products planned on the device /
     // on the host (after reading the expert counts back), since creation

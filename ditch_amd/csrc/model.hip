@@ -873,7 +873,12 @@ void model_set(ditch_hip_model *m, int layer, int slot, int expert, const ditch_
     if (m->expert_budget > 0 &&
         (slot == DITCH_SLOT_EXPERT_GATE || slot == DITCH_SLOT_EXPERT_UP || slot == DITCH_SLOT_EXPERT_DOWN)) {
         DITCH_CHECK(!m->cache, DITCH_INVALID_ARGUMENT, "expert registered after the expert cache was built");
-        stream_out(*mt, m->expert_pinned, m->expert_pinned_exhausted);
+        uint64_t limit = EXPERT_PINNED_LIMIT;
+        if (const char *ev = getenv("DITCH_HIP_EXPERT_PINNED_LIMIT")) limit = strtoull(ev, nullptr, 10);
+        const uint64_t routed = std::max<uint64_t>(
+            1, (uint64_t)std::count_if(m->moe_layers.begin(), m->moe_layers.end(), [](uint8_t f) { return f != 0; }));
+        if (m->expert_pinned_layer.size() != m->layers.size()) m->expert_pinned_layer.assign(m->layers.size(), 0);
+        stream_out(*mt, m->expert_pinned_layer[layer], limit / routed, m->expert_pinned, m->expert_pinned_exhausted);
     }
 }
 
