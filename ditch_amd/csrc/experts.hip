@@ -104,10 +104,10 @@ TileView view_at(const Mat &mt, const uint8_t *base) {
 
 ExpertCache::~ExpertCache() {
     if (copy) (void)hipStreamSynchronize(copy);
-    for (Slot &sl : slots) {
-        if (sl.used) (void)hipEventDestroy(sl.used);
+    for (Slot &sl : slots)
         if (sl.loaded) (void)hipEventDestroy(sl.loaded);
-    }
+    for (hipEvent_t ev : use_ev)
+        if (ev) (void)hipEventDestroy(ev);
     for (int b = 0; b < NSTAGE; b++) {
         if (stage[b]) (void)hipHostFree(stage[b]);
         if (stage_done[b]) (void)hipEventDestroy(stage_done[b]);
@@ -141,10 +141,8 @@ static ExpertCache &cache_of(ditch_hip_model *m) {
         c->slot_bytes = slot;
         c->arena = (uint8_t *)dev_alloc(n * slot);
         c->slots.resize(n);
-        for (auto &sl : c->slots) {
-            DITCH_TRY_HIP(hipEventCreateWithFlags(&sl.used, hipEventDisableTiming));
-            DITCH_TRY_HIP(hipEventCreateWithFlags(&sl.loaded, hipEventDisableTiming));
-        }
+        for (auto &sl : c->slots) DITCH_TRY_HIP(hipEventCreateWithFlags(&sl.loaded, hipEventDisableTiming));
+        for (hipEvent_t &ev : c->use_ev) DITCH_TRY_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
         DITCH_TRY_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking));
         c->last_used.resize(m->layers.size());
         c->resident_layer.assign(m->layers.size(), 0);
@@ -253,7 +251,10 @@ static void stage_copy(ExpertCache &c, uint8_t *dst, const uint8_t *src, size_t 
 static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64_t e) {
     auto &sl = c.slots[i];
     if (sl.layer >= 0) c.evictions++;
-    if (sl.used_pending) DITCH_TRY_HIP(hipStreamWaitEvent(c.copy, sl.used, 0));
+    if (sl.use_serial > c.released_done && sl.use_serial > c.copy_waited) {
+        DITCH_TRY_HIP(hipStreamWaitEvent(c.copy, c.use_ev[sl.use_serial % ExpertCache::USE_RING], 0));
+        c.copy_waited = sl.use_serial;
+    }
     const Layer &L = m->layers[layer];
     uint8_t *base = c.arena + (uint64_t)i * c.slot_bytes;
     uint64_t off = 0;
@@ -273,7 +274,7 @@ static void fill(ExpertCache &c, ditch_hip_model *m, int i, int64_t layer, int64
     c.where[slot_key(layer, e)] = i;
     c.resident_layer[layer]++;
     sl.cheap = L.eg[e].hm.pinned && L.eu[e].hm.pinned && L.ed[e].hm.pinned;
-    sl.used_pending = false;
+    sl.load_serial = ++c.loads;
     sl.prefetched = false;
     sl.stamp = ++c.clock;
 }
@@ -304,6 +305,8 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
             c.slots[i].pins++;
         }
     }
+    uint64_t newest = 0;
+    int newest_slot = -1;
     size_t k = from;
     for (; k < experts.size(); k++) {
         const int64_t e = experts[k];
@@ -334,9 +337,15 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
         }
         auto &sl = c.slots[i];
         sl.stamp = ++c.clock;
-        DITCH_TRY_HIP(hipStreamWaitEvent(s, sl.loaded, 0));
+        if (sl.load_serial > newest) {
+            newest = sl.load_serial;
+            newest_slot = i;
+        }
         got.push_back(i);
     }
+    // the copy stream is in order: its newest fill among the chunk's slots
+    // done means all of them are
+    if (newest_slot >= 0) DITCH_TRY_HIP(hipStreamWaitEvent(s, c.slots[newest_slot].loaded, 0));
     // the resident experts past the chunk: unpinned again (a later chunk
     // takes them)
     for (; k < experts.size(); k++)
@@ -349,12 +358,17 @@ std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vec
 // the stream has passed this point.
 void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_t s) {
     ExpertCache &c = *m->cache;
+    const uint64_t k = ++c.released;
+    DITCH_TRY_HIP(hipEventRecord(c.use_ev[k % ExpertCache::USE_RING], s));
     for (int i : slots) {
         auto &sl = c.slots[i];
-        DITCH_TRY_HIP(hipEventRecord(sl.used, s));
-        sl.used_pending = true;
+        sl.use_serial = k;
         sl.pins--;
     }
+}
+
+void cache_synced(ditch_hip_model *m) {
+    if (m->cache) m->cache->released_done = m->cache->released;
 }
 
 // After layer `layer`: copy ahead the experts the next routed layers (up to

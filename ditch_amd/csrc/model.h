@@ -87,12 +87,21 @@ struct ExpertCache {
         int64_t layer = -1, expert = -1;
         int pins = 0;
         uint64_t stamp = 0;
-        bool used_pending = false;  // `used` recorded since the last load
         bool prefetched = false;    // filled ahead of use (prefetch, warm): its first use counts as a miss
         bool cheap = false;         // its three blobs are in pinned host memory: a refill is DMA only
-        hipEvent_t used = nullptr;   // the compute stream's last use
+        uint64_t use_serial = 0;     // the release (chunk) that last used it, 0: none
+        uint64_t load_serial = 0;    // the fill that last loaded it
         hipEvent_t loaded = nullptr; // the copy stream's last fill
     };
+    // One event per released chunk, recorded on the compute stream, in a
+    // ring: a slot's refill waits on its last chunk's event unless the host
+    // has seen that release complete (a synchronisation of the compute
+    // stream) or the copy stream already waits on a later one. An event the
+    // ring re-records marks a later point of the same stream, so a late wait
+    // on it is only longer, never short.
+    static constexpr int USE_RING = 64;
+    hipEvent_t use_ev[USE_RING] = {};
+    uint64_t released = 0, released_done = 0, copy_waited = 0, loads = 0;
     uint64_t capacity = 0, slot_bytes = 0, clock = 0;
     uint8_t *arena = nullptr;
     std::vector<Slot> slots;
@@ -119,6 +128,8 @@ struct Layer;
 std::vector<int> cache_acquire(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts, size_t from,
                                hipStream_t s);
 void cache_release(ditch_hip_model *m, const std::vector<int> &slots, hipStream_t s);
+// The compute stream was synchronised: every chunk released on it is done.
+void cache_synced(ditch_hip_model *m);
 void cache_note_layer(ditch_hip_model *m, int64_t layer, const std::vector<int32_t> &experts);
 void cache_prefetch_next(ditch_hip_model *m, int64_t layer);
 struct HotExpert {

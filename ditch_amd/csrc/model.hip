@@ -253,6 +253,65 @@ __global__ void mla_assemble_kernel(float *k, float *v, const float *kvb, const 
     }
 }
 
+// MLA keys and values written straight into the KV cache, one block per row
+// (the assembly of model.zig:3330-3341 and the RoPE of model.zig:4253-4295
+// in one pass): head h's key is [kv_b nope part | k_pe], k_pe (the row's
+// kv_a tail, shared by every head) rotated once per row; its value is [kv_b
+// v part | 0]; the queries' rope coordinates are rotated in place. The same
+// values as assembling k and v per head and rotating each head's copy of
+// k_pe, without the two row-sized intermediates. Needs hd == nope + rd and
+// every width a multiple of 4 (float4 rows).
+struct MlaCacheArgs {
+    float *q;
+    const float *kvb, *kva;
+    float *kc, *vc;
+    const ditch_row *rows;
+    const float *cos_t, *sin_t;
+    int64_t heads, hd, nope, rd, vd, kv_lora, half, rope_len, T, nb, kvd;
+    int style;
+};
+
+__global__ __launch_bounds__(256) void mla_rope_cache_kernel(MlaCacheArgs a) {
+    __shared__ __align__(16) float kpe[512];
+    const int64_t i = blockIdx.x;
+    const int64_t pos = a.rows[i].pos, b = a.rows[i].b;
+    if (b >= a.nb || pos >= a.T) return;  // outside the KV cache: the row is skipped
+    const int64_t p = pos < a.rope_len - 1 ? pos : a.rope_len - 1;
+    const float *cr = a.cos_t + p * a.half, *sr = a.sin_t + p * a.half;
+    const bool gptj = a.style == DITCH_ROPE_GPTJ;
+    const float *pe = a.kva + i * (a.kv_lora + a.rd) + a.kv_lora;
+    for (int64_t d = threadIdx.x; d < a.rd; d += blockDim.x) {
+        float y = pe[d];
+        if (d < 2 * a.half) {
+            const int64_t j = gptj ? d / 2 : d % a.half;
+            const int64_t ia = gptj ? 2 * j : j, ib = gptj ? 2 * j + 1 : j + a.half;
+            const float x1 = pe[ia], x2 = pe[ib], c = cr[j], sn = sr[j];
+            y = d == ia ? __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)) : __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sn));
+        }
+        kpe[d] = y;
+    }
+    // the queries' rope pairs, one pair a thread (in place)
+    float *qr = a.q + i * a.heads * a.hd + a.nope;
+    for (int64_t t = threadIdx.x; t < a.heads * a.half; t += blockDim.x) {
+        const int64_t h = t / a.half, j = t % a.half;
+        float *x = qr + h * a.hd;
+        const int64_t ia = gptj ? 2 * j : j, ib = gptj ? 2 * j + 1 : j + a.half;
+        const float x1 = x[ia], x2 = x[ib], c = cr[j], sn = sr[j];
+        x[ia] = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn));
+        x[ib] = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sn));
+    }
+    __syncthreads();
+    const int64_t hd4 = a.hd / 4, kvb_row = a.heads * (a.nope + a.vd);
+    const float *src = a.kvb + i * kvb_row;
+    float4 *kd = (float4 *)(a.kc + (b * a.T + pos) * a.kvd), *vdst = (float4 *)(a.vc + (b * a.T + pos) * a.kvd);
+    for (int64_t t = threadIdx.x; t < a.heads * hd4; t += blockDim.x) {
+        const int64_t h = t / hd4, d = (t % hd4) * 4;
+        const float *hs = src + h * (a.nope + a.vd);
+        kd[t] = d < a.nope ? *(const float4 *)(hs + d) : *(const float4 *)(kpe + (d - a.nope));
+        vdst[t] = d < a.vd ? *(const float4 *)(hs + a.nope + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 // Router (moe.zig:1011-1101) for one token per thread: softmax or sigmoid
 // scores, correction bias, group-limited masking, top-k with strict '>',
 // renormalisation and scaling.
@@ -1146,6 +1205,7 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
     std::vector<int32_t> hc(E), ho(E);
     DITCH_TRY_HIP(hipMemcpyAsync(hc.data(), counts, E * 4, hipMemcpyDeviceToHost, s));
     DITCH_TRY_HIP(hipStreamSynchronize(s));
+    cache_synced(m);
     int32_t acc = 0, max_cnt = 0;
     for (int64_t e = 0; e < E; e++) {
         ho[e] = acc;
@@ -1245,7 +1305,10 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
             // a layer in several chunks: the host tables of this chunk go out
             // of scope before the next is built (the degraded case, when the
             // cache holds fewer experts than the layer routes to)
-            if (from + cnt < used.size()) DITCH_TRY_HIP(hipStreamSynchronize(s));
+            if (from + cnt < used.size()) {
+                DITCH_TRY_HIP(hipStreamSynchronize(s));
+                cache_synced(m);
+            }
         }
         from += cnt;
     }
@@ -1342,6 +1405,9 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
         } else {
             launch_rmsnorm(h, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
         }
+        // MLA: keys and values go to the cache in one kernel with the RoPE
+        bool mla_fused = false;
+        const float *mla_kvb = nullptr, *mla_kva = nullptr;
         if (c.mla) {
             int64_t nope = (int64_t)c.qk_nope_dim, rd = (int64_t)c.qk_rope_dim, kvl = (int64_t)c.kv_lora_rank;
             if (L.q_a.ok()) {
@@ -1359,9 +1425,16 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             launch_rmsnorm_strided(ckv, kva, L.kv_a_norm.p, L.kv_a_norm.len, n, kvl, kvl + rd, kvl, c.mla_norm_eps, s);
             float *kvb = m->o.get<float>(n * nh * (nope + vd));
             mm(m, L.kv_b, kvb, ckv, n, nullptr, 0, s);
-            hipLaunchKernelGGL(mla_assemble_kernel, dim3(grid_for(n * nh * hd)), dim3(256), 0, s, kk, vv, kvb, kva, n,
-                               nh, hd, nope, rd, vd, kvl);
-            DITCH_TRY_HIP(hipGetLastError());
+            mla_fused = !c.qk_norm && hd == nope + rd && rd <= 512 && vd <= hd && hd % 4 == 0 && nope % 4 == 0 &&
+                        vd % 4 == 0 && kvl % 4 == 0 && rd % 4 == 0 && 2 * (int64_t)(c.rotary_dim / 2) <= rd;
+            if (mla_fused) {
+                mla_kvb = kvb;
+                mla_kva = kva;
+            } else {
+                hipLaunchKernelGGL(mla_assemble_kernel, dim3(grid_for(n * nh * hd)), dim3(256), 0, s, kk, vv, kvb, kva,
+                                   n, nh, hd, nope, rd, vd, kvl);
+                DITCH_TRY_HIP(hipGetLastError());
+            }
         } else {
             mm_act(m, L.q, q, hact, n, L.q_bias.p, 0, s);
             mm_act(m, L.k, kk, hact, n, L.k_bias.p, 0, s);
@@ -1411,7 +1484,14 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
         ra.style = c.rope_style;
         ra.dense = q_rope_in_attn ? dense_flag : nullptr;
         ra.q_in_attn = q_rope_in_attn ? 1 : 0;
-        hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
+        if (mla_fused) {
+            MlaCacheArgs ma{q, mla_kvb, mla_kva, kc, vc, d_rows, m->rope_cos, m->rope_sin, nh, hd,
+                            (int64_t)c.qk_nope_dim, (int64_t)c.qk_rope_dim, vd, (int64_t)c.kv_lora_rank, ra.half,
+                            ra.rope_len, T, B, kvd, c.rope_style};
+            hipLaunchKernelGGL(mla_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ma);
+        } else {
+            hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)n), dim3(256), 0, s, ra);
+        }
         DITCH_TRY_HIP(hipGetLastError());
         AttnArgs aa{q, kc, vc, att, d_rows, n, nh, nh / nkv, hd, vd, T, kvd, c.attn_scale, nullptr, 0, B, nullptr};
         Act aact{att, nullptr, 0};
