@@ -1322,12 +1322,24 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         int64_t si = L.sh_gate.t->v.rows;
         DITCH_CHECK(L.sh_up.ok() && L.sh_down.ok() && L.sh_up.t->v.rows == si && L.sh_down.t->v.cols == si,
                     DITCH_INVALID_ARGUMENT, "forward: shared expert gate/up/down widths disagree");
-        float *sgb = m->g.get<float>(n * si), *sub = m->u.get<float>(n * si);
-        mm(m, L.sh_gate, sgb, h, n, nullptr, 0, s);
-        mm(m, L.sh_up, sub, h, n, nullptr, 0, s);
-        launch_gated_act(0, sgb, sgb, sub, n, si, si, si, s);
         esh = m->e_shared.get<float>(n * hidden);
-        mm(m, L.sh_down, esh, sgb, n, nullptr, 0, s);
+        if (n >= 128 && L.sh_gate.rank == 0 && L.sh_up.rank == 0 && tile_glu_takes(L.sh_gate.t->v, L.sh_up.t->v, n) &&
+            frag_only(L.sh_down, n)) {
+            // gate, up and the activation in one tiled product whose epilogue
+            // writes the down product's fragments (as the dense layers' MLP)
+            const int64_t ldk_h = split_ldk(hidden), ldk_i = split_ldk(si);
+            void *hs = m->hs.get<uint8_t>(split_bytes_ldk(n, ldk_h, 2));
+            launch_split(hs, h, nullptr, n, hidden, hidden, ldk_h, 2, s);
+            void *as = m->acts.get<uint8_t>(split_bytes_ldk(n, ldk_i, 2));
+            launch_tile_glu(L.sh_gate.t->v, L.sh_up.t->v, 0, nullptr, as, ldk_i, hs, ldk_h, n, s);
+            mm_act(m, L.sh_down, esh, Act{nullptr, as, ldk_i}, n, nullptr, 0, s);
+        } else {
+            float *sgb = m->g.get<float>(n * si), *sub = m->u.get<float>(n * si);
+            mm(m, L.sh_gate, sgb, h, n, nullptr, 0, s);
+            mm(m, L.sh_up, sub, h, n, nullptr, 0, s);
+            launch_gated_act(0, sgb, sgb, sub, n, si, si, si, s);
+            mm(m, L.sh_down, esh, sgb, n, nullptr, 0, s);
+        }
     }
     // a wave of 64 threads covers 256 columns; grid_for's block count keeps
     // every grid-stride step a whole number of waves
@@ -1413,14 +1425,14 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             if (L.q_a.ok()) {
                 int64_t qlr = (int64_t)c.q_lora_rank;
                 float *qa = m->mla_a.get<float>(n * qlr);
-                mm(m, L.q_a, qa, h, n, nullptr, 0, s);
+                mm_act(m, L.q_a, qa, hact, n, nullptr, 0, s);
                 launch_rmsnorm(qa, qa, L.q_a_norm.p, L.q_a_norm.len, n, qlr, c.mla_norm_eps, 0, s);
                 mm(m, L.q_b, q, qa, n, nullptr, 0, s);
             } else {
-                mm(m, L.q_b, q, h, n, nullptr, 0, s);
+                mm_act(m, L.q_b, q, hact, n, nullptr, 0, s);
             }
             float *kva = m->mla_b.get<float>(n * (kvl + rd));
-            mm(m, L.kv_a, kva, h, n, nullptr, 0, s);
+            mm_act(m, L.kv_a, kva, hact, n, nullptr, 0, s);
             float *ckv = m->mla_c.get<float>(n * kvl);
             launch_rmsnorm_strided(ckv, kva, L.kv_a_norm.p, L.kv_a_norm.len, n, kvl, kvl + rd, kvl, c.mla_norm_eps, s);
             float *kvb = m->o.get<float>(n * nh * (nope + vd));
