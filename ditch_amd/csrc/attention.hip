@@ -71,7 +71,7 @@ __device__ __forceinline__ floatx4 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl,
 // same either way: chunks past its own last key give it scores of -inf,
 // exp 0 and no change to its sums.
 template <int HD, int VD, int NW, bool SPLIT, bool RB = false>
-__global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_mfma_kernel(AttnArgs a) {
     constexpr int KRS = HD + 8;  // K row stride (bf16): 16 keys of one read hit distinct banks
     constexpr int VRS = AK + 8;  // transposed V row stride (bf16)
     constexpr int QS = HD / 32;  // k steps of the scores
@@ -92,13 +92,24 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int wr = RB ? 16 * wave : 0;                   // the wave's first row within the workgroup's
-    const int64_t r0 = (int64_t)blockIdx.x * NR + wr;    // the wave's first row
-    const int64_t hkv = blockIdx.y;
+    // (row block, KV head) of this workgroup: the hardware deals workgroups
+    // to the 8 XCDs in turn, so consecutive ids are remapped to give each
+    // XCD a contiguous run of row blocks of one head (the row blocks of a
+    // prompt read the same keys and values, then from that XCD's L2)
+    uint32_t bx, by;
+    {
+        const uint32_t X = gridDim.x, N = X * gridDim.y, L = blockIdx.x + X * blockIdx.y;
+        const uint32_t per = N / 8, G = L < per * 8 ? (L % 8) * per + L / 8 : L;
+        bx = G % X;
+        by = G / X;
+    }
+    const int64_t r0 = (int64_t)bx * NR + wr;    // the wave's first row
+    const int64_t hkv = by;
     const int64_t hq = RB ? 0 : (int64_t)blockIdx.z * NW + wave;  // query head within the group
     const bool head_ok = hq < a.groups;
     const int64_t h = hkv * a.groups + (head_ok ? hq : 0);
     if (threadIdx.x < NR) {
-        int64_t r = (int64_t)blockIdx.x * NR + threadIdx.x;
+        int64_t r = (int64_t)bx * NR + threadIdx.x;
         // rows outside the KV cache are skipped like the padding rows
         const bool in = r < a.n && (int64_t)a.rows[r].b < a.nb && (int64_t)a.rows[r].pos < a.T;
         rb[threadIdx.x] = in ? (int32_t)a.rows[r].b : -1;
@@ -250,24 +261,21 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(AttnArgs a) {
         }
     };
 
+    // lane i (< NR) holds row i's prompt and position: the row sets below
+    // are wave ballots
+    const int lb = lane < NR ? rb[lane] : -1, lp = lane < NR ? rp[lane] : -1;
     uint64_t done = 0;
     for (;;) {
-        // the next prompt among the workgroup's rows
-        int first = -1;
-        for (int i = 0; i < NR; i++)
-            if (!((done >> i) & 1) && rb[i] >= 0) {
-                first = i;
-                break;
-            }
-        if (first < 0) break;
-        const int64_t b = rb[first];
-        uint64_t in_mask = 0;
-        int kmax = -1;
-        for (int i = 0; i < NR; i++)
-            if (rb[i] == b) {
-                in_mask |= (uint64_t)1 << i;
-                kmax = rp[i] > kmax ? rp[i] : kmax;
-            }
+        // the next prompt among the workgroup's rows (the first row not done)
+        const uint64_t open = __ballot(lb >= 0) & ~done;
+        if (open == 0) break;
+        const int first = __builtin_ctzll(open);
+        const int64_t b = __builtin_amdgcn_readlane(lb, first);
+        const uint64_t in_mask = __ballot(lb == b);
+        int kmax = lb == b ? lp : -1;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
+        kmax = __builtin_amdgcn_readfirstlane(kmax);
         done |= in_mask;
         // this lane's row (c16) position, and those of its four output rows
         const int row_pos = ((in_mask >> (wr + c16)) & 1) ? rp[wr + c16] : -1;
