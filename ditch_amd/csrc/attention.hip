@@ -196,7 +196,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     auto stage_v = [&](int64_t b, int64_t c0, int64_t kmax) {
         const float *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
         for (int i = threadIdx.x; i < (AK / 2) * (VD / 4); i += nthreads) {
-            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const int kp = i % (AK / 2), d = (i / (AK / 2)) * 4;
             const int64_t p = c0 + 2 * kp;
             float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
             if (p <= kmax) v0 = *(const float4 *)(vb + p * a.kvd + d);
@@ -210,13 +210,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             }
         }
     };
-    // values of the same keys: item = (key pair, 4 dims), written transposed [dim][key]
+    // values of the same keys: item = (key pair, 4 dims), written transposed
+    // [dim][key]; the key pair runs fastest over the lanes, so the 64 lanes'
+    // 32-bit writes of a wave fall in 64 distinct banks
     auto load_v = [&](int64_t b, int64_t c0, int64_t kmax) {
         const float *vb = a.vc + (b * a.T) * a.kvd + hkv * a.hd;
 #pragma unroll
         for (int t = 0; t < VI; t++) {
             const int i = threadIdx.x + t * nthreads;
-            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const int kp = i % (AK / 2), d = (i / (AK / 2)) * 4;
             const int64_t p = c0 + 2 * kp;
             vr[t][0] = vr[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < (AK / 2) * (VD / 4)) {
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int t = 0; t < VI; t++) {
             const int i = threadIdx.x + t * nthreads;
             if (i >= (AK / 2) * (VD / 4)) continue;
-            const int kp = i / (VD / 4), d = (i % (VD / 4)) * 4;
+            const int kp = i % (AK / 2), d = (i / (AK / 2)) * 4;
             const float x0[4] = {vr[t][0].x, vr[t][0].y, vr[t][0].z, vr[t][0].w};
             const float x1[4] = {vr[t][1].x, vr[t][1].y, vr[t][1].z, vr[t][1].w};
 #pragma unroll
