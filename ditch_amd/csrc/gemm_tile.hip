@@ -1472,14 +1472,31 @@ void launch_tile_gemm_grouped(const GroupSeg *d_segs, const GroupSeg *h_segs, un
 void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const GroupSeg *h_gate,
                              const GroupSeg *h_up, unsigned nseg, uint32_t act, float *out, void *xs_out,
                              int64_t ldk_out, const float *x, int64_t ldx, const int32_t *row_index, DevBuf *ws,
-                             DevBuf *meta, hipStream_t s) {
+                             DevBuf *meta, hipStream_t s, int64_t n_tok) {
     DITCH_CHECK(tile_glu_takes(h_gate[0].w, h_up[0].w, 128), DITCH_INVALID_ARGUMENT,
                 "grouped GLU: gate and up must share format and shape");
     DITCH_CHECK(!xs_out || ldk_out * 32 >= h_gate[0].w.rows, DITCH_INVALID_ARGUMENT,
                 "grouped GLU: output fragments too short");
-    const GroupedPlan g = grouped_plan(h_gate, nseg, x, ldx, row_index, nullptr, ws, meta, s);
+    // the tokens' terms once, token-major, for the tiles to gather
+    const bool tok = n_tok > 0 && h_gate[0].w.tf != TF_Q8;
+    const int64_t kt0 = split_k_tiles(h_gate[0].w);
+    void *xt = nullptr;
+    if (tok) {
+        xt = ws->get<uint8_t>((size_t)(n_tok * kt0 * 2 * 64));
+        const int64_t total = n_tok * kt0 * 4;
+        hipLaunchKernelGGL(split_tok_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (u32x4 *)xt, x,
+                           n_tok, ldx, h_gate[0].w.cols, kt0);
+        DITCH_TRY_HIP(hipGetLastError());
+    }
+    const GroupedPlan g = grouped_plan(h_gate, nseg, x, ldx, row_index, xt, ws, meta, s);
     if (g.blocks == 0) return;
     TileGemmParams p{};
+    if (tok) {
+        p.a_tok = (const u32x4 *)xt;
+        p.a_prow = g.dm;
+        p.a_map = row_index;
+        p.a_tok_stride = kt0 * 2 * 64;
+    }
     p.w = h_gate[0].w;
     p.w2 = h_up[0].w;
     p.act = act;

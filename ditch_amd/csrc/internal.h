@@ -360,11 +360,14 @@ void launch_tile_gemm_grouped_dev(const GroupSeg *d_segs, const TileView &w0, fl
                                   const float *delta_xa = nullptr, int delta_stride = 0);
 // Routed gate/up in one tiled product: act(x gate_z^T) * (x up_z^T) per
 // segment z, as f32 rows of out (may be NULL) and as the down product's
-// activation fragments xs_out (ldk_out k tiles, grouped row order)
+// activation fragments xs_out (ldk_out k tiles, grouped row order). n_tok >
+// 0: x holds n_tok token rows, split once token-major and gathered per pair
+// by the tiles (cheaper than splitting every pair's row when the segments
+// cover at least n_tok pairs).
 void launch_tile_glu_grouped(const GroupSeg *d_gate, const GroupSeg *d_up, const GroupSeg *h_gate,
                              const GroupSeg *h_up, unsigned nseg, uint32_t act, float *out, void *xs_out,
                              int64_t ldk_out, const float *x, int64_t ldx, const int32_t *row_index, DevBuf *ws,
-                             DevBuf *meta, hipStream_t s);
+                             DevBuf *meta, hipStream_t s, int64_t n_tok = 0);
 
 // attention.hip: prompt attention (model.zig:2935-2986) on the fp32 MFMA for
 // the head shapes it takes; q [n][heads][hd], caches [prompt][T][kvd], out

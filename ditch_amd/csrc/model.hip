@@ -1273,8 +1273,11 @@ static void moe_forward(ditch_hip_model *m, Layer &L, float *x, const float *h, 
         if (fused) {
             const int64_t ldk_d = split_k_tiles(vd);
             void *fr = m->acts.get<uint8_t>(split_bytes_ldk(grouped_blocks(sg.data(), nseg) * 16, ldk_d, 2));
+            // a chunk of at least n pairs: the n token rows split once and gathered
+            const int64_t chunk_pairs = (int64_t)sg[nseg - 1].off + sg[nseg - 1].cnt - sg[0].off;
             launch_tile_glu_grouped(dsegs, dsegs + nseg, sg.data(), su.data(), nseg, 0, max_rank > 0 ? gate : nullptr,
-                                    fr, ldk_d, h, hidden, pair_token, &m->xsplit, &m->gmeta, s);
+                                    fr, ldk_d, h, hidden, pair_token, &m->xsplit, &m->gmeta, s,
+                                    chunk_pairs >= n ? n : 0);
             dfr = fr;
         } else {
             launch_matmul_grouped(dsegs, sg.data(), nseg, vg.tf, inter, hidden, max_cnt, gate, h, pair_token, nullptr, 0,
