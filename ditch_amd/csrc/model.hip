@@ -1412,7 +1412,13 @@ void model_forward(ditch_hip_model *m, const uint32_t *d_tokens, const ditch_row
             launch_rmsnorm_split_mx(hm, ldst, nullptr, x, L.attn_norm.p, L.attn_norm.len, n, hidden, c.rms_eps, 0, s);
             hact = Act{nullptr, nullptr, 0, hm, ldst};
         } else if (frags) {
-            const bool f32_needed = c.mla || !frag_only(L.q, n) || !frag_only(L.k, n) || !frag_only(L.v, n);
+            // the f32 rows only for a product that cannot take the fragments
+            // alone (MLA: q_a and kv_a, or q_b without a q_a; an MXFP4 one
+            // keeps its scaled-MFMA path, which splits the f32 rows itself)
+            const Mat &mq = L.q_a.ok() ? L.q_a : L.q_b;
+            const bool f32_needed =
+                c.mla ? !frag_only(L.kv_a, n) || !frag_only(mq, n) || mx_only(L.kv_a, n) || mx_only(mq, n)
+                      : !frag_only(L.q, n) || !frag_only(L.k, n) || !frag_only(L.v, n);
             void *hs = m->hs.get<uint8_t>(split_bytes_ldk(n, ldk_h, 2));
             launch_rmsnorm_split(hs, ldk_h, f32_needed ? h : nullptr, x, L.attn_norm.p, L.attn_norm.len, n, hidden,
                                  c.rms_eps, 0, s);
