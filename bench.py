@@ -30,7 +30,8 @@ Beside it, in the same JSON line:
   c5           - configs[4] (`--no-c5` skips it; skipped with the reason when
                  host memory is short): DeepSeek-V3-shaped FP8, 12 layers,
                  256 experts streamed through a 96 GB HBM cache, 16 x 256
-                 tokens;
+                 tokens, with its CPU baseline (a one-prompt sample of the
+                 dense and the first routed layer, scaled);
   cpu_baseline - the CPU oracle (oracle/cpu_ref.c, built -march=native on
                  this host) on a sample of the benchmark's prompts at the
                  full depth, with the GPU's logits compared on that sample.
@@ -209,7 +210,7 @@ def c4_spec(layers, distinct=4, seed=21):
     return spec
 
 
-def c5_spec(distinct_experts=8, seed=5):
+def c5_spec(distinct_experts=8, seed=5, layers=None):
     """DeepSeek-V3-shaped first 12 layers (d 7168, MLA q_lora
     1536 / kv_lora 512 / nope 128 / rope 64 / v 128 over 128 heads, 3 dense
     layers of FFN 18432, then 256 routed experts of FFN 2048 top-8 of 8
@@ -223,7 +224,7 @@ def c5_spec(distinct_experts=8, seed=5):
     c = C5
     rng = np.random.default_rng(seed)
     h, nh, hd = c["hidden"], c["heads"], c["nope"] + c["rope"]
-    E, mi, V, L = c["experts"], c["moe_inter"], c["vocab"], c["layers"]
+    E, mi, V, L = c["experts"], c["moe_inter"], c["vocab"], layers or c["layers"]
     moe = [0] * c["dense_layers"] + [1] * (L - c["dense_layers"])
     spec = ModelSpec(hidden=h, inter=c["dense_ff"], layers=L, heads=nh, kv_heads=nh, head_dim=hd,
                      v_head_dim=c["v_dim"], vocab=V, rms_eps=1e-6, tie_embeddings=0, rope_theta=10000.0,
@@ -593,6 +594,48 @@ def c4_cpu_leg(spec, cfg, fwd, layers_run=4):
             "cpu_seconds": round(secs, 2)}
 
 
+def c5_cpu_leg(layers_run=4):
+    """The oracle on configs[4]'s first prompt (256 tokens) through its first
+    `layers_run` layers (the 3 dense layers and the first routed one; FP8
+    experts kept packed and decoded per use, the reference's streamed mode),
+    scaled to a step's 16 prompts and 12 layers: tokens/s on this host's
+    cores. A prompt is the unit: each one's routed layer decodes the experts
+    it uses again (about 8 tokens an expert), so the figure is that of a
+    prompt-at-a-time CPU run, not of one batch over all 16."""
+    from oracle import ref as oref
+    c = C5
+    cores = cpu_share()
+    spec = c5_spec(layers=layers_run)
+    tokens, rows, last = make_batch(dict(prompts=c["prompts"], tokens=c["tokens"], vocab=c["vocab"]))
+    T = c["tokens"]
+    with tempfile.TemporaryDirectory() as d:
+        so = os.path.join(d, "libcpu_ref_native.so")
+        try:
+            oref.build(so, arch="native")
+        except Exception:
+            so = oref.LIB
+        m = oref.RefModel(spec, path=so, threads=cores, keep_packed=True)
+        dense = c["dense_layers"]
+        times = []
+        for hi in (dense, layers_run):  # the dense layers alone, then with the routed one
+            m.limit_layers(0, hi)
+            t0 = time.perf_counter()
+            m.forward(tokens[:T], [tuple(x) for x in rows[:T]], capture_rows=[T - 1], logit_rows=[T - 1])
+            times.append(time.perf_counter() - t0)
+        m.free()
+    t_dense, t_all = times
+    routed = (t_all - t_dense) / (layers_run - dense)  # one routed layer of one prompt
+    full = c["prompts"] * (t_dense + routed * (c["layers"] - dense))
+    return {"value": round(c["prompts"] * T / full, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": (f"oracle/cpu_ref.c -O3 -march=native, {cores} threads: 1 prompt x {T} tokens through its "
+                       f"{dense} dense layers ({t_dense:.1f}s) and through those and the first routed layer "
+                       f"({t_all:.1f}s), both with lm_head; the routed layer's time taken for each of the "
+                       f"{c['layers'] - dense}, scaled to {c['prompts']} prompts; FP8 experts decoded per use, "
+                       "again for each prompt"),
+            "cpu_seconds": round(t_dense + t_all, 2)}
+
+
 def c2_cpu_leg(reps_s=2.0):
     """The oracle's dequant-fused matmulT (tensor.zig:827-913 restated) on
     configs[1]'s Q8_0 14336 x 4096 weight for each M, on this host's cores."""
@@ -825,6 +868,8 @@ def main():
     ap.add_argument("--no-c1", action="store_true")
     ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c4-layers", type=int, default=48)
+    ap.add_argument("--c5-cpu", action="store_true", help="with --kernel-only c5: also time the oracle on a C5 "
+                    "sample (one prompt through the dense layers, then with the first routed layer)")
     ap.add_argument("--no-c5", action="store_true", help="skip configs[4] (it pins ~48 GB and holds ~100 GB of "
                                                          "host memory)")
     ap.add_argument("--no-trial", action="store_true", help="skip the decode / residual-mean / apply timings")
@@ -865,7 +910,10 @@ def main():
         print(json.dumps({"kernel_only": "c4", "c4": c4_leg(dev, args.steps, args.warmup, args.c4_layers)}))
         return
     if args.kernel_only == "c5":
-        print(json.dumps({"kernel_only": "c5", "c5": c5_leg(dev, args.steps, args.warmup)}))
+        c5 = c5_leg(dev, args.steps, args.warmup)
+        if args.c5_cpu:
+            c5["cpu_baseline"] = c5_cpu_leg()
+        print(json.dumps({"kernel_only": "c5", "c5": c5}))
         return
 
     head = forward_leg(dev, fmt, cfg, args.steps, args.warmup)
@@ -907,6 +955,9 @@ def main():
             c5 = c5_leg(dev, args.steps, args.warmup)
             log(f"c5: {c5['ms_per_step']} ms/step ({c5['tokens_per_s']} tokens/s), host->HBM "
                 f"{c5['host_to_hbm_GB_s_over_step']} GB/s over the step")
+            if not args.no_cpu:
+                c5["cpu_baseline"] = c5_cpu_leg()
+                log(f"c5 cpu baseline: {c5['cpu_baseline']['value']} tokens/s ({c5['cpu_baseline']['cpu_seconds']}s)")
     cpu, parity = None, None
     if not args.no_cpu:
         t0 = time.time()
