@@ -1237,6 +1237,11 @@ __global__ void ksplit_reduce_kernel(TileGemmParams p) {
 static int tile_ksplit(int64_t tiles, int64_t stages) {
     int ks = 1;
     while (ks < 8 && tiles * ks < 256 && stages / (2 * ks) >= 4) ks *= 2;
+    // a last round of workgroups at most half full on a long K (C5's o and
+    // dense down products, 896 tiles of 256-288 stages): two parts fill
+    // whole rounds, and the partial sums' reduce costs less than the idle
+    // half round
+    if (ks == 1 && tiles > 256 && tiles % 256 != 0 && tiles % 256 <= 128 && stages >= 128) ks = 2;
     return ks;
 }
 
