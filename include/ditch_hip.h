@@ -447,11 +447,13 @@ typedef struct ditch_expert_cache_stats {
     uint64_t warmed;      /* experts copied in by ditch_hip_model_warm_experts */
     uint64_t bytes_staged; /* of bytes_read, through the pinned staging ring  */
 } ditch_expert_cache_stats;
-/* The experts' host copies are pinned up to 48 GiB per model (the
- * environment variable DITCH_HIP_EXPERT_PINNED_LIMIT, in bytes, read at
- * registration, overrides it) and while pinning succeeds; the rest stay in
- * pageable memory and reach the cache through a small pinned staging ring,
- * as stream.zig's pinned buffers feed the reference's expert cache.
+/* The experts' host copies are pinned up to 48 GiB per model, shared
+ * evenly by its routed layers (the environment variable
+ * DITCH_HIP_EXPERT_PINNED_LIMIT, in bytes, read at registration, overrides
+ * the total) and while pinning succeeds; the rest stay in pageable memory
+ * and reach the cache through a small pinned staging ring, as stream.zig's
+ * pinned buffers feed the reference's expert cache. Refills prefer pinned
+ * experts, and copies ahead spread a cache's shortfall over the layers.
  * Zeros before the first forward of a streaming model. An expert copied in
  * ahead of its use (prefetched or warmed) counts as a miss at its first use
  * (expert_cache.zig:403-410).                                              */
