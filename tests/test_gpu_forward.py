@@ -95,6 +95,10 @@ SYNTH = {
     # final norm through the logit rows' index, MLA's q_a norm in place)
     "dense_bf16_h512": lambda: mg.dense("bf16", hidden=512, inter=1024, heads=8, kv_heads=2, head_dim=64),
     "mla_fp8_qlora512": lambda: mg.mla("fp8", q_lora=512),
+    # head widths that are not multiples of 4 (kv_a 82 rows): the keys and
+    # values assembled per head and rotated by the general RoPE kernel, not
+    # the float4 cache kernel; head_dim 48 on the per-row attention
+    "mla_fp8_odd_widths": lambda: mg.mla("fp8", nope=30, rope=18, v_dim=30),
     "moe_int4_repeated_selections": lambda: mg.moe("int4", experts=8, top_k=4, sigmoid=True, n_group=4,
                                                    topk_group=1),
 }
