@@ -1220,12 +1220,33 @@ void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n,
 // out[t][r] = sum over the split-K parts (in part order) + delta + bias (+ out)
 __global__ void ksplit_reduce_kernel(TileGemmParams p) {
     const int64_t rows = p.w.rows, total = p.n * rows;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const TileOut to{p.out, p.ldo, p.n, rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
+                     p.delta_stride};
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    if (rows % 4 == 0) {
+        // four consecutive outputs of one token a thread: 16-byte loads of
+        // every part, one division for the four
+        for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 4 * j < total; j += step) {
+            const int64_t i = 4 * j, t = i / rows, r = i % rows;
+            float4 v = *(const float4 *)(p.part + i);
+            for (int k = 1; k < p.ksplit; k++) {
+                const float4 w = *(const float4 *)(p.part + (int64_t)k * total + i);
+                v.x = __fadd_rn(v.x, w.x);
+                v.y = __fadd_rn(v.y, w.y);
+                v.z = __fadd_rn(v.z, w.z);
+                v.w = __fadd_rn(v.w, w.w);
+            }
+            tile_store(to, t, r, v.x);
+            tile_store(to, t, r + 1, v.y);
+            tile_store(to, t, r + 2, v.z);
+            tile_store(to, t, r + 3, v.w);
+        }
+        return;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
         const int64_t t = i / rows, r = i % rows;
         float v = p.part[i];
         for (int k = 1; k < p.ksplit; k++) v = __fadd_rn(v, p.part[(int64_t)k * total + i]);
-        const TileOut to{p.out, p.ldo, p.n, rows, p.bias, p.accumulate, p.delta_b, p.delta_xa, p.delta_rank,
-                         p.delta_stride};
         tile_store(to, t, r, v);
     }
 }
