@@ -46,6 +46,11 @@ struct SplitParams {
     int64_t n, ldx, K;
     int64_t kt_total;  // k tiles per 16-token block (the fragments' ldk)
     int64_t m16;       // 16-token blocks
+    // optional: a delta's A [rank][K]; each 32-column k tile's x . A^T
+    // partial sums go to xa_part [n][kt_total][rank]
+    const float *da = nullptr;
+    float *xa_part = nullptr;
+    int rank = 0;
 };
 
 template <int XT>
@@ -79,10 +84,41 @@ __global__ __launch_bounds__(256) void split_kernel(SplitParams p) {
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = 0.f;
     }
+    if (p.xa_part) {
+        // the k tile's x . A^T: each lane's 8 products in column order, then
+        // its k quarters added pairwise ((q0 + q1) + (q2 + q3))
+        for (int j = 0; j < p.rank; j++) {
+            const float *aj = p.da + (int64_t)j * p.K + k0;
+            float s = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) s = __builtin_fmaf(v[q], k0 + q < p.K ? aj[q] : 0.f, s);
+            s = __fadd_rn(s, __shfl_xor(s, 16, 64));
+            s = __fadd_rn(s, __shfl_xor(s, 32, 64));
+            if ((lane >> 4) == 0 && tok < p.n) p.xa_part[(tok * p.kt_total + kt) * p.rank + j] = s;
+        }
+    }
     u32x4 w[XT];
     a_words<false, XT>(v, w);
 #pragma unroll
     for (int e = 0; e < XT; e++) p.xs[(f * XT + e) * 64 + lane] = w[e];
+}
+
+// xa[t][j] = the k tiles' partial sums of split_kernel, one wave a token:
+// lane l adds tiles l, l + 64, ... in order, then the lanes' sums are added
+// pairwise (xor 32, 16, .., 1)
+__global__ __launch_bounds__(256) void xa_tiles_reduce_kernel(float *xa, const float *part, int64_t n,
+                                                              int64_t kt_total, int rank) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= n) return;
+    const float *pp = part + t * kt_total * rank;
+    for (int j = 0; j < rank; j++) {
+        float s = 0.f;
+        for (int64_t kt = lane; kt < kt_total; kt += 64) s = __fadd_rn(s, pp[kt * rank + j]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 64));
+        if (lane == 0) xa[t * rank + j] = s;
+    }
 }
 
 // Token-major activation terms for the routed products: out[token][k tile]
@@ -1205,6 +1241,31 @@ int64_t split_k_tiles(const TileView &w) {
 bool tile_gemm_takes(const TileView &w, int64_t n) {
     if (!w.fast || n < 32) return false;
     return w.tf == TF_BF16 || w.tf == TF_MX4 || w.tf == TF_FP8 || w.tf == TF_INT4 || w.tf == TF_Q8;
+}
+
+bool launch_matmul_delta_split(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
+                               const float *da, int rank, float *xa, hipStream_t s, DevBuf *ws) {
+    if (!ws || ep.exact || rank <= 0 || mx_gemm_takes(w, n) || !tile_gemm_takes(w, n)) return false;
+    const int64_t ldk = split_k_tiles(w);
+    const size_t xb = (split_bytes_ldk(n, ldk, 2) + 255) & ~(size_t)255;
+    const size_t pb = tile_part_bytes(w, n, 2);
+    const size_t qb = ((size_t)n * ldk * rank * 4 + 255) & ~(size_t)255;
+    if (ws->borrowed && xb + pb + qb > ws->bytes) return false;
+    uint8_t *xs = ws->get<uint8_t>(xb + pb + qb);
+    float *xpart = (float *)(xs + xb + pb);
+    SplitParams sp{(u32x4 *)xs, x, nullptr, nullptr, n, w.cols, w.cols, ldk, (n + 15) / 16};
+    sp.da = da;
+    sp.xa_part = xpart;
+    sp.rank = rank;
+    const int64_t total = sp.m16 * ldk * 64;
+    hipLaunchKernelGGL(split_kernel<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp);
+    DITCH_TRY_HIP(hipGetLastError());
+    hipLaunchKernelGGL(xa_tiles_reduce_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, xa, xpart, n, ldk, rank);
+    DITCH_TRY_HIP(hipGetLastError());
+    MatmulEpilogue e2 = ep;
+    e2.delta_xa = xa;
+    launch_tile_gemm(w, out, w.rows, xs, ldk, n, 2, e2, s, pb ? (float *)(xs + xb) : nullptr);
+    return true;
 }
 
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,

@@ -266,6 +266,13 @@ inline int64_t split_ldk(int64_t K) { return (K + 127) / 128 * 4; }
 inline size_t split_bytes_ldk(int64_t n, int64_t ldk, int xt) { return (size_t)((n + 15) / 16) * ldk * xt * 1024; }
 void launch_split(void *xs, const float *x, const int32_t *row_index, int64_t n, int64_t ldx, int64_t K,
                   int64_t ldk, int xt, hipStream_t s);
+// The tiled product over f32 rows x with a delta (ep.delta_b, ep.delta_rank)
+// whose x . A^T the activation split forms on the way (one partial sum per
+// 32-column k tile, added by a wave per token into xa [n][rank]): one pass
+// over x instead of two. False
+// (nothing launched) when the tiled product does not take w.
+bool launch_matmul_delta_split(const TileView &w, float *out, const float *x, int64_t n, const MatmulEpilogue &ep,
+                               const float *da, int rank, float *xa, hipStream_t s, DevBuf *ws);
 // part: f32 scratch of tile_part_bytes(w, n, xt) bytes for split-K partial
 // sums (NULL: no split)
 size_t tile_part_bytes(const TileView &w, int64_t n, int xt);

@@ -1085,6 +1085,13 @@ static void mm_act(ditch_hip_model *m, const Mat &mt, float *out, const Act &x, 
     if (mt.rank > 0) {
         DITCH_CHECK(x.f32, DITCH_INVALID_ARGUMENT, "forward: a delta needs the f32 activation");
         float *xa = m->xa.get<float>((size_t)n * mt.rank);
+        if (!x.xs && !x.xm) {
+            // the split of the f32 rows forms x . A^T on the way
+            MatmulEpilogue e2 = ep;
+            e2.delta_b = mt.db;
+            e2.delta_rank = mt.rank;
+            if (launch_matmul_delta_split(mt.t->v, out, x.f32, n, e2, mt.da, mt.rank, xa, s, &m->xsplit)) return;
+        }
         launch_delta_xa(xa, x.f32, mt.da, n, mt.t->v.cols, mt.rank, s);
         ep.delta_b = mt.db;
         ep.delta_xa = xa;
