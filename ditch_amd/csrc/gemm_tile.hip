@@ -234,7 +234,7 @@ __device__ __forceinline__ void tile_store(const TileOut &p, int64_t tok, int64_
     if (p.delta_rank > 0) {
         float d = 0.f;
         for (int j = 0; j < p.delta_rank; j++)
-            d = __fadd_rn(d, __fmul_rn(p.delta_b[row * p.delta_rank + j], p.delta_xa[tok * p.delta_stride + j]));
+            d = __builtin_fmaf(p.delta_b[row * p.delta_rank + j], p.delta_xa[tok * p.delta_stride + j], d);
         v = __fadd_rn(v, d);
     }
     if (p.bias) v = __fadd_rn(v, p.bias[row]);
@@ -324,7 +324,7 @@ __device__ __forceinline__ void tile_store_block(const TileOut &p, const int64_t
 #pragma unroll
                         for (int i = 0; i < NI; i++)
 #pragma unroll
-                            for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[jj][i], xj[jj][r]));
+                            for (int r = 0; r < 4; r++) d[i][r] = __builtin_fmaf(bj[jj][i], xj[jj][r], d[i][r]);
                     }
                 }
             } else {
@@ -337,7 +337,7 @@ __device__ __forceinline__ void tile_store_block(const TileOut &p, const int64_t
 #pragma unroll
                     for (int i = 0; i < NI; i++)
 #pragma unroll
-                        for (int r = 0; r < 4; r++) d[i][r] = __fadd_rn(d[i][r], __fmul_rn(bj[i], xj[r]));
+                        for (int r = 0; r < 4; r++) d[i][r] = __builtin_fmaf(bj[i], xj[r], d[i][r]);
                 }
             }
 #pragma unroll
